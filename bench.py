@@ -1,0 +1,278 @@
+#!/usr/bin/env python3
+"""Benchmark of the S6 latent decode-attention path on one MI355X (Ouro-1.4B shape, B = 64, context 8192).
+
+One step = the attention path of one full S6 decode step: 24 layers x 4 loops, each loop running the absorbed query
+(A_t GEMM + latent RoPE), the exact window over the last 32 tokens plus the current one, the paged latent history
+(loop 0 reads the 256-wide loop-1 latent, loops 1-3 the 512-wide main latent), the B_t projection and the LSE merge.
+Inputs are synthetic and random-init, resident in HBM before timing; the whole step is captured once in a HIP graph
+and replayed. Prints one JSON line (the value is microseconds per layer = step time / 24; lower is better).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = 'latent decode-attn µs/layer + HBM GB/s (% peak), Ouro-1.4B S6, B=64 ctx 8K'
+PEAK_HBM_GBPS = 8000.0
+LAYERS, LOOPS, HEADS, HEAD_DIM, RANK, RANK1, WINDOW, BLOCK = 24, 4, 16, 128, 512, 256, 32, 16
+MAX_POSITION = 65536
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument('--gpus', type=int, default=1)
+    p.add_argument('--steps', type=int, default=20)
+    p.add_argument('--warmup', type=int, default=3)
+    p.add_argument('--batch', type=int, default=64)
+    p.add_argument('--context', type=int, default=8192, help='history tokens before the decoded token')
+    p.add_argument('--splits', type=int, default=0, help='KV splits (0: the MI355X policy)')
+    p.add_argument('--kernel-only', action='store_true', help='only launch the main-latent history op (profiling)')
+    p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--seed', type=int, default=0)
+    return p.parse_args()
+
+
+class Workload:
+    """Random-init caches, tables and readers of the whole model's attention path (one decode step of B rows)."""
+
+    def __init__(self, ops, layer, B, hist, splits, seed, device):
+        g = torch.Generator(device=device).manual_seed(seed)
+        self.B, self.hist, self.device = B, hist, device
+        self.seq_len = hist + 1                                   # the decoded token is already in the exact cache
+        self.n_latent = max(hist - WINDOW, 0)
+        cols = -(-self.seq_len // BLOCK)
+        self.cols = cols
+        pool = B * cols + 1                                       # page 0: the null page
+        randn = lambda *shape, std=1.0: (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std
+                                         ).to(torch.bfloat16)
+        perm = lambda n: (torch.randperm(n - 1, generator=g, device=device) + 1).to(torch.int32)
+        self.lat_table = {RANK: perm(pool)[:B * cols].view(B, cols).contiguous(),
+                          RANK1: perm(pool)[:B * cols].view(B, cols).contiguous()}
+        self.lat = []
+        for _ in range(LAYERS):
+            self.lat.append({w: torch.empty(pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(
+                generator=g) for w in (RANK, RANK1)})
+        # exact caches: a sliding window of W + 1 rows per request and loop; freed pages are the null page
+        first_col, last_col = max(0, self.seq_len - 1 - WINDOW) // BLOCK, (self.seq_len - 1) // BLOCK
+        win_cols = last_col - first_col + 1
+        ex_pool = B * win_cols + 1
+        self.ex_table = []
+        for _ in range(LOOPS):
+            t = torch.zeros(B, cols, dtype=torch.int32, device=device)
+            t[:, first_col:last_col + 1] = perm(ex_pool)[:B * win_cols].view(B, win_cols)
+            self.ex_table.append(t)
+        self.exact = [[randn(ex_pool, HEADS, BLOCK, 2 * HEAD_DIM) for _ in range(LOOPS)] for _ in range(LAYERS)]
+        std = 1 / math.sqrt(2048)
+        self.readers = [_Reader(randn(HEADS, HEAD_DIM, RANK1, std=std), randn(HEADS, RANK1, HEAD_DIM, std=std),
+                                randn(3, HEADS, HEAD_DIM, RANK, std=std), randn(3, HEADS, RANK, HEAD_DIM, std=std))
+                        for _ in range(LAYERS)]
+        inv = layer.latent_inv_freq(HEAD_DIM, 1e6).to(device)
+        self.tables = {w: layer.latent_rope_table(MAX_POSITION, inv, w, torch.bfloat16) for w in (RANK, RANK1)}
+        self.q_pre = [randn(B, HEADS, HEAD_DIM) for _ in range(LOOPS)]
+        self.q_rope = [randn(B, HEADS, HEAD_DIM) for _ in range(LOOPS)]
+        self.positions = torch.full((B,), hist, dtype=torch.int64, device=device)
+        self.qsl = torch.arange(B + 1, dtype=torch.int32, device=device)
+        self.seq_lens = torch.full((B,), self.seq_len, dtype=torch.int32, device=device)
+        self.splits = splits
+        self.workspace = ops.S6Workspace(HEADS, RANK, B * splits)
+        self.ops, self.layer = ops, layer
+
+    def step(self):
+        ops, layer = self.ops, self.layer
+        ctx = layer.StepContext(self.positions, self.qsl, self.seq_lens, 1, self.B, self.tables, HEAD_DIM ** -0.5,
+                                ops.HIP_BACKENDS, self.workspace, self.splits, window=WINDOW,
+                                max_seqlen_k=self.seq_len)
+        outs = []
+        for loop in range(LOOPS):
+            w = RANK1 if loop == 0 else RANK
+            for i in range(LAYERS):
+                sl = self.readers[i]
+                q_lat = ctx.latent_query(sl, loop, self.q_pre[loop])
+                outs.append(layer.attend(sl, loop, q_lat, self.q_rope[loop], None, None, self.lat[i][w],
+                                         self.lat_table[w], None, None, ctx, (self.exact[i][loop], self.ex_table[loop])))
+        return outs
+
+    def history_bytes_per_layer(self):
+        return self.B * self.n_latent * (2 * RANK1 + 3 * 2 * RANK) * 2
+
+    def window_bytes_per_layer(self):
+        keys = min(self.seq_len, WINDOW + 1)
+        return self.B * LOOPS * keys * HEADS * 2 * HEAD_DIM * 2
+
+
+class _Reader:
+    def __init__(self, A1, B1, A, B):
+        self.A1, self.B1, self.A, self.B = A1, B1, A, B
+        self.rank1, self.rank, self.loops = RANK1, RANK, LOOPS
+
+    def readers(self, loop):
+        return (self.A1, self.B1, RANK1) if loop == 0 else (self.A[loop - 1], self.B[loop - 1], RANK)
+
+
+def time_graph(fn, steps, warmup):
+    """Capture ``fn`` in a HIP graph, replay ``warmup`` times untimed, then time ``steps`` replays with events."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def history_op_roofline(wl, iters=50):
+    """Average duration of the main-latent history attention op (history_split + history_combine launches), timed
+    with HIP events on the stream it runs on, and the algorithmic bytes it reads."""
+    ops = wl.ops
+    ctx_lat = torch.full((wl.B,), wl.n_latent, dtype=torch.int32, device=wl.device)
+    q = torch.randn(wl.B, HEADS, RANK, device=wl.device).to(torch.bfloat16) * (RANK ** -0.5)
+    layers = [wl.lat[i][RANK] for i in range(LAYERS)]
+
+    def run(i):
+        return ops.history_attention(q, layers[i % LAYERS], wl.lat_table[RANK], ctx_lat, HEAD_DIM ** -0.5, wl.splits,
+                                     wl.workspace, None, None, 'hip')
+
+    for i in range(5):
+        run(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(iters):
+        run(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000 / iters
+    nbytes = wl.B * wl.n_latent * 2 * RANK * 2
+    return us, nbytes
+
+
+def cpu_baseline(wl, tokens=8):
+    """The numpy oracle of one main loop and one loop-1 call of a layer on ``tokens`` rows of the same workload,
+    scaled to B rows x (1 + 3) loops: microseconds per layer on the host cores."""
+    from oracle import bf16, s6_oracle as O
+    cores = len(os.sched_getaffinity(0))
+    B, n, hist = wl.B, wl.n_latent, wl.hist
+    idx = torch.arange(tokens, device=wl.device)
+    timings = {}
+    for w in (RANK, RANK1):
+        layer0 = wl.lat[0][w]
+        pages = wl.lat_table[w][:tokens, :-(-n // BLOCK)].long()
+        rows = layer0[pages.reshape(-1), 0].view(tokens, -1, 2 * w)[:, :n]       # [tokens, n, 2w] gathered on GPU
+        rows_h = rows.float().cpu().numpy().reshape(tokens * (rows.shape[1] // BLOCK), 1, BLOCK, 2 * w)
+        table = np.arange(tokens * (rows.shape[1] // BLOCK), dtype=np.int32).reshape(tokens, -1)
+        q = (torch.randn(tokens, HEADS, w, device=wl.device) * w ** -0.5).to(torch.bfloat16).float().cpu().numpy()
+        q_rope = wl.q_rope[1][:tokens].float().cpu().numpy()
+        loop = 0 if w == RANK1 else 1
+        _, Bw, _ = wl.readers[0].readers(loop)
+        Bw = Bw.float().cpu().numpy()
+        ex = wl.exact[0][loop]
+        ex_h = ex.float().cpu().numpy()
+        ex_table = wl.ex_table[loop][:tokens].cpu().numpy()
+        qsl = np.arange(tokens + 1)
+        seq = np.full(tokens, wl.seq_len)
+        ctx_lat = np.full(tokens, n)
+
+        def run():
+            return O.attend_decode(q, q_rope, Bw, rows_h[..., :w], rows_h[..., w:], table, ctx_lat, ex_h[..., :HEAD_DIM],
+                                   ex_h[..., HEAD_DIM:], ex_table, qsl, seq, WINDOW, HEAD_DIM ** -0.5,
+                                   np.zeros(tokens, bool))
+        run()
+        reps = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            reps.append(time.perf_counter() - t0)
+        timings[w] = float(np.median(reps))
+        del rows, rows_h
+    per_layer_s = (timings[RANK1] + 3 * timings[RANK]) * B / tokens
+    return {'value': per_layer_s * 1e6, 'unit': 'us/layer', 'cores': cores, 'kind': 'port',
+            'sample': f'numpy oracle of attend_decode (window + latent history + B_t + merge, fp32) on {tokens} of the '
+                      f'{B} rows, one loop-1 call and one main-latent call of layer 0 (median of 3 after 1 warm-up), '
+                      f'scaled x{B // tokens} rows x (1 + 3) loops; extrapolated'}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get('WORLD_SIZE', '1'))
+    if args.gpus != 1 or world != 1:
+        print('bench.py measures one GPU: the S6 decode path shards by sequence with no exchange, and this build has '
+              'no multi-GPU path; run with --gpus 1', file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print('bench.py needs an MI355X GPU', file=sys.stderr)
+        sys.exit(2)
+    pkg = importlib.import_module('hybrid-latent-attention_amd')
+    ops, layer = pkg.s6_ops, pkg.s6_layer
+    device = torch.device('cuda:0')
+    torch.cuda.set_device(device)
+    cus = pkg._lib.device_cus(0)
+    splits = args.splits or ops.mi355x_kv_splits(args.context, args.batch, cus)
+    print(f'bench: building workload B={args.batch} ctx={args.context} splits={splits} cus={cus}', file=sys.stderr,
+          flush=True)
+    wl = Workload(ops, layer, args.batch, args.context, splits, args.seed, device)
+    torch.cuda.synchronize()
+
+    if args.kernel_only:
+        us, nbytes = history_op_roofline(wl, iters=max(args.steps, 1))
+        print(json.dumps({'kernel': 'history_attention main latent', 'us_per_launch': us,
+                          'gbps': nbytes / us / 1e3}), flush=True)
+        return
+
+    print('bench: capturing the decode step', file=sys.stderr, flush=True)
+    ms = time_graph(wl.step, args.steps, args.warmup)
+    us_layer = ms * 1000 / LAYERS
+    hist_bytes, win_bytes = wl.history_bytes_per_layer(), wl.window_bytes_per_layer()
+    layer_gbps = (hist_bytes + win_bytes) / (us_layer * 1e3)
+    print('bench: history op roofline', file=sys.stderr, flush=True)
+    op_us, op_bytes = history_op_roofline(wl)
+    achieved = op_bytes / (op_us * 1e3)
+    base = None
+    if not args.no_cpu_baseline:
+        print('bench: cpu baseline', file=sys.stderr, flush=True)
+        base = cpu_baseline(wl)
+    result = {
+        'metric': METRIC, 'value': round(us_layer, 3), 'unit': 'us/layer', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': False, 'scaling': 'weak',
+        'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic (random-init caches, readers and queries)',
+        'config': {'workload': f'Ouro-1.4B S6 decode attention path, {LAYERS} layers x {LOOPS} loops, '
+                               f'B={args.batch}, context {args.context}, W={WINDOW}, block {BLOCK}',
+                   'global_batch': args.batch, 'seq_len': args.context, 'parallelism': 'none (1 GPU)',
+                   'kv_splits': splits, 'hip_graph': True},
+        'tokens_per_s': round(args.batch / (ms / 1000), 1),
+        'hbm_gbps': round(layer_gbps, 1), 'hbm_frac': round(layer_gbps / PEAK_HBM_GBPS, 4),
+        'bytes_per_layer': {'latent_history': hist_bytes, 'exact_window': win_bytes},
+        'roofline': {'kernel': 'history_attention main latent (history_split + history_combine)', 'bound': 'hbm',
+                     'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
+                     'frac': round(achieved / PEAK_HBM_GBPS, 4), 'traffic': None, 'us_per_launch': round(op_us, 2),
+                     'algorithmic_bytes_per_launch': op_bytes},
+        'cpu_baseline': base,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()

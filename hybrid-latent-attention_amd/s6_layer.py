@@ -1,0 +1,200 @@
+"""S6 attention of one layer x loop on MI355X: the interface of ``hla/vllm_latent/s6_layer.py`` over the HIP ops.
+
+The adapter builds one ``StepContext`` per step and, per layer and loop, calls ``latent_query`` before the
+(in-place) exact RoPE, then ``attend``, ``write_rows`` and ``committed_row``. Latent RoPE reads persistent per-width
+``[max_position, w]`` tables built once by ``latent_rope_table``. Everything here is sync-free and loops over no
+requests; ``sl`` is the layer's ``LatentLayer``-shaped module (``readers(loop)``, ``write1``, ``write_step``,
+``rank``, ``rank1``, ``loops``; ``hla/latent/register.py:28-95``).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, s6_ops
+
+
+def latent_inv_freq(head_dim, theta):
+    """The teacher's ``head_dim/2`` RoPE frequencies (HF/vLLM ``inv_freq``; ``hla/vllm_latent/s6_layer.py:16-18``)."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
+
+
+def latent_rope_table(max_position, inv_freq, width, dtype):
+    """``[max_position, width]`` = ``[cos | sin]`` halves of the latent angles; the teacher frequencies are reused
+    round-robin over the ``width/2`` rotation pairs, angle ``p * inv_freq`` in fp32, then cast
+    (``hla/vllm_latent/s6_layer.py:21-29``)."""
+    pair = torch.arange(width // 2, device=inv_freq.device) % inv_freq.shape[0]
+    angle = torch.arange(max_position, device=inv_freq.device).float()[:, None] * inv_freq[pair][None, :]
+    return torch.cat((angle.cos(), angle.sin()), -1).to(dtype)
+
+
+def latent_query(q_pre_rope, A, positions, table, backend, flat=False):
+    """``[T,H,d]`` pre-RoPE query -> latent-rotated ``[T,H,w]`` (contiguous) = RoPE(einsum('thd,hdr->thr', q, A)).
+
+    One fused HIP launch (absorption GEMM on MFMA with the latent RoPE in its epilogue); follows
+    ``hla/vllm_latent/s6_layer.py:32-40``. ``flat`` is accepted for signature parity: the kernel writes its own
+    contiguous output.
+    """
+    s6_ops._backend('rope', backend)
+    s6_ops._dev(q_pre_rope, A, positions, table)
+    s6_ops._bf16('q_pre_rope', q_pre_rope)
+    s6_ops._bf16('A', A)
+    s6_ops._bf16('table', table)
+    T, H, d = q_pre_rope.shape
+    w = A.shape[-1]
+    if A.shape[:2] != (H, d) or table.shape[1] != w:
+        raise ValueError(f'A {tuple(A.shape)} / table {tuple(table.shape)} do not match q {tuple(q_pre_rope.shape)}')
+    out = torch.empty(T, H, w, dtype=q_pre_rope.dtype, device=q_pre_rope.device)
+    pos = s6_ops._int('positions', positions, torch.int64)
+    _lib.call('hla_s6_absorb', _lib.ptr(q_pre_rope), T, H, d, q_pre_rope.stride(0), q_pre_rope.stride(1), _lib.ptr(A),
+              A.stride(0), A.stride(1), w, _lib.ptr(out), out.stride(0), out.stride(1), _lib.ptr(pos), _lib.ptr(table),
+              table.shape[0], table.stride(0), _lib.stream(out.device))
+    return out
+
+
+def absorb_out(o_lat, B):
+    """``einsum('thr,hrd->thd', o_lat, B)`` on MFMA (the ``B_t`` projection of ``hla/vllm_latent/s6_layer.py:114``)."""
+    s6_ops._bf16('o_lat', o_lat)
+    s6_ops._bf16('B', B)
+    T, H, r = o_lat.shape
+    d = B.shape[-1]
+    out = torch.empty(T, H, d, dtype=o_lat.dtype, device=o_lat.device)
+    _lib.call('hla_s6_absorb', _lib.ptr(o_lat), T, H, r, o_lat.stride(0), o_lat.stride(1), _lib.ptr(B), B.stride(0),
+              B.stride(1), d, _lib.ptr(out), out.stride(0), out.stride(1), None, None, 0, 0, _lib.stream(out.device))
+    return out
+
+
+class StepContext:
+    """Per-step tensors shared by every layer and loop (``hla/vllm_latent/s6_layer.py:43-84``).
+
+    ``query_start_loc=None`` means a metadata-less (profiling) step: one request spanning all tokens, no history and
+    no cache writes (``md_present`` False), workspace still allocated. ``tables`` maps a latent width to its
+    persistent ``[max_position, w]`` RoPE table. Token -> request, ``ctx`` and ``ctx_latent`` come from one HIP
+    launch; all shapes depend only on ``num_tokens`` and host ints; nothing here syncs with the host.
+    """
+
+    def __init__(self, positions, query_start_loc, seq_lens, max_query_len, num_tokens, tables, scale, backends,
+                 workspace=None, num_kv_splits=1, rope_flat=False, window=0, max_seqlen_k=0):
+        device = positions.device
+        self.window, self.max_seqlen_k = window, max_seqlen_k
+        self.positions, self.tables, self.scale, self.backends = positions, tables, scale, backends
+        self.workspace, self.num_kv_splits, self.rope_flat = workspace, num_kv_splits, rope_flat
+        self.history_needed = True
+        self.md_present = query_start_loc is not None
+        if not self.md_present:
+            query_start_loc = torch.tensor([0, num_tokens], dtype=torch.int32, device=device)
+            seq_lens, max_query_len = query_start_loc[1:], num_tokens
+        self.query_start_loc, self.seq_lens, self.max_query_len = query_start_loc, seq_lens, max_query_len
+        qsl = s6_ops._int('query_start_loc', query_start_loc, torch.int32)
+        seq = s6_ops._int('seq_lens', seq_lens, torch.int32)
+        R = qsl.shape[0] - 1
+        self.token_requests = torch.empty(num_tokens, dtype=torch.int64, device=device)
+        self.valid = torch.empty(num_tokens, dtype=torch.bool, device=device)
+        self.ctx = torch.empty(num_tokens, dtype=torch.int32, device=device)
+        self.ctx_latent = torch.empty(num_tokens, dtype=torch.int32, device=device)
+        _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, _lib.ptr(seq), num_tokens, int(window or 0),
+                  _lib.ptr(self.token_requests), _lib.ptr(self.valid), _lib.ptr(self.ctx), _lib.ptr(self.ctx_latent),
+                  None, _lib.stream(device))
+        self.invalid, self.empty = ~self.valid, self.ctx == 0
+        self.empty_latent = self.ctx_latent == 0
+        self._block_tables = {}
+        if workspace is not None:
+            workspace.ensure(device)
+
+    def block_table(self, table):
+        """Per-token gather of a per-request block table, done once per distinct tensor per step."""
+        key = table.data_ptr()
+        if key not in self._block_tables:
+            if table.dtype != torch.int32 or table.stride(-1) != 1:
+                raise ValueError('block tables must be int32 with a unit last stride')
+            T, cols = self.token_requests.shape[0], table.shape[1]
+            out = torch.empty(T, cols, dtype=torch.int32, device=table.device)
+            _lib.call('hla_s6_gather_block_table', _lib.ptr(table), table.stride(0), table.shape[0], cols,
+                      _lib.ptr(self.token_requests), T, _lib.ptr(out), out.stride(0), _lib.stream(table.device))
+            self._block_tables[key] = out
+        return self._block_tables[key]
+
+    def latent_query(self, sl, loop, q_pre_rope):
+        A, _, width = sl.readers(loop)
+        return latent_query(q_pre_rope, A, self.positions, self.tables[width], self.backends.rope, self.rope_flat)
+
+
+def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_scale, ctx, window=None):
+    """One softmax over the paged latent history (fully visible) and the causal current chunk
+    (``hla/vllm_latent/s6_layer.py:87-115``).
+
+    ``q_lat`` comes from ``StepContext.latent_query``; ``q_rope``, ``k_rope``, ``v`` are ``[T,H,d]``; ``cache`` is the
+    layer's ``[num_blocks,1,block,2w]`` tensor or None (no history); ``block_table`` is the per-request table;
+    ``window`` is ``(exact_cache, per-request block_table)`` or None. Returns ``[T,H,d]`` with ``~valid`` rows zeroed.
+    """
+    fused = window is not None and ctx.md_present and ctx.max_query_len == 1
+    if fused:
+        o_chunk, lse_chunk = s6_ops.window_attention_fa(q_rope, window[0], window[1], ctx.query_start_loc, ctx.seq_lens,
+                                                        ctx.window, ctx.scale, ctx.max_seqlen_k, ctx.invalid)
+    else:
+        o_chunk, lse_chunk = s6_ops.chunk_attention(q_rope, k_rope, v, ctx.query_start_loc, ctx.max_query_len,
+                                                    ctx.invalid, ctx.scale, ctx.backends.chunk)
+    if cache is None or not ctx.md_present or not ctx.history_needed:
+        return o_chunk.masked_fill_(ctx.invalid[:, None, None], 0)
+    if window is not None and not fused:
+        o_win, lse_win = s6_ops.window_history_fa(q_rope, window[0], ctx.block_table(window[1]), ctx.ctx, ctx.window,
+                                                  ctx.scale, ctx.max_seqlen_k, ctx.empty)
+        o_chunk, lse_chunk = s6_ops.merge_lse(o_chunk, lse_chunk, o_win, lse_win)
+    _, B, _ = sl.readers(loop)
+    o_hist, lse_hist = s6_ops.history_attention(q_lat, cache, ctx.block_table(block_table), ctx.ctx_latent, ctx.scale,
+                                                ctx.num_kv_splits, ctx.workspace, k_scale, v_scale,
+                                                ctx.backends.history, ctx.empty_latent)
+    o_hist = absorb_out(o_hist, B)
+    return s6_ops.merge_states(o_hist, lse_hist, o_chunk, lse_chunk, ctx.invalid, ctx.backends.merge)
+
+
+@dataclass
+class WriterState:
+    reg: torch.Tensor | None = None
+    first: torch.Tensor | None = None
+
+
+def write_rows(sl, loop, h, state=None):
+    """Writer accumulation on the attention input ``h[T, hidden]`` of this loop (``LatentLayer.write_step``/``write1``;
+    ``hla/vllm_latent/s6_layer.py:124-132``). Loop 0 produces the loop-1 row ``first``; later loops accumulate ``reg``."""
+    if loop == 0:
+        return WriterState(None, sl.write1(h))
+    return WriterState(sl.write_step(h, loop, state.reg), None)
+
+
+def committed_row(sl, loop, state, ctx):
+    """``(key[T,w], value[T,w])`` to store after this loop: loop-1 row at loop 0, main row at the last loop, else None
+    (``hla/vllm_latent/s6_layer.py:135-147``). The K half is rotated in place by the latent RoPE kernel."""
+    if loop == 0:
+        row, width = state.first, sl.rank1
+    elif loop == sl.loops - 1:
+        row, width = state.reg, sl.rank
+    else:
+        return None
+    return s6_ops.latent_rope(row[:, :width], ctx.positions, ctx.tables[width], ctx.backends.rope), row[:, width:]
+
+
+def slot_mapping(ctx, block_table, block_size):
+    """Cache slot per token (``table[req, pos // block] * block + pos % block``, -1 on padding) for the row commit."""
+    T = ctx.token_requests.shape[0]
+    slots = torch.empty(T, dtype=torch.int64, device=block_table.device)
+    pos = s6_ops._int('positions', ctx.positions, torch.int64)
+    _lib.call('hla_s6_slot_mapping', _lib.ptr(block_table), block_table.stride(0), block_table.shape[1],
+              _lib.ptr(ctx.token_requests),
+              _lib.ptr(ctx.valid), _lib.ptr(pos), T, int(block_size), _lib.ptr(slots), _lib.stream(block_table.device))
+    return slots
+
+
+def store_rows(key, value, slots, cache):
+    """Slot-mapped store of ``[key | value]`` rows into a ``[num_blocks, 1, block, 2w]`` latent cache (negative slots
+    skipped): the ``unified_kv_cache_update`` of ``hla/vllm_latent/ouro_latent.py:127-129``."""
+    s6_ops._bf16('key', key)
+    s6_ops._bf16('value', value)
+    s6_ops._bf16('cache', cache)
+    T, w = key.shape
+    if cache.shape[-1] != 2 * w:
+        raise ValueError(f'cache rows are {cache.shape[-1]} wide, rows to store are 2 x {w}')
+    _lib.call('hla_s6_store_rows', _lib.ptr(key), key.stride(0), _lib.ptr(value), value.stride(0), T, w,
+              _lib.ptr(slots), _lib.ptr(cache), cache.stride(0), cache.stride(2), cache.shape[2], cache.shape[0],
+              _lib.stream(cache.device))

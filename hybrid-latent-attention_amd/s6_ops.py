@@ -1,0 +1,369 @@
+"""S6 serving ops on MI355X: the operator interface of ``hla/vllm_latent/s6_ops.py`` over hand-written HIP kernels.
+
+Same names, argument meaning, output layouts and error behaviour as the reference module, with exactly one
+implementation: the gfx950 kernels of ``libhla_s6.so`` (C ABI in ``include/hla_s6.h``). There is no torch
+or CPU path; the only accepted ``backend`` string is ``'hip'`` and any other raises ``ValueError`` as the
+reference does for an unknown backend. Contracts shared by all ops (``hla/vllm_latent/s6_ops.py:1-10``):
+outputs are normalized attention outputs, ``lse`` is a contiguous fp32 ``[H, T]`` natural-log LSE over already
+scaled scores, empty rows give ``lse = -inf`` and ``o = 0``, no NaN leaves a merge. Every op enqueues on the
+current stream, allocates only its outputs (through torch's caching allocator) and never syncs with the host,
+so every op is safe under HIP graph capture.
+"""
+from __future__ import annotations
+
+from collections import namedtuple
+
+import torch
+
+from . import _lib
+
+INF = float('inf')
+HIP = 'hip'
+Backends = namedtuple('Backends', 'history chunk merge rope')
+HIP_BACKENDS = Backends(HIP, HIP, HIP, HIP)
+BF16, I32, I64 = torch.bfloat16, torch.int32, torch.int64
+
+
+def _backend(kind: str, backend: str) -> None:
+    if backend != HIP:
+        raise ValueError(f'Unknown {kind} backend {backend!r}')
+
+
+def _dev(*tensors) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError('S6 ops run on the GPU only; got a tensor on ' + str(t.device))
+
+
+def _bf16(name: str, t: torch.Tensor) -> None:
+    if t.dtype != BF16:
+        raise ValueError(f'{name} must be bfloat16, got {t.dtype}')
+    if t.stride(-1) != 1:
+        raise ValueError(f'{name} needs a unit last-dim stride')
+
+
+def _int(name: str, t: torch.Tensor, dtype) -> torch.Tensor:
+    if t.dtype != dtype:
+        raise ValueError(f'{name} must be {dtype}, got {t.dtype}')
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _mask(t):
+    if t is None:
+        return None
+    if t.dtype != torch.bool:
+        raise ValueError('masks must be torch.bool')
+    return t.contiguous()
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# Latent RoPE (hla/vllm_latent/s6_ops.py:23-58)
+# ----------------------------------------------------------------------------------------------------------------
+
+def latent_rope(x, positions, table, backend):
+    """Neox RoPE of ``x`` IN PLACE by ``table[positions]`` (``[max_position, w] = [cos | sin]``); returns ``x``.
+
+    ``x`` is ``[T, w]``, ``[T, H, w]`` (any token/head stride, unit last stride) or ``[T, H*w]``; ``positions`` int64
+    ``[T]``. Per element: ``x*cos + rotate_half(x)*sin`` with bf16 rounding after each product and the sum, the op
+    order of the torch formula (``hla/vllm_latent/s6_ops.py:32-36``).
+    """
+    _backend('rope', backend)
+    _dev(x, positions, table)
+    _bf16('x', x)
+    _bf16('table', table)
+    w = table.shape[1]
+    T = x.shape[0]
+    if x.dim() == 3:
+        if x.shape[-1] != w:
+            raise ValueError(f'x width {x.shape[-1]} != table width {w}')
+        heads, st, sh = x.shape[1], x.stride(0), x.stride(1)
+    elif x.dim() == 2:
+        if x.shape[1] % w:
+            raise ValueError(f'x width {x.shape[1]} is not a multiple of the table width {w}')
+        heads, st, sh = x.shape[1] // w, x.stride(0), w
+    else:
+        raise ValueError('x must be [T, w], [T, H, w] or [T, H*w]')
+    pos = _int('positions', positions, I64)
+    _lib.call('hla_s6_latent_rope', _lib.ptr(x), T, heads, w, st, sh, _lib.ptr(pos), _lib.ptr(table), table.shape[0],
+              table.stride(0), _lib.stream(x.device))
+    return x
+
+
+def probe_latent_rope(table, heads=2, tokens=3):
+    """Runtime check of the head-stride handling of the RoPE kernel (``hla/vllm_latent/s6_ops.py:44-58``).
+
+    Rotates an einsum-shaped ``[T, H, w]`` view (head stride ``T*w``) and a contiguous ``[T, H*w]`` copy of the
+    same values; returns ``(flat, exact)`` = ``(False, True)`` when both agree bit for bit and raises otherwise.
+    """
+    w = table.shape[1]
+    gen = torch.Generator(device=table.device).manual_seed(0)
+    x = torch.randn(heads, tokens, w, dtype=table.dtype, device=table.device, generator=gen).transpose(0, 1)
+    pos = torch.randint(0, table.shape[0], (tokens,), device=table.device, generator=gen)
+    flat = x.reshape(tokens, -1).clone()
+    out = latent_rope(x.clone(), pos, table, HIP)   # clone() keeps the [T, H, w] transposed strides
+    ref = latent_rope(flat, pos, table, HIP).view(tokens, heads, w)
+    if not torch.equal(out, ref):
+        raise RuntimeError('latent RoPE kernel disagrees between strided and flat layouts')
+    return False, True
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# Step metadata (hla/vllm_latent/s6_ops.py:61-114)
+# ----------------------------------------------------------------------------------------------------------------
+
+def token_requests(query_start_loc, num_tokens):
+    """Request index per token (int64, clamped into range) and ``valid = arange(T) < query_start_loc[-1]``."""
+    _dev(query_start_loc)
+    qsl = _int('query_start_loc', query_start_loc, I32)
+    R = qsl.shape[0] - 1
+    req = torch.empty(num_tokens, dtype=I64, device=qsl.device)
+    valid = torch.empty(num_tokens, dtype=torch.bool, device=qsl.device)
+    _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, None, num_tokens, 0, _lib.ptr(req), _lib.ptr(valid),
+              None, None, None, _lib.stream(qsl.device))
+    return req, valid
+
+
+def history_lengths(seq_lens, query_start_loc):
+    """Per-request history length ``seq_len - query_len``, clamped at 0 (negative at FULL-graph capture)."""
+    _dev(seq_lens, query_start_loc)
+    qsl = _int('query_start_loc', query_start_loc, I32)
+    seq = _int('seq_lens', seq_lens, I32)
+    R = qsl.shape[0] - 1
+    hist = torch.empty(R, dtype=I32, device=qsl.device)
+    _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, _lib.ptr(seq), 0, 0, None, None, None, None, _lib.ptr(hist),
+              _lib.stream(qsl.device))
+    return hist
+
+
+def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_blocks=1):
+    """KV splits of the paged-history kernel for a step of ``num_tokens`` rows (``hla/vllm_latent/s6_ops.py:76-89``).
+
+    1 above ``split_max_tokens``; otherwise enough ``rows x head_blocks x splits`` workgroups to cover every compute
+    unit twice, floored by one split per 512 keys (rounded to a power of two) and capped at ``2 * sm_count`` and at
+    one split per 32 keys. Depends on constants and the row count only, so a captured graph of a batch size
+    always replays the split count it was captured with. ``sm_count`` is the CU count on MI355X (256).
+    """
+    if num_tokens > split_max_tokens:
+        return 1
+    by_length = 1 << (max(1, max_seq_len // 512) - 1).bit_length()
+    by_occupancy = -(-2 * sm_count // (num_tokens * head_blocks))
+    return max(1, min(max(by_length, by_occupancy), 2 * sm_count, -(-max_seq_len // 32)))
+
+
+def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, workgroups_per_cu=4, min_keys_per_split=256):
+    """Split count of the history kernel on MI355X: about ``workgroups_per_cu`` workgroups per compute unit over the
+    step's rows, never splits shorter than ``min_keys_per_split`` keys (each split writes a 16 x width fp32 partial,
+    so short splits turn into workspace traffic). A function of constants and the row count only (graph-stable).
+    The kernel partitions every row in chunks sized from the longest row of the step, so rows of a ragged batch
+    use a number of splits proportional to their length."""
+    by_occupancy = -(-workgroups_per_cu * cu_count // max(1, num_tokens))
+    by_length = max(1, -(-max_seq_len // min_keys_per_split))
+    return max(1, min(by_occupancy, by_length, 65535))
+
+
+class S6Workspace:
+    """Persistent fp32 split-partials buffer of the history kernel (``hla/vllm_latent/s6_ops.py:92-114``).
+
+    Sized for ``rows_x_splits`` (the largest ``num_tokens * num_kv_splits`` a step can request) at ``heads x
+    (width_max + 1)`` floats per row-split, allocated once on first use and never grown: an oversized request
+    raises ``RuntimeError`` instead of reallocating.
+    """
+
+    def __init__(self, heads, width_max, rows_x_splits):
+        self.floats = rows_x_splits * heads * (width_max + 1)
+        self.buffer = None
+
+    def ensure(self, device):
+        if self.buffer is None:
+            self.buffer = torch.empty(self.floats, dtype=torch.float32, device=device)
+        return self.buffer
+
+    def attn_logits(self, tokens, heads, splits, width, device=None):
+        need = tokens * heads * splits * (width + 1)
+        buffer = self.ensure(device)
+        if need > buffer.numel():
+            raise RuntimeError(f'S6 workspace overflow: need {need} floats, have {buffer.numel()}')
+        return buffer[:need].view(tokens, heads, splits, width + 1)
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# Paged latent history (hla/vllm_latent/s6_ops.py:117-222)
+# ----------------------------------------------------------------------------------------------------------------
+
+def history_attention(q_lat, cache, block_table, ctx, scale, num_kv_splits, workspace, k_scale, v_scale, backend,
+                      empty=None):
+    """Fully visible attention of ``q_lat[T,H,W]`` over the first ``ctx[t]`` paged latent rows of an MQA S6 cache.
+
+    ``cache`` is the logical vLLM layout ``[num_blocks, 1, block, 2W]`` (K then V on the last dim, any strides).
+    """
+    W = q_lat.shape[-1]
+    return history_attention_kv(q_lat, cache[..., :W], cache[..., W:], block_table, ctx, scale, num_kv_splits,
+                                workspace, k_scale, v_scale, backend, empty)
+
+
+def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, k_scale, v_scale, backend,
+                         empty=None, mla=False, bt_rows=None):
+    """Fully visible attention of ``q[T,16,L]`` over the first ``ctx[t]`` paged rows of ``k``/``v``
+    ``[num_blocks, 1, block, L]`` (MQA, page/row strides shared by K and V, unit last stride).
+
+    ``block_table[T, max_blocks]`` int32 is per token (or per request with ``bt_rows[t]`` naming the row of token
+    ``t``), ``ctx[T]`` int32. Only block-table columns ``< ceil(ctx[t] / block)`` are read. Returns
+    ``(o[T,H,L] bf16, lse[H,T] fp32)``; empty rows give ``o = 0``, ``lse = -inf``. ``k_scale``/``v_scale`` belong
+    to quantized caches, which the S6 adapter rejects (``hla/vllm_latent/ouro_latent.py:103-104``): they are
+    accepted and unused. ``empty`` is derived from ``ctx`` inside the kernel and is accepted for signature parity.
+    """
+    _backend('history', backend)
+    if mla:
+        raise ValueError('MLA-style rows (value = prefix of key) are not part of the S6 path')
+    _dev(q, k, v, block_table, ctx)
+    _bf16('q', q)
+    _bf16('k', k)
+    _bf16('v', v)
+    T, H, L = q.shape
+    if k.dim() != 4 or v.dim() != 4 or k.shape[1] != 1 or v.shape[1] != 1:
+        raise ValueError('history attention expects an MQA cache [num_blocks, 1, block, width]')
+    if k.shape[-1] != L or v.shape[-1] != L:
+        raise ValueError(f'latent widths differ: q {L}, k {k.shape[-1]}, v {v.shape[-1]}')
+    if k.stride(0) != v.stride(0) or k.stride(2) != v.stride(2):
+        raise ValueError('K and V must share page and row strides (halves of one cache)')
+    if block_table.dtype != I32 or block_table.stride(-1) != 1:
+        raise ValueError('block_table must be int32 with a unit last stride')
+    ctx = _int('ctx', ctx, I32)
+    if ctx.shape[0] != T:
+        raise ValueError(f'ctx has {ctx.shape[0]} rows for {T} tokens')
+    if bt_rows is None and block_table.shape[0] < T:
+        raise ValueError(f'block_table has {block_table.shape[0]} rows for {T} tokens')
+    o = torch.empty(T, H, L, dtype=BF16, device=q.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
+    splits = int(num_kv_splits)
+    ws = None
+    if splits > 1:
+        if workspace is None:
+            raise RuntimeError('history attention with num_kv_splits > 1 needs an S6Workspace')
+        ws = workspace.attn_logits(T, H, splits, L, q.device)
+    rows = None if bt_rows is None else _int('bt_rows', bt_rows, I64)
+    _lib.call('hla_s6_history_attention', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k), _lib.ptr(v),
+              k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0),
+              block_table.shape[1], _lib.ptr(rows),
+              _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o),
+              o.stride(0), o.stride(1), _lib.ptr(lse), _lib.stream(q.device))
+    return o, lse
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# Current chunk, exact window and merges (hla/vllm_latent/s6_ops.py:234-361)
+# ----------------------------------------------------------------------------------------------------------------
+
+def chunk_attention(q, k, v, query_start_loc, max_query_len, invalid, scale, backend):
+    """Causal attention within each request's current chunk (``q, k, v`` are ``[T,H,d]``).
+
+    Returns ``(o[T,H,d] bf16, lse[H,T] fp32)``; tokens past ``query_start_loc[-1]`` (the ``invalid`` rows) give
+    ``o = 0``, ``lse = -inf``. ``max_query_len`` and ``invalid`` are accepted for signature parity.
+    """
+    _backend('chunk', backend)
+    _dev(q, k, v, query_start_loc)
+    for name, t in (('q', q), ('k', k), ('v', v)):
+        _bf16(name, t)
+    qsl = _int('query_start_loc', query_start_loc, I32)
+    T, H, d = q.shape
+    o = torch.empty(T, H, d, dtype=BF16, device=q.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
+    _lib.call('hla_s6_chunk_attention', _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), T, H, d, q.stride(0), q.stride(1),
+              k.stride(0), k.stride(1), v.stride(0), v.stride(1), _lib.ptr(qsl), qsl.shape[0] - 1, float(scale),
+              _lib.ptr(o), o.stride(0), o.stride(1), _lib.ptr(lse), _lib.stream(q.device))
+    return o, lse
+
+
+def merge_states(o_hist, lse_hist, o_chunk, lse_chunk, invalid, backend):
+    """LSE merge of two partial softmaxes; ``[T,H,D]`` outputs, ``[H,T]`` fp32 lse; ``invalid`` rows are zeroed.
+
+    ``+inf`` lse counts as empty (the FA2 empty-key convention); both sides empty give 0.
+    """
+    _backend('merge', backend)
+    _dev(o_hist, lse_hist, o_chunk, lse_chunk)
+    _bf16('o_hist', o_hist)
+    _bf16('o_chunk', o_chunk)
+    T, H, D = o_chunk.shape
+    out = torch.empty(T, H, D, dtype=BF16, device=o_chunk.device)
+    lh, lc = lse_hist.float().contiguous(), lse_chunk.float().contiguous()
+    _lib.call('hla_s6_merge_states', _lib.ptr(o_hist), o_hist.stride(0), o_hist.stride(1), _lib.ptr(lh),
+              _lib.ptr(o_chunk), o_chunk.stride(0), o_chunk.stride(1), _lib.ptr(lc), _lib.ptr(_mask(invalid)), T, H, D,
+              0, _lib.ptr(out), out.stride(0), out.stride(1), None, _lib.stream(out.device))
+    return out
+
+
+def merge_lse(o1, lse1, o2, lse2):
+    """LSE merge that also returns the merged lse (``[T,H,d]`` outputs, ``[H,T]`` lse); both empty -> 0, -inf.
+    NaN entries of either output (scratch rows) count as 0."""
+    _dev(o1, lse1, o2, lse2)
+    _bf16('o1', o1)
+    _bf16('o2', o2)
+    T, H, D = o1.shape
+    out = torch.empty(T, H, D, dtype=BF16, device=o1.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=o1.device)
+    l1, l2 = lse1.float().contiguous(), lse2.float().contiguous()
+    _lib.call('hla_s6_merge_states', _lib.ptr(o1), o1.stride(0), o1.stride(1), _lib.ptr(l1), _lib.ptr(o2),
+              o2.stride(0), o2.stride(1), _lib.ptr(l2), None, T, H, D, 1, _lib.ptr(out), out.stride(0), out.stride(1),
+              _lib.ptr(lse), _lib.stream(out.device))
+    return out, lse
+
+
+def _exact_call(q, cache, block_table, mode, qsl, seq_lens, ctx, window, scale, bt_rows=None):
+    _dev(q, cache, block_table)
+    _bf16('q', q)
+    _bf16('cache', cache)
+    T, H, d = q.shape
+    if cache.dim() != 4 or cache.shape[1] != H or cache.shape[-1] != 2 * d:
+        raise ValueError(f'exact cache must be [num_blocks, {H}, block, {2 * d}], got {tuple(cache.shape)}')
+    if block_table.dtype != I32 or block_table.stride(-1) != 1:
+        raise ValueError('block_table must be int32 with a unit last stride')
+    R = 0 if qsl is None else qsl.shape[0] - 1
+    if mode == 0 and (block_table.shape[0] < R or seq_lens.shape[0] < R):
+        raise ValueError(f'per-request block_table / seq_lens need {R} rows')
+    if mode == 1 and (ctx.shape[0] != T or (bt_rows is None and block_table.shape[0] < T)):
+        raise ValueError(f'per-token block_table / ctx need {T} rows')
+    o = torch.empty(T, H, d, dtype=BF16, device=q.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
+    _lib.call('hla_s6_window_attention', _lib.ptr(q), T, H, d, q.stride(0), q.stride(1), _lib.ptr(cache),
+              _lib.ptr(cache[..., d:]), cache.stride(0), cache.stride(2), cache.stride(1), cache.shape[2],
+              cache.shape[0], _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(bt_rows),
+              mode, _lib.ptr(qsl),
+              _lib.ptr(seq_lens), R, _lib.ptr(ctx), int(window), float(scale), _lib.ptr(o), o.stride(0), o.stride(1),
+              _lib.ptr(lse), _lib.stream(q.device))
+    return o, lse
+
+
+def window_attention(q, cache, block_table, ctx, window, scale):
+    """Exact attention of ``q[T,H,d]`` (roped) over history rows ``[ctx[t] - window, ctx[t])`` of a paged exact cache.
+
+    ``cache`` is the TRITON_ATTN logical layout ``[num_blocks, H, block, 2d]`` (K then V), ``block_table[T, *]`` per
+    token. Rows without window history give ``o = 0``, ``lse = -inf``.
+    """
+    return _exact_call(q, cache, block_table, 1, None, None, _int('ctx', ctx, I32), window, scale)
+
+
+def window_attention_fa(q, cache, block_table, query_start_loc, seq_lens, window, scale, max_seqlen_k, invalid):
+    """Decode exact window: keys ``[seq_len - 1 - window, seq_len - 1]`` (the window history plus the current token,
+    already written) of a TRITON_ATTN cache ``[nb, H, block, 2d]``, per-request ``block_table`` / ``seq_lens``.
+
+    Returns ``(o[T,H,d], lse[H,T] fp32)``; ``invalid`` rows (tokens past ``query_start_loc[-1]``) get ``o = 0``,
+    ``lse = -inf``. ``max_seqlen_k`` and ``invalid`` are accepted for signature parity.
+    """
+    qsl = _int('query_start_loc', query_start_loc, I32)
+    return _exact_call(q, cache, block_table, 0, qsl, _int('seq_lens', seq_lens, I32), None, window, scale)
+
+
+def window_history_fa(q, cache, token_block_table, ctx, window, scale, max_seqlen_k, empty):
+    """Exact window over history keys only (non-decode steps): token ``t`` reads rows ``[ctx[t] - window, ctx[t])``
+    with a per-token table; rows without history (``empty``) give ``o = 0``, ``lse = -inf``."""
+    return _exact_call(q, cache, token_block_table, 1, None, None, _int('ctx', ctx, I32), window, scale)
+
+
+def select_backends(head_size=128):
+    """The HIP kernel set; raises ``RuntimeError`` when no GPU or no library is available."""
+    if not torch.cuda.is_available():
+        raise RuntimeError('S6 serving ops require a GPU (gfx950)')
+    if head_size != 128:
+        raise RuntimeError(f'exact-window kernels are built for head_size 128, not {head_size}')
+    _lib.load()
+    return HIP_BACKENDS

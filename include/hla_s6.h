@@ -1,0 +1,168 @@
+/*
+ * hla_s6.h -- C ABI of the MI355X (gfx950) S6 latent decode-attention library (libhla_s6.so).
+ *
+ * Every entry point takes plain device pointers, element strides (in elements of the pointed-to
+ * type), sizes and a hipStream_t passed as `void *` (NULL = the null stream). The library never
+ * allocates or frees device memory, never synchronizes with the host, keeps no per-call global state
+ * and only enqueues kernels on the given stream, so every call is safe under HIP graph capture.
+ * Floating-point tensors are bf16 (raw 16-bit patterns, `void *`) unless declared `float *`;
+ * `lse` outputs are contiguous fp32 [H, T] natural-log log-sum-exps of the already-scaled scores.
+ *
+ * Conventions shared by every attention entry point (hla/vllm_latent/s6_ops.py:1-10):
+ * an empty row gives o = 0 and lse = -inf; +inf lse counts as empty in merges; padding
+ * (invalid) rows are zeroed; no NaN leaves a merge.
+ *
+ * Return value: HLA_S6_OK or one of the error codes below; hla_s6_last_error() returns the
+ * message of the calling thread's last failure. No exception crosses the ABI.
+ */
+#ifndef HLA_S6_H
+#define HLA_S6_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HLA_S6_ABI_VERSION 1
+
+#define HLA_S6_OK 0
+#define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
+#define HLA_S6_EUNSUPPORTED 2 /* shape outside the compiled kernels       (Python: ValueError)   */
+#define HLA_S6_EWORKSPACE 3   /* caller workspace too small               (Python: RuntimeError) */
+#define HLA_S6_ELAUNCH 4      /* HIP launch / runtime error               (Python: RuntimeError) */
+#define HLA_S6_EDEVICE 5      /* no usable gfx950 device                  (Python: RuntimeError) */
+
+int hla_s6_abi_version(void);
+const char *hla_s6_last_error(void);
+
+/* Number of compute units of `device` (the `sm_count` argument of num_kv_splits,
+ * hla/vllm_latent/ouro_latent.py:204). */
+int hla_s6_device_cus(int device, int *cus);
+
+/* ---- a1: step metadata ------------------------------------------------------------------------
+ * Replaces s6_ops.token_requests (hla/vllm_latent/s6_ops.py:61-68), s6_ops.history_lengths
+ * (hla/vllm_latent/s6_ops.py:71-73) and the ctx / ctx_latent math of StepContext.__init__
+ * (hla/vllm_latent/s6_layer.py:64-70).
+ *   query_start_loc [num_reqs + 1] int32, seq_lens [num_reqs] int32.
+ *   seq_lens may be NULL when ctx, ctx_latent and history are NULL.
+ *   Outputs (each nullable): token_requests [num_tokens] int64 (clamped to num_reqs - 1),
+ *   valid [num_tokens] uint8 (t < query_start_loc[num_reqs]), ctx [num_tokens] int32
+ *   (history length of the token's request, 0 on padding), ctx_latent [num_tokens] int32
+ *   (max(ctx - window, 0), ctx when window == 0), history [num_reqs] int32. */
+int hla_s6_step_metadata(const int32_t *query_start_loc, int32_t num_reqs, const int32_t *seq_lens,
+                         int32_t num_tokens, int32_t window, int64_t *token_requests, uint8_t *valid,
+                         int32_t *ctx, int32_t *ctx_latent, int32_t *history, void *stream);
+
+/* Replaces StepContext.block_table (hla/vllm_latent/s6_layer.py:75-80):
+ * out[t, c] = table[token_requests[t], c] for c < cols. */
+int hla_s6_gather_block_table(const int32_t *table, int64_t table_stride, int32_t num_reqs, int32_t cols,
+                              const int64_t *token_requests, int32_t num_tokens, int32_t *out,
+                              int64_t out_stride, void *stream);
+
+/* ---- a2/a3: latent RoPE -----------------------------------------------------------------------
+ * Replaces s6_ops.latent_rope with the in-place kernel semantics (hla/vllm_latent/s6_ops.py:23-41):
+ * x[t, h, :width] <- x*cos + rotate_half(x)*sin with table[positions[t]] = [cos | sin] halves
+ * (width/2 each, row stride table_stride), bf16 rounding after each of the three products/sums as
+ * the torch formula does. x is [num_tokens, num_heads, width] with strides (stride_t, stride_h, 1).
+ * Positions are clamped into [0, table_rows). */
+int hla_s6_latent_rope(void *x, int32_t num_tokens, int32_t num_heads, int32_t width, int64_t stride_t,
+                       int64_t stride_h, const int64_t *positions, const void *table, int32_t table_rows,
+                       int64_t table_stride, void *stream);
+
+/* ---- a3/a5: absorbed projections ----------------------------------------------------------------
+ * out[t, h, :n_dim] = x[t, h, :k_dim] @ w[h, :k_dim, :n_dim] (bf16 operands, fp32 accumulation, bf16
+ * result), i.e. torch.einsum('thd,hdr->thr') of the A_t absorption (hla/vllm_latent/s6_layer.py:37)
+ * and of the B_t projection (hla/vllm_latent/s6_layer.py:114). When rope_table != NULL the latent
+ * RoPE of hla_s6_latent_rope is applied to the rounded product before it is stored, which fuses
+ * s6_layer.latent_query (hla/vllm_latent/s6_layer.py:32-40). x, w and out need a unit last stride;
+ * w is [H, k_dim, n_dim] with strides (w_sh, w_sk, 1). k_dim % 32 == 0, n_dim % 64 == 0. */
+int hla_s6_absorb(const void *x, int32_t num_tokens, int32_t num_heads, int32_t k_dim, int64_t x_st,
+                  int64_t x_sh, const void *w, int64_t w_sh, int64_t w_sk, int32_t n_dim, void *out,
+                  int64_t o_st, int64_t o_sh, const int64_t *positions, const void *rope_table,
+                  int32_t table_rows, int64_t table_stride, void *stream);
+
+/* ---- a4: paged latent-history attention --------------------------------------------------------
+ * Replaces s6_ops.history_attention / history_attention_kv for the MQA S6 cache
+ * (hla/vllm_latent/s6_ops.py:117-161; semantics of _history_reference, 204-222): fully visible
+ * softmax of q[t] (num_heads == 16 query heads, width in {128, 256, 512, 1024}) over the first
+ * ctx[t] rows of the paged latent cache. Row j of token t is at
+ *   k_cache + block_table[row(t)*bt_stride + j / block_size] * page_stride + (j % block_size) * row_stride
+ * (and likewise for v_cache), row(t) = bt_rows ? bt_rows[t] : t; only table columns
+ * < ceil(ctx[t] / block_size) are read. Metadata outside the buffers never faults: a row reads at most
+ * bt_cols * block_size keys and page ids are clamped into [0, num_blocks). block_size % 16 == 0; q, K and V rows need a unit last
+ * stride and 16-byte alignment. num_splits >= 1 partitions each row's keys (split-KV); partials
+ * go to `workspace` (fp32, caller-owned, >= num_tokens * num_splits * 16 * (width + 1) floats when
+ * num_splits > 1; unused when num_splits == 1). Outputs o [T, 16, width] bf16 (strides o_st, o_sh, 1)
+ * and lse [16, T] fp32. */
+int hla_s6_history_attention(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                             int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
+                             int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
+                             const int32_t *block_table, int64_t bt_stride, int32_t bt_cols, const int64_t *bt_rows,
+                             const int32_t *ctx, float scale, int32_t num_splits, float *workspace,
+                             int64_t workspace_floats, void *out, int64_t o_st, int64_t o_sh, float *lse,
+                             void *stream);
+
+/* ---- a6/a7: exact-window attention over the per-loop exact paged cache --------------------------
+ * The exact cache is the TRITON_ATTN layout [num_blocks, block, H, 2d] (K then V per head); key row j of
+ * head h is at k_cache + block_table[row*bt_stride + j / block_size] * page_stride
+ * + (j % block_size) * row_stride + h * head_stride (likewise v_cache).
+ * mode 0 replaces s6_ops.window_attention_fa (hla/vllm_latent/s6_ops.py:317-331): per-request tables
+ *   (row = request of the token); query i of a request with Lq queries sits at p = seq_len - Lq + i and
+ *   reads keys [max(0, p - window), p] (causal, window_size = (window, 0)); tokens >= query_start_loc[num_reqs]
+ *   get o = 0, lse = -inf.
+ * mode 1 replaces s6_ops.window_history_fa / s6_ops.window_attention (hla/vllm_latent/s6_ops.py:290-314,
+ *   334-350): token t reads history rows [max(0, ctx[t] - window), ctx[t]) with row = bt_rows ? bt_rows[t] : t.
+ * Keys at table columns >= bt_cols are not read and page ids are clamped into [0, num_blocks).
+ * head_dim == 128. Outputs o [T, H, 128] bf16 and lse [H, T] fp32. */
+int hla_s6_window_attention(const void *q, int32_t num_tokens, int32_t num_heads, int32_t head_dim, int64_t q_st,
+                            int64_t q_sh, const void *k_cache, const void *v_cache, int64_t page_stride,
+                            int64_t row_stride, int64_t head_stride, int32_t block_size, int64_t num_blocks,
+                            const int32_t *block_table, int64_t bt_stride, int32_t bt_cols, const int64_t *bt_rows,
+                            int32_t mode,
+                            const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs,
+                            const int32_t *ctx, int32_t window, float scale, void *out, int64_t o_st,
+                            int64_t o_sh, float *lse, void *stream);
+
+/* ---- a7: causal current-chunk attention ---------------------------------------------------------
+ * Replaces s6_ops.chunk_attention (hla/vllm_latent/s6_ops.py:234-259): token i of request r attends
+ * causally to the tokens [query_start_loc[r], i] of its own chunk; tokens >= query_start_loc[num_reqs] get
+ * o = 0, lse = -inf. q, k, v are [T, H, 128] bf16 with unit last stride. */
+int hla_s6_chunk_attention(const void *q, const void *k, const void *v, int32_t num_tokens, int32_t num_heads,
+                           int32_t head_dim, int64_t q_st, int64_t q_sh, int64_t k_st, int64_t k_sh,
+                           int64_t v_st, int64_t v_sh, const int32_t *query_start_loc, int32_t num_reqs,
+                           float scale, void *out, int64_t o_st, int64_t o_sh, float *lse, void *stream);
+
+/* ---- a8: LSE merge of two partial attentions -----------------------------------------------------
+ * mode 0 replaces s6_ops.merge_states (hla/vllm_latent/s6_ops.py:262-284): +inf lse counts as empty,
+ *   both empty -> 0, rows with invalid[t] != 0 -> 0 (invalid nullable); lse_out must be NULL.
+ * mode 1 replaces s6_ops.merge_lse (hla/vllm_latent/s6_ops.py:353-361): NaN inputs become 0, the merged
+ *   lse = peak + log(w_a + w_b) is written to lse_out ([H, T] fp32, nullable).
+ * head_dim % 8 == 0; o tensors need a unit last stride. */
+int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float *lse_a, const void *o_b,
+                        int64_t b_st, int64_t b_sh, const float *lse_b, const uint8_t *invalid,
+                        int32_t num_tokens, int32_t num_heads, int32_t head_dim, int32_t mode, void *out,
+                        int64_t o_st, int64_t o_sh, float *lse_out, void *stream);
+
+/* ---- a10 (slot-mapped row commit) -----------------------------------------------------------------
+ * Slot of each token: block_table[token_requests[t], positions[t] / block_size] * block_size
+ * + positions[t] % block_size, -1 for padding (valid[t] == 0). Closed form of
+ * hla/tests/test_s6_serving.py:54 and the padding convention of hla/vllm_latent/ouro_latent.py:8-9.
+ * A position beyond the table (column >= bt_cols) also maps to -1. */
+int hla_s6_slot_mapping(const int32_t *block_table, int64_t bt_stride, int32_t bt_cols,
+                        const int64_t *token_requests, const uint8_t *valid, const int64_t *positions,
+                        int32_t num_tokens, int32_t block_size, int64_t *slots, void *stream);
+
+/* Replaces unified_kv_cache_update of a committed latent row (hla/vllm_latent/ouro_latent.py:127-129):
+ * the row [key[t, :width] | value[t, :width]] is stored at page slots[t] / block_size, row
+ * slots[t] % block_size of `cache` (negative slots and slots past num_blocks * block_size skipped).
+ * key/value need a unit last stride. */
+int hla_s6_store_rows(const void *key, int64_t k_st, const void *value, int64_t v_st, int32_t num_tokens,
+                      int32_t width, const int64_t *slots, void *cache, int64_t page_stride, int64_t row_stride,
+                      int32_t block_size, int64_t num_blocks, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HLA_S6_H */

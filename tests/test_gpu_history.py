@@ -1,0 +1,125 @@
+"""GPU parity of the paged latent-history kernel (split-KV, MFMA) against the fp32 oracle.
+
+The grid follows the reference GPU test (hla/tests/test_s6_ops_gpu.py:43-57): widths, block sizes, split counts,
+ctx pattern [5000, 1000, 17, 1, 0] and batch sizes 1 / 8 / 33, random block tables whose stale columns point at a
++inf-poisoned null page. Tolerance: max-abs 2e-2 and relative L2 5e-3 on o, 1e-3 on lse."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16
+from oracle import s6_oracle as O
+from s6util import (NAN_BF16, assert_attention_close, assert_lse_close, dev_bf16, dev_i32, dev_i64, host_f32,
+                    latent_cache_bits, random_bits, token_tables)
+
+pytestmark = pytest.mark.gpu
+SCALE = 1 / math.sqrt(128)
+
+
+def run_history(ops, q_bits, cache_bits, table, ctx, splits, bt_rows=None):
+    T, H, w = q_bits.shape
+    q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    ws = ops.S6Workspace(H, w, T * splits)
+    o, lse = ops.history_attention_kv(q, cache[..., :w], cache[..., w:], dev_i32(table), dev_i32(ctx), SCALE, splits,
+                                      ws, None, None, 'hip', bt_rows=None if bt_rows is None else dev_i64(bt_rows))
+    return host_f32(o), host_f32(lse)
+
+
+def oracle_history(q_bits, cache_bits, table, ctx):
+    w = q_bits.shape[-1]
+    cf = bf16.to_f32(cache_bits)
+    return O.history_attention(bf16.to_f32(q_bits), cf[..., :w], cf[..., w:], table, ctx, SCALE)
+
+
+def check(o, lse, want_o, want_lse, ctx):
+    assert_attention_close(o, want_o)
+    assert_lse_close(lse, want_lse)
+    empty = np.asarray(ctx) == 0
+    assert (o[empty] == 0).all() and np.isneginf(lse[:, empty]).all()
+
+
+@pytest.mark.parametrize('width', [1024, 512, 256, 128])
+@pytest.mark.parametrize('block', [16, 32])
+@pytest.mark.parametrize('splits', [1, 4, 16])
+def test_history_matches_oracle(ops, width, block, splits):
+    rng = np.random.default_rng(width + block + splits)
+    num_blocks = 1024 if block == 16 else 512
+    cache = latent_cache_bits(rng, num_blocks, block, width)
+    cols = -(-5000 // block)
+    for batch in (1, 8, 33):
+        print(f'case width={width} block={block} splits={splits} batch={batch}', flush=True)
+        ctx = np.array(([5000, 1000, 17, 1, 0] * 7)[:batch], np.int32)
+        table = token_tables(rng, ctx, block, num_blocks, cols)
+        q = random_bits(rng, (batch, 16, width))
+        o, lse = run_history(ops, q, cache, table, ctx, splits)
+        check(o, lse, *oracle_history(q, cache, table, ctx), ctx)
+
+
+@pytest.mark.parametrize('splits', [1, 7])
+def test_history_nan_tails_and_page_ids_do_not_leak(ops, splits):
+    """Rows past ctx inside a row's last page are NaN: they must not reach o or lse."""
+    rng = np.random.default_rng(11)
+    width, block, nb = 512, 16, 600
+    ctx = np.array([1, 15, 16, 17, 33, 250, 1000, 31], np.int32)
+    cache = latent_cache_bits(rng, nb, block, width)
+    table = token_tables(rng, ctx, block, nb, 70, distinct=True)
+    for t, n in enumerate(ctx):
+        if n % block:
+            cache[table[t, n // block], 0, n % block:] = NAN_BF16
+    q = random_bits(rng, (len(ctx), 16, width))
+    o, lse = run_history(ops, q, cache, table, ctx, splits)
+    check(o, lse, *oracle_history(q, cache, table, ctx), ctx)   # the oracle reads rows < ctx only
+
+
+def test_history_per_request_table_rows(ops):
+    """bt_rows maps tokens onto a per-request table: same result as the gathered per-token table."""
+    rng = np.random.default_rng(12)
+    width, block, nb = 256, 16, 400
+    req_ctx = np.array([700, 3, 0, 129], np.int32)
+    table = token_tables(rng, req_ctx, block, nb, 50)
+    cache = latent_cache_bits(rng, nb, block, width)
+    rows = np.array([0, 0, 1, 3, 3, 3, 2], np.int64)
+    ctx = req_ctx[rows]
+    q = random_bits(rng, (len(rows), 16, width))
+    o, lse = run_history(ops, q, cache, table, ctx, 4, bt_rows=rows)
+    o2, lse2 = run_history(ops, q, cache, table[rows], ctx, 4)
+    np.testing.assert_array_equal(o, o2)
+    np.testing.assert_array_equal(lse, lse2)
+    check(o, lse, *oracle_history(q, cache, table[rows], ctx), ctx)
+
+
+def test_history_contiguous_rows_of_the_hf_engine(ops):
+    """The HF engine's packed rows [B, N, 1536] = [K 512 | V 512 | K1 256 | V1 256] read with identity paging."""
+    rng = np.random.default_rng(13)
+    B, N = 3, 1024
+    rows = random_bits(rng, (B, N, 1536))
+    ctx = np.array([1024, 700, 9], np.int32)
+    packed = dev_bf16(rows)
+    pages = packed.view(B * N // 16, 1, 16, 1536)
+    table = (np.arange(B)[:, None] * (N // 16) + np.arange(N // 16)[None]).astype(np.int32)
+    for (k0, w) in ((0, 512), (1024, 256)):
+        q = random_bits(rng, (B, 16, w))
+        o, lse = ops.history_attention_kv(dev_bf16(q), pages[..., k0:k0 + w], pages[..., k0 + w:k0 + 2 * w],
+                                          dev_i32(table), dev_i32(ctx), SCALE, 4, ops.S6Workspace(16, w, B * 4), None,
+                                          None, 'hip')
+        rf = bf16.to_f32(rows).reshape(B * N // 16, 1, 16, 1536)
+        want_o, want_lse = O.history_attention(bf16.to_f32(q), rf[..., k0:k0 + w], rf[..., k0 + w:k0 + 2 * w], table,
+                                               ctx, SCALE)
+        check(host_f32(o), host_f32(lse), want_o, want_lse, ctx)
+
+
+def test_split_counts_agree(ops):
+    """The split partition changes only the summation order: every split count gives the same answer."""
+    rng = np.random.default_rng(14)
+    width, block, nb = 512, 16, 2048
+    ctx = rng.integers(1024, 8192, 12).astype(np.int32)
+    cache = latent_cache_bits(rng, nb, block, width)
+    table = token_tables(rng, ctx, block, nb, 512)
+    q = random_bits(rng, (len(ctx), 16, width), 1 / math.sqrt(512))
+    ref = run_history(ops, q, cache, table, ctx, 1)
+    for splits in (2, 16, 64, 200):
+        o, lse = run_history(ops, q, cache, table, ctx, splits)
+        assert_attention_close(o, ref[0], f'splits={splits}', max_abs=1e-2, rel=2e-3)
+        assert_lse_close(lse, ref[1], atol=1e-4)

@@ -1,0 +1,260 @@
+"""GPU parity of the small ops through the C ABI: step metadata, block-table gather, slot mapping and row store
+(bit-exact), latent RoPE (bit-exact to the torch op order), the A_t / B_t MFMA GEMMs, the exact-window and chunk
+kernels and the LSE merges (north-star tolerances against the fp32 oracle)."""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16
+from oracle import s6_oracle as O
+from s6util import (assert_attention_close, assert_lse_close, dev_bf16, dev_i32, dev_i64, host_f32, random_bits)
+
+pytestmark = pytest.mark.gpu
+KNOWN = json.load(open(os.path.join(os.path.dirname(__file__), 'golden', 'known_answers.json')))
+CUDA = 'cuda'
+
+
+# ------------------------------------------------------------------------------------------------ metadata
+
+@pytest.mark.parametrize('case', KNOWN['token_requests']['cases'], ids=lambda c: str(c['qsl']) + f"/T{c['num_tokens']}")
+def test_token_requests_known_answers(ops, case):
+    req, valid = ops.token_requests(dev_i32(case['qsl']), case['num_tokens'])
+    assert req.dtype == torch.int64 and valid.dtype == torch.bool
+    assert req.tolist() == case['req'] and valid.tolist() == [bool(v) for v in case['valid']]
+
+
+@pytest.mark.parametrize('case', KNOWN['history_lengths']['cases'], ids=lambda c: str(c['qsl']))
+def test_history_lengths_known_answers(ops, case):
+    assert ops.history_lengths(dev_i32(case['seq_lens']), dev_i32(case['qsl'])).tolist() == case['expected']
+
+
+def test_step_context_random_ragged_is_bit_exact(layer):
+    rng = np.random.default_rng(0)
+    for trial in range(5):
+        R = int(rng.integers(1, 40))
+        lens = rng.integers(0, 6, R)
+        lens[rng.random(R) < 0.3] = 1
+        qsl = np.concatenate(([0], np.cumsum(lens))).astype(np.int32)
+        pad_req = int(rng.integers(0, 3))
+        qsl = np.concatenate((qsl, [qsl[-1]] * pad_req)).astype(np.int32)
+        T = int(qsl[-1]) + int(rng.integers(0, 4))
+        seq = np.concatenate((lens + rng.integers(0, 9000, R), np.zeros(pad_req, np.int64))).astype(np.int32)
+        window = int(rng.choice([0, 32]))
+        ctx = layer.StepContext(dev_i64(np.arange(T)), dev_i32(qsl), dev_i32(seq), int(lens.max()), T, {}, 1.0,
+                                None, window=window)
+        req, valid, c, cl = O.step_context(qsl, seq, T, window)
+        assert ctx.token_requests.tolist() == req.tolist(), trial
+        assert ctx.valid.tolist() == valid.tolist() and ctx.ctx.tolist() == c.tolist()
+        assert ctx.ctx_latent.tolist() == cl.tolist()
+        assert torch.equal(ctx.invalid, ~ctx.valid) and torch.equal(ctx.empty, ctx.ctx == 0)
+        table = rng.integers(0, 1000, (qsl.shape[0] - 1, 7)).astype(np.int32)
+        got = ctx.block_table(dev_i32(table))
+        assert got.tolist() == O.token_block_table(table, req).tolist()
+
+
+def test_step_context_known_mixed_step(layer):
+    g = KNOWN['step_context_mixed']
+    ctx = layer.StepContext(dev_i64([5, 2, 1, 1]), dev_i32(g['qsl']), dev_i32(g['seq_lens']), 1, g['num_tokens'], {},
+                            1.0, None)
+    assert ctx.token_requests.tolist() == g['token_requests'] and ctx.ctx.tolist() == g['ctx']
+    prof = layer.StepContext(dev_i64(np.arange(5)), None, None, None, 5, {}, 1.0, None)
+    assert not prof.md_present and prof.valid.all() and (prof.ctx == 0).all() and prof.max_query_len == 5
+
+
+def test_rollout_rows_slot_mapping_and_store(layer):
+    """Slot mapping + row store reproduce the reference's bit-exact rollout-cache rows."""
+    g = KNOWN['rollout_rows']
+    bs = g['block_size']
+    pos = np.array(g['positions'])
+    ctx = layer.StepContext(dev_i64(pos), dev_i32([0, 3]), dev_i32([3]), 3, 3, {}, 1.0, None)
+    rows = []
+    for part in ('main', 'l1'):
+        p = g[part]
+        w = p['row_width'] // 2
+        want_cache = torch.arange(p['num_blocks'] * bs * 2 * w, dtype=torch.float32).view(p['num_blocks'], 1, bs, 2 * w)
+        slots = layer.slot_mapping(ctx, dev_i32([p['table']]), bs)
+        assert slots.tolist() == O.slot_mapping(np.array([p['table']]), np.zeros(3, np.int64), np.ones(3, bool), pos,
+                                                bs).tolist()
+        # store the expected rows through the kernel into an empty cache, then read them back by slot
+        src = want_cache.view(-1, 2 * w)[slots.cpu()].to(torch.bfloat16).to(CUDA)
+        cache = torch.full((p['num_blocks'], 1, bs, 2 * w), float('nan'), dtype=torch.bfloat16, device=CUDA)
+        layer.store_rows(src[:, :w].contiguous(), src[:, w:].contiguous(), slots, cache)
+        rows.append(cache.view(-1, 2 * w)[slots].float().cpu())
+    assert torch.cat(rows, -1).tolist() == [[float(x) for x in r] for r in g['expected_rows']]
+
+
+def test_slot_mapping_padding_and_out_of_table_positions(layer):
+    ctx = layer.StepContext(dev_i64([0, 5, 9, 1]), dev_i32([0, 1, 2, 3]), dev_i32([1, 6, 10]), 1, 4, {}, 1.0, None)
+    slots = layer.slot_mapping(ctx, dev_i32([[3, 0], [7, 8], [4, 4]]), 4)
+    assert slots.tolist() == [12, 33, -1, -1]     # pos 9 is past the 2-column table; token 3 is padding
+
+
+# ------------------------------------------------------------------------------------------------ RoPE / GEMMs
+
+def _table(layer, width, rows=4096, theta=1e6):
+    inv = layer.latent_inv_freq(128, theta).to(CUDA)
+    return layer.latent_rope_table(rows, inv, width, torch.bfloat16)
+
+
+@pytest.mark.parametrize('width', [512, 256])
+def test_latent_rope_layouts_bit_exact(ops, layer, width):
+    rng = np.random.default_rng(4)
+    T, H = 33, 16
+    table = _table(layer, width)
+    table_h = host_f32(table)
+    pos = rng.integers(0, table.shape[0], T)
+    q = dev_bf16(random_bits(rng, (H, T, width))).transpose(0, 1)          # einsum-shaped, head stride T*w
+    row = dev_bf16(random_bits(rng, (T, 2 * width)))
+    flat = q.reshape(T, -1).clone()
+    want_q = O.latent_rope(host_f32(q), pos, table_h, rounding=True)
+    want_row = O.latent_rope(host_f32(row[:, :width]), pos, table_h, rounding=True)
+    v_before = row[:, width:].clone()
+    got_q = ops.latent_rope(q.clone(), dev_i64(pos), table, 'hip')
+    got_row = ops.latent_rope(row[:, :width], dev_i64(pos), table, 'hip')
+    got_flat = ops.latent_rope(flat, dev_i64(pos), table, 'hip')
+    assert got_row.data_ptr() == row.data_ptr() and got_row.stride() == (2 * width, 1)
+    np.testing.assert_array_equal(host_f32(got_q), want_q)
+    np.testing.assert_array_equal(host_f32(got_row), want_row)
+    np.testing.assert_array_equal(host_f32(got_flat).reshape(T, H, width), want_q)
+    assert torch.equal(row[:, width:], v_before)
+    assert ops.probe_latent_rope(table, 16) == (False, True)
+
+
+@pytest.mark.parametrize('T', [1, 64, 200])
+@pytest.mark.parametrize('width', [512, 256])
+def test_latent_query_fused_absorb_rope(layer, T, width):
+    rng = np.random.default_rng(5)
+    table = _table(layer, width)
+    q = random_bits(rng, (T, 16, 128))
+    A = random_bits(rng, (16, 128, width), 1 / math.sqrt(2048))
+    pos = rng.integers(0, table.shape[0], T)
+    got = layer.latent_query(dev_bf16(q), dev_bf16(A), dev_i64(pos), table, 'hip')
+    want = O.latent_query(bf16.to_f32(q), bf16.to_f32(A), pos, host_f32(table), rounding=True)
+    assert got.shape == (T, 16, width) and got.is_contiguous()
+    assert_attention_close(host_f32(got), want, 'q_lat', max_abs=2e-2, rel=5e-3)
+
+
+@pytest.mark.parametrize('T', [1, 64, 130])
+@pytest.mark.parametrize('r', [512, 256])
+def test_out_projection_gemm(layer, T, r):
+    rng = np.random.default_rng(6)
+    o = random_bits(rng, (T, 16, r))
+    B = random_bits(rng, (16, r, 128), 1 / math.sqrt(2048))
+    got = layer.absorb_out(dev_bf16(o), dev_bf16(B))
+    want = O.absorb(bf16.to_f32(o), bf16.to_f32(B), rounding=False)
+    assert_attention_close(host_f32(got), want, 'o_B')
+
+
+# ------------------------------------------------------------------------------------------------ exact window / chunk
+
+def _exact_cache(rng, nb, H, block, d):
+    bits = random_bits(rng, (nb, H, block, 2 * d))
+    bits[0] = 0x7F80
+    return bits
+
+
+@pytest.mark.parametrize('window', [0, 1, 32, 100])
+def test_window_decode(ops, window):
+    rng = np.random.default_rng(7)
+    H, d, block, nb = 16, 128, 16, 300
+    seq_lens = np.array([1, 2, 20, 33, 34, 200, 1000, 65], np.int32)
+    R = len(seq_lens)
+    pad_req = 2
+    qsl = np.concatenate((np.arange(R + 1), [R] * pad_req)).astype(np.int32)
+    T = R + 3                                        # three padding tokens
+    seq_all = np.concatenate((seq_lens, np.zeros(pad_req, np.int32))).astype(np.int32)
+    cache = _exact_cache(rng, nb, H, block, d)
+    cols = 70
+    table = np.zeros((R + pad_req, cols), np.int32)
+    for r in range(R):
+        need = -(-int(seq_lens[r]) // block)
+        table[r, :need] = rng.integers(1, nb, need)
+    q = random_bits(rng, (T, H, d))
+    scale = 1 / math.sqrt(d)
+    invalid = np.arange(T) >= R
+    o, lse = ops.window_attention_fa(dev_bf16(q), dev_bf16(cache), dev_i32(table), dev_i32(qsl), dev_i32(seq_all),
+                                     window, scale, 0, torch.as_tensor(invalid, device=CUDA))
+    cf = bf16.to_f32(cache)
+    want_o, want_lse = O.window_decode(bf16.to_f32(q), cf[..., :d], cf[..., d:], table, qsl, seq_all, window, scale,
+                                       invalid)
+    assert_attention_close(host_f32(o), want_o, 'window o')
+    assert_lse_close(host_f32(lse), want_lse)
+    assert (host_f32(o)[invalid] == 0).all()
+
+
+@pytest.mark.parametrize('window', [1, 32])
+def test_window_history(ops, window):
+    rng = np.random.default_rng(8)
+    H, d, block, nb = 16, 128, 16, 200
+    ctx = np.array([0, 1, 5, 31, 32, 33, 500, 0, 77], np.int32)
+    cache = _exact_cache(rng, nb, H, block, d)
+    table = np.zeros((len(ctx), 40), np.int32)
+    for t, c in enumerate(ctx):
+        need = -(-int(c) // block)
+        table[t, :need] = rng.integers(1, nb, need)
+    q = random_bits(rng, (len(ctx), H, d))
+    o, lse = ops.window_history_fa(dev_bf16(q), dev_bf16(cache), dev_i32(table), dev_i32(ctx), window, 0.1, 0,
+                                   torch.as_tensor(ctx == 0, device=CUDA))
+    cf = bf16.to_f32(cache)
+    want_o, want_lse = O.window_history(bf16.to_f32(q), cf[..., :d], cf[..., d:], table, ctx, window, 0.1)
+    assert_attention_close(host_f32(o), want_o, 'window-history o')
+    assert_lse_close(host_f32(lse), want_lse)
+    o2, lse2 = ops.window_attention(dev_bf16(q), dev_bf16(cache), dev_i32(table), dev_i32(ctx), window, 0.1)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+
+
+def test_chunk_attention(ops):
+    rng = np.random.default_rng(9)
+    H, d = 16, 128
+    qsl = np.array([0, 5, 6, 20, 20, 20], np.int32)   # mixed: two padded requests, four padding tokens
+    T = 24
+    q, k, v = (random_bits(rng, (T, H, d)) for _ in range(3))
+    invalid = np.arange(T) >= 20
+    o, lse = ops.chunk_attention(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_i32(qsl), 14,
+                                 torch.as_tensor(invalid, device=CUDA), 1 / math.sqrt(d), 'hip')
+    want_o, want_lse = O.chunk_attention(bf16.to_f32(q), bf16.to_f32(k), bf16.to_f32(v), qsl, invalid, 1 / math.sqrt(d))
+    assert o.is_contiguous() and lse.is_contiguous() and lse.shape == (H, T)
+    assert_attention_close(host_f32(o), want_o, 'chunk o')
+    assert_lse_close(host_f32(lse), want_lse)
+
+
+# ------------------------------------------------------------------------------------------------ merges
+
+def test_merge_states_edge_cases(ops):
+    rng = np.random.default_rng(10)
+    T, H, D = 8, 16, 128
+    oh, oc = random_bits(rng, (T, H, D)), random_bits(rng, (T, H, D))
+    lh = (rng.standard_normal((H, T)) * 3).astype(np.float32)
+    lc = (rng.standard_normal((H, T)) * 3).astype(np.float32)
+    lh[:, 0] = -np.inf            # empty history -> chunk output
+    lc[:, 1] = np.inf             # FA2 empty-key convention -> history output
+    lh[:, 2] = lc[:, 2] = -np.inf  # both empty (padding row)
+    invalid = np.zeros(T, bool)
+    invalid[2] = invalid[7] = True
+    out = ops.merge_states(dev_bf16(oh), torch.as_tensor(lh, device=CUDA), dev_bf16(oc),
+                           torch.as_tensor(lc, device=CUDA), torch.as_tensor(invalid, device=CUDA), 'hip')
+    want = O.merge_states(bf16.to_f32(oh), lh, bf16.to_f32(oc), lc, invalid)
+    got = host_f32(out)
+    assert_attention_close(got, want, 'merge')
+    assert (got[2] == 0).all() and (got[7] == 0).all()
+    np.testing.assert_array_equal(got[0], bf16.to_f32(oc)[0])
+    np.testing.assert_array_equal(got[1], bf16.to_f32(oh)[1])
+
+
+def test_merge_lse(ops):
+    rng = np.random.default_rng(11)
+    T, H, D = 6, 16, 128
+    o1, o2 = random_bits(rng, (T, H, D)), random_bits(rng, (T, H, D))
+    o1[0] = 0x7FC0                 # scratch NaN row of an empty side
+    l1 = (rng.standard_normal((H, T)) * 2).astype(np.float32)
+    l2 = (rng.standard_normal((H, T)) * 2).astype(np.float32)
+    l1[:, 0] = -np.inf
+    l1[:, 3] = l2[:, 3] = -np.inf
+    out, lse = ops.merge_lse(dev_bf16(o1), torch.as_tensor(l1, device=CUDA), dev_bf16(o2), torch.as_tensor(l2, device=CUDA))
+    want, want_lse = O.merge_lse(bf16.to_f32(o1), l1, bf16.to_f32(o2), l2)
+    assert_attention_close(host_f32(out), want, 'merge_lse')
+    assert_lse_close(host_f32(lse), want_lse)

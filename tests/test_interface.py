@@ -1,0 +1,127 @@
+"""CPU checks of the drop-in boundary: the C ABI library loads and exports every symbol of include/hla_s6.h with
+the declared arity; the Python mirror keeps the reference's operator names and parameter lists and its host-side
+error behaviour; the product package never reaches the oracle."""
+import ast
+import inspect
+import json
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, 'include', 'hla_s6.h')
+PKG_DIR = os.path.join(ROOT, 'hybrid-latent-attention_amd')
+IFACE = json.load(open(os.path.join(ROOT, 'tests', 'golden', 'reference_interface.json')))
+KNOWN = json.load(open(os.path.join(ROOT, 'tests', 'golden', 'known_answers.json')))
+
+
+def header_declarations():
+    text = re.sub(r'/\*.*?\*/', '', open(HEADER).read(), flags=re.S)
+    decls = {}
+    for m in re.finditer(r'^(?:int|const char \*)\s*(hla_s6_\w+)\s*\(([^)]*)\)\s*;', text, re.M):
+        params = m.group(2).strip()
+        decls[m.group(1)] = 0 if params in ('', 'void') else params.count(',') + 1
+    return decls
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.load()
+    decls = header_declarations()
+    assert len(decls) >= 12
+    assert set(decls) == set(pkg._lib.SIGNATURES), 'header and ctypes binding disagree'
+    for name, arity in decls.items():
+        assert hasattr(lib, name), f'{name} not exported by libhla_s6.so'
+        assert len(pkg._lib.SIGNATURES[name]) == arity, f'{name}: binding has {len(pkg._lib.SIGNATURES[name])} args'
+    assert lib.hla_s6_abi_version() == pkg._lib.ABI_VERSION
+
+
+def _params(obj):
+    return list(inspect.signature(obj).parameters)
+
+
+@pytest.mark.parametrize('module', ['s6_ops', 's6_layer'])
+def test_reference_parameter_lists(pkg, module):
+    mod = getattr(pkg, module)
+    for qual, want in IFACE[module].items():
+        obj = mod
+        for part in qual.split('.'):
+            obj = getattr(obj, part)
+        got = _params(obj)
+        assert got[:len(want)] == want, f'{module}.{qual}: {got} != {want}'
+        for extra in list(inspect.signature(obj).parameters.values())[len(want):]:
+            assert extra.default is not inspect.Parameter.empty, f'{module}.{qual}: extra {extra.name} has no default'
+
+
+@pytest.mark.parametrize('case', KNOWN['num_kv_splits']['cases'], ids=lambda c: str(c['args']))
+def test_num_kv_splits_known_answers(ops, case):
+    assert ops.num_kv_splits(*case['args']) == case['expected']
+
+
+def test_workspace_sizing_and_overflow(ops):
+    g = KNOWN['workspace']
+    ws = ops.S6Workspace(heads=g['heads'], width_max=g['width_max'], rows_x_splits=g['rows_x_splits'])
+    assert ws.floats == g['floats'] and ws.buffer is None
+    view = ws.attn_logits(*g['view_args'], torch.device('cpu'))
+    assert list(view.shape) == g['view_shape'] and view.dtype == torch.float32
+    assert view.data_ptr() == ws.buffer.data_ptr() and ws.ensure('cpu') is ws.buffer
+    with pytest.raises(RuntimeError, match='overflow'):
+        ws.attn_logits(*g['overflow_args'])
+
+
+def test_unknown_backends_raise_value_error(ops, layer):
+    ones = torch.ones(1, 1, 8)
+    i32 = torch.zeros(1, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        ops.history_attention(ones, ones[None], i32[None], i32, 1.0, 1, None, None, None, 'triton')
+    with pytest.raises(ValueError):
+        ops.chunk_attention(ones, ones, ones, torch.tensor([0, 1], dtype=torch.int32), 1,
+                            torch.zeros(1, dtype=torch.bool), 1.0, 'flash')
+    with pytest.raises(ValueError):
+        ops.merge_states(ones, ones[0], ones, ones[0], torch.zeros(1, dtype=torch.bool), 'vllm')
+    with pytest.raises(ValueError):
+        ops.latent_rope(ones, torch.zeros(1, dtype=torch.int64), ones[0], 'torch')
+    with pytest.raises(ValueError):
+        layer.latent_query(ones, ones, torch.zeros(1, dtype=torch.int64), ones[0], 'vllm')
+
+
+def test_cpu_tensors_are_rejected(ops):
+    """No CPU path: a host tensor is an error, never a fallback."""
+    q = torch.zeros(1, 16, 512, dtype=torch.bfloat16)
+    cache = torch.zeros(2, 1, 16, 1024, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match='GPU only'):
+        ops.history_attention(q, cache, torch.zeros(1, 1, dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
+                              1.0, 1, None, None, None, 'hip')
+
+
+def test_select_backends_needs_a_gpu(ops):
+    if torch.cuda.is_available():
+        assert ops.select_backends() == ops.HIP_BACKENDS
+    else:
+        with pytest.raises(RuntimeError):
+            ops.select_backends()
+
+
+def test_product_never_imports_the_oracle():
+    for dirpath, _, files in os.walk(PKG_DIR):
+        for f in files:
+            if f.endswith('.py'):
+                tree = ast.parse(open(os.path.join(dirpath, f)).read())
+                for node in ast.walk(tree):
+                    names = []
+                    if isinstance(node, ast.Import):
+                        names = [a.name for a in node.names]
+                    elif isinstance(node, ast.ImportFrom):
+                        names = [node.module or '']
+                    assert not any(n.split('.')[0] == 'oracle' for n in names), f'{f} imports the oracle'
+
+
+def test_library_status_codes_map_to_reference_exceptions(pkg):
+    lib = pkg._lib
+    with pytest.raises(ValueError):   # EUNSUPPORTED: 8 query heads
+        lib.call('hla_s6_history_attention', None, 1, 8, 512, 0, 0, None, None, 0, 0, 16, 1, None, 0, 1, None, None,
+                 1.0, 1, None, 0, None, 0, 0, None, None)
+    with pytest.raises(RuntimeError, match='workspace overflow'):   # EWORKSPACE before any launch
+        lib.call('hla_s6_history_attention', 16, 1, 16, 512, 512, 512, 16, 16, 1024, 1024, 16, 1, 16, 0, 1, None, 16,
+                 1.0, 4, 16, 10, 16, 512, 512, 16, None)

@@ -1,0 +1,329 @@
+"""Pins of the floating-point oracle functions: independent float64 per-token loops on tiny inputs, the
+joint-softmax identity of the merges, closed forms of RoPE and the GEMMs, and planted mistakes that each pin
+must catch. CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import bf16
+from oracle import s6_oracle as O
+
+INF = np.inf
+
+
+def _softmax64(scores, values):
+    scores = np.asarray(scores, np.float64)
+    m = scores.max()
+    p = np.exp(scores - m)
+    return (p / p.sum()) @ np.asarray(values, np.float64), m + math.log(p.sum())
+
+
+# ---------------------------------------------------------------------------------------------- history
+
+def paged_setup(block, width, heads, kvh=1, num_blocks=64, ctx=(0, 1, 17, 40, 5, 0), seed=0):
+    rng = np.random.default_rng(seed)
+    cache = rng.standard_normal((num_blocks, kvh, block, 2 * width)).astype(np.float32)
+    cache[0] = INF                           # null block: any unmasked read of it is loud
+    q = rng.standard_normal((len(ctx), heads, width)).astype(np.float32)
+    table = rng.integers(1, num_blocks, (len(ctx), 12)).astype(np.int32)
+    ctx = np.array(ctx, np.int32)
+    needed = (ctx + block - 1) // block
+    table[np.arange(12)[None] >= needed[:, None]] = 0   # stale columns point at the poisoned block
+    return q, cache, table, ctx
+
+
+def check_history(o, lse, q, cache, table, ctx, scale, tol=1e-5):
+    T, H, w = q.shape
+    kvh, block = cache.shape[1], cache.shape[2]
+    group = H // kvh
+    assert o.shape == (T, H, w) and lse.shape == (H, T)
+    for t, n in enumerate(ctx.tolist()):
+        if n == 0:
+            assert (o[t] == 0).all() and (lse[:, t] == -INF).all()
+            continue
+        for h in range(H):
+            g = h // group
+            rows = np.stack([cache[int(table[t, j // block]), g, j % block] for j in range(n)]).astype(np.float64)
+            scores = rows[:, :w] @ q[t, h].astype(np.float64) * scale
+            out, l = _softmax64(scores, rows[:, w:])
+            np.testing.assert_allclose(lse[h, t], l, rtol=tol, atol=tol)
+            np.testing.assert_allclose(o[t, h], out, rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize('block', [4, 8, 16])
+@pytest.mark.parametrize('heads,kvh', [(2, 1), (4, 2), (16, 1)])
+def test_history_matches_explicit_softmax(block, heads, kvh):
+    width = 8
+    q, cache, table, ctx = paged_setup(block, width, heads, kvh)
+    scale = 1 / math.sqrt(width)
+    o, lse = O.history_attention(q, cache[..., :width], cache[..., width:], table, ctx, scale)
+    assert np.isfinite(o).all() and not np.isnan(lse).any()
+    check_history(o, lse, q, cache, table, ctx, scale)
+
+
+# ---------------------------------------------------------------------------------------------- chunk
+
+def test_chunk_is_block_diagonal_causal():
+    heads, dim = 2, 8
+    qsl, T = np.array([0, 3, 4, 6, 6], np.int32), 8     # prefill 3, decode 1, prefill 2, padded request, 2 padding tokens
+    rng = np.random.default_rng(2)
+    q, k, v = rng.standard_normal((3, T, heads, dim)).astype(np.float32)
+    invalid = np.arange(T) >= 6
+    o, lse = O.chunk_attention(q, k, v, qsl, invalid, 1 / math.sqrt(dim))
+    assert (o[6:] == 0).all() and (lse[:, 6:] == -INF).all()
+    for r in range(3):
+        s, e = qsl[r], qsl[r + 1]
+        for i in range(s, e):
+            for h in range(heads):
+                sc = k[s:i + 1, h].astype(np.float64) @ q[i, h].astype(np.float64) / math.sqrt(dim)
+                out, l = _softmax64(sc, v[s:i + 1, h])
+                np.testing.assert_allclose(lse[h, i], l, rtol=1e-5, atol=1e-6)
+                np.testing.assert_allclose(o[i, h], out, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------- merges
+
+def partial(scores, values):
+    T, H, _ = scores.shape
+    o = np.zeros((T, H, values.shape[-1]))
+    lse = np.full((H, T), -INF)
+    for t in range(T):
+        for h in range(H):
+            if np.isfinite(scores[t, h]).any():
+                o[t, h], lse[h, t] = _softmax64(scores[t, h], values[t])
+    return o, lse
+
+
+def joint(s1, v1, s2, v2):
+    return partial(np.concatenate((s1, s2), -1), np.concatenate((v1, v2), 1))
+
+
+def test_merge_states_is_joint_softmax():
+    T, H, D, n1, n2 = 6, 2, 8, 5, 3
+    rng = np.random.default_rng(3)
+    s1, s2 = rng.standard_normal((T, H, n1)) * 3, rng.standard_normal((T, H, n2)) * 3
+    v1, v2 = rng.standard_normal((T, n1, D)), rng.standard_normal((T, n2, D))
+    s1[1] = -INF
+    s2[2] = -INF
+    s1[3] = s2[3] = -INF
+    o1, l1 = partial(s1, v1)
+    o2, l2 = partial(s2, v2)
+    invalid = np.array([0, 0, 0, 0, 0, 1], bool)
+    out = O.merge_states(o1, l1, o2, l2, invalid)
+    want, _ = joint(s1, v1, s2, v2)
+    want[invalid] = 0
+    np.testing.assert_allclose(out, want, rtol=2e-5, atol=2e-6)
+    assert (out[3] == 0).all() and (out[5] == 0).all()
+
+
+def test_merge_states_plus_inf_is_empty():
+    rng = np.random.default_rng(4)
+    o_h, o_c = rng.standard_normal((2, 1, 8)), rng.standard_normal((2, 1, 8))
+    lse_h, lse_c = np.zeros((1, 2)), np.array([[INF, 0.0]])
+    out = O.merge_states(o_h, lse_h, o_c, lse_c, np.zeros(2, bool))
+    np.testing.assert_allclose(out[0], o_h[0], rtol=1e-6)
+    np.testing.assert_allclose(out[1], (o_h[1] + o_c[1]) / 2, rtol=1e-6)
+
+
+def test_merge_lse_is_joint_softmax_and_its_lse():
+    T, H, D = 5, 3, 8
+    rng = np.random.default_rng(5)
+    s1, s2 = rng.standard_normal((T, H, 4)) * 2, rng.standard_normal((T, H, 6)) * 2
+    v1, v2 = rng.standard_normal((T, 4, D)), rng.standard_normal((T, 6, D))
+    s1[0] = -INF
+    s1[4] = s2[4] = -INF
+    o1, l1 = partial(s1, v1)
+    o2, l2 = partial(s2, v2)
+    o1[0] = np.nan                                # a scratch (empty) row of the first partial
+    out, lse = O.merge_lse(o1, l1, o2, l2)
+    want, want_lse = joint(s1, v1, s2, v2)
+    np.testing.assert_allclose(out, want, rtol=2e-5, atol=2e-6)
+    np.testing.assert_allclose(lse[:, :4], want_lse[:, :4], rtol=1e-6)
+    assert (lse[:, 4] == -INF).all() and (out[4] == 0).all()
+
+
+# ---------------------------------------------------------------------------------------------- exact window
+
+def exact_cache(rng, num_blocks, heads, block, d):
+    cache = rng.standard_normal((num_blocks, heads, block, 2 * d)).astype(np.float32)
+    cache[0] = INF
+    return cache
+
+
+def test_window_decode_matches_explicit_keys():
+    """Decode (one query per request): keys [seq_len - 1 - W, seq_len - 1] of the request's exact paged cache."""
+    rng = np.random.default_rng(6)
+    H, d, block, W = 2, 8, 4, 5
+    seq_lens = np.array([1, 3, 6, 12, 9], np.int32)
+    R = len(seq_lens)
+    qsl = np.arange(R + 1, dtype=np.int32)
+    T = R + 2                                       # two padding tokens
+    cache = exact_cache(rng, 40, H, block, d)
+    table = np.zeros((R, 4), np.int32)
+    perm = rng.permutation(np.arange(1, 40))
+    for r in range(R):
+        need = (seq_lens[r] + block - 1) // block
+        table[r, :need] = perm[4 * r:4 * r + need]
+    q = rng.standard_normal((T, H, d)).astype(np.float32)
+    invalid = np.arange(T) >= R
+    scale = 0.3
+    o, lse = O.window_decode(q, cache[..., :d], cache[..., d:], table, qsl, seq_lens, W, scale, invalid)
+    for t in range(T):
+        if invalid[t]:
+            assert (o[t] == 0).all() and (lse[:, t] == -INF).all()
+            continue
+        keys = list(range(max(0, seq_lens[t] - 1 - W), seq_lens[t]))
+        for h in range(H):
+            rows = np.stack([cache[table[t, p // block], h, p % block] for p in keys]).astype(np.float64)
+            out, l = _softmax64(rows[:, :d] @ q[t, h].astype(np.float64) * scale, rows[:, d:])
+            np.testing.assert_allclose(o[t, h], out, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(lse[h, t], l, rtol=1e-5, atol=1e-6)
+
+
+def test_window_decode_multi_query_is_bottom_right_causal():
+    """Lq > 1: query i of the request sits at seq_len - Lq + i (FA2 bottom-right alignment)."""
+    rng = np.random.default_rng(7)
+    H, d, block, W = 2, 8, 4, 3
+    seq_lens, qsl = np.array([7], np.int32), np.array([0, 3], np.int32)
+    cache = exact_cache(rng, 8, H, block, d)
+    table = np.array([[3, 5]], np.int32)
+    q = rng.standard_normal((3, H, d)).astype(np.float32)
+    o, lse = O.window_decode(q, cache[..., :d], cache[..., d:], table, qsl, seq_lens, W, 1.0, np.zeros(3, bool))
+    for i in range(3):
+        p = 7 - 3 + i
+        keys = list(range(max(0, p - W), p + 1))
+        rows = np.stack([cache[table[0, k // block], 0, k % block] for k in keys]).astype(np.float64)
+        out, _ = _softmax64(rows[:, :d] @ q[i, 0].astype(np.float64), rows[:, d:])
+        np.testing.assert_allclose(o[i, 0], out, rtol=1e-5, atol=1e-6)
+
+
+def test_window_history_rows_before_ctx():
+    rng = np.random.default_rng(8)
+    H, d, block, W = 2, 8, 4, 4
+    ctx = np.array([0, 1, 3, 4, 9, 16], np.int32)
+    cache = exact_cache(rng, 32, H, block, d)
+    table = rng.integers(1, 32, (len(ctx), 4)).astype(np.int32)
+    q = rng.standard_normal((len(ctx), H, d)).astype(np.float32)
+    o, lse = O.window_history(q, cache[..., :d], cache[..., d:], table, ctx, W, 0.5)
+    for t, c in enumerate(ctx):
+        if c == 0:
+            assert (o[t] == 0).all() and (lse[:, t] == -INF).all()
+            continue
+        keys = list(range(max(0, c - W), c))
+        for h in range(H):
+            rows = np.stack([cache[table[t, p // block], h, p % block] for p in keys]).astype(np.float64)
+            out, l = _softmax64(rows[:, :d] @ q[t, h].astype(np.float64) * 0.5, rows[:, d:])
+            np.testing.assert_allclose(o[t, h], out, rtol=1e-5, atol=1e-6)
+            np.testing.assert_allclose(lse[h, t], l, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------------------------------------- RoPE / GEMM
+
+def test_latent_rope_is_pairwise_rotation():
+    rng = np.random.default_rng(9)
+    head_dim, width, max_pos, T, H = 16, 24, 64, 7, 3
+    inv = O.latent_inv_freq(head_dim, 1e4)
+    table = O.latent_rope_table(max_pos, inv, width)
+    pos = rng.integers(0, max_pos, T)
+    x = rng.standard_normal((T, H, width)).astype(np.float32)
+    y = O.latent_rope(x, pos, table, rounding=False)
+    half = width // 2
+    for t in range(T):
+        ang = pos[t] * inv[np.arange(half) % inv.shape[0]].astype(np.float64)
+        c, s = np.cos(ang), np.sin(ang)
+        x1, x2 = x[t, :, :half].astype(np.float64), x[t, :, half:].astype(np.float64)
+        np.testing.assert_allclose(y[t, :, :half], x1 * c - x2 * s, rtol=1e-5, atol=1e-5)
+        np.testing.assert_allclose(y[t, :, half:], x2 * c + x1 * s, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), np.linalg.norm(x, axis=-1), rtol=1e-5)
+
+
+def test_latent_rope_rounding_is_per_op_bf16():
+    rng = np.random.default_rng(10)
+    table = bf16.round_bf16(O.latent_rope_table(32, O.latent_inv_freq(16, 1e6), 16))
+    x = bf16.round_bf16(rng.standard_normal((5, 2, 16)).astype(np.float32))
+    pos = rng.integers(0, 32, 5)
+    y = O.latent_rope(x, pos, table, rounding=True)
+    assert (bf16.round_bf16(y) == y).all()
+    yr = O.latent_rope(x, pos, table, rounding=False)
+    assert np.abs(y - yr).max() <= 2 ** -7 * np.abs(yr).max() + 1e-6
+
+
+def test_absorb_is_batched_gemm():
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((5, 3, 32)).astype(np.float32)
+    w = rng.standard_normal((3, 32, 16)).astype(np.float32)
+    out = O.absorb(x, w, rounding=False, dtype=np.float64)
+    for t in range(5):
+        for h in range(3):
+            np.testing.assert_allclose(out[t, h], x[t, h].astype(np.float64) @ w[h].astype(np.float64), rtol=1e-12)
+
+
+def test_bf16_conversions():
+    vals = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -2.5, 0.0, INF, -INF, 3.0e38], np.float32)
+    bits = bf16.from_f32(vals)
+    assert bf16.to_f32(bits).tolist()[:5] == [1.0, 1.0, 1 + 2 ** -6, -2.5, 0.0]   # ties to even
+    assert bits[5] == 0x7F80 and bits[6] == 0xFF80
+    assert np.isnan(bf16.to_f32(bf16.from_f32(np.array([np.nan], np.float32))))[0]
+    r = np.random.default_rng(0).standard_normal(1000).astype(np.float32)
+    assert (bf16.from_f32(bf16.to_f32(bf16.from_f32(r))) == bf16.from_f32(r)).all()
+
+
+# ---------------------------------------------------------------------------------------------- composite
+
+def test_attend_decode_is_one_joint_softmax():
+    """History (through A_t/B_t absorption) + exact window + LSE merge equals one softmax over the union of keys,
+    the semantics of the HF engine's mixed_attention (hla/latent/batched_engine.py:154-182) with a window."""
+    rng = np.random.default_rng(12)
+    H, d, r, block, W = 2, 8, 12, 4, 3
+    seq_lens = np.array([9, 2, 14], np.int32)
+    R = len(seq_lens)
+    qsl = np.arange(R + 1, dtype=np.int32)
+    ctx = seq_lens - 1
+    ctx_lat = np.maximum(ctx - W, 0)
+    lat = rng.standard_normal((30, 1, block, 2 * r)).astype(np.float32)
+    ex = rng.standard_normal((30, H, block, 2 * d)).astype(np.float32)
+    table = np.stack([rng.permutation(np.arange(1, 30))[:4] for _ in range(R)]).astype(np.int32)
+    q_lat = rng.standard_normal((R, H, r)).astype(np.float32)
+    q_rope = rng.standard_normal((R, H, d)).astype(np.float32)
+    B = rng.standard_normal((H, r, d)).astype(np.float32)
+    out = O.attend_decode(q_lat, q_rope, B, lat[..., :r], lat[..., r:], table, ctx_lat, ex[..., :d], ex[..., d:],
+                          table, qsl, seq_lens, W, 0.4, np.zeros(R, bool), rounding=False, dtype=np.float64)
+    for t in range(R):
+        for h in range(H):
+            hist = [lat[table[t, j // block], 0, j % block].astype(np.float64) for j in range(ctx_lat[t])]
+            win = [ex[table[t, p // block], h, p % block].astype(np.float64)
+                   for p in range(max(0, seq_lens[t] - 1 - W), seq_lens[t])]
+            s = [row[:r] @ q_lat[t, h] * 0.4 for row in hist] + [row[:d] @ q_rope[t, h] * 0.4 for row in win]
+            vals = [row[r:] @ B[h] for row in hist] + [row[d:] for row in win]
+            want, _ = _softmax64(np.array(s), np.array(vals))
+            np.testing.assert_allclose(out[t, h], want, rtol=1e-6, atol=1e-6)   # the merge is fp32, as in the reference
+
+
+# ---------------------------------------------------------------------------------------------- planted mistakes
+
+def test_planted_mistakes_fail_the_pins():
+    """Plausible oracle mistakes (dropped key, wrong scale, swapped heads, sign of the rotation) fail a pin."""
+    width, heads = 8, 2
+    q, cache, table, ctx = paged_setup(8, width, heads)
+    scale = 1 / math.sqrt(width)
+    k, v = cache[..., :width], cache[..., width:]
+    cases = {
+        'dropped last key': lambda: O.history_attention(q, k, v, table, np.maximum(ctx - 1, 0), scale),
+        'wrong scale': lambda: O.history_attention(q, k, v, table, ctx, scale * 1.01),
+        'swapped heads': lambda: tuple(x[..., ::-1, :] if x.ndim == 3 else x[::-1]
+                                       for x in O.history_attention(q, k, v, table, ctx, scale)),
+        'K/V swapped': lambda: O.history_attention(q, v, k, table, ctx, scale),
+    }
+    for name, planted in cases.items():
+        o, lse = planted()
+        with pytest.raises(AssertionError):
+            check_history(o, lse, q, cache, table, ctx, scale)
+    rng = np.random.default_rng(9)
+    inv = O.latent_inv_freq(16, 1e4)
+    table_r = O.latent_rope_table(16, inv, 8)
+    x = rng.standard_normal((3, 1, 8)).astype(np.float32)
+    pos = np.array([1, 5, 9])
+    wrong = x * np.concatenate((table_r[pos, :4], table_r[pos, :4]), -1)[:, None] - \
+        O.rotate_half(x) * np.concatenate((table_r[pos, 4:], table_r[pos, 4:]), -1)[:, None]
+    assert not np.allclose(wrong, O.latent_rope(x, pos, table_r, rounding=False), atol=1e-3)
