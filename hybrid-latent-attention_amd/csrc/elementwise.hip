@@ -125,6 +125,7 @@ __global__ void slot_mapping_kernel(const int32_t* bt, int64_t bs_stride, int co
   slots[t] = (int64_t)bt[treq[t] * bs_stride + p / block] * block + p % block;
 }
 
+template <bool VEC>
 __global__ void store_rows_kernel(const uint16_t* key, int64_t k_st, const uint16_t* value, int64_t v_st, int width,
                                   const int64_t* slots, uint16_t* cache, int64_t page_stride, int64_t row_stride,
                                   int block, int64_t num_blocks) {
@@ -132,12 +133,17 @@ __global__ void store_rows_kernel(const uint16_t* key, int64_t k_st, const uint1
   const int64_t slot = slots[t];
   if (slot < 0 || slot >= num_blocks * block) return;
   uint16_t* dst = cache + (slot / block) * page_stride + (slot % block) * row_stride;
-  const int chunks = width / 8;
-  for (int c = threadIdx.x; c < 2 * chunks; c += blockDim.x) {
-    const bool is_v = c >= chunks;
-    const int cc = (is_v ? c - chunks : c) * 8;
-    const u32x4 val = ld16((is_v ? value + (int64_t)t * v_st : key + (int64_t)t * k_st) + cc);
-    st16(dst + (is_v ? width : 0) + cc, val);
+  const uint16_t* ks = key + (int64_t)t * k_st;
+  const uint16_t* vs = value + (int64_t)t * v_st;
+  if (VEC) {  // 16-byte pieces
+    const int chunks = width / 8;
+    for (int c = threadIdx.x; c < 2 * chunks; c += blockDim.x) {
+      const bool is_v = c >= chunks;
+      const int cc = (is_v ? c - chunks : c) * 8;
+      st16(dst + (is_v ? width : 0) + cc, ld16((is_v ? vs : ks) + cc));
+    }
+  } else {
+    for (int c = threadIdx.x; c < 2 * width; c += blockDim.x) dst[c] = c < width ? ks[c] : vs[c - width];
   }
 }
 
@@ -223,15 +229,21 @@ extern "C" int hla_s6_slot_mapping(const int32_t* block_table, int64_t bt_stride
 extern "C" int hla_s6_store_rows(const void* key, int64_t k_st, const void* value, int64_t v_st, int32_t num_tokens,
                                  int32_t width, const int64_t* slots, void* cache, int64_t page_stride,
                                  int64_t row_stride, int32_t block_size, int64_t num_blocks, void* stream) {
-  HLA_REQUIRE(num_tokens >= 0 && width > 0 && width % 8 == 0 && block_size > 0, HLA_S6_EINVAL,
-              "store_rows: width must be a positive multiple of 8");
+  HLA_REQUIRE(num_tokens >= 0 && width > 0 && block_size > 0 && num_blocks >= 1, HLA_S6_EINVAL,
+              "store_rows: bad width, block size or cache size");
   if (num_tokens == 0) return HLA_S6_OK;
   HLA_REQUIRE(key && value && slots && cache, HLA_S6_EINVAL, "store_rows: null pointer");
-  HLA_REQUIRE(aligned16(key) && aligned16(value) && aligned16(cache) && k_st % 8 == 0 && v_st % 8 == 0 &&
-                  page_stride % 8 == 0 && row_stride % 8 == 0,
-              HLA_S6_EINVAL, "store_rows: rows must be 16-byte aligned");
-  hipLaunchKernelGGL(store_rows_kernel, dim3(num_tokens), dim3(128), 0, as_stream(stream),
-                     static_cast<const uint16_t*>(key), k_st, static_cast<const uint16_t*>(value), v_st, width, slots,
-                     static_cast<uint16_t*>(cache), page_stride, row_stride, block_size, num_blocks);
+  const bool vec = width % 8 == 0 && aligned16(key) && aligned16(value) && aligned16(cache) && k_st % 8 == 0 &&
+                   v_st % 8 == 0 && page_stride % 8 == 0 && row_stride % 8 == 0;
+  const auto* k = static_cast<const uint16_t*>(key);
+  const auto* v = static_cast<const uint16_t*>(value);
+  auto* c = static_cast<uint16_t*>(cache);
+  if (vec) {
+    hipLaunchKernelGGL(store_rows_kernel<true>, dim3(num_tokens), dim3(128), 0, as_stream(stream), k, k_st, v, v_st,
+                       width, slots, c, page_stride, row_stride, block_size, num_blocks);
+  } else {
+    hipLaunchKernelGGL(store_rows_kernel<false>, dim3(num_tokens), dim3(128), 0, as_stream(stream), k, k_st, v, v_st,
+                       width, slots, c, page_stride, row_stride, block_size, num_blocks);
+  }
   return check_launch("store_rows");
 }

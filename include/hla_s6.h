@@ -156,7 +156,8 @@ int hla_s6_slot_mapping(const int32_t *block_table, int64_t bt_stride, int32_t b
 /* Replaces unified_kv_cache_update of a committed latent row (hla/vllm_latent/ouro_latent.py:127-129):
  * the row [key[t, :width] | value[t, :width]] is stored at page slots[t] / block_size, row
  * slots[t] % block_size of `cache` (negative slots and slots past num_blocks * block_size skipped).
- * key/value need a unit last stride. */
+ * key/value need a unit last stride; rows move in 16-byte pieces when width % 8 == 0 and the rows are
+ * 16-byte aligned, element by element otherwise. */
 int hla_s6_store_rows(const void *key, int64_t k_st, const void *value, int64_t v_st, int32_t num_tokens,
                       int32_t width, const int64_t *slots, void *cache, int64_t page_stride, int64_t row_stride,
                       int32_t block_size, int64_t num_blocks, void *stream);

@@ -67,7 +67,7 @@ class DecodeCase:
         ctx_lat_t = np.where(invalid, 0, ctx_lat[req])
         return O.attend_decode(bf16.to_f32(q_lat_bits), bf16.to_f32(q_rope_bits), bf16.to_f32(B), lat[..., :w],
                                lat[..., w:], lat_tab, ctx_lat_t, ex[..., :D], ex[..., D:], self.tables['exact'],
-                               self.qsl, seq_all, W, SCALE, invalid, rounding=True)
+                               self.qsl, seq_all, W, SCALE, invalid, rounding=False)
 
     def run(self, layer, ops, ctx, loop, q_lat_bits, q_rope_bits):
         _, w = self.reader_bits(loop)
@@ -164,7 +164,7 @@ def test_prefill_and_mixed_branch(ops, layer):
     latf, exf = bf16.to_f32(lat), bf16.to_f32(ex)
     want = O.attend_chunk(bf16.to_f32(q_lat), bf16.to_f32(q_rope), bf16.to_f32(k_rope), bf16.to_f32(v), bf16.to_f32(B),
                           latf[..., :w], latf[..., w:], {'latent': lt[req], 'exact': et[req]}, c, cl, qsl, W, SCALE,
-                          ~valid, exf[..., :D], exf[..., D:], rounding=True)
+                          ~valid, exf[..., :D], exf[..., D:], rounding=False)
     got = host_f32(out)
     assert_attention_close(got, want)
     assert (got[~valid] == 0).all()
