@@ -12,7 +12,7 @@ import os
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, 'libhla_s6.so')
+LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
 ABI_VERSION = 1
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
@@ -34,6 +34,9 @@ SIGNATURES = {
                                 I32, P, I32, F32, P, I64, I64, P, P],
     'hla_s6_chunk_attention': [P, P, P, I32, I32, I32, I64, I64, I64, I64, I64, I64, P, I32, F32, P, I64, I64, P, P],
     'hla_s6_merge_states': [P, I64, I64, P, P, I64, I64, P, P, I32, I32, I32, I32, P, I64, I64, P, P],
+    'hla_s6_attend_decode': [P, I64, I64, I32, P, P, I64, I64, I32, I64, P, I64, I32, P, P, P, I64, I64, P, P, I64, I64,
+                             I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32, F32, I32, P, I64, P,
+                             P, P, P, P, I64, I64, P],
     'hla_s6_slot_mapping': [P, I64, I32, P, P, P, I32, I32, P, P],
     'hla_s6_store_rows': [P, I64, P, I64, I32, I32, P, P, I64, I64, I32, I64, P],
 }

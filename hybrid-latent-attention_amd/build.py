@@ -35,21 +35,22 @@ def hipcc() -> str:
     return path
 
 
-def _compile(src: str, obj: str) -> str:
-    cmd = [hipcc(), *FLAGS, '-c', os.path.join(CSRC, src), '-o', obj]
+def _compile(src: str, obj: str, defines=()) -> str:
+    cmd = [hipcc(), *FLAGS, *(f'-D{d}' for d in defines), '-c', os.path.join(CSRC, src), '-o', obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src}:\n{proc.stdout}\n{proc.stderr}')
     return obj
 
 
-def build(verbose: bool = False) -> str:
-    """Compile every HIP source for gfx950 and link ``libhla_s6.so`` next to this file; returns its path."""
-    out = os.path.join(HERE, LIB_NAME)
+def build(verbose: bool = False, out: str | None = None, defines=()) -> str:
+    """Compile every HIP source for gfx950 and link ``libhla_s6.so`` (next to this file unless ``out`` names another
+    path; ``defines`` are extra ``NAME=VALUE`` preprocessor definitions); returns its path."""
+    out = out or os.path.join(HERE, LIB_NAME)
     with tempfile.TemporaryDirectory(prefix='hla_build_') as tmp:
         objs = [os.path.join(tmp, s.replace('.hip', '.o')) for s in SOURCES]
         with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as pool:
-            list(pool.map(_compile, SOURCES, objs))
+            list(pool.map(lambda so: _compile(*so, defines), zip(SOURCES, objs)))
         tmp_out = os.path.join(tmp, LIB_NAME)
         cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', *objs, '-o', tmp_out,
                '-Wl,-rpath,/opt/rocm/lib']

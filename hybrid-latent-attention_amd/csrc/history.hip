@@ -1,29 +1,56 @@
-// Paged latent-history attention for the S6 MQA cache (16 query heads share one latent row).
+// Paged latent-history attention for the S6 MQA cache (16 query heads share one latent row), and the fused
+// decode attention of one layer x loop built on it.
 //
-// Kernel 1 (history_split): one workgroup per (token, KV split), 4 waves. Wave w owns the latent
-// columns [w*R/4, (w+1)*R/4) of the query, of K and of V. Keys are walked in tiles of 16 rows (a
-// tile never crosses a page since the page size is a multiple of 16):
-//   * S^T[16 keys x 16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16. Each wave contracts its own
-//     latent quarter: K rows are loaded straight into the MFMA A-operand layout (lane l: key l%16,
-//     8 consecutive latent columns), Q^T is the B operand, held in registers for the whole row.
-//     The four quarter partials are summed through LDS (one barrier per tile, double-buffered).
-//   * online softmax in the exp2 domain on the 4 keys x 1 head each lane owns (cross-lane max/sum
-//     over the 4 lane groups sharing a head);
-//   * O^T[16 cols x 16 heads] += V^T . P^T on v_mfma_f32_16x16x16_bf16: P^T comes straight from the
-//     softmax registers (the S^T output layout is the B-operand layout), V^T is read from a
-//     wave-private LDS copy of the wave's V columns (transposing 16-bit reads).
+// history_split: one workgroup per (token, KV split), 4 waves. Wave w owns the latent columns
+// [w*R/4, (w+1)*R/4) of the query, of K and of V. Keys are walked in tiles of 16 rows (a tile never crosses a
+// page since the page size is a multiple of 16):
+//   * S^T[16 keys x 16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16. Each wave contracts its own latent quarter:
+//     K rows are loaded straight into the MFMA A-operand layout (lane l: key l%16, 8 consecutive latent columns),
+//     Q^T is the B operand, held in registers for the whole row. The four quarter partials are summed through
+//     LDS (one barrier per tile, double-buffered).
+//   * online softmax in the exp2 domain on the 4 keys x 1 head each lane owns (cross-lane max/sum over the 4
+//     lane groups sharing a head);
+//   * O^T[16 cols x 16 heads] += V^T . P^T on v_mfma_f32_16x16x16_bf16: P^T comes straight from the softmax
+//     registers (the S^T output layout is the B-operand layout), V^T is read from a wave-private LDS copy of the
+//     wave's V columns (transposing 16-bit reads).
 //   * K/V loads of the next two tiles are in flight while a tile is computed.
-// Each split writes its normalized partial output and natural-log LSE to the fp32 workspace
-// (or, with a single split, the final bf16 output and LSE directly).
-// Kernel 2 (history_combine): LSE reduction of the split partials into o [T,16,R] bf16, lse [16,T].
-#include "common.h"
+// With one split the workgroup writes the final bf16 output and lse. With several, each split writes its
+// normalized partial and lse to the fp32 workspace and history_combine (one workgroup per token and head)
+// reduces them by LSE in a second launch. (Reducing in the last split of each row instead needs agent-scope
+// release fences or L2-bypassing partials; both measured slower on MI355X than the extra launch.)
+// Optionally one more row of workgroups (blockIdx.y == num_splits) computes the decode exact window of every
+// token (exact.h), so the decode step runs its history and window attention in one launch.
+#include "exact.h"
 
 namespace hla {
+
+int absorb_merge(const void* x, int32_t num_tokens, int32_t num_heads, int32_t k_dim, int64_t x_st, int64_t x_sh,
+                 const void* w, int64_t w_sh, int64_t w_sk, int32_t n_dim, const float* lse_x, const void* o_b,
+                 int64_t b_st, int64_t b_sh, const float* lse_b, const uint8_t* invalid, void* out, int64_t o_st,
+                 int64_t o_sh, hipStream_t stream);
+
 namespace {
 
 constexpr int kHeads = 16;
 constexpr int kTile = 16;
 constexpr int kThreads = 256;
+constexpr int kMaxSplits = 1024;
+
+struct WindowPart {  // decode exact window, computed by the extra row of workgroups
+  ExactSource src;
+  const uint16_t* q;
+  int64_t q_st, q_sh;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int bt_cols;
+  const int32_t* qsl;
+  const int32_t* seq_lens;
+  int num_reqs;
+  int window;
+  uint16_t* out;  // [T, 16, 128]
+  int64_t o_st, o_sh;
+  float* lse;  // [16, T]
+};
 
 struct HistoryParams {
   const uint16_t* q;
@@ -41,11 +68,13 @@ struct HistoryParams {
   float scale_log2;
   int num_splits;
   int T;
-  float* ws_o;    // [T][S][16][R]
-  float* ws_lse;  // [T][S][16]
+  float* ws_o;      // [T][S][16][R]
+  float* ws_lse;    // [T][S][16]
   uint16_t* out;
   int64_t o_st, o_sh;
   float* lse;  // [16][T]
+  bool has_window;
+  WindowPart win;
 };
 
 template <int R>
@@ -138,6 +167,18 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   }
 }
 
+// The decode exact window of token t for all 16 heads (4 heads per wave).
+__device__ void window_token(const WindowPart& w, int T, float scale_log2, int t, int wave, int lane) {
+  int req, lo, hi;
+  decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi);
+  ExactSource src = w.src;
+  hi = (int)min((int64_t)hi, (int64_t)w.bt_cols * src.block_size);
+  src.table_row = w.bt + (int64_t)req * w.bt_stride;
+  for (int h = wave; h < kHeads; h += 4)
+    exact_row(src, w.q + (int64_t)t * w.q_st + (int64_t)h * w.q_sh, scale_log2, lo, hi, h, lane,
+              w.out + (int64_t)t * w.o_st + (int64_t)h * w.o_sh, w.lse + (int64_t)h * T + t);
+}
+
 template <int R>
 __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
   using G = Geo<R>;
@@ -147,14 +188,18 @@ __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
 
   const int t = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int hq = lane & 15, g = lane >> 4;
   const int S = a.num_splits;
+  if (s == S) {  // the window row (uniform over the workgroup)
+    window_token(a.win, a.T, a.scale_log2, t, wave, lane);
+    return;
+  }
+  const int hq = lane & 15, g = lane >> 4;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;  // keys the block table can address
   const int n = (int)min((int64_t)a.ctx[t], cap);
   const int tiles = (n + kTile - 1) / kTile;
 
-  // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that
-  // rows of a ragged batch get split counts proportional to their length and every split has equal work.
+  // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
+  // ragged batch get split counts proportional to their length and every split has equal work.
   int chunk = tiles;
   if (S > 1) {
     int mx = 0;
@@ -169,6 +214,7 @@ __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
   const int j_begin = s * chunk;
   const int j_end = min(tiles, j_begin + chunk);
   const int col0 = wave * G::QW;
+  const int64_t part_row = ((int64_t)t * S + s) * kHeads + hq;
 
   if (j_begin >= j_end) {  // nothing to read in this split (uniform over the workgroup)
     if (S == 1) {
@@ -176,123 +222,131 @@ __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
 #pragma unroll
       for (int nt = 0; nt < G::NT; ++nt) *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{0u, 0u};
       if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = -INFINITY;
-    } else if (wave == 0 && g == 0) {
-      a.ws_lse[((int64_t)t * S + s) * kHeads + hq] = -INFINITY;
+      return;
     }
-    return;
-  }
-
-  const int32_t* btr = a.bt + (a.bt_rows ? a.bt_rows[t] : (int64_t)t) * a.bt_stride;
-
-  u32x4 qreg[G::KI];
-  {
-    const uint16_t* qp = a.q + (int64_t)t * a.q_st + (int64_t)hq * a.q_sh + col0 + 8 * g;
-#pragma unroll
-    for (int i = 0; i < G::KI; ++i) qreg[i] = ld16(qp + 32 * i);
-  }
-
-  floatx4 oacc[G::NT];
-#pragma unroll
-  for (int nt = 0; nt < G::NT; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
-
-  uint16_t* vs0 = v_lds[wave][0];
-  uint16_t* vs1 = v_lds[wave][1];
-  TileRegs<R> ra, rb;
-  load_tile<R>(a, btr, n, j_begin, col0, lane, ra);
-  if (j_begin + 1 < j_end) load_tile<R>(a, btr, n, j_begin + 1, col0, lane, rb);
-  for (int j = j_begin; j < j_end; j += 2) {
-    floatx4 sa = stage_a<R>(ra, qreg, vs0, lane);
-    if (j + 2 < j_end) load_tile<R>(a, btr, n, j + 2, col0, lane, ra);
-    stage_b<R>(sa, s_lds[0], vs0, j * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
-    if (j + 1 < j_end) {
-      floatx4 sb = stage_a<R>(rb, qreg, vs1, lane);
-      if (j + 3 < j_end) load_tile<R>(a, btr, n, j + 3, col0, lane, rb);
-      stage_b<R>(sb, s_lds[1], vs1, (j + 1) * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
-    }
-  }
-
-  const float inv = 1.0f / l;
-  const float lse = (m + log2f(l)) * kLn2;
-  if (S == 1) {
-    uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
-#pragma unroll
-    for (int nt = 0; nt < G::NT; ++nt) {
-      const floatx4 o = oacc[nt] * inv;
-      *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
-    }
-    if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = lse;
+    if (wave == 0 && g == 0) a.ws_lse[part_row] = -INFINITY;
   } else {
-    const int64_t row = ((int64_t)t * S + s) * kHeads + hq;
-    float* wp = a.ws_o + row * R + col0 + 4 * g;
+    const int32_t* btr = a.bt + (a.bt_rows ? a.bt_rows[t] : (int64_t)t) * a.bt_stride;
+    u32x4 qreg[G::KI];
+    {
+      const uint16_t* qp = a.q + (int64_t)t * a.q_st + (int64_t)hq * a.q_sh + col0 + 8 * g;
+#pragma unroll
+      for (int i = 0; i < G::KI; ++i) qreg[i] = ld16(qp + 32 * i);
+    }
+    floatx4 oacc[G::NT];
+#pragma unroll
+    for (int nt = 0; nt < G::NT; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+
+    uint16_t* vs0 = v_lds[wave][0];
+    uint16_t* vs1 = v_lds[wave][1];
+    TileRegs<R> ra, rb;
+    load_tile<R>(a, btr, n, j_begin, col0, lane, ra);
+    if (j_begin + 1 < j_end) load_tile<R>(a, btr, n, j_begin + 1, col0, lane, rb);
+    for (int j = j_begin; j < j_end; j += 2) {
+      floatx4 sa = stage_a<R>(ra, qreg, vs0, lane);
+      if (j + 2 < j_end) load_tile<R>(a, btr, n, j + 2, col0, lane, ra);
+      stage_b<R>(sa, s_lds[0], vs0, j * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
+      if (j + 1 < j_end) {
+        floatx4 sb = stage_a<R>(rb, qreg, vs1, lane);
+        if (j + 3 < j_end) load_tile<R>(a, btr, n, j + 3, col0, lane, rb);
+        stage_b<R>(sb, s_lds[1], vs1, (j + 1) * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
+      }
+    }
+
+    const float inv = 1.0f / l;
+    const float lse = (m + log2f(l)) * kLn2;
+    if (S == 1) {
+      uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
+#pragma unroll
+      for (int nt = 0; nt < G::NT; ++nt) {
+        const floatx4 o = oacc[nt] * inv;
+        *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+      }
+      if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = lse;
+      return;
+    }
+    float* wp = a.ws_o + part_row * R + col0 + 4 * g;
 #pragma unroll
     for (int nt = 0; nt < G::NT; ++nt) *reinterpret_cast<floatx4*>(wp + 16 * nt) = oacc[nt] * inv;
-    if (wave == 0 && g == 0) a.ws_lse[row] = lse;
+    if (wave == 0 && g == 0) a.ws_lse[part_row] = lse;
   }
 }
 
-// One workgroup per (token, head); thread i owns output columns [4i, 4i+4).
+// Split reduction: one workgroup per (token, head), thread i owns output columns [4i, 4i+4).
 template <int R>
-__global__ __launch_bounds__(R / 4) void history_combine(const float* ws_o, const float* ws_lse, int S, int T,
-                                                         uint16_t* out, int64_t o_st, int64_t o_sh, float* lse) {
+__global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
   const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
-  const float* ls = ws_lse + (int64_t)t * S * kHeads + h;
+  const int S = a.num_splits;
+  const float* ls = a.ws_lse + (int64_t)t * S * kHeads + h;
   float mx = -INFINITY;
   for (int s = 0; s < S; ++s) mx = fmaxf(mx, ls[(int64_t)s * kHeads]);
-  uint16_t* op = out + (int64_t)t * o_st + (int64_t)h * o_sh + 4 * i;
+  uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * i;
   if (mx == -INFINITY) {
     *reinterpret_cast<uint2*>(op) = uint2{0u, 0u};
-    if (i == 0) lse[(int64_t)h * T + t] = -INFINITY;
+    if (i == 0) a.lse[(int64_t)h * a.T + t] = -INFINITY;
     return;
   }
+  const float* base = a.ws_o + ((int64_t)t * S * kHeads + h) * R + 4 * i;
   float den = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < S; ++s) {
-    const float ls_s = ls[(int64_t)s * kHeads];
-    if (ls_s == -INFINITY) continue;
-    const float w = __expf(ls_s - mx);
+  int s = 0;
+  for (; s + 8 <= S; s += 8) {  // eight partial rows in flight
+    floatx4 o[8];
+    float w[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      o[u] = *reinterpret_cast<const floatx4*>(base + (int64_t)(s + u) * kHeads * R);
+      const float l_s = ls[(int64_t)(s + u) * kHeads];
+      w[u] = l_s == -INFINITY ? 0.f : __expf(l_s - mx);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      den += w[u];
+      acc += w[u] == 0.f ? floatx4{0.f, 0.f, 0.f, 0.f} : o[u] * w[u];
+    }
+  }
+  for (; s < S; ++s) {
+    const float l_s = ls[(int64_t)s * kHeads];
+    if (l_s == -INFINITY) continue;
+    const float w = __expf(l_s - mx);
     den += w;
-    const floatx4 o = *reinterpret_cast<const floatx4*>(ws_o + (((int64_t)t * S + s) * kHeads + h) * R + 4 * i);
-    acc += o * w;
+    acc += *reinterpret_cast<const floatx4*>(base + (int64_t)s * kHeads * R) * w;
   }
   acc = acc * (1.0f / den);
   *reinterpret_cast<uint2*>(op) = uint2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
-  if (i == 0) lse[(int64_t)h * T + t] = mx + logf(den);
+  if (i == 0) a.lse[(int64_t)h * a.T + t] = mx + logf(den);
 }
 
 template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
-  dim3 grid(p.T, p.num_splits);
+  dim3 grid(p.T, p.num_splits + (p.has_window ? 1 : 0));
   hipLaunchKernelGGL(history_split<R>, grid, dim3(kThreads), 0, stream, p);
   int rc = check_launch("history_split");
-  if (rc != HLA_S6_OK || p.num_splits == 1) return rc;
-  hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(R / 4), 0, stream, p.ws_o, p.ws_lse, p.num_splits,
-                     p.T, p.out, p.o_st, p.o_sh, p.lse);
-  return check_launch("history_combine");
+  if (rc == HLA_S6_OK && p.num_splits > 1) {
+    hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(R / 4), 0, stream, p);
+    rc = check_launch("history_combine");
+  }
+  return rc;
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-}  // namespace
-}  // namespace hla
-
-extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,
-                                        int64_t q_st, int64_t q_sh, const void* k_cache, const void* v_cache,
-                                        int64_t page_stride, int64_t row_stride, int32_t block_size,
-                                        int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
-                                        int32_t bt_cols, const int64_t* bt_rows,
-                                        const int32_t* ctx, float scale, int32_t num_splits, float* workspace,
-                                        int64_t workspace_floats, void* out, int64_t o_st, int64_t o_sh, float* lse,
-                                        void* stream) {
-  using namespace hla;
+int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t num_heads, int32_t width, int64_t q_st,
+                 int64_t q_sh, const void* k_cache, const void* v_cache, int64_t page_stride, int64_t row_stride,
+                 int32_t block_size, int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                 int32_t bt_cols, const int64_t* bt_rows, const int32_t* ctx, float scale, int32_t num_splits,
+                 float* workspace, int64_t workspace_floats, void* out, int64_t o_st,
+                 int64_t o_sh, float* lse) {
   HLA_REQUIRE(num_tokens >= 0, HLA_S6_EINVAL, "history_attention: negative token count");
-  HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED, "history_attention: %d query heads (the kernel is built for 16)",
-              num_heads);
+  HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED,
+              "history_attention: %d query heads (the kernel is built for 16)", num_heads);
   HLA_REQUIRE(width == 128 || width == 256 || width == 512 || width == 1024, HLA_S6_EUNSUPPORTED,
               "history_attention: latent width %d not in {128, 256, 512, 1024}", width);
   HLA_REQUIRE(block_size > 0 && block_size % kTile == 0, HLA_S6_EUNSUPPORTED,
               "history_attention: block size %d is not a positive multiple of 16", block_size);
-  HLA_REQUIRE(num_splits >= 1, HLA_S6_EINVAL, "history_attention: num_kv_splits must be >= 1");
+  HLA_REQUIRE(num_splits >= 1 && num_splits <= kMaxSplits, HLA_S6_EINVAL,
+              "history_attention: num_kv_splits must be in [1, %d]", kMaxSplits);
   HLA_REQUIRE(num_blocks >= 1 && bt_cols >= 0, HLA_S6_EINVAL, "history_attention: empty cache or bad table width");
   if (num_tokens == 0) return HLA_S6_OK;
   HLA_REQUIRE(q && k_cache && v_cache && block_table && ctx && out && lse, HLA_S6_EINVAL,
@@ -309,8 +363,7 @@ extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32
                 "S6 workspace overflow: need %lld floats, have %lld", (long long)need, (long long)workspace_floats);
     HLA_REQUIRE(aligned16(workspace), HLA_S6_EINVAL, "history_attention: workspace must be 16-byte aligned");
   }
-  HLA_REQUIRE(num_splits <= 65535, HLA_S6_EINVAL, "history_attention: too many splits");
-  HistoryParams p;
+  p = HistoryParams{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
   p.q_sh = q_sh;
@@ -334,11 +387,92 @@ extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
-  hipStream_t st = as_stream(stream);
+  return HLA_S6_OK;
+}
+
+int dispatch(const HistoryParams& p, int width, hipStream_t st) {
   switch (width) {
     case 128: return launch<128>(p, st);
     case 256: return launch<256>(p, st);
     case 512: return launch<512>(p, st);
     default: return launch<1024>(p, st);
   }
+}
+
+}  // namespace
+}  // namespace hla
+
+extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                                        int64_t q_st, int64_t q_sh, const void* k_cache, const void* v_cache,
+                                        int64_t page_stride, int64_t row_stride, int32_t block_size,
+                                        int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                                        int32_t bt_cols, const int64_t* bt_rows, const int32_t* ctx, float scale,
+                                        int32_t num_splits, float* workspace, int64_t workspace_floats, void* out,
+                                        int64_t o_st, int64_t o_sh, float* lse,
+                                        void* stream) {
+  using namespace hla;
+  HistoryParams p;
+  int rc = fill_history(p, q, num_tokens, num_heads, width, q_st, q_sh, k_cache, v_cache, page_stride, row_stride,
+                        block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
+                        workspace, workspace_floats, out, o_st, o_sh, lse);
+  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_attend_decode(
+    const void* q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void* lat_k, const void* lat_v,
+    int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size, int64_t lat_num_blocks,
+    const int32_t* lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols, const int64_t* token_requests,
+    const int32_t* ctx_latent, const void* q_rope, int64_t qr_st, int64_t qr_sh, const void* ex_k, const void* ex_v,
+    int64_t ex_page_stride, int64_t ex_row_stride, int64_t ex_head_stride, int32_t ex_block_size,
+    int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
+    const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
+    int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
+    int32_t num_splits, float* workspace, int64_t workspace_floats, void* o_hist,
+    float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+  using namespace hla;
+  HistoryParams p;
+  int rc = fill_history(p, q_lat, num_tokens, num_heads, width, ql_st, ql_sh, lat_k, lat_v, lat_page_stride,
+                        lat_row_stride, block_size, lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols,
+                        token_requests, ctx_latent, scale, num_splits, workspace, workspace_floats, o_hist,
+                        (int64_t)num_heads * width, width, lse_hist);
+  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  HLA_REQUIRE(q_rope && ex_k && ex_v && ex_table && query_start_loc && seq_lens && num_reqs >= 1 && B && o_win &&
+                  lse_win && out && token_requests,
+              HLA_S6_EINVAL, "attend_decode: null pointer argument");
+  HLA_REQUIRE(window >= 0 && ex_block_size > 0 && ex_num_blocks >= 1 && ex_bt_cols >= 0, HLA_S6_EINVAL,
+              "attend_decode: bad window, exact block size, cache size or table width");
+  HLA_REQUIRE(aligned16(q_rope) && qr_st % 8 == 0 && qr_sh % 8 == 0 && aligned16(ex_k) && aligned16(ex_v) &&
+                  ex_page_stride % 8 == 0 && ex_row_stride % 8 == 0 && ex_head_stride % 8 == 0 && aligned16(o_win),
+              HLA_S6_EINVAL, "attend_decode: exact rows must be 16-byte aligned");
+  p.has_window = true;
+  WindowPart& w = p.win;
+  w.src.k = static_cast<const uint16_t*>(ex_k);
+  w.src.v = static_cast<const uint16_t*>(ex_v);
+  w.src.paged = true;
+  w.src.page_stride = ex_page_stride;
+  w.src.row_stride = ex_row_stride;
+  w.src.head_stride = ex_head_stride;
+  w.src.num_blocks = ex_num_blocks;
+  w.src.block_size = ex_block_size;
+  w.q = static_cast<const uint16_t*>(q_rope);
+  w.q_st = qr_st;
+  w.q_sh = qr_sh;
+  w.bt = ex_table;
+  w.bt_stride = ex_bt_stride;
+  w.bt_cols = ex_bt_cols;
+  w.qsl = query_start_loc;
+  w.seq_lens = seq_lens;
+  w.num_reqs = num_reqs;
+  w.window = window;
+  w.out = static_cast<uint16_t*>(o_win);
+  w.o_st = (int64_t)num_heads * kExactDim;
+  w.o_sh = kExactDim;
+  w.lse = lse_win;
+  hipStream_t st = as_stream(stream);
+  rc = dispatch(p, width, st);
+  if (rc != HLA_S6_OK) return rc;
+  return absorb_merge(o_hist, num_tokens, num_heads, width, (int64_t)num_heads * width, width, B, b_sh, b_sr,
+                      kExactDim, lse_hist, o_win, (int64_t)num_heads * kExactDim, kExactDim, lse_win, invalid, out,
+                      o_st, o_sh, st);
 }

@@ -1,27 +1,15 @@
 // Exact (per-head K/V) attention over short key ranges: the decode sliding window over the exact paged
-// cache, the history-only window of prefill/mixed steps, and the causal current chunk.
-//
-// One wave per (token, head). The 64 lanes form 4 groups of 16; a group takes one key per step and
-// each lane holds 8 of the 128 head dims, so a key row (K or V, 256 bytes) is one coalesced 16-byte
-// load per lane. Scores are reduced inside the 16-lane group; every group keeps its own online
-// softmax state (max, sum, 8 output dims) and the four groups are merged by LSE at the end.
-#include "common.h"
+// cache, the history-only window of prefill/mixed steps, and the causal current chunk. One wave per
+// (token, head) running exact_row (exact.h).
+#include "exact.h"
 
 namespace hla {
 namespace {
 
-constexpr int kDim = 128;
-
 struct ExactParams {
   const uint16_t* q;
   int64_t q_st, q_sh;
-  const uint16_t* k;
-  const uint16_t* v;
-  // paged source (window): page/row/head strides; dense source (chunk): token/head strides
-  int64_t page_stride, row_stride, head_stride;
-  int64_t k_st, k_sh, v_st, v_sh;
-  int block_size;
-  int64_t num_blocks;
+  ExactSource src;
   const int32_t* bt;
   int64_t bt_stride;
   int bt_cols;
@@ -39,49 +27,21 @@ struct ExactParams {
   float* lse;
 };
 
-// Request index of token t: searchsorted(qsl[1:], t, right=True) clamped to num_reqs - 1.
-__device__ __forceinline__ int request_of(const int32_t* qsl, int R, int t) {
-  int lo = 1, hi = R + 1;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (qsl[mid] > t) hi = mid;
-    else lo = mid + 1;
-  }
-  return min(lo - 1, R - 1);
-}
-
-__device__ __forceinline__ float group_sum16(float v) {
-  v += __shfl_xor(v, 1);
-  v += __shfl_xor(v, 2);
-  v += __shfl_xor(v, 4);
-  return v + __shfl_xor(v, 8);
-}
-
 __global__ __launch_bounds__(256) void exact_attention(ExactParams a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pair = blockIdx.x * 4 + wave;
   if (pair >= a.T * a.H) return;
   const int t = pair / a.H, h = pair % a.H;
-  const int grp = lane >> 4, d0 = (lane & 15) * 8;
-
   int lo = 0, hi = 0;
   int64_t row = 0;
-  if (a.mode == 0 || a.mode == 2) {
-    const int R = a.num_reqs;
-    if (t < a.qsl[R]) {
-      const int req = request_of(a.qsl, R, t);
-      if (a.mode == 0) {
-        const int lq = a.qsl[req + 1] - a.qsl[req];
-        const int p = a.seq_lens[req] - lq + (t - a.qsl[req]);
-        if (p >= 0) {
-          lo = max(0, p - a.window);
-          hi = p + 1;
-        }
-        row = req;
-      } else {
-        lo = a.qsl[req];
-        hi = t + 1;
-      }
+  if (a.mode == 0) {
+    int req;
+    decode_window_range(a.qsl, a.seq_lens, a.num_reqs, t, a.window, req, lo, hi);
+    row = req;
+  } else if (a.mode == 2) {
+    if (t < a.qsl[a.num_reqs]) {
+      lo = a.qsl[request_of(a.qsl, a.num_reqs, t)];
+      hi = t + 1;
     }
   } else {
     const int c = a.ctx[t];
@@ -89,86 +49,13 @@ __global__ __launch_bounds__(256) void exact_attention(ExactParams a) {
     hi = c;
     row = a.bt_rows ? a.bt_rows[t] : (int64_t)t;
   }
-
-  if (a.mode != 2) hi = (int)min((int64_t)hi, (int64_t)a.bt_cols * a.block_size);  // keys the table addresses
-
-  float qf[8];
-  {
-    const u32x4 qv = ld16(a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh + d0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      qf[2 * e] = lo_bf(qv[e]) * a.scale_log2;
-      qf[2 * e + 1] = hi_bf(qv[e]) * a.scale_log2;
-    }
+  ExactSource src = a.src;
+  if (src.paged) {
+    hi = (int)min((int64_t)hi, (int64_t)a.bt_cols * src.block_size);  // keys the block table addresses
+    src.table_row = a.bt + row * a.bt_stride;
   }
-  float m = -INFINITY, l = 0.f, o[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) o[e] = 0.f;
-
-  const int32_t* btr = a.bt ? a.bt + row * a.bt_stride : nullptr;
-  for (int kb = lo; kb < hi; kb += 4) {
-    const int key = kb + grp;
-    const bool valid = key < hi;
-    u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-    if (valid) {
-      const uint16_t *kp, *vp;
-      if (a.mode == 2) {
-        kp = a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + d0;
-        vp = a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + d0;
-      } else {
-        const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
-        const int64_t off = page * a.page_stride +
-                            (int64_t)(key % a.block_size) * a.row_stride + (int64_t)h * a.head_stride + d0;
-        kp = a.k + off;
-        vp = a.v + off;
-      }
-      kv = ld16(kp);
-      vv = ld16(vp);
-    }
-    float dot = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) dot += qf[2 * e] * lo_bf(kv[e]) + qf[2 * e + 1] * hi_bf(kv[e]);
-    dot = group_sum16(dot);
-    if (valid) {
-      const float m_new = fmaxf(m, dot);
-      const float alpha = fast_exp2(m - m_new);
-      const float p = fast_exp2(dot - m_new);
-      l = l * alpha + p;
-      m = m_new;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[2 * e] = o[2 * e] * alpha + p * lo_bf(vv[e]);
-        o[2 * e + 1] = o[2 * e + 1] * alpha + p * hi_bf(vv[e]);
-      }
-    }
-  }
-
-  // LSE merge of the four group partials.
-  float M = fmaxf(m, __shfl_xor(m, 16));
-  M = fmaxf(M, __shfl_xor(M, 32));
-  uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + d0;
-  if (M == -INFINITY) {
-    if (grp == 0) st16(op, u32x4{0u, 0u, 0u, 0u});
-    if (lane == 0) a.lse[(int64_t)h * a.T + t] = -INFINITY;
-    return;
-  }
-  const float sc = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
-  float L = l * sc;
-  L += __shfl_xor(L, 16);
-  L += __shfl_xor(L, 32);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float x = o[e] * sc;
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
-    o[e] = x;
-  }
-  if (grp == 0) {
-    const float inv = 1.0f / L;
-    st16(op, u32x4{pack2(o[0] * inv, o[1] * inv), pack2(o[2] * inv, o[3] * inv), pack2(o[4] * inv, o[5] * inv),
-                   pack2(o[6] * inv, o[7] * inv)});
-  }
-  if (lane == 0) a.lse[(int64_t)h * a.T + t] = (M + log2f(L)) * kLn2;
+  exact_row(src, a.q + (int64_t)t * a.q_st + (int64_t)h * a.q_sh, a.scale_log2, lo, hi, h, lane,
+            a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh, a.lse + (int64_t)h * a.T + t);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -193,7 +80,7 @@ extern "C" int hla_s6_window_attention(const void* q, int32_t num_tokens, int32_
                                        float scale, void* out, int64_t o_st, int64_t o_sh, float* lse, void* stream) {
   using namespace hla;
   HLA_REQUIRE(num_tokens >= 0 && num_heads > 0, HLA_S6_EINVAL, "window_attention: bad token/head count");
-  HLA_REQUIRE(head_dim == kDim, HLA_S6_EUNSUPPORTED, "window_attention: head_dim %d (the kernel is built for 128)",
+  HLA_REQUIRE(head_dim == kExactDim, HLA_S6_EUNSUPPORTED, "window_attention: head_dim %d (the kernel is built for 128)",
               head_dim);
   HLA_REQUIRE(mode == 0 || mode == 1, HLA_S6_EINVAL, "window_attention: mode must be 0 (decode) or 1 (history)");
   HLA_REQUIRE(window >= 0, HLA_S6_EINVAL, "window_attention: negative window");
@@ -213,13 +100,14 @@ extern "C" int hla_s6_window_attention(const void* q, int32_t num_tokens, int32_
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
   p.q_sh = q_sh;
-  p.k = static_cast<const uint16_t*>(k_cache);
-  p.v = static_cast<const uint16_t*>(v_cache);
-  p.page_stride = page_stride;
-  p.row_stride = row_stride;
-  p.head_stride = head_stride;
-  p.block_size = block_size;
-  p.num_blocks = num_blocks;
+  p.src.k = static_cast<const uint16_t*>(k_cache);
+  p.src.v = static_cast<const uint16_t*>(v_cache);
+  p.src.paged = true;
+  p.src.page_stride = page_stride;
+  p.src.row_stride = row_stride;
+  p.src.head_stride = head_stride;
+  p.src.block_size = block_size;
+  p.src.num_blocks = num_blocks;
   p.bt = block_table;
   p.bt_stride = bt_stride;
   p.bt_cols = bt_cols;
@@ -247,7 +135,7 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
                                       float* lse, void* stream) {
   using namespace hla;
   HLA_REQUIRE(num_tokens >= 0 && num_heads > 0, HLA_S6_EINVAL, "chunk_attention: bad token/head count");
-  HLA_REQUIRE(head_dim == kDim, HLA_S6_EUNSUPPORTED, "chunk_attention: head_dim %d (the kernel is built for 128)",
+  HLA_REQUIRE(head_dim == kExactDim, HLA_S6_EUNSUPPORTED, "chunk_attention: head_dim %d (the kernel is built for 128)",
               head_dim);
   if (num_tokens == 0) return HLA_S6_OK;
   HLA_REQUIRE(q && k && v && query_start_loc && num_reqs >= 1 && out && lse, HLA_S6_EINVAL,
@@ -260,13 +148,14 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
   p.q_sh = q_sh;
-  p.k = static_cast<const uint16_t*>(k);
-  p.v = static_cast<const uint16_t*>(v);
-  p.k_st = k_st;
-  p.k_sh = k_sh;
-  p.v_st = v_st;
-  p.v_sh = v_sh;
-  p.block_size = 1;
+  p.src.k = static_cast<const uint16_t*>(k);
+  p.src.v = static_cast<const uint16_t*>(v);
+  p.src.paged = false;
+  p.src.k_st = k_st;
+  p.src.k_sh = k_sh;
+  p.src.v_st = v_st;
+  p.src.v_sh = v_sh;
+  p.src.block_size = 1;
   p.mode = 2;
   p.qsl = query_start_loc;
   p.num_reqs = num_reqs;

@@ -127,26 +127,83 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     ``q_lat`` comes from ``StepContext.latent_query``; ``q_rope``, ``k_rope``, ``v`` are ``[T,H,d]``; ``cache`` is the
     layer's ``[num_blocks,1,block,2w]`` tensor or None (no history); ``block_table`` is the per-request table;
     ``window`` is ``(exact_cache, per-request block_table)`` or None. Returns ``[T,H,d]`` with ``~valid`` rows zeroed.
+    Decode steps with history run as one fused call (history + exact window in one launch, the split reduction,
+    then the ``B_t`` projection fused with the LSE merge); other steps compose the single ops in the reference's
+    order.
     """
     fused = window is not None and ctx.md_present and ctx.max_query_len == 1
+    has_history = cache is not None and ctx.md_present and ctx.history_needed
+    if fused and has_history:
+        return _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window)
     if fused:
         o_chunk, lse_chunk = s6_ops.window_attention_fa(q_rope, window[0], window[1], ctx.query_start_loc, ctx.seq_lens,
                                                         ctx.window, ctx.scale, ctx.max_seqlen_k, ctx.invalid)
     else:
         o_chunk, lse_chunk = s6_ops.chunk_attention(q_rope, k_rope, v, ctx.query_start_loc, ctx.max_query_len,
                                                     ctx.invalid, ctx.scale, ctx.backends.chunk)
-    if cache is None or not ctx.md_present or not ctx.history_needed:
+    if not has_history:
         return o_chunk.masked_fill_(ctx.invalid[:, None, None], 0)
-    if window is not None and not fused:
+    if window is not None:
         o_win, lse_win = s6_ops.window_history_fa(q_rope, window[0], ctx.block_table(window[1]), ctx.ctx, ctx.window,
                                                   ctx.scale, ctx.max_seqlen_k, ctx.empty)
         o_chunk, lse_chunk = s6_ops.merge_lse(o_chunk, lse_chunk, o_win, lse_win)
     _, B, _ = sl.readers(loop)
-    o_hist, lse_hist = s6_ops.history_attention(q_lat, cache, ctx.block_table(block_table), ctx.ctx_latent, ctx.scale,
-                                                ctx.num_kv_splits, ctx.workspace, k_scale, v_scale,
-                                                ctx.backends.history, ctx.empty_latent)
+    w = q_lat.shape[-1]
+    o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
+                                                   ctx.scale, ctx.num_kv_splits, ctx.workspace, k_scale, v_scale,
+                                                   ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests)
     o_hist = absorb_out(o_hist, B)
     return s6_ops.merge_states(o_hist, lse_hist, o_chunk, lse_chunk, ctx.invalid, ctx.backends.merge)
+
+
+def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
+    """Decode branch with history: one ``hla_s6_attend_decode`` call (three launches)."""
+    for kind in ('history', 'merge', 'chunk'):
+        s6_ops._backend(kind, getattr(ctx.backends, kind))
+    _, B, _ = sl.readers(loop)
+    exact, ex_table = window
+    s6_ops._dev(q_lat, q_rope, cache, block_table, exact, ex_table, B)
+    for name, t in (('q_lat', q_lat), ('q_rope', q_rope), ('cache', cache), ('exact cache', exact), ('B', B)):
+        s6_ops._bf16(name, t)
+    T, H, w = q_lat.shape
+    d = q_rope.shape[-1]
+    if cache.dim() != 4 or cache.shape[1] != 1 or cache.shape[-1] != 2 * w:
+        raise ValueError(f'latent cache must be [num_blocks, 1, block, {2 * w}], got {tuple(cache.shape)}')
+    if exact.dim() != 4 or exact.shape[1] != H or exact.shape[-1] != 2 * d:
+        raise ValueError(f'exact cache must be [num_blocks, {H}, block, {2 * d}], got {tuple(exact.shape)}')
+    if B.shape != (H, w, d):
+        raise ValueError(f'B must be [{H}, {w}, {d}], got {tuple(B.shape)}')
+    for name, tab in (('block_table', block_table), ('exact block_table', ex_table)):
+        if tab.dtype != torch.int32 or tab.stride(-1) != 1:
+            raise ValueError(f'{name} must be int32 with a unit last stride')
+    qsl = s6_ops._int('query_start_loc', ctx.query_start_loc, torch.int32)
+    seq = s6_ops._int('seq_lens', ctx.seq_lens, torch.int32)
+    R = qsl.shape[0] - 1
+    if block_table.shape[0] < R or ex_table.shape[0] < R or seq.shape[0] < R:
+        raise ValueError(f'per-request tables and seq_lens need {R} rows')
+    dev = q_lat.device
+    o_hist = torch.empty(T, H, w, dtype=torch.bfloat16, device=dev)
+    lse_hist = torch.empty(H, T, dtype=torch.float32, device=dev)
+    o_win = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
+    lse_win = torch.empty(H, T, dtype=torch.float32, device=dev)
+    out = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
+    splits = int(ctx.num_kv_splits)
+    ws = None
+    if splits > 1:
+        if ctx.workspace is None:
+            raise RuntimeError('history attention with num_kv_splits > 1 needs an S6Workspace')
+        ws = ctx.workspace.attn_logits(T, H, splits, w, dev)
+    _lib.call('hla_s6_attend_decode', _lib.ptr(q_lat), q_lat.stride(0), q_lat.stride(1), w, _lib.ptr(cache),
+              _lib.ptr(cache[..., w:]), cache.stride(0), cache.stride(2), cache.shape[2], cache.shape[0],
+              _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(ctx.token_requests),
+              _lib.ptr(ctx.ctx_latent), _lib.ptr(q_rope), q_rope.stride(0), q_rope.stride(1), _lib.ptr(exact),
+              _lib.ptr(exact[..., d:]), exact.stride(0), exact.stride(2), exact.stride(1), exact.shape[2],
+              exact.shape[0], _lib.ptr(ex_table), ex_table.stride(0), ex_table.shape[1], _lib.ptr(qsl), _lib.ptr(seq),
+              R, int(ctx.window), _lib.ptr(B), B.stride(0), B.stride(1), _lib.ptr(ctx.invalid), T, H, float(ctx.scale),
+              splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o_hist),
+              _lib.ptr(lse_hist), _lib.ptr(o_win), _lib.ptr(lse_win), _lib.ptr(out), out.stride(0), out.stride(1),
+              _lib.stream(dev))
+    return out
 
 
 @dataclass

@@ -150,7 +150,7 @@ def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_bloc
     return max(1, min(max(by_length, by_occupancy), 2 * sm_count, -(-max_seq_len // 32)))
 
 
-def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, workgroups_per_cu=4, min_keys_per_split=256):
+def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, workgroups_per_cu=2, min_keys_per_split=256):
     """Split count of the history kernel on MI355X: about ``workgroups_per_cu`` workgroups per compute unit over the
     step's rows, never splits shorter than ``min_keys_per_split`` keys (each split writes a 16 x width fp32 partial,
     so short splits turn into workspace traffic). A function of constants and the row count only (graph-stable).
@@ -158,7 +158,7 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, workgroups_per_cu=4,
     use a number of splits proportional to their length."""
     by_occupancy = -(-workgroups_per_cu * cu_count // max(1, num_tokens))
     by_length = max(1, -(-max_seq_len // min_keys_per_split))
-    return max(1, min(by_occupancy, by_length, 65535))
+    return max(1, min(by_occupancy, by_length, 1024))
 
 
 class S6Workspace:

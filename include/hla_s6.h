@@ -76,7 +76,7 @@ int hla_s6_latent_rope(void *x, int32_t num_tokens, int32_t num_heads, int32_t w
  * and of the B_t projection (hla/vllm_latent/s6_layer.py:114). When rope_table != NULL the latent
  * RoPE of hla_s6_latent_rope is applied to the rounded product before it is stored, which fuses
  * s6_layer.latent_query (hla/vllm_latent/s6_layer.py:32-40). x, w and out need a unit last stride;
- * w is [H, k_dim, n_dim] with strides (w_sh, w_sk, 1). k_dim % 32 == 0, n_dim % 64 == 0. */
+ * w is [H, k_dim, n_dim] with strides (w_sh, w_sk, 1). k_dim in {128, 256, 512, 1024}, n_dim % 64 == 0. */
 int hla_s6_absorb(const void *x, int32_t num_tokens, int32_t num_heads, int32_t k_dim, int64_t x_st,
                   int64_t x_sh, const void *w, int64_t w_sh, int64_t w_sk, int32_t n_dim, void *out,
                   int64_t o_st, int64_t o_sh, const int64_t *positions, const void *rope_table,
@@ -91,10 +91,11 @@ int hla_s6_absorb(const void *x, int32_t num_tokens, int32_t num_heads, int32_t 
  * (and likewise for v_cache), row(t) = bt_rows ? bt_rows[t] : t; only table columns
  * < ceil(ctx[t] / block_size) are read. Metadata outside the buffers never faults: a row reads at most
  * bt_cols * block_size keys and page ids are clamped into [0, num_blocks). block_size % 16 == 0; q, K and V rows need a unit last
- * stride and 16-byte alignment. num_splits >= 1 partitions each row's keys (split-KV); partials
- * go to `workspace` (fp32, caller-owned, >= num_tokens * num_splits * 16 * (width + 1) floats when
- * num_splits > 1; unused when num_splits == 1). Outputs o [T, 16, width] bf16 (strides o_st, o_sh, 1)
- * and lse [16, T] fp32. */
+ * stride and 16-byte alignment. num_splits in [1, 1024] partitions each row's keys (split-KV): every row
+ * is cut in chunks sized from the longest row of the call, partials go to `workspace` (fp32, caller-owned,
+ * >= num_tokens * num_splits * 16 * (width + 1) floats; unused when num_splits == 1) and a second launch
+ * reduces them by LSE. Calls that share a workspace must not overlap in time.
+ * Outputs o [T, 16, width] bf16 (strides o_st, o_sh, 1) and lse [16, T] fp32. */
 int hla_s6_history_attention(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
                              int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
                              int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
@@ -143,6 +144,30 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
                         int64_t b_st, int64_t b_sh, const float *lse_b, const uint8_t *invalid,
                         int32_t num_tokens, int32_t num_heads, int32_t head_dim, int32_t mode, void *out,
                         int64_t o_st, int64_t o_sh, float *lse_out, void *stream);
+
+/* ---- a9: fused decode attention of one layer x loop --------------------------------------------------
+ * Replaces the decode branch of s6_layer.attend (hla/vllm_latent/s6_layer.py:97-100,110-115):
+ * window_attention_fa + history_attention + the B_t einsum + merge_states, in three launches:
+ *   1. the history kernels of hla_s6_history_attention over q_lat and the latent cache (per-request table
+ *      `lat_table`, row of token t = token_requests[t], ctx_latent[t] rows); the split kernel also runs one
+ *      extra row of workgroups computing the exact decode window of every token (mode 0 of
+ *      hla_s6_window_attention over q_rope and the loop's exact cache);
+ *   2. out = merge(bf16(o_hist @ B[h]), o_win) with the merge_states conventions (invalid rows zeroed).
+ * The intermediates o_hist [T, 16, width] bf16, lse_hist [16, T], o_win [T, 16, 128] bf16 and lse_win [16, T]
+ * are caller-owned contiguous buffers (they hold the two partial attentions on return). B is [16, width, 128]
+ * with strides (b_sh, b_sr, 1). Workspace as for hla_s6_history_attention. */
+int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void *lat_k,
+                         const void *lat_v, int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size,
+                         int64_t lat_num_blocks, const int32_t *lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols,
+                         const int64_t *token_requests, const int32_t *ctx_latent, const void *q_rope, int64_t qr_st,
+                         int64_t qr_sh, const void *ex_k, const void *ex_v, int64_t ex_page_stride,
+                         int64_t ex_row_stride, int64_t ex_head_stride, int32_t ex_block_size, int64_t ex_num_blocks,
+                         const int32_t *ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
+                         const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs, int32_t window,
+                         const void *B, int64_t b_sh, int64_t b_sr, const uint8_t *invalid, int32_t num_tokens,
+                         int32_t num_heads, float scale, int32_t num_splits, float *workspace,
+                         int64_t workspace_floats, void *o_hist, float *lse_hist, void *o_win,
+                         float *lse_win, void *out, int64_t o_st, int64_t o_sh, void *stream);
 
 /* ---- a10 (slot-mapped row commit) -----------------------------------------------------------------
  * Slot of each token: block_table[token_requests[t], positions[t] / block_size] * block_size
