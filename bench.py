@@ -14,6 +14,7 @@ import importlib
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -25,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = 'latent decode-attn µs/layer + HBM GB/s (% peak), Ouro-1.4B S6, B=64 ctx 8K'
 PEAK_HBM_GBPS = 8000.0
+TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'history_split_512_b64_ctx8192_pmc.md')
 LAYERS, LOOPS, HEADS, HEAD_DIM, RANK, RANK1, WINDOW, BLOCK = 24, 4, 16, 128, 512, 256, 32, 16
 MAX_POSITION = 65536
 
@@ -36,17 +38,23 @@ def parse():
     p.add_argument('--warmup', type=int, default=3)
     p.add_argument('--batch', type=int, default=64)
     p.add_argument('--context', type=int, default=8192, help='history tokens before the decoded token')
-    p.add_argument('--splits', type=int, default=0, help='KV splits (0: the MI355X policy)')
-    p.add_argument('--kernel-only', action='store_true', help='only launch the main-latent history op (profiling)')
+    p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
+    p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
+    p.add_argument('--width', type=int, default=512, choices=(256, 512), help='latent width of --kernel-only')
+    p.add_argument('--copy-calibration', action='store_true',
+                   help='only run a plain 1 GiB device copy three times (scales the FETCH_SIZE / WRITE_SIZE counters '
+                        'of a PMC profile to bytes)')
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--seed', type=int, default=0)
+    p.add_argument('--table', choices=('random', 'identity'), default='random',
+                   help='latent block tables: a random permutation of the page pool, or pages in order')
     return p.parse_args()
 
 
 class Workload:
     """Random-init caches, tables and readers of the whole model's attention path (one decode step of B rows)."""
 
-    def __init__(self, ops, layer, B, hist, splits, seed, device):
+    def __init__(self, ops, layer, B, hist, splits, seed, device, table='random'):
         g = torch.Generator(device=device).manual_seed(seed)
         self.B, self.hist, self.device = B, hist, device
         self.seq_len = hist + 1                                   # the decoded token is already in the exact cache
@@ -57,8 +65,9 @@ class Workload:
         randn = lambda *shape, std=1.0: (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std
                                          ).to(torch.bfloat16)
         perm = lambda n: (torch.randperm(n - 1, generator=g, device=device) + 1).to(torch.int32)
-        self.lat_table = {RANK: perm(pool)[:B * cols].view(B, cols).contiguous(),
-                          RANK1: perm(pool)[:B * cols].view(B, cols).contiguous()}
+        lat_pages = perm if table == 'random' else (lambda n: torch.arange(1, n, dtype=torch.int32, device=device))
+        self.lat_table = {RANK: lat_pages(pool)[:B * cols].view(B, cols).contiguous(),
+                          RANK1: lat_pages(pool)[:B * cols].view(B, cols).contiguous()}
         self.lat = []
         for _ in range(LAYERS):
             self.lat.append({w: torch.empty(pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(
@@ -84,15 +93,15 @@ class Workload:
         self.positions = torch.full((B,), hist, dtype=torch.int64, device=device)
         self.qsl = torch.arange(B + 1, dtype=torch.int32, device=device)
         self.seq_lens = torch.full((B,), self.seq_len, dtype=torch.int32, device=device)
-        self.splits = splits
-        self.workspace = ops.S6Workspace(HEADS, RANK, B * splits)
+        self.splits = splits                                      # {latent width: KV splits}
+        self.workspace = ops.S6Workspace.for_splits(HEADS, B, splits)
         self.ops, self.layer = ops, layer
 
     def step(self):
         ops, layer = self.ops, self.layer
         ctx = layer.StepContext(self.positions, self.qsl, self.seq_lens, 1, self.B, self.tables, HEAD_DIM ** -0.5,
-                                ops.HIP_BACKENDS, self.workspace, self.splits, window=WINDOW,
-                                max_seqlen_k=self.seq_len)
+                                ops.HIP_BACKENDS, self.workspace, self.splits[RANK], window=WINDOW,
+                                max_seqlen_k=self.seq_len, kv_splits_by_width=self.splits)
         outs = []
         for loop in range(LOOPS):
             w = RANK1 if loop == 0 else RANK
@@ -143,31 +152,51 @@ def time_graph(fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
-def history_op_roofline(wl, iters=50):
-    """Average duration of the main-latent history attention op (history_split + history_combine launches), timed
-    with HIP events on the stream it runs on, and the algorithmic bytes it reads."""
+def measured_traffic(path=TRAFFIC_PROFILE):
+    """HBM bytes per launch of the roofline kernel from its committed rocprofv3 PMC summary (FETCH_SIZE and
+    WRITE_SIZE scaled by a plain-copy calibration), or None when the summary is absent."""
+    try:
+        with open(path) as f:
+            m = re.search(r'^traffic_bytes_per_launch:\s*(\d+)', f.read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def history_roofline(wl, iters=50, width=RANK):
+    """The dominant kernel of the step, the split-KV history kernel (stage 1 of the history op), launched alone
+    over the main latent of every layer in turn: its average duration from HIP events on the stream it runs on,
+    the average duration of the stage-2 reduction likewise, and the algorithmic bytes stage 1 reads (every latent
+    K and V row of every token once)."""
     ops = wl.ops
     ctx_lat = torch.full((wl.B,), wl.n_latent, dtype=torch.int32, device=wl.device)
-    q = torch.randn(wl.B, HEADS, RANK, device=wl.device).to(torch.bfloat16) * (RANK ** -0.5)
-    layers = [wl.lat[i][RANK] for i in range(LAYERS)]
+    q = torch.randn(wl.B, HEADS, width, device=wl.device).to(torch.bfloat16) * (width ** -0.5)
+    caches = [wl.lat[i][width] for i in range(LAYERS)]
+    splits = wl.splits[width]
 
-    def run(i):
-        return ops.history_attention(q, layers[i % LAYERS], wl.lat_table[RANK], ctx_lat, HEAD_DIM ** -0.5, wl.splits,
-                                     wl.workspace, None, None, 'hip')
+    def stage1(i):
+        c = caches[i % LAYERS]
+        return ops.history_partials(q, c[..., :width], c[..., width:], wl.lat_table[width], ctx_lat, HEAD_DIM ** -0.5,
+                                    splits, wl.workspace)
 
-    for i in range(5):
-        run(i)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(iters):
-        run(i)
-    end.record(stream)
-    torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1000 / iters
-    nbytes = wl.B * wl.n_latent * 2 * RANK * 2
-    return us, nbytes
+    def timed(fn):
+        for i in range(5):
+            fn(i)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(iters):
+            fn(i)
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1000 / iters
+
+    us = timed(stage1)
+    part = stage1(0)
+    us_reduce = timed(lambda i: ops.history_reduce(part))
+    nbytes = wl.B * wl.n_latent * 2 * width * 2
+    return us, us_reduce, nbytes
 
 
 def cpu_baseline(wl, tokens=8):
@@ -225,21 +254,29 @@ def main():
     if not torch.cuda.is_available():
         print('bench.py needs an MI355X GPU', file=sys.stderr)
         sys.exit(2)
-    pkg = importlib.import_module('hybrid-latent-attention_amd')
-    ops, layer = pkg.s6_ops, pkg.s6_layer
     device = torch.device('cuda:0')
     torch.cuda.set_device(device)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.int32, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'copy_bytes': src.numel() * 4, 'copies': 3}), flush=True)
+        return
+    pkg = importlib.import_module('hybrid-latent-attention_amd')
+    ops, layer = pkg.s6_ops, pkg.s6_layer
     cus = pkg._lib.device_cus(0)
-    splits = args.splits or ops.mi355x_kv_splits(args.context, args.batch, cus)
+    splits = {w: args.splits or ops.mi355x_kv_splits(args.context, args.batch, cus, width=w) for w in (RANK, RANK1)}
     print(f'bench: building workload B={args.batch} ctx={args.context} splits={splits} cus={cus}', file=sys.stderr,
           flush=True)
-    wl = Workload(ops, layer, args.batch, args.context, splits, args.seed, device)
+    wl = Workload(ops, layer, args.batch, args.context, splits, args.seed, device, args.table)
     torch.cuda.synchronize()
 
     if args.kernel_only:
-        us, nbytes = history_op_roofline(wl, iters=max(args.steps, 1))
-        print(json.dumps({'kernel': 'history_attention main latent', 'us_per_launch': us,
-                          'gbps': nbytes / us / 1e3}), flush=True)
+        us, us_reduce, nbytes = history_roofline(wl, iters=max(args.steps, 1), width=args.width)
+        print(json.dumps({'kernel': f'history_split width {args.width}', 'splits': splits[args.width],
+                          'us_per_launch': us, 'gbps': nbytes / us / 1e3, 'reduce_us': us_reduce}), flush=True)
         return
 
     print('bench: capturing the decode step', file=sys.stderr, flush=True)
@@ -247,8 +284,8 @@ def main():
     us_layer = ms * 1000 / LAYERS
     hist_bytes, win_bytes = wl.history_bytes_per_layer(), wl.window_bytes_per_layer()
     layer_gbps = (hist_bytes + win_bytes) / (us_layer * 1e3)
-    print('bench: history op roofline', file=sys.stderr, flush=True)
-    op_us, op_bytes = history_op_roofline(wl)
+    print('bench: history kernel roofline', file=sys.stderr, flush=True)
+    op_us, reduce_us, op_bytes = history_roofline(wl)
     achieved = op_bytes / (op_us * 1e3)
     base = None
     if not args.no_cpu_baseline:
@@ -265,10 +302,11 @@ def main():
         'tokens_per_s': round(args.batch / (ms / 1000), 1),
         'hbm_gbps': round(layer_gbps, 1), 'hbm_frac': round(layer_gbps / PEAK_HBM_GBPS, 4),
         'bytes_per_layer': {'latent_history': hist_bytes, 'exact_window': win_bytes},
-        'roofline': {'kernel': 'history_attention main latent (history_split + history_combine)', 'bound': 'hbm',
-                     'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
-                     'frac': round(achieved / PEAK_HBM_GBPS, 4), 'traffic': None, 'us_per_launch': round(op_us, 2),
-                     'algorithmic_bytes_per_launch': op_bytes},
+        'roofline': {'kernel': f'history_split<{RANK}> (split-KV latent history, {splits[RANK]} splits)',
+                     'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBPS, 'unit': 'GB/s',
+                     'frac': round(achieved / PEAK_HBM_GBPS, 4), 'traffic': measured_traffic(),
+                     'us_per_launch': round(op_us, 2), 'algorithmic_bytes_per_launch': op_bytes,
+                     'reduce_us_per_launch': round(reduce_us, 2)},
         'cpu_baseline': base,
     }
     print(json.dumps(result), flush=True)

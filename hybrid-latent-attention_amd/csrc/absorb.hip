@@ -7,15 +7,13 @@
 // B operand is one 16-byte LDS read per lane. Epilogues:
 //   * STORE: bf16 result;
 //   * ROPE: latent RoPE of the bf16-rounded product (fused latent_query); the four column tiles are then
-//     {c, c+16, c+N/2, c+N/2+16}, so every lane holds both rotation partners of its outputs;
-//   * MERGE: the decode merge of the B_t-projected history output with the exact-window partial
-//     (merge_states semantics, invalid rows zeroed) - the projection and the merge in one launch.
+//     {c, c+16, c+N/2, c+N/2+16}, so every lane holds both rotation partners of its outputs.
 #include "common.h"
 
 namespace hla {
 namespace {
 
-enum Epilogue { kStore = 0, kRope = 1, kMerge = 2 };
+enum Epilogue { kStore = 0, kRope = 1 };
 
 struct AbsorbParams {
   const uint16_t* x;
@@ -30,12 +28,6 @@ struct AbsorbParams {
   const uint16_t* table;
   int table_rows;
   int64_t table_stride;
-  // MERGE
-  const float* lse_x;     // [H, T] lse of the projected side
-  const uint16_t* o_b;    // [T, H, N] other partial
-  int64_t b_st, b_sh;
-  const float* lse_b;     // [H, T]
-  const uint8_t* invalid; // [T] nullable
 };
 
 template <int K, int EPI>
@@ -76,6 +68,21 @@ __global__ __launch_bounds__(256) void absorb_kernel(AbsorbParams a) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) xa[i] = ta < a.T ? ld16(xrow + 32 * i) : u32x4{0u, 0u, 0u, 0u};
   }
+  // RoPE epilogue operands (positions, then the table rows) in flight with the slab
+  float rcos[4][2], rsin[4][2];
+  if (EPI == kRope) {
+    const int half = a.N / 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = min(t0 + 4 * g + r, a.T - 1);
+      const uint16_t* tr = a.table + min(max(a.pos[t], (int64_t)0), (int64_t)a.table_rows - 1) * a.table_stride;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        rcos[r][i] = bf2f(tr[ct[i] + l16]);
+        rsin[r][i] = bf2f(tr[half + ct[i] + l16]);
+      }
+    }
+  }
   // transpose the slab into LDS: wt[col][k]
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
@@ -110,36 +117,13 @@ __global__ __launch_bounds__(256) void absorb_kernel(AbsorbParams a) {
     uint16_t* orow = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh;
     if (EPI == kRope) {
       const int half = a.N / 2;
-      const uint16_t* tr = a.table + min(max(a.pos[t], (int64_t)0), (int64_t)a.table_rows - 1) * a.table_stride;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int c = ct[i] + l16;
         const float x1 = rbf(acc[i][r]), x2 = rbf(acc[i + 2][r]);
-        const float cs = bf2f(tr[c]), sn = bf2f(tr[half + c]);
+        const float cs = rcos[r][i], sn = rsin[r][i];
         orow[c] = f2bf(rbf(x1 * cs) - rbf(x2 * sn));
         orow[c + half] = f2bf(rbf(x2 * cs) + rbf(x1 * sn));
-      }
-    } else if (EPI == kMerge) {
-      const int64_t li = (int64_t)h * a.T + t;
-      float lx = a.lse_x[li], lb = a.lse_b[li];
-      if (lx == INFINITY) lx = -INFINITY;  // +inf lse counts as empty
-      if (lb == INFINITY) lb = -INFINITY;
-      float peak = fmaxf(lx, lb);
-      if (isinf(peak)) peak = 0.f;
-      float wx = expf(lx - peak), wb = expf(lb - peak);
-      const float total = wx + wb;
-      if (total > 0.f) {
-        wx /= total;
-        wb /= total;
-      } else {
-        wx = wb = 0.f;
-      }
-      const bool dead = a.invalid && a.invalid[t];
-      const uint16_t* brow = a.o_b + (int64_t)t * a.b_st + (int64_t)h * a.b_sh;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = ct[i] + l16;
-        orow[c] = dead ? (uint16_t)0 : f2bf(rbf(acc[i][r]) * wx + bf2f(brow[c]) * wb);
       }
     } else {
 #pragma unroll
@@ -190,34 +174,6 @@ int check_common(const void* x, int32_t num_tokens, int32_t num_heads, int32_t k
 }
 
 }  // namespace
-
-int absorb_merge(const void* x, int32_t num_tokens, int32_t num_heads, int32_t k_dim, int64_t x_st, int64_t x_sh,
-                 const void* w, int64_t w_sh, int64_t w_sk, int32_t n_dim, const float* lse_x, const void* o_b,
-                 int64_t b_st, int64_t b_sh, const float* lse_b, const uint8_t* invalid, void* out, int64_t o_st,
-                 int64_t o_sh, hipStream_t stream) {
-  int rc = check_common(x, num_tokens, num_heads, k_dim, x_st, x_sh, w, w_sh, w_sk, n_dim, out);
-  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
-  HLA_REQUIRE(lse_x && o_b && lse_b, HLA_S6_EINVAL, "absorb merge: null partial");
-  AbsorbParams p = {};
-  p.x = static_cast<const uint16_t*>(x);
-  p.x_st = x_st;
-  p.x_sh = x_sh;
-  p.w = static_cast<const uint16_t*>(w);
-  p.w_sh = w_sh;
-  p.w_sk = w_sk;
-  p.out = static_cast<uint16_t*>(out);
-  p.o_st = o_st;
-  p.o_sh = o_sh;
-  p.T = num_tokens;
-  p.N = n_dim;
-  p.lse_x = lse_x;
-  p.o_b = static_cast<const uint16_t*>(o_b);
-  p.b_st = b_st;
-  p.b_sh = b_sh;
-  p.lse_b = lse_b;
-  p.invalid = invalid;
-  return launch_k<kMerge>(p, k_dim, num_heads, stream);
-}
 
 }  // namespace hla
 

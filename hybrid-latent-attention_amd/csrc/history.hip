@@ -1,35 +1,54 @@
 // Paged latent-history attention for the S6 MQA cache (16 query heads share one latent row), and the fused
 // decode attention of one layer x loop built on it.
 //
-// history_split: one workgroup per (token, KV split), 4 waves. Wave w owns the latent columns
-// [w*R/4, (w+1)*R/4) of the query, of K and of V. Keys are walked in tiles of 16 rows (a tile never crosses a
+// history_split: one workgroup per (token, KV split), one wave per 128 latent columns (4 waves for the 512-wide
+// main latent, 2 for the 256-wide loop-1 latent). Wave w owns the latent columns [128w, 128w + 128) of the query,
+// of K and of V. Keys are walked in tiles of 16 rows (a tile never crosses a
 // page since the page size is a multiple of 16):
-//   * S^T[16 keys x 16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16. Each wave contracts its own latent quarter:
-//     K rows are loaded straight into the MFMA A-operand layout (lane l: key l%16, 8 consecutive latent columns),
-//     Q^T is the B operand, held in registers for the whole row. The four quarter partials are summed through
-//     LDS (one barrier per tile, double-buffered).
+//   * S^T[16 keys x 16 heads] = K . Q^T on v_mfma_f32_16x16x32_bf16. Each wave contracts its own 128 columns:
+//     K rows are loaded coalesced (4 rows x 256 bytes per instruction), staged in wave-private LDS and read back
+//     in the MFMA A-operand layout (lane l: key l%16, 8 consecutive latent columns); Q^T is the B operand, held
+//     in registers for the whole row. The per-wave partials are summed through LDS (one barrier per tile, two
+//     buffers alternating by tile parity).
 //   * online softmax in the exp2 domain on the 4 keys x 1 head each lane owns (cross-lane max/sum over the 4
 //     lane groups sharing a head);
 //   * O^T[16 cols x 16 heads] += V^T . P^T on v_mfma_f32_16x16x16_bf16: P^T comes straight from the softmax
 //     registers (the S^T output layout is the B-operand layout), V^T is read from a wave-private LDS copy of the
 //     wave's V columns (transposing 16-bit reads).
-//   * K/V loads of the next two tiles are in flight while a tile is computed.
+//   * the K/V loads of the next tile are in flight while a tile is computed.
 // With one split the workgroup writes the final bf16 output and lse. With several, each split writes its
 // normalized partial and lse to the fp32 workspace and history_combine (one workgroup per token and head)
 // reduces them by LSE in a second launch. (Reducing in the last split of each row instead needs agent-scope
 // release fences or L2-bypassing partials; both measured slower on MI355X than the extra launch.)
-// Optionally one more row of workgroups (blockIdx.y == num_splits) computes the decode exact window of every
-// token (exact.h), so the decode step runs its history and window attention in one launch.
+// For the fused decode step the split workgroups of a token also compute its exact decode window (exact.h), the
+// heads spread over the splits, so history and window attention run in one launch; decode_epilogue then reduces
+// the split partials, applies B_t and merges with the window in a second one.
 #include "exact.h"
 
 namespace hla {
 
-int absorb_merge(const void* x, int32_t num_tokens, int32_t num_heads, int32_t k_dim, int64_t x_st, int64_t x_sh,
-                 const void* w, int64_t w_sh, int64_t w_sk, int32_t n_dim, const float* lse_x, const void* o_b,
-                 int64_t b_st, int64_t b_sh, const float* lse_b, const uint8_t* invalid, void* out, int64_t o_st,
-                 int64_t o_sh, hipStream_t stream);
-
 namespace {
+
+// Tuning of the split kernel: tiles in flight per workgroup, V copies in LDS, non-temporal K/V loads,
+// waves-per-EU hint, K staged through LDS, latent columns per wave.
+#ifndef HLA_HIST_DEPTH
+#define HLA_HIST_DEPTH 1
+#endif
+#ifndef HLA_HIST_VBUF
+#define HLA_HIST_VBUF 1
+#endif
+#ifndef HLA_HIST_NT
+#define HLA_HIST_NT 1
+#endif
+#ifndef HLA_HIST_WPE
+#define HLA_HIST_WPE 3  // keeps the accumulators out of AGPRs: 3 waves per SIMD instead of 2
+#endif
+#ifndef HLA_HIST_KLDS
+#define HLA_HIST_KLDS 1
+#endif
+#ifndef HLA_HIST_WCOLS
+#define HLA_HIST_WCOLS 128
+#endif
 
 constexpr int kHeads = 16;
 constexpr int kTile = 16;
@@ -74,12 +93,16 @@ struct HistoryParams {
   int64_t o_st, o_sh;
   float* lse;  // [16][T]
   bool has_window;
+  bool direct;   // one split writing the final output and lse (else split partials to the workspace)
+  bool combine;  // launch history_combine after the split kernel (with more than one split)
   WindowPart win;
 };
 
 template <int R>
 struct Geo {
-  static constexpr int QW = R / 4;          // latent columns per wave
+  static constexpr int WAVES = R >= HLA_HIST_WCOLS ? R / HLA_HIST_WCOLS : 1;  // one wave per 128 latent columns
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int QW = R / WAVES;      // latent columns per wave
   static constexpr int KI = QW / 32;        // 16-byte K pieces per lane per tile (= MFMA k-steps)
   static constexpr int VC = QW / 32;        // 16-byte V chunks per lane per tile
   static constexpr int NT = QW / 16;        // 16-column O^T tiles per wave
@@ -94,6 +117,14 @@ struct TileRegs {
   u32x4 v[Geo<R>::VC];
 };
 
+__device__ __forceinline__ u32x4 ld_stream(const uint16_t* p) {
+#if HLA_HIST_NT
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#else
+  return ld16(p);
+#endif
+}
+
 template <int R>
 __device__ __forceinline__ void load_tile(const HistoryParams& a, const int32_t* btr, int n, int j, int col0,
                                           int lane, TileRegs<R>& r) {
@@ -102,23 +133,35 @@ __device__ __forceinline__ void load_tile(const HistoryParams& a, const int32_t*
   const int64_t page = min(max((int64_t)btr[key0 / a.block_size], (int64_t)0), a.num_blocks - 1);
   const int64_t base = page * a.page_stride + (int64_t)(key0 % a.block_size) * a.row_stride + col0;
   const int hq = lane & 15, g = lane >> 4;
+#if HLA_HIST_KLDS
+  (void)hq;
+  (void)g;
+#pragma unroll
+  for (int it = 0; it < G::KI; ++it) {  // same coalesced chunk layout as V: 4 rows x 256 bytes per instruction
+    const int c = it * 64 + lane;
+    const int key = c / G::CPR;
+    r.k[it] = (key0 + key < n) ? ld_stream(a.k + base + (int64_t)key * a.row_stride + (c % G::CPR) * 8)
+                               : u32x4{0u, 0u, 0u, 0u};
+  }
+#else
   const bool kval = key0 + hq < n;
   const uint16_t* kp = a.k + base + (int64_t)hq * a.row_stride + 8 * g;
 #pragma unroll
-  for (int i = 0; i < G::KI; ++i) r.k[i] = kval ? ld16(kp + 32 * i) : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < G::KI; ++i) r.k[i] = kval ? ld_stream(kp + 32 * i) : u32x4{0u, 0u, 0u, 0u};
+#endif
 #pragma unroll
   for (int it = 0; it < G::VC; ++it) {
     const int c = it * 64 + lane;
     const int key = c / G::CPR;
     const int cc = (c % G::CPR) * 8;
-    r.v[it] = (key0 + key < n) ? ld16(a.v + base + (int64_t)key * a.row_stride + cc) : u32x4{0u, 0u, 0u, 0u};
+    r.v[it] = (key0 + key < n) ? ld_stream(a.v + base + (int64_t)key * a.row_stride + cc) : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
-// Stage A: V -> wave-private LDS, quarter-latent S^T partial. Consumes the tile registers.
+// Stage A: K and V -> wave-private LDS, the wave's partial of S^T. Consumes the tile registers.
 template <int R>
 __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&qreg)[Geo<R>::KI], uint16_t* vs,
-                                           int lane) {
+                                           uint16_t* ks, int lane) {
   using G = Geo<R>;
 #pragma unroll
   for (int it = 0; it < G::VC; ++it) {
@@ -126,8 +169,21 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
     st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.v[it]);
   }
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#if HLA_HIST_KLDS
+#pragma unroll
+  for (int it = 0; it < G::KI; ++it) {
+    const int c = it * 64 + lane;
+    st16(ks + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.k[it]);
+  }
+  const int hq = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < G::KI; ++i)
+    acc = mfma16x16x32(*reinterpret_cast<const u32x4*>(ks + hq * G::VS + 32 * i + 8 * g), qreg[i], acc);
+#else
+  (void)ks;
 #pragma unroll
   for (int i = 0; i < G::KI; ++i) acc = mfma16x16x32(r.k[i], qreg[i], acc);
+#endif
   return acc;
 }
 
@@ -138,7 +194,9 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   using G = Geo<R>;
   sx[wave * 64 + lane] = sacc;
   __syncthreads();
-  const floatx4 s = ((sx[lane] + sx[64 + lane]) + sx[128 + lane]) + sx[192 + lane];
+  floatx4 s = sx[lane];
+#pragma unroll
+  for (int w = 1; w < G::WAVES; ++w) s += sx[w * 64 + lane];
   const int hq = lane & 15, g = lane >> 4;
   const int kb = key0 + 4 * g;
   float sc[4];
@@ -167,32 +225,38 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   }
 }
 
-// The decode exact window of token t for all 16 heads (4 heads per wave).
-__device__ void window_token(const WindowPart& w, int T, float scale_log2, int t, int wave, int lane) {
+// The decode exact window of token t for the heads of split s: heads s + S*(wave + waves*i), so the S splits of a
+// token share its 16 heads (two per split at S = 8 with 4 waves) and no workgroup is added to the grid.
+__device__ void window_heads(const WindowPart& w, int T, float scale_log2, int t, int s, int S, int wave, int waves,
+                             int lane) {
+  int h = s + S * wave;
+  if (h >= kHeads) return;
   int req, lo, hi;
   decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi);
   ExactSource src = w.src;
   hi = (int)min((int64_t)hi, (int64_t)w.bt_cols * src.block_size);
   src.table_row = w.bt + (int64_t)req * w.bt_stride;
-  for (int h = wave; h < kHeads; h += 4)
+  for (; h < kHeads; h += waves * S)
     exact_row(src, w.q + (int64_t)t * w.q_st + (int64_t)h * w.q_sh, scale_log2, lo, hi, h, lane,
               w.out + (int64_t)t * w.o_st + (int64_t)h * w.o_sh, w.lse + (int64_t)h * T + t);
 }
 
 template <int R>
-__global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
+__global__ __launch_bounds__(Geo<R>::THREADS)
+#if HLA_HIST_WPE
+__attribute__((amdgpu_waves_per_eu(HLA_HIST_WPE, HLA_HIST_WPE)))
+#endif
+void history_split(HistoryParams a) {
   using G = Geo<R>;
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[4][2][G::VBUF];
-  __shared__ floatx4 s_lds[2][4 * 64];
-  __shared__ int red_lds[kThreads / 64];
+  constexpr int DEPTH = HLA_HIST_DEPTH, NVB = HLA_HIST_VBUF;
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][NVB][G::VBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][HLA_HIST_KLDS ? G::VBUF : 8];
+  __shared__ floatx4 s_lds[2][G::WAVES * 64];
+  __shared__ int red_lds[G::WAVES];
 
   const int t = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int S = a.num_splits;
-  if (s == S) {  // the window row (uniform over the workgroup)
-    window_token(a.win, a.T, a.scale_log2, t, wave, lane);
-    return;
-  }
   const int hq = lane & 15, g = lane >> 4;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;  // keys the block table can address
   const int n = (int)min((int64_t)a.ctx[t], cap);
@@ -203,21 +267,23 @@ __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
   int chunk = tiles;
   if (S > 1) {
     int mx = 0;
-    for (int i = tid; i < a.T; i += kThreads) mx = max(mx, (int)min((int64_t)a.ctx[i], cap));
+    for (int i = tid; i < a.T; i += G::THREADS) mx = max(mx, (int)min((int64_t)a.ctx[i], cap));
     for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
     if (lane == 0) red_lds[wave] = mx;
     __syncthreads();
-    mx = max(max(red_lds[0], red_lds[1]), max(red_lds[2], red_lds[3]));
+    for (int w = 0; w < G::WAVES; ++w) mx = max(mx, red_lds[w]);
     const int max_tiles = (mx + kTile - 1) / kTile;
     chunk = (max_tiles + S - 1) / S;
   }
+  // the token's exact-window heads of this split (the fused decode step), before its history tiles
+  if (a.has_window) window_heads(a.win, a.T, a.scale_log2, t, s, S, wave, G::WAVES, lane);
   const int j_begin = s * chunk;
   const int j_end = min(tiles, j_begin + chunk);
   const int col0 = wave * G::QW;
   const int64_t part_row = ((int64_t)t * S + s) * kHeads + hq;
 
   if (j_begin >= j_end) {  // nothing to read in this split (uniform over the workgroup)
-    if (S == 1) {
+    if (a.direct) {
       uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
 #pragma unroll
       for (int nt = 0; nt < G::NT; ++nt) *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{0u, 0u};
@@ -238,25 +304,29 @@ __global__ __launch_bounds__(kThreads) void history_split(HistoryParams a) {
     for (int nt = 0; nt < G::NT; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
 
-    uint16_t* vs0 = v_lds[wave][0];
-    uint16_t* vs1 = v_lds[wave][1];
-    TileRegs<R> ra, rb;
-    load_tile<R>(a, btr, n, j_begin, col0, lane, ra);
-    if (j_begin + 1 < j_end) load_tile<R>(a, btr, n, j_begin + 1, col0, lane, rb);
-    for (int j = j_begin; j < j_end; j += 2) {
-      floatx4 sa = stage_a<R>(ra, qreg, vs0, lane);
-      if (j + 2 < j_end) load_tile<R>(a, btr, n, j + 2, col0, lane, ra);
-      stage_b<R>(sa, s_lds[0], vs0, j * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
-      if (j + 1 < j_end) {
-        floatx4 sb = stage_a<R>(rb, qreg, vs1, lane);
-        if (j + 3 < j_end) load_tile<R>(a, btr, n, j + 3, col0, lane, rb);
-        stage_b<R>(sb, s_lds[1], vs1, (j + 1) * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
+    // DEPTH register sets: tile j + u lives in regs[u] (compile-time index), refilled with tile j + u + DEPTH as
+    // soon as stage A has consumed it. The score exchange alternates between two LDS buffers by tile parity; a
+    // wave-private V copy may be reused by the next tile because the wave's own LDS accesses stay in order.
+    TileRegs<R> regs[DEPTH];
+#pragma unroll
+    for (int u = 0; u < DEPTH; ++u)
+      if (j_begin + u < j_end) load_tile<R>(a, btr, n, j_begin + u, col0, lane, regs[u]);
+    for (int j = j_begin; j < j_end; j += DEPTH) {
+#pragma unroll
+      for (int u = 0; u < DEPTH; ++u) {
+        const int jt = j + u;
+        if (jt < j_end) {
+          uint16_t* vs = v_lds[wave][jt % NVB];
+          floatx4 sa = stage_a<R>(regs[u], qreg, vs, k_lds[wave], lane);
+          if (jt + DEPTH < j_end) load_tile<R>(a, btr, n, jt + DEPTH, col0, lane, regs[u]);
+          stage_b<R>(sa, s_lds[jt & 1], vs, jt * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
+        }
       }
     }
 
     const float inv = 1.0f / l;
     const float lse = (m + log2f(l)) * kLn2;
-    if (S == 1) {
+    if (a.direct) {
       uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
 #pragma unroll
       for (int nt = 0; nt < G::NT; ++nt) {
@@ -318,15 +388,202 @@ __global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
   if (i == 0) a.lse[(int64_t)h * a.T + t] = mx + logf(den);
 }
 
+// ---- decode epilogue --------------------------------------------------------------------------------------------
+// out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for kEpiTokens tokens of one head per workgroup:
+//   1. o_hist: LSE reduction of the split partials (or the direct bf16 output with one split), rounded to bf16 as the
+//      history op's output is, kept in LDS;
+//   2. the B_t product as a GEMV: wave q sums rows [q*R/4, (q+1)*R/4) of B[h]; lane (g, c) = (lane/16, lane%16)
+//      reads row 4*step + g, output columns [8c, 8c+8) (one 16-byte load: a wave instruction covers 4 whole B rows)
+//      and accumulates TB x 8 outputs; the 16 partials of each output (4 waves x 4 lane groups) are summed in LDS;
+//   3. the merge_states LSE merge with the window partial (invalid rows zeroed), rounded once to bf16.
+constexpr int kEpiTokens = 4;
+
+struct EpilogueParams {
+  int T, S;
+  const float* ws_o;     // [T][S][16][R] (S > 1)
+  const float* ws_lse;   // [T][S][16]
+  const uint16_t* o_hist;  // [T][16][R] bf16 (S == 1)
+  const float* lse_hist;   // [16][T] (S == 1)
+  const uint16_t* B;
+  int64_t b_sh, b_sr;
+  const uint16_t* o_win;   // [T][16][128]
+  const float* lse_win;    // [16][T]
+  const uint8_t* invalid;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+};
+
+template <int R>
+__global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
+  constexpr int TB = kEpiTokens, D = kExactDim, C4 = R / 4;
+  constexpr int IPT = (TB * C4 + kThreads - 1) / kThreads;  // combine items (token, 4 columns) per thread
+  constexpr int NB = R / 16;                                 // B rows per lane in the GEMV
+  constexpr int PB = NB <= 32 ? NB : 0;                      // rows prefetched into registers
+  __shared__ float o_s[TB][R];
+  __shared__ float lse_s[TB];
+  __shared__ floatx4 part[16][TB][D / 4];
+  const int h = blockIdx.y, t0 = blockIdx.x * TB, tid = threadIdx.x;
+  const int S = a.S;
+  const int q = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
+  u32x4 bv[PB > 0 ? PB : 1];
+  const uint16_t* brow = a.B + (int64_t)h * a.b_sh + (int64_t)(q * (R / 4) + g) * a.b_sr + 8 * c;
+
+  // 1. history output of the TB tokens. Every load of the phase is issued before the first wait: the split
+  //    partials and their lse (an empty split left no partial; a select drops it, so its bytes never matter),
+  //    then this lane's B rows for the GEMV; the splits are reduced online in chunks of eight.
+  if (S > 1) {
+    float m[IPT], den[IPT];
+    floatx4 acc[IPT];
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      m[it] = -INFINITY;
+      den[it] = 0.f;
+      acc[it] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s0 = 0; s0 < S; s0 += 8) {
+      float ls[IPT][8];
+      floatx4 o[IPT][8];
+#pragma unroll
+      for (int it = 0; it < IPT; ++it) {
+        const int item = tid + it * kThreads, tb = item / C4, c4 = item % C4, t = t0 + tb;
+        const bool ok = item < TB * C4 && t < a.T;
+        const int64_t row = ((int64_t)t * S) * kHeads + h;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int s = s0 + u;
+          ls[it][u] = ok && s < S ? a.ws_lse[row + (int64_t)s * kHeads] : -INFINITY;
+          o[it][u] = ok && s < S ? *reinterpret_cast<const floatx4*>(a.ws_o + (row + (int64_t)s * kHeads) * R + 4 * c4)
+                                 : floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      if (s0 == 0) {
+#pragma unroll
+        for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
+      }
+#pragma unroll
+      for (int it = 0; it < IPT; ++it) {
+        float mx = m[it];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) mx = fmaxf(mx, ls[it][u]);
+        if (mx == -INFINITY) continue;
+        const float scale = __expf(m[it] - mx);  // 0 while m == -inf
+        den[it] *= scale;
+        acc[it] = acc[it] * scale;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const float w = ls[it][u] == -INFINITY ? 0.f : __expf(ls[it][u] - mx);
+          den[it] += w;
+          acc[it] += ls[it][u] == -INFINITY ? floatx4{0.f, 0.f, 0.f, 0.f} : o[it][u] * w;
+        }
+        m[it] = mx;
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int item = tid + it * kThreads;
+      if (item >= TB * C4) continue;
+      const int tb = item / C4, c4 = item % C4;
+      const floatx4 o = m[it] == -INFINITY ? floatx4{0.f, 0.f, 0.f, 0.f} : acc[it] * (1.0f / den[it]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o_s[tb][4 * c4 + e] = rbf(o[e]);
+      if (c4 == 0) lse_s[tb] = m[it] == -INFINITY ? -INFINITY : m[it] + logf(den[it]);
+    }
+  } else {
+#pragma unroll
+    for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
+    if (tid < TB) lse_s[tid] = t0 + tid < a.T ? a.lse_hist[(int64_t)h * a.T + t0 + tid] : -INFINITY;
+    for (int item = tid; item < TB * R / 2; item += kThreads) {
+      const int tb = item / (R / 2), c2 = item % (R / 2), t = t0 + tb;
+      const uint32_t w2 = t < a.T ? *reinterpret_cast<const uint32_t*>(a.o_hist + ((int64_t)t * kHeads + h) * R + 2 * c2)
+                                  : 0u;
+      o_s[tb][2 * c2] = lo_bf(w2);
+      o_s[tb][2 * c2 + 1] = hi_bf(w2);
+    }
+  }
+  __syncthreads();
+
+  // 2. GEMV with B[h]
+  {
+    float acc[TB][8];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[tb][e] = 0.f;
+#pragma unroll
+    for (int step = 0; step < NB; ++step) {
+      const u32x4 bs = PB > 0 ? bv[step < PB ? step : 0] : ld16(brow + (int64_t)(4 * step) * a.b_sr);
+      float b[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        b[2 * e] = lo_bf(bs[e]);
+        b[2 * e + 1] = hi_bf(bs[e]);
+      }
+      const int r = q * (R / 4) + 4 * step + g;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        const float o = o_s[tb][r];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[tb][e] += o * b[e];
+      }
+    }
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      part[q * 4 + g][tb][2 * c] = floatx4{acc[tb][0], acc[tb][1], acc[tb][2], acc[tb][3]};
+      part[q * 4 + g][tb][2 * c + 1] = floatx4{acc[tb][4], acc[tb][5], acc[tb][6], acc[tb][7]};
+    }
+  }
+  __syncthreads();
+
+  // 3. merge with the window partial
+  for (int item = tid; item < TB * D / 2; item += kThreads) {
+    const int tb = item / (D / 2), dp = item % (D / 2), t = t0 + tb;
+    if (t >= a.T) continue;
+    float y0 = 0.f, y1 = 0.f;
+    const float* pf = reinterpret_cast<const float*>(&part[0][tb][0]) + 2 * dp;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      y0 += pf[p * TB * D];
+      y1 += pf[p * TB * D + 1];
+    }
+    float lx = lse_s[tb], lb = a.lse_win[(int64_t)h * a.T + t];
+    if (lx == INFINITY) lx = -INFINITY;  // +inf lse counts as empty
+    if (lb == INFINITY) lb = -INFINITY;
+    float peak = fmaxf(lx, lb);
+    if (isinf(peak)) peak = 0.f;
+    float wx = expf(lx - peak), wb = expf(lb - peak);
+    const float total = wx + wb;
+    if (total > 0.f) {
+      wx /= total;
+      wb /= total;
+    } else {
+      wx = wb = 0.f;
+    }
+    const uint32_t ow = *reinterpret_cast<const uint32_t*>(a.o_win + ((int64_t)t * kHeads + h) * D + 2 * dp);
+    uint32_t res = pack2(rbf(y0) * wx + lo_bf(ow) * wb, rbf(y1) * wx + hi_bf(ow) * wb);
+    if (a.invalid && a.invalid[t]) res = 0u;
+    *reinterpret_cast<uint32_t*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 2 * dp) = res;
+  }
+}
+
+template <int R>
+int launch_epilogue(const EpilogueParams& e, hipStream_t stream) {
+  hipLaunchKernelGGL(decode_epilogue<R>, dim3((unsigned)((e.T + kEpiTokens - 1) / kEpiTokens), kHeads), dim3(kThreads),
+                     0, stream, e);
+  return check_launch("decode_epilogue");
+}
+
+template <int R>
+int launch_combine(const HistoryParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(R / 4), 0, stream, p);
+  return check_launch("history_combine");
+}
+
 template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
-  dim3 grid(p.T, p.num_splits + (p.has_window ? 1 : 0));
-  hipLaunchKernelGGL(history_split<R>, grid, dim3(kThreads), 0, stream, p);
+  dim3 grid(p.T, p.num_splits);
+  hipLaunchKernelGGL(history_split<R>, grid, dim3(Geo<R>::THREADS), 0, stream, p);
   int rc = check_launch("history_split");
-  if (rc == HLA_S6_OK && p.num_splits > 1) {
-    hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(R / 4), 0, stream, p);
-    rc = check_launch("history_combine");
-  }
+  if (rc == HLA_S6_OK && !p.direct && p.combine) rc = launch_combine<R>(p, stream);
   return rc;
 }
 
@@ -337,7 +594,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
                  int32_t block_size, int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
                  int32_t bt_cols, const int64_t* bt_rows, const int32_t* ctx, float scale, int32_t num_splits,
                  float* workspace, int64_t workspace_floats, void* out, int64_t o_st,
-                 int64_t o_sh, float* lse) {
+                 int64_t o_sh, float* lse, bool partials_only = false) {
   HLA_REQUIRE(num_tokens >= 0, HLA_S6_EINVAL, "history_attention: negative token count");
   HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED,
               "history_attention: %d query heads (the kernel is built for 16)", num_heads);
@@ -349,7 +606,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
               "history_attention: num_kv_splits must be in [1, %d]", kMaxSplits);
   HLA_REQUIRE(num_blocks >= 1 && bt_cols >= 0, HLA_S6_EINVAL, "history_attention: empty cache or bad table width");
   if (num_tokens == 0) return HLA_S6_OK;
-  HLA_REQUIRE(q && k_cache && v_cache && block_table && ctx && out && lse, HLA_S6_EINVAL,
+  HLA_REQUIRE(q && k_cache && v_cache && block_table && ctx && (partials_only || (out && lse)), HLA_S6_EINVAL,
               "history_attention: null pointer argument");
   HLA_REQUIRE(aligned16(q) && q_st % 8 == 0 && q_sh % 8 == 0, HLA_S6_EINVAL,
               "history_attention: q needs 16-byte aligned rows (unit last stride, strides multiple of 8)");
@@ -357,7 +614,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
               "history_attention: cache rows must be 16-byte aligned (strides multiple of 8 elements)");
   HLA_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7u) == 0 && o_st % 4 == 0 && o_sh % 4 == 0, HLA_S6_EINVAL,
               "history_attention: output rows must be 8-byte aligned");
-  if (num_splits > 1) {
+  if (num_splits > 1 || partials_only) {
     const int64_t need = (int64_t)num_tokens * num_splits * kHeads * (width + 1);
     HLA_REQUIRE(workspace != nullptr && workspace_floats >= need, HLA_S6_EWORKSPACE,
                 "S6 workspace overflow: need %lld floats, have %lld", (long long)need, (long long)workspace_floats);
@@ -387,6 +644,8 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
+  p.direct = num_splits == 1 && !partials_only;
+  p.combine = !partials_only;
   return HLA_S6_OK;
 }
 
@@ -396,6 +655,15 @@ int dispatch(const HistoryParams& p, int width, hipStream_t st) {
     case 256: return launch<256>(p, st);
     case 512: return launch<512>(p, st);
     default: return launch<1024>(p, st);
+  }
+}
+
+int dispatch_combine(const HistoryParams& p, int width, hipStream_t st) {
+  switch (width) {
+    case 128: return launch_combine<128>(p, st);
+    case 256: return launch_combine<256>(p, st);
+    case 512: return launch_combine<512>(p, st);
+    default: return launch_combine<1024>(p, st);
   }
 }
 
@@ -417,6 +685,52 @@ extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32
                         workspace, workspace_floats, out, o_st, o_sh, lse);
   if (rc != HLA_S6_OK || num_tokens == 0) return rc;
   return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_history_partials(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                                       int64_t q_st, int64_t q_sh, const void* k_cache, const void* v_cache,
+                                       int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
+                                       const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
+                                       const int64_t* bt_rows, const int32_t* ctx, float scale, int32_t num_splits,
+                                       float* workspace, int64_t workspace_floats, void* stream) {
+  using namespace hla;
+  HistoryParams p;
+  int rc = fill_history(p, q, num_tokens, num_heads, width, q_st, q_sh, k_cache, v_cache, page_stride, row_stride,
+                        block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
+                        workspace, workspace_floats, nullptr, 0, 0, nullptr, true);
+  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_history_reduce(const float* workspace, int64_t workspace_floats, int32_t num_tokens,
+                                     int32_t num_heads, int32_t width, int32_t num_splits, void* out, int64_t o_st,
+                                     int64_t o_sh, float* lse, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0, HLA_S6_EINVAL, "history_reduce: negative token count");
+  HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED,
+              "history_reduce: %d query heads (the kernel is built for 16)", num_heads);
+  HLA_REQUIRE(width == 128 || width == 256 || width == 512 || width == 1024, HLA_S6_EUNSUPPORTED,
+              "history_reduce: latent width %d not in {128, 256, 512, 1024}", width);
+  HLA_REQUIRE(num_splits >= 1 && num_splits <= kMaxSplits, HLA_S6_EINVAL,
+              "history_reduce: num_kv_splits must be in [1, %d]", kMaxSplits);
+  if (num_tokens == 0) return HLA_S6_OK;
+  const int64_t need = (int64_t)num_tokens * num_splits * kHeads * (width + 1);
+  HLA_REQUIRE(workspace != nullptr && workspace_floats >= need, HLA_S6_EWORKSPACE,
+              "S6 workspace overflow: need %lld floats, have %lld", (long long)need, (long long)workspace_floats);
+  HLA_REQUIRE(aligned16(workspace), HLA_S6_EINVAL, "history_reduce: workspace must be 16-byte aligned");
+  HLA_REQUIRE(out && lse, HLA_S6_EINVAL, "history_reduce: null pointer argument");
+  HLA_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7u) == 0 && o_st % 4 == 0 && o_sh % 4 == 0, HLA_S6_EINVAL,
+              "history_reduce: output rows must be 8-byte aligned");
+  HistoryParams p = {};
+  p.num_splits = num_splits;
+  p.T = num_tokens;
+  p.ws_o = const_cast<float*>(workspace);
+  p.ws_lse = p.ws_o + (int64_t)num_tokens * num_splits * kHeads * width;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_st = o_st;
+  p.o_sh = o_sh;
+  p.lse = lse;
+  return dispatch_combine(p, width, as_stream(stream));
 }
 
 extern "C" int hla_s6_attend_decode(
@@ -469,10 +783,33 @@ extern "C" int hla_s6_attend_decode(
   w.o_st = (int64_t)num_heads * kExactDim;
   w.o_sh = kExactDim;
   w.lse = lse_win;
+  HLA_REQUIRE((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && b_sh % 2 == 0 && b_sr % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) & 3u) == 0 && o_st % 2 == 0 && o_sh % 2 == 0,
+              HLA_S6_EINVAL, "attend_decode: B and out need 4-byte aligned pairs");
   hipStream_t st = as_stream(stream);
+  p.combine = false;  // the epilogue reduces the splits
   rc = dispatch(p, width, st);
   if (rc != HLA_S6_OK) return rc;
-  return absorb_merge(o_hist, num_tokens, num_heads, width, (int64_t)num_heads * width, width, B, b_sh, b_sr,
-                      kExactDim, lse_hist, o_win, (int64_t)num_heads * kExactDim, kExactDim, lse_win, invalid, out,
-                      o_st, o_sh, st);
+  EpilogueParams e = {};
+  e.T = num_tokens;
+  e.S = num_splits;
+  e.ws_o = p.ws_o;
+  e.ws_lse = p.ws_lse;
+  e.o_hist = static_cast<const uint16_t*>(o_hist);
+  e.lse_hist = lse_hist;
+  e.B = static_cast<const uint16_t*>(B);
+  e.b_sh = b_sh;
+  e.b_sr = b_sr;
+  e.o_win = static_cast<const uint16_t*>(o_win);
+  e.lse_win = lse_win;
+  e.invalid = invalid;
+  e.out = static_cast<uint16_t*>(out);
+  e.o_st = o_st;
+  e.o_sh = o_sh;
+  switch (width) {
+    case 128: return launch_epilogue<128>(e, st);
+    case 256: return launch_epilogue<256>(e, st);
+    case 512: return launch_epilogue<512>(e, st);
+    default: return launch_epilogue<1024>(e, st);
+  }
 }

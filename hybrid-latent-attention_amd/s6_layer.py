@@ -72,14 +72,18 @@ class StepContext:
     no cache writes (``md_present`` False), workspace still allocated. ``tables`` maps a latent width to its
     persistent ``[max_position, w]`` RoPE table. Token -> request, ``ctx`` and ``ctx_latent`` come from one HIP
     launch; all shapes depend only on ``num_tokens`` and host ints; nothing here syncs with the host.
+    ``kv_splits_by_width`` optionally overrides ``num_kv_splits`` per latent width (the history kernel's occupancy
+    depends on the width); the workspace must hold the largest of them.
     """
 
     def __init__(self, positions, query_start_loc, seq_lens, max_query_len, num_tokens, tables, scale, backends,
-                 workspace=None, num_kv_splits=1, rope_flat=False, window=0, max_seqlen_k=0):
+                 workspace=None, num_kv_splits=1, rope_flat=False, window=0, max_seqlen_k=0,
+                 kv_splits_by_width=None):
         device = positions.device
         self.window, self.max_seqlen_k = window, max_seqlen_k
         self.positions, self.tables, self.scale, self.backends = positions, tables, scale, backends
         self.workspace, self.num_kv_splits, self.rope_flat = workspace, num_kv_splits, rope_flat
+        self.kv_splits_by_width = dict(kv_splits_by_width or {})
         self.history_needed = True
         self.md_present = query_start_loc is not None
         if not self.md_present:
@@ -101,6 +105,10 @@ class StepContext:
         self._block_tables = {}
         if workspace is not None:
             workspace.ensure(device)
+
+    def kv_splits(self, width):
+        """History split count for a latent of ``width`` columns."""
+        return int(self.kv_splits_by_width.get(width, self.num_kv_splits))
 
     def block_table(self, table):
         """Per-token gather of a per-request block table, done once per distinct tensor per step."""
@@ -150,14 +158,15 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     _, B, _ = sl.readers(loop)
     w = q_lat.shape[-1]
     o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
-                                                   ctx.scale, ctx.num_kv_splits, ctx.workspace, k_scale, v_scale,
+                                                   ctx.scale, ctx.kv_splits(w), ctx.workspace, k_scale, v_scale,
                                                    ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests)
     o_hist = absorb_out(o_hist, B)
     return s6_ops.merge_states(o_hist, lse_hist, o_chunk, lse_chunk, ctx.invalid, ctx.backends.merge)
 
 
 def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
-    """Decode branch with history: one ``hla_s6_attend_decode`` call (three launches)."""
+    """Decode branch with history: one ``hla_s6_attend_decode`` call (two launches: the split history kernel, which
+    also computes the exact window, then the epilogue that reduces the splits, applies B_t and merges)."""
     for kind in ('history', 'merge', 'chunk'):
         s6_ops._backend(kind, getattr(ctx.backends, kind))
     _, B, _ = sl.readers(loop)
@@ -187,7 +196,7 @@ def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
     o_win = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
     lse_win = torch.empty(H, T, dtype=torch.float32, device=dev)
     out = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
-    splits = int(ctx.num_kv_splits)
+    splits = ctx.kv_splits(w)
     ws = None
     if splits > 1:
         if ctx.workspace is None:

@@ -150,13 +150,17 @@ def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_bloc
     return max(1, min(max(by_length, by_occupancy), 2 * sm_count, -(-max_seq_len // 32)))
 
 
-def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, workgroups_per_cu=2, min_keys_per_split=256):
-    """Split count of the history kernel on MI355X: about ``workgroups_per_cu`` workgroups per compute unit over the
-    step's rows, never splits shorter than ``min_keys_per_split`` keys (each split writes a 16 x width fp32 partial,
-    so short splits turn into workspace traffic). A function of constants and the row count only (graph-stable).
-    The kernel partitions every row in chunks sized from the longest row of the step, so rows of a ragged batch
-    use a number of splits proportional to their length."""
-    by_occupancy = -(-workgroups_per_cu * cu_count // max(1, num_tokens))
+def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per_cu=8, min_keys_per_split=256):
+    """Split count of the history kernel on MI355X for a ``width``-wide latent. The kernel runs one wave per 128
+    latent columns, so a split of one row is a workgroup of ``width / 128`` waves; the policy aims at
+    ``waves_per_cu`` resident waves per compute unit over the step's rows (8 keeps enough loads in flight to stream
+    HBM on gfx950 for both the 512- and the 256-wide latent) and never cuts splits shorter than
+    ``min_keys_per_split`` keys (each split writes a 16 x width fp32 partial, so short splits turn into workspace
+    traffic). A function of constants and the row count only (graph-stable). The kernel partitions every row in
+    chunks sized from the longest row of the step, so rows of a ragged batch use a number of splits proportional
+    to their length."""
+    waves_per_split = max(1, width // 128)
+    by_occupancy = -(-waves_per_cu * cu_count // max(1, num_tokens * waves_per_split))
     by_length = max(1, -(-max_seq_len // min_keys_per_split))
     return max(1, min(by_occupancy, by_length, 1024))
 
@@ -177,6 +181,13 @@ class S6Workspace:
         if self.buffer is None:
             self.buffer = torch.empty(self.floats, dtype=torch.float32, device=device)
         return self.buffer
+
+    @classmethod
+    def for_splits(cls, heads, tokens, splits_by_width):
+        """A workspace for ``tokens`` rows at every ``{width: splits}`` pair of ``splits_by_width``."""
+        ws = cls(heads, 0, 0)
+        ws.floats = max(tokens * heads * s * (w + 1) for w, s in splits_by_width.items())
+        return ws
 
     def attn_logits(self, tokens, heads, splits, width, device=None):
         need = tokens * heads * splits * (width + 1)
@@ -213,6 +224,57 @@ def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, worksp
     accepted and unused. ``empty`` is derived from ``ctx`` inside the kernel and is accepted for signature parity.
     """
     _backend('history', backend)
+    T, H, L, ctx, rows = _history_operands(q, k, v, block_table, ctx, mla, bt_rows)
+    o = torch.empty(T, H, L, dtype=BF16, device=q.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
+    splits = int(num_kv_splits)
+    ws = None
+    if splits > 1:
+        if workspace is None:
+            raise RuntimeError('history attention with num_kv_splits > 1 needs an S6Workspace')
+        ws = workspace.attn_logits(T, H, splits, L, q.device)
+    _lib.call('hla_s6_history_attention', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k), _lib.ptr(v),
+              k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0),
+              block_table.shape[1], _lib.ptr(rows),
+              _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o),
+              o.stride(0), o.stride(1), _lib.ptr(lse), _lib.stream(q.device))
+    return o, lse
+
+
+def history_partials(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, bt_rows=None):
+    """Stage 1 of the history op alone, the split kernel (``hla/vllm_latent/s6_ops.py:186-196``): writes the
+    normalized per-split partials and their lse to ``workspace`` for any ``num_kv_splits >= 1`` and returns the
+    workspace view ``[T, H, splits, width + 1]`` (its layout is private to the HIP library). Operands and checks as
+    ``history_attention_kv``; ``history_reduce`` completes the op bitwise."""
+    T, H, L, ctx, rows = _history_operands(q, k, v, block_table, ctx, False, bt_rows)
+    splits = int(num_kv_splits)
+    if workspace is None:
+        raise RuntimeError('history partials need an S6Workspace')
+    ws = workspace.attn_logits(T, H, splits, L, q.device)
+    _lib.call('hla_s6_history_partials', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k), _lib.ptr(v),
+              k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0),
+              block_table.shape[1], _lib.ptr(rows), _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), ws.numel(),
+              _lib.stream(q.device))
+    return ws
+
+
+def history_reduce(partials):
+    """Stage 2 of the history op (``hla/vllm_latent/s6_ops.py:202``, ``_decode_softmax_reducev_fwd``): the LSE
+    reduction of the split partials ``history_partials`` returned. Returns ``(o[T,H,L] bf16, lse[H,T] fp32)``."""
+    _dev(partials)
+    if partials.dtype != torch.float32 or partials.dim() != 4 or not partials.is_contiguous():
+        raise ValueError('history_reduce expects the fp32 workspace view returned by history_partials')
+    T, H, S, L1 = partials.shape
+    L = L1 - 1
+    o = torch.empty(T, H, L, dtype=BF16, device=partials.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=partials.device)
+    _lib.call('hla_s6_history_reduce', _lib.ptr(partials), partials.numel(), T, H, L, S, _lib.ptr(o), o.stride(0),
+              o.stride(1), _lib.ptr(lse), _lib.stream(partials.device))
+    return o, lse
+
+
+def _history_operands(q, k, v, block_table, ctx, mla, bt_rows):
+    """Checks of the history operands; returns ``(T, H, L, ctx int32, bt_rows int64 or None)``."""
     if mla:
         raise ValueError('MLA-style rows (value = prefix of key) are not part of the S6 path')
     _dev(q, k, v, block_table, ctx)
@@ -233,21 +295,8 @@ def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, worksp
         raise ValueError(f'ctx has {ctx.shape[0]} rows for {T} tokens')
     if bt_rows is None and block_table.shape[0] < T:
         raise ValueError(f'block_table has {block_table.shape[0]} rows for {T} tokens')
-    o = torch.empty(T, H, L, dtype=BF16, device=q.device)
-    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
-    splits = int(num_kv_splits)
-    ws = None
-    if splits > 1:
-        if workspace is None:
-            raise RuntimeError('history attention with num_kv_splits > 1 needs an S6Workspace')
-        ws = workspace.attn_logits(T, H, splits, L, q.device)
     rows = None if bt_rows is None else _int('bt_rows', bt_rows, I64)
-    _lib.call('hla_s6_history_attention', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k), _lib.ptr(v),
-              k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0),
-              block_table.shape[1], _lib.ptr(rows),
-              _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o),
-              o.stride(0), o.stride(1), _lib.ptr(lse), _lib.stream(q.device))
-    return o, lse
+    return T, H, L, ctx, rows
 
 
 # ----------------------------------------------------------------------------------------------------------------

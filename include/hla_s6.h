@@ -104,6 +104,23 @@ int hla_s6_history_attention(const void *q, int32_t num_tokens, int32_t num_head
                              int64_t workspace_floats, void *out, int64_t o_st, int64_t o_sh, float *lse,
                              void *stream);
 
+/* The two launches of hla_s6_history_attention as separate calls, as the reference launches the
+ * stage-1 split kernel and the stage-2 LSE reduction separately (hla/vllm_latent/s6_ops.py:186-202,
+ * _fwd_grouped_kernel_stage1 then _decode_softmax_reducev_fwd). hla_s6_history_partials writes the
+ * per-split normalized partials and their lse to `workspace` for every num_splits >= 1 (same
+ * arguments and checks as hla_s6_history_attention); hla_s6_history_reduce reads them back and writes
+ * o and lse exactly as hla_s6_history_attention does (bitwise: the same kernels). The workspace layout
+ * is private to the library: o partials [T][S][16][width] then lse [T][S][16], fp32. */
+int hla_s6_history_partials(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                            int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
+                            int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
+                            const int32_t *block_table, int64_t bt_stride, int32_t bt_cols, const int64_t *bt_rows,
+                            const int32_t *ctx, float scale, int32_t num_splits, float *workspace,
+                            int64_t workspace_floats, void *stream);
+int hla_s6_history_reduce(const float *workspace, int64_t workspace_floats, int32_t num_tokens, int32_t num_heads,
+                          int32_t width, int32_t num_splits, void *out, int64_t o_st, int64_t o_sh, float *lse,
+                          void *stream);
+
 /* ---- a6/a7: exact-window attention over the per-loop exact paged cache --------------------------
  * The exact cache is the TRITON_ATTN layout [num_blocks, block, H, 2d] (K then V per head); key row j of
  * head h is at k_cache + block_table[row*bt_stride + j / block_size] * page_stride

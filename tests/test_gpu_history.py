@@ -123,3 +123,29 @@ def test_split_counts_agree(ops):
         o, lse = run_history(ops, q, cache, table, ctx, splits)
         assert_attention_close(o, ref[0], f'splits={splits}')
         assert_lse_close(lse, ref[1])
+
+
+@pytest.mark.parametrize('width', [512, 256])
+@pytest.mark.parametrize('splits', [1, 3, 8])
+def test_two_stage_history_is_bitwise_the_op(ops, width, splits):
+    """history_partials + history_reduce (the reference's stage-1 / stage-2 launches) give exactly the bytes of
+    history_attention_kv, including empty rows, and match the oracle."""
+    rng = np.random.default_rng(7 * width + splits)
+    block, num_blocks = 16, 600
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    ctx = np.array([4100, 999, 16, 1, 0, 2500], np.int32)
+    table = token_tables(rng, ctx, block, num_blocks, -(-4100 // block))
+    q_bits = random_bits(rng, (ctx.shape[0], 16, width))
+    q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    k, v, bt, c = cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx)
+    ws = ops.S6Workspace(16, width, ctx.shape[0] * splits)
+    o_ref, lse_ref = ops.history_attention_kv(q, k, v, bt, c, SCALE, splits, ws, None, None, 'hip')
+    o_ref, lse_ref = o_ref.clone(), lse_ref.clone()
+    part = ops.history_partials(q, k, v, bt, c, SCALE, splits, ws)
+    assert tuple(part.shape) == (ctx.shape[0], 16, splits, width + 1)
+    o, lse = ops.history_reduce(part)
+    assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
+    assert torch.equal(lse, lse_ref)
+    check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table, ctx), ctx)
+    with pytest.raises(RuntimeError, match='S6Workspace'):
+        ops.history_partials(q, k, v, bt, c, SCALE, splits, None)

@@ -59,6 +59,24 @@ def test_num_kv_splits_known_answers(ops, case):
     assert ops.num_kv_splits(*case['args']) == case['expected']
 
 
+def test_mi355x_split_policy(ops):
+    # 8 resident waves per CU: a 512-wide split is a 4-wave workgroup, a 256-wide one 2 waves, a 128-wide one 1 wave
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=512) == 8
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=256) == 16
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 32
+    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 32         # capped by 256-key splits
+    assert ops.mi355x_kv_splits(300, 1, 256) == 2
+    assert ops.mi355x_kv_splits(1, 4096, 256) == 1
+    assert ops.mi355x_kv_splits(10 ** 6, 1, 256, width=128) == 1024    # the kernel's maximum
+
+
+def test_workspace_for_several_widths(ops):
+    ws = ops.S6Workspace.for_splits(16, 64, {512: 8, 256: 16})
+    assert ws.floats == max(64 * 16 * 8 * 513, 64 * 16 * 16 * 257)
+    for w, s in ((512, 8), (256, 16)):
+        assert tuple(ws.attn_logits(64, 16, s, w, 'cpu').shape) == (64, 16, s, w + 1)
+
+
 def test_workspace_sizing_and_overflow(ops):
     g = KNOWN['workspace']
     ws = ops.S6Workspace(heads=g['heads'], width_max=g['width_max'], rows_x_splits=g['rows_x_splits'])
