@@ -164,12 +164,14 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
 
 /* ---- a9: fused decode attention of one layer x loop --------------------------------------------------
  * Replaces the decode branch of s6_layer.attend (hla/vllm_latent/s6_layer.py:97-100,110-115):
- * window_attention_fa + history_attention + the B_t einsum + merge_states, in three launches:
- *   1. the history kernels of hla_s6_history_attention over q_lat and the latent cache (per-request table
- *      `lat_table`, row of token t = token_requests[t], ctx_latent[t] rows); the split kernel also runs one
- *      extra row of workgroups computing the exact decode window of every token (mode 0 of
- *      hla_s6_window_attention over q_rope and the loop's exact cache);
- *   2. out = merge(bf16(o_hist @ B[h]), o_win) with the merge_states conventions (invalid rows zeroed).
+ * window_attention_fa + history_attention + the B_t einsum + merge_states, in two launches:
+ *   1. the split kernel of hla_s6_history_partials over q_lat and the latent cache (per-request table
+ *      `lat_table`, row of token t = token_requests[t], ctx_latent[t] rows); the workgroups of token t also
+ *      compute its exact decode window (mode 0 of hla_s6_window_attention over q_rope and the loop's exact
+ *      cache), its 16 heads spread over the token's splits;
+ *   2. an epilogue that reduces the split partials by LSE (o_hist rounded to bf16 as the history op returns
+ *      it), then writes out = merge(bf16(o_hist @ B[h]), o_win) with the merge_states conventions (invalid
+ *      rows zeroed).
  * The intermediates o_hist [T, 16, width] bf16, lse_hist [16, T], o_win [T, 16, 128] bf16 and lse_win [16, T]
  * are caller-owned contiguous buffers (they hold the two partial attentions on return). B is [16, width, 128]
  * with strides (b_sh, b_sr, 1). Workspace as for hla_s6_history_attention. */
