@@ -92,6 +92,7 @@ struct HistoryParams {
   uint16_t* out;
   int64_t o_st, o_sh;
   float* lse;  // [16][T]
+  int group;     // tokens per workgroup (history_group when > 1)
   bool has_window;
   bool direct;   // one split writing the final output and lse (else split partials to the workspace)
   bool combine;  // launch history_combine after the split kernel (with more than one split)
@@ -343,6 +344,207 @@ void history_split(HistoryParams a) {
   }
 }
 
+// ---- multi-query history ------------------------------------------------------------------------------
+// history_group: the split kernel for steps with several query rows per request (chunked prefill). One
+// workgroup serves NQ consecutive tokens; the tokens that share a block-table row read each K/V tile once.
+// Stage A: K and V -> wave-private LDS, the wave's partial of S^T for each of the NQ tokens (the K operand is read
+// from LDS once per k-step and reused by every token). Consumes the tile registers.
+template <int R, int NQ>
+__device__ __forceinline__ void group_stage_a(const TileRegs<R>& r, const u32x4 (&qreg)[NQ][Geo<R>::KI], uint16_t* vs,
+                                        uint16_t* ks, int lane, int count, floatx4 (&sacc)[NQ]) {
+  using G = Geo<R>;
+#pragma unroll
+  for (int it = 0; it < G::KI; ++it) {
+    const int c = it * 64 + lane;
+    st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.v[it]);
+    st16(ks + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.k[it]);
+  }
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) sacc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int hq = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < G::KI; ++i) {
+    const u32x4 kop = *reinterpret_cast<const u32x4*>(ks + hq * G::VS + 32 * i + 8 * g);
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+      if (NQ == 1 || u < count) sacc[u] = mfma16x16x32(kop, qreg[u][i], sacc[u]);
+  }
+}
+
+// Stage B: exchange the S partials, online softmax per token, O^T += V^T P^T (the V^T operand is read once and
+// reused by every token). Keys >= n[u] are masked for token u.
+template <int R, int NQ>
+__device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4* sx, const uint16_t* vs, int key0,
+                                        const int (&n)[NQ], int count, float scale_log2, int wave, int lane,
+                                        floatx4 (&oacc)[NQ][Geo<R>::NT], float (&m)[NQ], float (&l)[NQ]) {
+  using G = Geo<R>;
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) sx[(u * G::WAVES + wave) * 64 + lane] = sacc[u];
+  __syncthreads();
+  const int hq = lane & 15, g = lane >> 4;
+  const int kb = key0 + 4 * g;
+    // Several tokens: the running maximum m is only raised (and O rescaled) when a tile's maximum exceeds it by
+    // more than kLazy in the exp2 domain, so p <= 2^kLazy and most tiles accumulate into O without a rescale.
+    constexpr float kLazy = 8.f;
+    short4v pb[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      if (u >= count) continue;
+      floatx4 s = sx[u * G::WAVES * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < G::WAVES; ++w) s += sx[(u * G::WAVES + w) * 64 + lane];
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = (kb + r < n[u]) ? s[r] * scale_log2 : -INFINITY;
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mx = wave_max16x4(mx);
+      const bool raise = mx > m[u] + kLazy;  // per head (lane column); false while the token has no key yet
+      if (__any(raise)) {
+        const float m_new = raise ? mx : m[u];
+        const float alpha = fast_exp2(m[u] - m_new);  // 0 on the first raise (m = -inf)
+        l[u] *= alpha;
+#pragma unroll
+        for (int nt = 0; nt < G::NT; ++nt) oacc[u][nt] = oacc[u][nt] * alpha;
+        m[u] = m_new;
+      }
+      const float m_use = m[u] == -INFINITY ? 0.f : m[u];
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_use);
+      l[u] += wave_sum16x4((p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pb[u][r] = (short)f2bf(p[r]);
+    }
+#pragma unroll
+    for (int nt = 0; nt < G::NT; ++nt) {
+      short4v va;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) va[e] = (short)vs[(4 * g + e) * G::VS + 16 * nt + hq];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u)
+        if (u < count) oacc[u][nt] = mfma16x16x16(va, pb[u], oacc[u][nt]);
+    }
+}
+
+__device__ __forceinline__ int64_t table_row(const HistoryParams& a, int t) {
+  return a.bt_rows ? a.bt_rows[t] : (int64_t)t;
+}
+
+// Writes token t's result of split s: the normalized output and lse (one split) or the split partial.
+template <int R>
+__device__ __forceinline__ void store_split(const HistoryParams& a, int t, int s, int col0, int wave, int lane,
+                                            const floatx4 (&oacc)[Geo<R>::NT], float m, float l) {
+  using G = Geo<R>;
+  const int hq = lane & 15, g = lane >> 4;
+  const bool any = l > 0.f;
+  const float inv = any ? 1.0f / l : 0.f;
+  const float lse = any ? (m + log2f(l)) * kLn2 : -INFINITY;
+  if (a.direct) {
+    uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
+#pragma unroll
+    for (int nt = 0; nt < G::NT; ++nt) {
+      const floatx4 o = oacc[nt] * inv;
+      *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+    }
+    if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = lse;
+    return;
+  }
+  const int64_t part_row = ((int64_t)t * a.num_splits + s) * kHeads + hq;
+  float* wp = a.ws_o + part_row * R + col0 + 4 * g;
+#pragma unroll
+  for (int nt = 0; nt < G::NT; ++nt) *reinterpret_cast<floatx4*>(wp + 16 * nt) = oacc[nt] * inv;
+  if (wave == 0 && g == 0) a.ws_lse[part_row] = lse;
+}
+
+// One workgroup per (group of NQ consecutive tokens, KV split). The tokens of a group that share a block-table row
+// (one request of a chunked-prefill step) are processed together, every K/V tile read once for all of them; a
+// group that spans several rows takes one pass per row.
+template <int R, int NQ>
+__global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a) {
+  using G = Geo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][G::VBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][G::VBUF];
+  __shared__ floatx4 s_lds[2][NQ * G::WAVES * 64];
+  __shared__ int red_lds[G::WAVES];
+
+  const int s = blockIdx.y;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int S = a.num_splits;
+  const int hq = lane & 15, g = lane >> 4;
+  const int64_t cap = (int64_t)a.bt_cols * a.block_size;  // keys the block table can address
+  const int col0 = wave * G::QW;
+
+  // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
+  // ragged batch get split counts proportional to their length and every split has equal work.
+  int chunk = 1 << 30;
+  if (S > 1) {
+    int mx = 0;
+    for (int i = tid; i < a.T; i += G::THREADS) mx = max(mx, (int)min((int64_t)a.ctx[i], cap));
+    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+    if (lane == 0) red_lds[wave] = mx;
+    __syncthreads();
+    for (int w = 0; w < G::WAVES; ++w) mx = max(mx, red_lds[w]);
+    const int max_tiles = (mx + kTile - 1) / kTile;
+    chunk = (max_tiles + S - 1) / S;
+  }
+  const int t_begin = blockIdx.x * NQ, t_end = min(t_begin + NQ, a.T);
+
+  int par = 0;  // score-exchange buffer of the next tile; alternates over every tile of every pass
+  for (int tp = t_begin; tp < t_end;) {
+    const int64_t row = table_row(a, tp);
+    int te = tp + 1;
+    while (te < t_end && table_row(a, te) == row) ++te;
+    const int count = te - tp;
+    int n[NQ];
+    int n_max = 0;
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      n[u] = u < count ? (int)min((int64_t)a.ctx[tp + u], cap) : 0;
+      n_max = max(n_max, n[u]);
+    }
+    const int tiles = (n_max + kTile - 1) / kTile;
+    const int j_begin = S > 1 ? s * chunk : 0;
+    const int j_end = min(tiles, j_begin + (S > 1 ? chunk : tiles));
+
+    floatx4 oacc[NQ][G::NT];
+    float m[NQ], l[NQ];
+#pragma unroll
+    for (int u = 0; u < NQ; ++u) {
+      m[u] = -INFINITY;
+      l[u] = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < G::NT; ++nt) oacc[u][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    if (j_begin < j_end) {  // uniform over the workgroup
+      const int32_t* btr = a.bt + row * a.bt_stride;
+      u32x4 qreg[NQ][G::KI];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) {
+        const uint16_t* qp = a.q + (int64_t)(tp + min(u, count - 1)) * a.q_st + (int64_t)hq * a.q_sh + col0 + 8 * g;
+#pragma unroll
+        for (int i = 0; i < G::KI; ++i) qreg[u][i] = ld16(qp + 32 * i);
+      }
+      // The next tile's registers are loaded as soon as stage A has consumed the current ones. The score exchange
+      // alternates between two LDS buffers, so a wave writing the next tile's partials never touches the buffer
+      // a slower wave may still be reading (the barrier in between orders them); the wave-private K/V copies may
+      // be rewritten by the next tile because a wave's own LDS accesses stay in order.
+      TileRegs<R> regs;
+      load_tile<R>(a, btr, n_max, j_begin, col0, lane, regs);
+      for (int jt = j_begin; jt < j_end; ++jt) {
+        floatx4 sa[NQ];
+        group_stage_a<R, NQ>(regs, qreg, v_lds[wave], k_lds[wave], lane, count, sa);
+        if (jt + 1 < j_end) load_tile<R>(a, btr, n_max, jt + 1, col0, lane, regs);
+        group_stage_b<R, NQ>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane, oacc, m, l);
+        par ^= 1;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NQ; ++u)
+      if (u < count) store_split<R>(a, tp + u, s, col0, wave, lane, oacc[u], m[u], l[u]);
+    tp = te;
+  }
+}
+
 // Split reduction: one workgroup per (token, head), thread i owns output columns [4i, 4i+4).
 template <int R>
 __global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
@@ -580,8 +782,13 @@ int launch_combine(const HistoryParams& p, hipStream_t stream) {
 
 template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
-  dim3 grid(p.T, p.num_splits);
-  hipLaunchKernelGGL(history_split<R>, grid, dim3(Geo<R>::THREADS), 0, stream, p);
+  if (p.group > 1) {
+    const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
+    if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
+    else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(history_split<R>, dim3(p.T, p.num_splits), dim3(Geo<R>::THREADS), 0, stream, p);
+  }
   int rc = check_launch("history_split");
   if (rc == HLA_S6_OK && !p.direct && p.combine) rc = launch_combine<R>(p, stream);
   return rc;
@@ -644,6 +851,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
+  p.group = 1;
   p.direct = num_splits == 1 && !partials_only;
   p.combine = !partials_only;
   return HLA_S6_OK;
@@ -684,6 +892,24 @@ extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32
                         block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
                         workspace, workspace_floats, out, o_st, o_sh, lse);
   if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_history_attention_grouped(
+    const void* q, int32_t num_tokens, int32_t num_heads, int32_t width, int64_t q_st, int64_t q_sh,
+    const void* k_cache, const void* v_cache, int64_t page_stride, int64_t row_stride, int32_t block_size,
+    int64_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols, const int64_t* bt_rows,
+    const int32_t* ctx, float scale, int32_t num_splits, float* workspace, int64_t workspace_floats, void* out,
+    int64_t o_st, int64_t o_sh, float* lse, int32_t group, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(group == 1 || group == 2 || group == 4, HLA_S6_EUNSUPPORTED,
+              "history_attention: group of %d tokens (built for 1, 2, 4)", group);
+  HistoryParams p;
+  int rc = fill_history(p, q, num_tokens, num_heads, width, q_st, q_sh, k_cache, v_cache, page_stride, row_stride,
+                        block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
+                        workspace, workspace_floats, out, o_st, o_sh, lse);
+  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  p.group = group;
   return dispatch(p, width, as_stream(stream));
 }
 

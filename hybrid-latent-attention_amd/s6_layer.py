@@ -84,6 +84,8 @@ class StepContext:
         self.positions, self.tables, self.scale, self.backends = positions, tables, scale, backends
         self.workspace, self.num_kv_splits, self.rope_flat = workspace, num_kv_splits, rope_flat
         self.kv_splits_by_width = dict(kv_splits_by_width or {})
+        # query rows per workgroup of the history kernel in multi-query steps (1, 2 or 4)
+        self.history_group = 1
         self.history_needed = True
         self.md_present = query_start_loc is not None
         if not self.md_present:
@@ -159,7 +161,8 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     w = q_lat.shape[-1]
     o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
                                                    ctx.scale, ctx.kv_splits(w), ctx.workspace, k_scale, v_scale,
-                                                   ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests)
+                                                   ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests,
+                                                   tokens_per_group=ctx.history_group)
     o_hist = absorb_out(o_hist, B)
     return s6_ops.merge_states(o_hist, lse_hist, o_chunk, lse_chunk, ctx.invalid, ctx.backends.merge)
 

@@ -149,3 +149,41 @@ def test_two_stage_history_is_bitwise_the_op(ops, width, splits):
     check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table, ctx), ctx)
     with pytest.raises(RuntimeError, match='S6Workspace'):
         ops.history_partials(q, k, v, bt, c, SCALE, splits, None)
+
+
+@pytest.mark.parametrize('width', [512, 256])
+@pytest.mark.parametrize('splits', [1, 5])
+@pytest.mark.parametrize('group', [2, 4])
+def test_grouped_history_matches_oracle(ops, width, splits, group):
+    """Chunked-prefill shape: requests of 5, 3, 1, 8 and 2 query rows whose rows share the request's table row.
+    Request 0 has one ctx for every row (vLLM prefill), request 1 a causal ctx per row (K-hop), request 2 no
+    history, request 3 decreasing ctx, request 4 a short one. Groups straddle requests."""
+    rng = np.random.default_rng(100 * width + 10 * splits + group)
+    block, num_blocks = 16, 1200
+    lens = [5, 3, 1, 8, 2]
+    req = np.repeat(np.arange(len(lens)), lens)
+    ctx = np.concatenate([np.full(5, 3000), 700 + np.arange(3), [0], 1200 - 37 * np.arange(8), [40, 41]])
+    ctx = ctx.astype(np.int32)
+    per_req = np.array([ctx[req == r].max() for r in range(len(lens))])
+    table = token_tables(rng, per_req, block, num_blocks, -(-3000 // block))
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    q_bits = random_bits(rng, (len(ctx), 16, width))
+    q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    ws = ops.S6Workspace(16, width, len(ctx) * splits)
+    o, lse = ops.history_attention_kv(q, cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx), SCALE,
+                                      splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=group)
+    o, lse = host_f32(o), host_f32(lse)
+    check(o, lse, *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
+    o1, lse1 = run_history(ops, q_bits, cache_bits, table, ctx, splits, bt_rows=req)
+    assert_attention_close(o, o1, 'grouped vs one token per workgroup')
+    assert_lse_close(lse, lse1)
+
+
+def test_grouped_history_rejects_unsupported_group(ops):
+    q = torch.zeros(2, 16, 512, dtype=torch.bfloat16, device='cuda')
+    cache = torch.zeros(4, 1, 16, 1024, dtype=torch.bfloat16, device='cuda')
+    table = torch.zeros(2, 1, dtype=torch.int32, device='cuda')
+    ctx = torch.ones(2, dtype=torch.int32, device='cuda')
+    with pytest.raises(ValueError, match='group'):
+        ops.history_attention_kv(q, cache[..., :512], cache[..., 512:], table, ctx, SCALE, 1, None, None, None, 'hip',
+                                 tokens_per_group=3)
