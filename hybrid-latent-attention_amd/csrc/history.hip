@@ -49,6 +49,9 @@ namespace {
 #ifndef HLA_HIST_WCOLS
 #define HLA_HIST_WCOLS 128
 #endif
+#ifndef HLA_HIST_VTR
+#define HLA_HIST_VTR 1  // V^T operands by ds_read_b64_tr_b16 (else four 16-bit LDS reads)
+#endif
 
 constexpr int kHeads = 16;
 constexpr int kTile = 16;
@@ -108,8 +111,9 @@ struct Geo {
   static constexpr int VC = QW / 32;        // 16-byte V chunks per lane per tile
   static constexpr int NT = QW / 16;        // 16-column O^T tiles per wave
   static constexpr int CPR = QW / 8;        // 16-byte chunks per V row (wave's columns)
-  static constexpr int VS = QW + 8;         // LDS row stride of the V copy, in bf16
-  static constexpr int VBUF = kTile * VS;   // one wave buffer, in bf16
+  static constexpr int VS = QW + 8;         // LDS row stride of the K copy, in bf16 (conflict-free row reads)
+  static constexpr int VSV = QW + (HLA_HIST_VTR ? 16 : 8);  // of the V copy (conflict-free transposed reads)
+  static constexpr int VBUF = kTile * VSV;  // one wave buffer, in bf16
 };
 
 template <int R>
@@ -167,7 +171,7 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
 #pragma unroll
   for (int it = 0; it < G::VC; ++it) {
     const int c = it * 64 + lane;
-    st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.v[it]);
+    st16(vs + (c / G::CPR) * G::VSV + (c % G::CPR) * 8, r.v[it]);
   }
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #if HLA_HIST_KLDS
@@ -186,6 +190,23 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
   for (int i = 0; i < G::KI; ++i) acc = mfma16x16x32(r.k[i], qreg[i], acc);
 #endif
   return acc;
+}
+
+// A operand of O^T += V^T P^T for output columns [16nt, 16nt + 16) of the wave's V copy: lane (g, hq) holds
+// V[4g + e][16nt + hq], e = 0..3. ds_read_b64_tr_b16 transposes within each 16-lane group: lane j of the group
+// reads row 4g + j/4, columns 16nt + 4(j%4) .. +3, and lane i receives element i%4 of lanes 4e + i/4.
+template <int R>
+__device__ __forceinline__ short4v vt_operand(const uint16_t* vs, int nt, int g, int hq) {
+  using G = Geo<R>;
+#if HLA_HIST_VTR
+  const uint16_t* p = vs + (4 * g + (hq >> 2)) * G::VSV + 16 * nt + 4 * (hq & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
+#else
+  short4v va;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) va[e] = (short)vs[(4 * g + e) * G::VSV + 16 * nt + hq];
+  return va;
+#endif
 }
 
 // Stage B: exchange S partials, online softmax, O^T += V^T P^T.
@@ -218,9 +239,7 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   for (int r = 0; r < 4; ++r) pb[r] = (short)f2bf(p[r]);
 #pragma unroll
   for (int nt = 0; nt < G::NT; ++nt) {
-    short4v va;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) va[e] = (short)vs[(4 * g + e) * G::VS + 16 * nt + hq];
+    const short4v va = vt_operand<R>(vs, nt, g, hq);
     oacc[nt] = oacc[nt] * alpha;
     oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
   }
@@ -356,7 +375,7 @@ __device__ __forceinline__ void group_stage_a(const TileRegs<R>& r, const u32x4 
 #pragma unroll
   for (int it = 0; it < G::KI; ++it) {
     const int c = it * 64 + lane;
-    st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.v[it]);
+    st16(vs + (c / G::CPR) * G::VSV + (c % G::CPR) * 8, r.v[it]);
     st16(ks + (c / G::CPR) * G::VS + (c % G::CPR) * 8, r.k[it]);
   }
 #pragma unroll
@@ -417,9 +436,7 @@ __device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4
     }
 #pragma unroll
     for (int nt = 0; nt < G::NT; ++nt) {
-      short4v va;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) va[e] = (short)vs[(4 * g + e) * G::VS + 16 * nt + hq];
+      const short4v va = vt_operand<R>(vs, nt, g, hq);
 #pragma unroll
       for (int u = 0; u < NQ; ++u)
         if (u < count) oacc[u][nt] = mfma16x16x16(va, pb[u], oacc[u][nt]);
