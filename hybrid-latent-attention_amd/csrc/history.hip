@@ -37,9 +37,6 @@ namespace {
 #ifndef HLA_HIST_VBUF
 #define HLA_HIST_VBUF 1
 #endif
-#ifndef HLA_HIST_NT
-#define HLA_HIST_NT 1
-#endif
 #ifndef HLA_HIST_WPE
 #define HLA_HIST_WPE 3  // keeps the accumulators out of AGPRs: 3 waves per SIMD instead of 2
 #endif
@@ -96,6 +93,7 @@ struct HistoryParams {
   int64_t o_st, o_sh;
   float* lse;  // [16][T]
   int group;     // tokens per workgroup (history_group when > 1)
+  bool shared_rows;  // tokens re-read the same rows (multi-query steps): cached instead of non-temporal loads
   bool has_window;
   bool direct;   // one split writing the final output and lse (else split partials to the workspace)
   bool combine;  // launch history_combine after the split kernel (with more than one split)
@@ -122,15 +120,15 @@ struct TileRegs {
   u32x4 v[Geo<R>::VC];
 };
 
+// K/V row loads: non-temporal when every row is read once (decode), cached when several tokens read the same rows
+// (multi-query steps), so that their re-reads hit the L2.
+template <bool NT>
 __device__ __forceinline__ u32x4 ld_stream(const uint16_t* p) {
-#if HLA_HIST_NT
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-#else
-  return ld16(p);
-#endif
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  else return ld16(p);
 }
 
-template <int R>
+template <int R, bool NT>
 __device__ __forceinline__ void load_tile(const HistoryParams& a, const int32_t* btr, int n, int j, int col0,
                                           int lane, TileRegs<R>& r) {
   using G = Geo<R>;
@@ -145,21 +143,21 @@ __device__ __forceinline__ void load_tile(const HistoryParams& a, const int32_t*
   for (int it = 0; it < G::KI; ++it) {  // same coalesced chunk layout as V: 4 rows x 256 bytes per instruction
     const int c = it * 64 + lane;
     const int key = c / G::CPR;
-    r.k[it] = (key0 + key < n) ? ld_stream(a.k + base + (int64_t)key * a.row_stride + (c % G::CPR) * 8)
+    r.k[it] = (key0 + key < n) ? ld_stream<NT>(a.k + base + (int64_t)key * a.row_stride + (c % G::CPR) * 8)
                                : u32x4{0u, 0u, 0u, 0u};
   }
 #else
   const bool kval = key0 + hq < n;
   const uint16_t* kp = a.k + base + (int64_t)hq * a.row_stride + 8 * g;
 #pragma unroll
-  for (int i = 0; i < G::KI; ++i) r.k[i] = kval ? ld_stream(kp + 32 * i) : u32x4{0u, 0u, 0u, 0u};
+  for (int i = 0; i < G::KI; ++i) r.k[i] = kval ? ld_stream<NT>(kp + 32 * i) : u32x4{0u, 0u, 0u, 0u};
 #endif
 #pragma unroll
   for (int it = 0; it < G::VC; ++it) {
     const int c = it * 64 + lane;
     const int key = c / G::CPR;
     const int cc = (c % G::CPR) * 8;
-    r.v[it] = (key0 + key < n) ? ld_stream(a.v + base + (int64_t)key * a.row_stride + cc) : u32x4{0u, 0u, 0u, 0u};
+    r.v[it] = (key0 + key < n) ? ld_stream<NT>(a.v + base + (int64_t)key * a.row_stride + cc) : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -261,7 +259,7 @@ __device__ void window_heads(const WindowPart& w, int T, float scale_log2, int t
               w.out + (int64_t)t * w.o_st + (int64_t)h * w.o_sh, w.lse + (int64_t)h * T + t);
 }
 
-template <int R>
+template <int R, bool NT>
 __global__ __launch_bounds__(Geo<R>::THREADS)
 #if HLA_HIST_WPE
 __attribute__((amdgpu_waves_per_eu(HLA_HIST_WPE, HLA_HIST_WPE)))
@@ -330,7 +328,7 @@ void history_split(HistoryParams a) {
     TileRegs<R> regs[DEPTH];
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u)
-      if (j_begin + u < j_end) load_tile<R>(a, btr, n, j_begin + u, col0, lane, regs[u]);
+      if (j_begin + u < j_end) load_tile<R, NT>(a, btr, n, j_begin + u, col0, lane, regs[u]);
     for (int j = j_begin; j < j_end; j += DEPTH) {
 #pragma unroll
       for (int u = 0; u < DEPTH; ++u) {
@@ -338,7 +336,7 @@ void history_split(HistoryParams a) {
         if (jt < j_end) {
           uint16_t* vs = v_lds[wave][jt % NVB];
           floatx4 sa = stage_a<R>(regs[u], qreg, vs, k_lds[wave], lane);
-          if (jt + DEPTH < j_end) load_tile<R>(a, btr, n, jt + DEPTH, col0, lane, regs[u]);
+          if (jt + DEPTH < j_end) load_tile<R, NT>(a, btr, n, jt + DEPTH, col0, lane, regs[u]);
           stage_b<R>(sa, s_lds[jt & 1], vs, jt * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
         }
       }
@@ -546,11 +544,11 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
       // a slower wave may still be reading (the barrier in between orders them); the wave-private K/V copies may
       // be rewritten by the next tile because a wave's own LDS accesses stay in order.
       TileRegs<R> regs;
-      load_tile<R>(a, btr, n_max, j_begin, col0, lane, regs);
+      load_tile<R, false>(a, btr, n_max, j_begin, col0, lane, regs);
       for (int jt = j_begin; jt < j_end; ++jt) {
         floatx4 sa[NQ];
         group_stage_a<R, NQ>(regs, qreg, v_lds[wave], k_lds[wave], lane, count, sa);
-        if (jt + 1 < j_end) load_tile<R>(a, btr, n_max, jt + 1, col0, lane, regs);
+        if (jt + 1 < j_end) load_tile<R, false>(a, btr, n_max, jt + 1, col0, lane, regs);
         group_stage_b<R, NQ>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane, oacc, m, l);
         par ^= 1;
       }
@@ -804,7 +802,9 @@ int launch(const HistoryParams& p, hipStream_t stream) {
     if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
-    hipLaunchKernelGGL(history_split<R>, dim3(p.T, p.num_splits), dim3(Geo<R>::THREADS), 0, stream, p);
+    const dim3 grid(p.T, p.num_splits);
+    if (p.shared_rows) hipLaunchKernelGGL((history_split<R, false>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
+    else hipLaunchKernelGGL((history_split<R, true>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   }
   int rc = check_launch("history_split");
   if (rc == HLA_S6_OK && !p.direct && p.combine) rc = launch_combine<R>(p, stream);
@@ -869,6 +869,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
   p.o_sh = o_sh;
   p.lse = lse;
   p.group = 1;
+  p.shared_rows = false;
   p.direct = num_splits == 1 && !partials_only;
   p.combine = !partials_only;
   return HLA_S6_OK;
@@ -917,7 +918,7 @@ extern "C" int hla_s6_history_attention_grouped(
     const void* k_cache, const void* v_cache, int64_t page_stride, int64_t row_stride, int32_t block_size,
     int64_t num_blocks, const int32_t* block_table, int64_t bt_stride, int32_t bt_cols, const int64_t* bt_rows,
     const int32_t* ctx, float scale, int32_t num_splits, float* workspace, int64_t workspace_floats, void* out,
-    int64_t o_st, int64_t o_sh, float* lse, int32_t group, void* stream) {
+    int64_t o_st, int64_t o_sh, float* lse, int32_t group, int32_t shared_rows, void* stream) {
   using namespace hla;
   HLA_REQUIRE(group == 1 || group == 2 || group == 4, HLA_S6_EUNSUPPORTED,
               "history_attention: group of %d tokens (built for 1, 2, 4)", group);
@@ -927,6 +928,7 @@ extern "C" int hla_s6_history_attention_grouped(
                         workspace, workspace_floats, out, o_st, o_sh, lse);
   if (rc != HLA_S6_OK || num_tokens == 0) return rc;
   p.group = group;
+  p.shared_rows = shared_rows != 0 || group > 1;
   return dispatch(p, width, as_stream(stream));
 }
 

@@ -162,7 +162,8 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
                                                    ctx.scale, ctx.kv_splits(w), ctx.workspace, k_scale, v_scale,
                                                    ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests,
-                                                   tokens_per_group=ctx.history_group)
+                                                   tokens_per_group=ctx.history_group,
+                                                   shared_rows=ctx.max_query_len > 1)
     o_hist = absorb_out(o_hist, B)
     return s6_ops.merge_states(o_hist, lse_hist, o_chunk, lse_chunk, ctx.invalid, ctx.backends.merge)
 

@@ -213,7 +213,7 @@ def history_attention(q_lat, cache, block_table, ctx, scale, num_kv_splits, work
 
 
 def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, k_scale, v_scale, backend,
-                         empty=None, mla=False, bt_rows=None, tokens_per_group=1):
+                         empty=None, mla=False, bt_rows=None, tokens_per_group=1, shared_rows=False):
     """Fully visible attention of ``q[T,16,L]`` over the first ``ctx[t]`` paged rows of ``k``/``v``
     ``[num_blocks, 1, block, L]`` (MQA, page/row strides shared by K and V, unit last stride).
 
@@ -224,6 +224,8 @@ def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, worksp
     accepted and unused. ``empty`` is derived from ``ctx`` inside the kernel and is accepted for signature parity.
     ``tokens_per_group`` (1, 2 or 4) lets one workgroup serve that many consecutive tokens that share a block-table
     row (the query rows of one request in a chunked-prefill step) from a single read of each K/V tile.
+    ``shared_rows`` declares that several tokens read the same rows, so K/V loads are cached for the re-reads
+    (decode steps read every row once and stream it past the caches).
     """
     _backend('history', backend)
     T, H, L, ctx, rows = _history_operands(q, k, v, block_table, ctx, mla, bt_rows)
@@ -239,10 +241,11 @@ def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, worksp
             k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(rows),
             _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o),
             o.stride(0), o.stride(1), _lib.ptr(lse))
-    if int(tokens_per_group) == 1:
+    if int(tokens_per_group) == 1 and not shared_rows:
         _lib.call('hla_s6_history_attention', *args, _lib.stream(q.device))
     else:
-        _lib.call('hla_s6_history_attention_grouped', *args, int(tokens_per_group), _lib.stream(q.device))
+        _lib.call('hla_s6_history_attention_grouped', *args, int(tokens_per_group), int(bool(shared_rows)),
+                  _lib.stream(q.device))
     return o, lse
 
 

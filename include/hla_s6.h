@@ -108,14 +108,16 @@ int hla_s6_history_attention(const void *q, int32_t num_tokens, int32_t num_head
  * hla/vllm_latent/s6_layer.py:97-115): one workgroup serves `group` (1, 2 or 4) consecutive tokens, and the
  * tokens of a group that share a block-table row (bt_rows[t] equal: one request) read each K/V tile once for all
  * of them; a group spanning two rows takes one pass per row. Each token still sees its own ctx[t] rows. Same
- * arguments, outputs and checks as hla_s6_history_attention. */
+ * arguments, outputs and checks as hla_s6_history_attention. shared_rows != 0 declares that several tokens read the
+ * same rows (any multi-query step, also with group == 1): K/V loads are then cached for the re-reads instead of
+ * non-temporal. */
 int hla_s6_history_attention_grouped(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
                                      int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
                                      int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
                                      const int32_t *block_table, int64_t bt_stride, int32_t bt_cols,
                                      const int64_t *bt_rows, const int32_t *ctx, float scale, int32_t num_splits,
                                      float *workspace, int64_t workspace_floats, void *out, int64_t o_st,
-                                     int64_t o_sh, float *lse, int32_t group, void *stream);
+                                     int64_t o_sh, float *lse, int32_t group, int32_t shared_rows, void *stream);
 
 /* The two launches of hla_s6_history_attention as separate calls, as the reference launches the
  * stage-1 split kernel and the stage-2 LSE reduction separately (hla/vllm_latent/s6_ops.py:186-202,

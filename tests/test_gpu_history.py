@@ -153,7 +153,7 @@ def test_two_stage_history_is_bitwise_the_op(ops, width, splits):
 
 @pytest.mark.parametrize('width', [512, 256])
 @pytest.mark.parametrize('splits', [1, 5])
-@pytest.mark.parametrize('group', [2, 4])
+@pytest.mark.parametrize('group', [1, 2, 4])
 def test_grouped_history_matches_oracle(ops, width, splits, group):
     """Chunked-prefill shape: requests of 5, 3, 1, 8 and 2 query rows whose rows share the request's table row.
     Request 0 has one ctx for every row (vLLM prefill), request 1 a causal ctx per row (K-hop), request 2 no
@@ -171,7 +171,8 @@ def test_grouped_history_matches_oracle(ops, width, splits, group):
     q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
     ws = ops.S6Workspace(16, width, len(ctx) * splits)
     o, lse = ops.history_attention_kv(q, cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx), SCALE,
-                                      splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=group)
+                                      splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=group,
+                                      shared_rows=True)
     o, lse = host_f32(o), host_f32(lse)
     check(o, lse, *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
     o1, lse1 = run_history(ops, q_bits, cache_bits, table, ctx, splits, bt_rows=req)
