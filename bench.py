@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = 'latent decode-attn µs/layer + HBM GB/s (% peak), Ouro-1.4B S6, B=64 ctx 8K'
 PEAK_HBM_GBPS = 8000.0
+PEAK_BF16_TFLOPS = 2500.0
 TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'history_split_512_b64_ctx8192_pmc.md')
 LAYERS, LOOPS, HEADS, HEAD_DIM, RANK, RANK1, WINDOW, BLOCK = 24, 4, 16, 128, 512, 256, 32, 16
 MAX_POSITION = 65536
@@ -36,8 +37,15 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--batch', type=int, default=64)
-    p.add_argument('--context', type=int, default=8192, help='history tokens before the decoded token')
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill'), default='decode',
+                   help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
+                        'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
+                        'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
+                        'history, one layer x 4 loops. Only decode prints the headline line.')
+    p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 32 / 8 / 4 by workload)')
+    p.add_argument('--context', type=int, default=0, help='history tokens before the step (default by workload)')
+    p.add_argument('--queries', type=int, default=512, help='new tokens per request of --workload prefill')
+    p.add_argument('--layers', type=int, default=0, help='layers (default: 24 for decode/ragged, 1 otherwise)')
     p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
     p.add_argument('--width', type=int, default=512, choices=(256, 512), help='latent width of --kernel-only')
@@ -52,72 +60,88 @@ def parse():
 
 
 class Workload:
-    """Random-init caches, tables and readers of the whole model's attention path (one decode step of B rows)."""
+    """Random-init caches, tables and readers of the model's attention path for one step: request r has ``hist[r]``
+    history tokens and ``queries`` new tokens (1: a decode step; more: a chunked-prefill step whose tokens are
+    already written to the exact cache), ``layers`` layers x 4 loops."""
 
-    def __init__(self, ops, layer, B, hist, splits, seed, device, table='random'):
+    def __init__(self, ops, layer, hist, queries, splits, seed, device, table='random', layers=LAYERS):
         g = torch.Generator(device=device).manual_seed(seed)
-        self.B, self.hist, self.device = B, hist, device
-        self.seq_len = hist + 1                                   # the decoded token is already in the exact cache
-        self.n_latent = max(hist - WINDOW, 0)
-        cols = -(-self.seq_len // BLOCK)
-        self.cols = cols
-        pool = B * cols + 1                                       # page 0: the null page
+        hist = [int(h) for h in hist]
+        B, Q = len(hist), int(queries)
+        self.B, self.Q, self.T, self.hist, self.layers, self.device = B, Q, B * Q, hist, layers, device
+        self.seq = [h + Q for h in hist]                          # the step's tokens are already in the exact cache
+        self.n_latent = [max(h - WINDOW, 0) for h in hist]
+        cols = [-(-s // BLOCK) for s in self.seq]
+        self.cols = max(cols)
         randn = lambda *shape, std=1.0: (torch.randn(*shape, generator=g, device=device, dtype=torch.float32) * std
                                          ).to(torch.bfloat16)
         perm = lambda n: (torch.randperm(n - 1, generator=g, device=device) + 1).to(torch.int32)
         lat_pages = perm if table == 'random' else (lambda n: torch.arange(1, n, dtype=torch.int32, device=device))
-        self.lat_table = {RANK: lat_pages(pool)[:B * cols].view(B, cols).contiguous(),
-                          RANK1: lat_pages(pool)[:B * cols].view(B, cols).contiguous()}
-        self.lat = []
-        for _ in range(LAYERS):
-            self.lat.append({w: torch.empty(pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(
-                generator=g) for w in (RANK, RANK1)})
-        # exact caches: a sliding window of W + 1 rows per request and loop; freed pages are the null page
-        first_col, last_col = max(0, self.seq_len - 1 - WINDOW) // BLOCK, (self.seq_len - 1) // BLOCK
-        win_cols = last_col - first_col + 1
-        ex_pool = B * win_cols + 1
-        self.ex_table = []
-        for _ in range(LOOPS):
-            t = torch.zeros(B, cols, dtype=torch.int32, device=device)
-            t[:, first_col:last_col + 1] = perm(ex_pool)[:B * win_cols].view(B, win_cols)
-            self.ex_table.append(t)
-        self.exact = [[randn(ex_pool, HEADS, BLOCK, 2 * HEAD_DIM) for _ in range(LOOPS)] for _ in range(LAYERS)]
+        pool = sum(cols) + 1                                      # page 0: the null page
+
+        def paged_table(first, last, pages):
+            t = torch.zeros(B, self.cols, dtype=torch.int32, device=device)
+            used = 0
+            for r in range(B):
+                n = last[r] - first[r] + 1
+                t[r, first[r]:last[r] + 1] = pages[used:used + n]
+                used += n
+            return t
+
+        self.lat_table = {w: paged_table([0] * B, [c - 1 for c in cols], lat_pages(pool)) for w in (RANK, RANK1)}
+        self.lat = [{w: torch.empty(pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(generator=g)
+                     for w in (RANK, RANK1)} for _ in range(layers)]
+        # exact caches: the window rows and the step's tokens per request and loop; freed pages are the null page
+        first = [max(0, h - WINDOW) // BLOCK for h in hist]
+        last = [(s - 1) // BLOCK for s in self.seq]
+        ex_pool = sum(l - f + 1 for f, l in zip(first, last)) + 1
+        self.ex_table = [paged_table(first, last, perm(ex_pool)) for _ in range(LOOPS)]
+        self.exact = [[randn(ex_pool, HEADS, BLOCK, 2 * HEAD_DIM) for _ in range(LOOPS)] for _ in range(layers)]
         std = 1 / math.sqrt(2048)
         self.readers = [_Reader(randn(HEADS, HEAD_DIM, RANK1, std=std), randn(HEADS, RANK1, HEAD_DIM, std=std),
                                 randn(3, HEADS, HEAD_DIM, RANK, std=std), randn(3, HEADS, RANK, HEAD_DIM, std=std))
-                        for _ in range(LAYERS)]
+                        for _ in range(layers)]
         inv = layer.latent_inv_freq(HEAD_DIM, 1e6).to(device)
         self.tables = {w: layer.latent_rope_table(MAX_POSITION, inv, w, torch.bfloat16) for w in (RANK, RANK1)}
-        self.q_pre = [randn(B, HEADS, HEAD_DIM) for _ in range(LOOPS)]
-        self.q_rope = [randn(B, HEADS, HEAD_DIM) for _ in range(LOOPS)]
-        self.positions = torch.full((B,), hist, dtype=torch.int64, device=device)
-        self.qsl = torch.arange(B + 1, dtype=torch.int32, device=device)
-        self.seq_lens = torch.full((B,), self.seq_len, dtype=torch.int32, device=device)
+        T = self.T
+        self.q_pre = [randn(T, HEADS, HEAD_DIM) for _ in range(LOOPS)]
+        self.q_rope = [randn(T, HEADS, HEAD_DIM) for _ in range(LOOPS)]
+        self.k_rope = [randn(T, HEADS, HEAD_DIM) for _ in range(LOOPS)] if Q > 1 else [None] * LOOPS
+        self.v = [randn(T, HEADS, HEAD_DIM) for _ in range(LOOPS)] if Q > 1 else [None] * LOOPS
+        self.positions = torch.tensor([h + i for h in hist for i in range(Q)], dtype=torch.int64, device=device)
+        self.qsl = (torch.arange(B + 1, dtype=torch.int32, device=device) * Q).contiguous()
+        self.seq_lens = torch.tensor(self.seq, dtype=torch.int32, device=device)
         self.splits = splits                                      # {latent width: KV splits}
-        self.workspace = ops.S6Workspace.for_splits(HEADS, B, splits)
+        self.workspace = ops.S6Workspace.for_splits(HEADS, T, splits)
         self.ops, self.layer = ops, layer
 
     def step(self):
         ops, layer = self.ops, self.layer
-        ctx = layer.StepContext(self.positions, self.qsl, self.seq_lens, 1, self.B, self.tables, HEAD_DIM ** -0.5,
-                                ops.HIP_BACKENDS, self.workspace, self.splits[RANK], window=WINDOW,
-                                max_seqlen_k=self.seq_len, kv_splits_by_width=self.splits)
+        ctx = layer.StepContext(self.positions, self.qsl, self.seq_lens, self.Q, self.T, self.tables,
+                                HEAD_DIM ** -0.5, ops.HIP_BACKENDS, self.workspace, self.splits[RANK], window=WINDOW,
+                                max_seqlen_k=max(self.seq), kv_splits_by_width=self.splits)
         outs = []
         for loop in range(LOOPS):
             w = RANK1 if loop == 0 else RANK
-            for i in range(LAYERS):
+            for i in range(self.layers):
                 sl = self.readers[i]
                 q_lat = ctx.latent_query(sl, loop, self.q_pre[loop])
-                outs.append(layer.attend(sl, loop, q_lat, self.q_rope[loop], None, None, self.lat[i][w],
-                                         self.lat_table[w], None, None, ctx, (self.exact[i][loop], self.ex_table[loop])))
+                outs.append(layer.attend(sl, loop, q_lat, self.q_rope[loop], self.k_rope[loop], self.v[loop],
+                                         self.lat[i][w], self.lat_table[w], None, None, ctx,
+                                         (self.exact[i][loop], self.ex_table[loop])))
         return outs
 
     def history_bytes_per_layer(self):
-        return self.B * self.n_latent * (2 * RANK1 + 3 * 2 * RANK) * 2
+        """Latent rows read once per request: (256 + 256) + 3 x (512 + 512) bf16 columns per row."""
+        return sum(self.n_latent) * (2 * RANK1 + 3 * 2 * RANK) * 2
+
+    def history_flops_per_layer(self):
+        """4 flops per (query row, latent row, latent column): scores and weighted values."""
+        return sum(4 * self.Q * HEADS * n * (RANK1 + 3 * RANK) for n in self.n_latent)
 
     def window_bytes_per_layer(self):
-        keys = min(self.seq_len, WINDOW + 1)
-        return self.B * LOOPS * keys * HEADS * 2 * HEAD_DIM * 2
+        keys = sum(min(s, WINDOW + self.Q) for s in self.seq)
+        return LOOPS * keys * HEADS * 2 * HEAD_DIM * 2
 
 
 class _Reader:
@@ -169,13 +193,13 @@ def history_roofline(wl, iters=50, width=RANK):
     the average duration of the stage-2 reduction likewise, and the algorithmic bytes stage 1 reads (every latent
     K and V row of every token once)."""
     ops = wl.ops
-    ctx_lat = torch.full((wl.B,), wl.n_latent, dtype=torch.int32, device=wl.device)
+    ctx_lat = torch.tensor(wl.n_latent, dtype=torch.int32, device=wl.device)
     q = torch.randn(wl.B, HEADS, width, device=wl.device).to(torch.bfloat16) * (width ** -0.5)
-    caches = [wl.lat[i][width] for i in range(LAYERS)]
+    caches = [wl.lat[i][width] for i in range(wl.layers)]
     splits = wl.splits[width]
 
     def stage1(i):
-        c = caches[i % LAYERS]
+        c = caches[i % len(caches)]
         return ops.history_partials(q, c[..., :width], c[..., width:], wl.lat_table[width], ctx_lat, HEAD_DIM ** -0.5,
                                     splits, wl.workspace)
 
@@ -195,7 +219,7 @@ def history_roofline(wl, iters=50, width=RANK):
     us = timed(stage1)
     part = stage1(0)
     us_reduce = timed(lambda i: ops.history_reduce(part))
-    nbytes = wl.B * wl.n_latent * 2 * width * 2
+    nbytes = sum(wl.n_latent) * 2 * width * 2
     return us, us_reduce, nbytes
 
 
@@ -204,8 +228,7 @@ def cpu_baseline(wl, tokens=8):
     scaled to B rows x (1 + 3) loops: microseconds per layer on the host cores."""
     from oracle import bf16, s6_oracle as O
     cores = len(os.sched_getaffinity(0))
-    B, n, hist = wl.B, wl.n_latent, wl.hist
-    idx = torch.arange(tokens, device=wl.device)
+    B, n, seq_len = wl.B, wl.n_latent[0], wl.seq[0]      # the decode workload: every row has the same history
     timings = {}
     for w in (RANK, RANK1):
         layer0 = wl.lat[0][w]
@@ -222,7 +245,7 @@ def cpu_baseline(wl, tokens=8):
         ex_h = ex.float().cpu().numpy()
         ex_table = wl.ex_table[loop][:tokens].cpu().numpy()
         qsl = np.arange(tokens + 1)
-        seq = np.full(tokens, wl.seq_len)
+        seq = np.full(tokens, seq_len)
         ctx_lat = np.full(tokens, n)
 
         def run():
@@ -242,6 +265,22 @@ def cpu_baseline(wl, tokens=8):
             'sample': f'numpy oracle of attend_decode (window + latent history + B_t + merge, fp32) on {tokens} of the '
                       f'{B} rows, one loop-1 call and one main-latent call of layer 0 (median of 3 after 1 warm-up), '
                       f'scaled x{B // tokens} rows x (1 + 3) loops; extrapolated'}
+
+
+def secondary(args, wl, B, context, layers, queries, splits):
+    """One JSON line for the ragged / long-context / multi-query workloads (not the headline metric)."""
+    ms = time_graph(wl.step, args.steps, args.warmup)
+    us_layer = ms * 1000 / layers
+    hist_bytes, flops = wl.history_bytes_per_layer(), wl.history_flops_per_layer()
+    gbps, tflops = hist_bytes / (us_layer * 1e3), flops / (us_layer * 1e6)
+    out = {'workload': args.workload, 'value': round(us_layer, 2), 'unit': 'us/layer', 'B': B, 'queries': queries,
+           'context': context, 'contexts': wl.hist if args.workload == 'ragged' else None, 'layers': layers,
+           'loops': LOOPS, 'kv_splits': splits, 'steps': args.steps, 'ms_per_step': round(ms, 4),
+           'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
+           'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
+           'history_tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
+           'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True}
+    print(json.dumps(out), flush=True)
 
 
 def main():
@@ -267,11 +306,24 @@ def main():
     pkg = importlib.import_module('hybrid-latent-attention_amd')
     ops, layer = pkg.s6_ops, pkg.s6_layer
     cus = pkg._lib.device_cus(0)
-    splits = {w: args.splits or ops.mi355x_kv_splits(args.context, args.batch, cus, width=w) for w in (RANK, RANK1)}
-    print(f'bench: building workload B={args.batch} ctx={args.context} splits={splits} cus={cus}', file=sys.stderr,
-          flush=True)
-    wl = Workload(ops, layer, args.batch, args.context, splits, args.seed, device, args.table)
+    defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
+                'prefill': (4, 8192, 1)}[args.workload]
+    B, context, layers = args.batch or defaults[0], args.context or defaults[1], args.layers or defaults[2]
+    queries = args.queries if args.workload == 'prefill' else 1
+    if args.workload == 'ragged':
+        hist = np.random.default_rng(args.seed).integers(1024, context + 1, B).tolist()
+    elif args.workload == 'prefill':
+        hist = [context + WINDOW] * B                          # `context` latent rows + the exact window
+    else:
+        hist = [context] * B
+    splits = {w: args.splits or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w)
+              for w in (RANK, RANK1)}
+    print(f'bench: building workload {args.workload} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
+          f'splits={splits} cus={cus}', file=sys.stderr, flush=True)
+    wl = Workload(ops, layer, hist, queries, splits, args.seed, device, args.table, layers)
     torch.cuda.synchronize()
+    if args.workload != 'decode' and not args.kernel_only:
+        return secondary(args, wl, B, context, layers, queries, splits)
 
     if args.kernel_only:
         us, us_reduce, nbytes = history_roofline(wl, iters=max(args.steps, 1), width=args.width)
@@ -281,7 +333,7 @@ def main():
 
     print('bench: capturing the decode step', file=sys.stderr, flush=True)
     ms = time_graph(wl.step, args.steps, args.warmup)
-    us_layer = ms * 1000 / LAYERS
+    us_layer = ms * 1000 / layers
     hist_bytes, win_bytes = wl.history_bytes_per_layer(), wl.window_bytes_per_layer()
     layer_gbps = (hist_bytes + win_bytes) / (us_layer * 1e3)
     print('bench: history kernel roofline', file=sys.stderr, flush=True)
@@ -295,11 +347,11 @@ def main():
         'metric': METRIC, 'value': round(us_layer, 3), 'unit': 'us/layer', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': False, 'scaling': 'weak',
         'vs_baseline': None, 'dtype': 'bf16', 'data': 'synthetic (random-init caches, readers and queries)',
-        'config': {'workload': f'Ouro-1.4B S6 decode attention path, {LAYERS} layers x {LOOPS} loops, '
-                               f'B={args.batch}, context {args.context}, W={WINDOW}, block {BLOCK}',
-                   'global_batch': args.batch, 'seq_len': args.context, 'parallelism': 'none (1 GPU)',
+        'config': {'workload': f'Ouro-1.4B S6 decode attention path, {layers} layers x {LOOPS} loops, '
+                               f'B={B}, context {context}, W={WINDOW}, block {BLOCK}',
+                   'global_batch': B, 'seq_len': context, 'parallelism': 'none (1 GPU)',
                    'kv_splits': splits, 'hip_graph': True},
-        'tokens_per_s': round(args.batch / (ms / 1000), 1),
+        'tokens_per_s': round(B / (ms / 1000), 1),
         'hbm_gbps': round(layer_gbps, 1), 'hbm_frac': round(layer_gbps / PEAK_HBM_GBPS, 4),
         'bytes_per_layer': {'latent_history': hist_bytes, 'exact_window': win_bytes},
         'roofline': {'kernel': f'history_split<{RANK}> (split-KV latent history, {splits[RANK]} splits)',

@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -41,10 +41,14 @@ SIGNATURES = {
     'hla_s6_merge_states': [P, I64, I64, P, P, I64, I64, P, P, I32, I32, I32, I32, P, I64, I64, P, P],
     'hla_s6_attend_decode': [P, I64, I64, I32, P, P, I64, I64, I32, I64, P, I64, I32, P, P, P, I64, I64, P, P, I64, I64,
                              I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32, F32, I32, P, I64, P,
-                             P, P, P, P, I64, I64, P],
+                             I64, P, P, P, P, P, I64, I64, P],
+    'hla_s6_split_plan_ints': [I32, I32],
+    'hla_s6_split_plan': [P, I32, I64, I32, P, I64, P],
     'hla_s6_slot_mapping': [P, I64, I32, P, P, P, I32, I32, P, P],
     'hla_s6_store_rows': [P, I64, P, I64, I32, I32, P, P, I64, I64, I32, I64, P],
 }
+
+RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64}
 
 _LIB = None
 
@@ -60,7 +64,7 @@ def load() -> ctypes.CDLL:
         for name, argtypes in SIGNATURES.items():
             fn = getattr(lib, name)
             fn.argtypes = argtypes
-            fn.restype = ctypes.c_char_p if name == 'hla_s6_last_error' else ctypes.c_int
+            fn.restype = RESTYPES.get(name, ctypes.c_int)
         version = lib.hla_s6_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f'libhla_s6.so ABI {version}, expected {ABI_VERSION}: rebuild the library')

@@ -92,6 +92,7 @@ struct HistoryParams {
   uint16_t* out;
   int64_t o_st, o_sh;
   float* lse;  // [16][T]
+  const int32_t* plan;  // precomputed split plan of the step (split_plan_kernel) or null
   int group;     // tokens per workgroup (history_group when > 1)
   bool shared_rows;  // tokens re-read the same rows (multi-query steps): cached instead of non-temporal loads
   bool has_window;
@@ -113,6 +114,140 @@ struct Geo {
   static constexpr int VSV = QW + (HLA_HIST_VTR ? 16 : 8);  // of the V copy (conflict-free transposed reads)
   static constexpr int VBUF = kTile * VSV;  // one wave buffer, in bf16
 };
+
+// Split plan shared by the split kernel and the kernels that reduce its partials. Every row of the call is cut in
+// chunks of `chunk` 16-row tiles; the grid has S slots per row, and
+//   chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S)))
+// keeps every row within its S slots while about T*S/2 slots get work however ragged the rows are (short rows take
+// few slots, long rows many, each holding equal work). Slot s of a row holds tiles [s*chunk, (s+1)*chunk); slots past
+// ceil(tiles / chunk) are empty.
+__device__ __forceinline__ int row_tiles(int32_t ctx, int64_t cap) {
+  return (int)((min((int64_t)ctx, cap) + kTile - 1) / kTile);
+}
+
+// Slots of a row that hold work under a plan of `chunk` tiles.
+__device__ __forceinline__ int used_slots(int32_t ctx, int64_t cap, int chunk) {
+  return (row_tiles(ctx, cap) + chunk - 1) / chunk;
+}
+
+// The plan's chunk. Must be called by every thread of the block (a multiple of 64 threads); `red` holds 2 * waves
+// int64.
+__device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_t* red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+  int mx = 0;
+  int64_t sum = 0;
+  for (int i = tid; i < T; i += blockDim.x) {
+    const int tiles = row_tiles(ctx[i], cap);
+    mx = max(mx, tiles);
+    sum += tiles;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    mx = max(mx, __shfl_xor(mx, off));
+    sum += __shfl_xor(sum, off);
+  }
+  if (lane == 0) {
+    red[2 * wave] = mx;
+    red[2 * wave + 1] = sum;
+  }
+  __syncthreads();
+  int64_t m = 0;
+  sum = 0;
+  for (int w = 0; w < waves; ++w) {
+    m = max(m, red[2 * w]);
+    sum += red[2 * w + 1];
+  }
+  const int64_t slots = (int64_t)T * S;
+  return (int)max((int64_t)1, max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
+}
+
+// Workgroups of the split kernel: the plan puts at most T*S/2 + T (row, chunk) items in the list.
+__host__ __device__ inline unsigned split_workgroups(int T, int S) { return S == 1 ? (unsigned)T : (unsigned)T * ((S + 1) / 2 + 1); }
+
+// Work item b of the step's list of (row, slot) pairs, rows in order, each row contributing its used slots:
+// row = -1 past the end of the list. The split kernel gives item b to the workgroup dispatched b-th, so consecutive
+// items land on consecutive XCDs (workgroups are dealt to the XCDs round-robin) and every XCD gets the same share
+// of the work, however ragged the rows are. Must be called by every thread (a multiple of 64 threads); `wsum` holds
+// one int per wave, `res` two ints.
+__device__ void find_item(const int32_t* ctx, int T, int64_t cap, int chunk, int b, int* wsum, int* res, int& row,
+                          int& slot) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, n = blockDim.x;
+  const int seg = (T + n - 1) / n, r0 = min(T, tid * seg), r1 = min(T, r0 + seg);
+  int cnt = 0;
+  for (int r = r0; r < r1; ++r) cnt += used_slots(ctx[r], cap, chunk);
+  int x = cnt;  // inclusive scan over the wave
+  for (int off = 1; off < 64; off <<= 1) {
+    const int v = __shfl_up(x, off);
+    if (lane >= off) x += v;
+  }
+  if (lane == 63) wsum[wave] = x;
+  if (tid == 0) res[0] = -1;
+  __syncthreads();
+  int hi = x;
+  for (int w = 0; w < wave; ++w) hi += wsum[w];
+  int lo = hi - cnt;
+  if (b >= lo && b < hi) {  // exactly one thread owns item b
+    for (int r = r0; r < r1; ++r) {
+      const int u = used_slots(ctx[r], cap, chunk);
+      if (b < lo + u) {
+        res[0] = r;
+        res[1] = b - lo;
+        break;
+      }
+      lo += u;
+    }
+  }
+  __syncthreads();
+  row = res[0];
+  slot = res[1];
+}
+
+// Plan layout (int32): [0] chunk, [1, 1 + T) used slots per row, then the work items' rows [NI] and slots [NI],
+// NI = split_workgroups(T, S); rows past the end of the list are -1.
+inline int64_t plan_ints(int T, int S) { return 1 + (int64_t)T + 2 * (int64_t)split_workgroups(T, S); }
+
+// The split plan of a step, computed once by one workgroup and read by every split kernel of the step (every layer
+// and loop with the same lengths and slot count) instead of being derived in each workgroup.
+__global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, int S, int32_t* plan) {
+  __shared__ int64_t red[8];
+  __shared__ int wsum[4];
+  __shared__ int carry_s;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int chunk = split_chunk(ctx, T, cap, S, red);
+  const int ni = (int)split_workgroups(T, S);
+  int32_t* used = plan + 1;
+  int32_t* rows = plan + 1 + T;
+  int32_t* slots = rows + ni;
+  if (tid == 0) {
+    plan[0] = chunk;
+    carry_s = 0;
+  }
+  for (int i = tid; i < ni; i += 256) rows[i] = -1;
+  __syncthreads();
+  for (int r0 = 0; r0 < T; r0 += 256) {  // rows in blocks of 256: exclusive prefix of the used slots
+    const int r = r0 + tid;
+    const int u = r < T ? used_slots(ctx[r], cap, chunk) : 0;
+    int x = u;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int v = __shfl_up(x, off);
+      if (lane >= off) x += v;
+    }
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int base = carry_s;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    const int first = base + x - u;
+    if (r < T) {
+      used[r] = u;
+      for (int c = 0; c < u; ++c) {
+        rows[first + c] = r;
+        slots[first + c] = c;
+      }
+    }
+    __syncthreads();
+    if (tid == 255) carry_s = base + x;
+    __syncthreads();
+  }
+}
 
 template <int R>
 struct TileRegs {
@@ -243,20 +378,19 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   }
 }
 
-// The decode exact window of token t for the heads of split s: heads s + S*(wave + waves*i), so the S splits of a
-// token share its 16 heads (two per split at S = 8 with 4 waves) and no workgroup is added to the grid.
-__device__ void window_heads(const WindowPart& w, int T, float scale_log2, int t, int s, int S, int wave, int waves,
-                             int lane) {
-  int h = s + S * wave;
-  if (h >= kHeads) return;
-  int req, lo, hi;
-  decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi);
-  ExactSource src = w.src;
-  hi = (int)min((int64_t)hi, (int64_t)w.bt_cols * src.block_size);
-  src.table_row = w.bt + (int64_t)req * w.bt_stride;
-  for (; h < kHeads; h += waves * S)
+// The decode exact windows of the step, one (token, head) row per wave: wave v of the grid (of nv) computes rows
+// v, v + nv, ... of the 16*T, so they spread over the first workgroups of every XCD and add no workgroup.
+__device__ void window_jobs(const WindowPart& w, int T, float scale_log2, int v, int nv, int lane) {
+  for (int j = v; j < kHeads * T; j += nv) {
+    const int t = j / kHeads, h = j % kHeads;
+    int req, lo, hi;
+    decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi);
+    ExactSource src = w.src;
+    hi = (int)min((int64_t)hi, (int64_t)w.bt_cols * src.block_size);
+    src.table_row = w.bt + (int64_t)req * w.bt_stride;
     exact_row(src, w.q + (int64_t)t * w.q_st + (int64_t)h * w.q_sh, scale_log2, lo, hi, h, lane,
               w.out + (int64_t)t * w.o_st + (int64_t)h * w.o_sh, w.lse + (int64_t)h * T + t);
+  }
 }
 
 template <int R, bool NT>
@@ -270,31 +404,37 @@ void history_split(HistoryParams a) {
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][NVB][G::VBUF];
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][HLA_HIST_KLDS ? G::VBUF : 8];
   __shared__ floatx4 s_lds[2][G::WAVES * 64];
-  __shared__ int red_lds[G::WAVES];
+  __shared__ int64_t red_lds[2 * G::WAVES];
+  __shared__ int item_lds[G::WAVES + 2];
 
-  const int t = blockIdx.x, s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int S = a.num_splits;
   const int hq = lane & 15, g = lane >> 4;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;  // keys the block table can address
+  const int b = blockIdx.x;                                 // dispatch order
+
+  // Split plan: every row is cut in chunks of `chunk` tiles (the same for every row of the step); workgroup b takes
+  // the b-th (row, chunk) pair of the step, so the work is balanced over the workgroups and the XCDs.
+  int t = b, s = 0, chunk = 0;
+  if (S > 1 && a.plan) {
+    const int ni = (int)split_workgroups(a.T, S);
+    chunk = a.plan[0];
+    t = a.plan[1 + a.T + b];
+    s = a.plan[1 + a.T + ni + b];
+  } else if (S > 1) {
+    chunk = split_chunk(a.ctx, a.T, cap, S, red_lds);
+    find_item(a.ctx, a.T, cap, chunk, b, item_lds, item_lds + G::WAVES, t, s);
+  }
+  // the exact decode windows (the fused decode step), spread over the first waves of the grid
+  if (a.has_window) window_jobs(a.win, a.T, a.scale_log2, b * G::WAVES + wave, gridDim.x * G::WAVES, lane);
+  if (S > 1 && b < a.T && wave == 0 && g == 0) {  // slots of row b past its work: an empty partial for stage 2
+    const int used = a.plan ? a.plan[1 + b] : used_slots(a.ctx[b], cap, chunk);
+    for (int e = used; e < S; ++e) a.ws_lse[((int64_t)b * S + e) * kHeads + hq] = -INFINITY;
+  }
+  if (t < 0) return;  // past the end of the work list (uniform over the workgroup)
   const int n = (int)min((int64_t)a.ctx[t], cap);
   const int tiles = (n + kTile - 1) / kTile;
-
-  // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
-  // ragged batch get split counts proportional to their length and every split has equal work.
-  int chunk = tiles;
-  if (S > 1) {
-    int mx = 0;
-    for (int i = tid; i < a.T; i += G::THREADS) mx = max(mx, (int)min((int64_t)a.ctx[i], cap));
-    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
-    if (lane == 0) red_lds[wave] = mx;
-    __syncthreads();
-    for (int w = 0; w < G::WAVES; ++w) mx = max(mx, red_lds[w]);
-    const int max_tiles = (mx + kTile - 1) / kTile;
-    chunk = (max_tiles + S - 1) / S;
-  }
-  // the token's exact-window heads of this split (the fused decode step), before its history tiles
-  if (a.has_window) window_heads(a.win, a.T, a.scale_log2, t, s, S, wave, G::WAVES, lane);
+  if (S == 1) chunk = tiles;
   const int j_begin = s * chunk;
   const int j_end = min(tiles, j_begin + chunk);
   const int col0 = wave * G::QW;
@@ -480,7 +620,7 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][G::VBUF];
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][G::VBUF];
   __shared__ floatx4 s_lds[2][NQ * G::WAVES * 64];
-  __shared__ int red_lds[G::WAVES];
+  __shared__ int64_t red_lds[2 * G::WAVES];
 
   const int s = blockIdx.y;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -491,17 +631,7 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
 
   // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
   // ragged batch get split counts proportional to their length and every split has equal work.
-  int chunk = 1 << 30;
-  if (S > 1) {
-    int mx = 0;
-    for (int i = tid; i < a.T; i += G::THREADS) mx = max(mx, (int)min((int64_t)a.ctx[i], cap));
-    for (int off = 32; off > 0; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
-    if (lane == 0) red_lds[wave] = mx;
-    __syncthreads();
-    for (int w = 0; w < G::WAVES; ++w) mx = max(mx, red_lds[w]);
-    const int max_tiles = (mx + kTile - 1) / kTile;
-    chunk = (max_tiles + S - 1) / S;
-  }
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
   const int t_begin = blockIdx.x * NQ, t_end = min(t_begin + NQ, a.T);
 
   int par = 0;  // score-exchange buffer of the next tile; alternates over every tile of every pass
@@ -560,12 +690,23 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
   }
 }
 
-// Split reduction: one workgroup per (token, head), thread i owns output columns [4i, 4i+4).
+// Split reduction: one workgroup per (token, head), thread i < R/4 owns output columns [4i, 4i+4).
 template <int R>
-__global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
+constexpr int combine_threads() { return R / 4 < 64 ? 64 : R / 4; }
+
+template <int R>
+__global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryParams a) {
+  __shared__ int64_t red[2 * combine_threads<R>() / 64];
   const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
-  const int S = a.num_splits;
-  const float* ls = a.ws_lse + (int64_t)t * S * kHeads + h;
+  const int S_all = a.num_splits;
+  // slots past the row's work hold lse = -inf; with the lengths at hand they are not read at all
+  int S = S_all;
+  if (a.ctx) {
+    const int64_t cap = (int64_t)a.bt_cols * a.block_size;
+    S = min(S_all, used_slots(a.ctx[t], cap, split_chunk(a.ctx, a.T, cap, S_all, red)));
+  }
+  if (i >= R / 4) return;
+  const float* ls = a.ws_lse + (int64_t)t * S_all * kHeads + h;
   float mx = -INFINITY;
   for (int s = 0; s < S; ++s) mx = fmaxf(mx, ls[(int64_t)s * kHeads]);
   uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * i;
@@ -574,31 +715,28 @@ __global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
     if (i == 0) a.lse[(int64_t)h * a.T + t] = -INFINITY;
     return;
   }
-  const float* base = a.ws_o + ((int64_t)t * S * kHeads + h) * R + 4 * i;
+  const float* base = a.ws_o + ((int64_t)t * S_all * kHeads + h) * R + 4 * i;
+  // Eight partial rows in flight. One code path for every slot count (a slot past S or without work adds an exact
+  // zero through fma(0, 0, acc)), so the result does not depend on how many empty slots are read.
   float den = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  int s = 0;
-  for (; s + 8 <= S; s += 8) {  // eight partial rows in flight
+  for (int s0 = 0; s0 < S; s0 += 8) {
     floatx4 o[8];
     float w[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      o[u] = *reinterpret_cast<const floatx4*>(base + (int64_t)(s + u) * kHeads * R);
-      const float l_s = ls[(int64_t)(s + u) * kHeads];
+      const bool in = s0 + u < S;
+      o[u] = in ? *reinterpret_cast<const floatx4*>(base + (int64_t)(s0 + u) * kHeads * R) : floatx4{0.f, 0.f, 0.f, 0.f};
+      const float l_s = in ? ls[(int64_t)(s0 + u) * kHeads] : -INFINITY;
       w[u] = l_s == -INFINITY ? 0.f : __expf(l_s - mx);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       den += w[u];
-      acc += w[u] == 0.f ? floatx4{0.f, 0.f, 0.f, 0.f} : o[u] * w[u];
+      const floatx4 ou = w[u] == 0.f ? floatx4{0.f, 0.f, 0.f, 0.f} : o[u];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(ou[e], w[u], acc[e]);
     }
-  }
-  for (; s < S; ++s) {
-    const float l_s = ls[(int64_t)s * kHeads];
-    if (l_s == -INFINITY) continue;
-    const float w = __expf(l_s - mx);
-    den += w;
-    acc += *reinterpret_cast<const floatx4*>(base + (int64_t)s * kHeads * R) * w;
   }
   acc = acc * (1.0f / den);
   *reinterpret_cast<uint2*>(op) = uint2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
@@ -606,14 +744,14 @@ __global__ __launch_bounds__(R / 4) void history_combine(HistoryParams a) {
 }
 
 // ---- decode epilogue --------------------------------------------------------------------------------------------
-// out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for kEpiTokens tokens of one head per workgroup:
+// out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for TB tokens of one head per workgroup (4, or
+// 1 for small steps so that the split reduction spreads over enough workgroups):
 //   1. o_hist: LSE reduction of the split partials (or the direct bf16 output with one split), rounded to bf16 as the
 //      history op's output is, kept in LDS;
 //   2. the B_t product as a GEMV: wave q sums rows [q*R/4, (q+1)*R/4) of B[h]; lane (g, c) = (lane/16, lane%16)
 //      reads row 4*step + g, output columns [8c, 8c+8) (one 16-byte load: a wave instruction covers 4 whole B rows)
 //      and accumulates TB x 8 outputs; the 16 partials of each output (4 waves x 4 lane groups) are summed in LDS;
 //   3. the merge_states LSE merge with the window partial (invalid rows zeroed), rounded once to bf16.
-constexpr int kEpiTokens = 4;
 
 struct EpilogueParams {
   int T, S;
@@ -630,15 +768,26 @@ struct EpilogueParams {
   int64_t o_st, o_sh;
 };
 
-template <int R>
+// Slots whose lse the epilogue stages in LDS: all of them with one token per workgroup, 256 with four.
+template <int TB>
+constexpr int kEpiSlots = TB == 1 ? kMaxSplits : 256;
+
+template <int R, int TB>
 __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
-  constexpr int TB = kEpiTokens, D = kExactDim, C4 = R / 4;
-  constexpr int IPT = (TB * C4 + kThreads - 1) / kThreads;  // combine items (token, 4 columns) per thread
-  constexpr int NB = R / 16;                                 // B rows per lane in the GEMV
-  constexpr int PB = NB <= 32 ? NB : 0;                      // rows prefetched into registers
+  constexpr int D = kExactDim, C4 = R / 4;
+  constexpr int ITEMS = TB * C4;                               // combine items (token, 4 columns)
+  constexpr int IPT = ITEMS > kThreads ? ITEMS / kThreads : 1;  // items per thread
+  constexpr int SG = ITEMS < kThreads ? kThreads / ITEMS : 1;   // slot groups: threads sharing one item's slots
+  constexpr int NB = R / 16;                                   // B rows per lane in the GEMV
+  constexpr int PB = NB <= 32 ? NB : 0;                        // rows prefetched into registers
+  static_assert(ITEMS % kThreads == 0 || kThreads % ITEMS == 0, "items must tile the workgroup");
   __shared__ float o_s[TB][R];
   __shared__ float lse_s[TB];
   __shared__ floatx4 part[16][TB][D / 4];
+  __shared__ float slot_lse[TB][kEpiSlots<TB>];  // lse of every slot of the TB tokens for head h
+  __shared__ int used_s[TB];
+  __shared__ float merge_m[SG > 1 ? SG : 1][SG > 1 ? ITEMS : 1], merge_d[SG > 1 ? SG : 1][SG > 1 ? ITEMS : 1];
+  __shared__ floatx4 merge_o[SG > 1 ? SG : 1][SG > 1 ? ITEMS : 1];
   const int h = blockIdx.y, t0 = blockIdx.x * TB, tid = threadIdx.x;
   const int S = a.S;
   const int q = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
@@ -649,6 +798,15 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
   //    partials and their lse (an empty split left no partial; a select drops it, so its bytes never matter),
   //    then this lane's B rows for the GEMV; the splits are reduced online in chunks of eight.
   if (S > 1) {
+    // Round one issues, before any wait: the lse of every slot of the TB tokens (into LDS), the first slots'
+    // partials whatever the plan (an unused slot holds lse = -inf and is dropped by a select), and this lane's B
+    // rows. The used slots of a row are a prefix (finite lse), so the LDS copy gives their count; only slots past
+    // the first round wait for it. Thread groups of SG share one item's slots (slot sg, sg + SG, ...).
+    const int sg = SG > 1 ? tid / ITEMS : 0;
+    for (int k = tid; k < TB * S; k += kThreads) {
+      const int tb = k / S, sl = k % S, t = t0 + tb;
+      slot_lse[tb][sl] = t < a.T ? a.ws_lse[((int64_t)t * S + sl) * kHeads + h] : -INFINITY;
+    }
     float m[IPT], den[IPT];
     floatx4 acc[IPT];
 #pragma unroll
@@ -657,26 +815,25 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       den[it] = 0.f;
       acc[it] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    for (int s0 = 0; s0 < S; s0 += 8) {
-      float ls[IPT][8];
-      floatx4 o[IPT][8];
+    float ls[IPT][8];
+    floatx4 o[IPT][8];
+    auto load = [&](int s0, const int (&lim)[IPT]) {  // slots s0 + sg + SG*u, u < 8
 #pragma unroll
       for (int it = 0; it < IPT; ++it) {
-        const int item = tid + it * kThreads, tb = item / C4, c4 = item % C4, t = t0 + tb;
-        const bool ok = item < TB * C4 && t < a.T;
+        const int item = (SG > 1 ? tid % ITEMS : tid) + it * kThreads, tb = item / C4, c4 = item % C4, t = t0 + tb;
+        const bool ok = t < a.T;
         const int64_t row = ((int64_t)t * S) * kHeads + h;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-          const int s = s0 + u;
-          ls[it][u] = ok && s < S ? a.ws_lse[row + (int64_t)s * kHeads] : -INFINITY;
-          o[it][u] = ok && s < S ? *reinterpret_cast<const floatx4*>(a.ws_o + (row + (int64_t)s * kHeads) * R + 4 * c4)
-                                 : floatx4{0.f, 0.f, 0.f, 0.f};
+          const int sl = s0 + sg + SG * u;
+          const bool use = ok && sl < lim[it];
+          ls[it][u] = use ? a.ws_lse[row + (int64_t)sl * kHeads] : -INFINITY;
+          o[it][u] = use ? *reinterpret_cast<const floatx4*>(a.ws_o + (row + (int64_t)sl * kHeads) * R + 4 * c4)
+                         : floatx4{0.f, 0.f, 0.f, 0.f};
         }
       }
-      if (s0 == 0) {
-#pragma unroll
-        for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
-      }
+    };
+    auto reduce = [&]() {  // online LSE combine of the eight loaded slots
 #pragma unroll
       for (int it = 0; it < IPT; ++it) {
         float mx = m[it];
@@ -694,11 +851,64 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
         }
         m[it] = mx;
       }
+    };
+    {
+      int all[IPT];
+#pragma unroll
+      for (int it = 0; it < IPT; ++it) all[it] = S;
+      load(0, all);
+    }
+#pragma unroll
+    for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
+    __syncthreads();
+    if (tid < TB) {
+      int u = 0;
+      while (u < S && slot_lse[tid][u] != -INFINITY) ++u;
+      used_s[tid] = u;
+    }
+    __syncthreads();
+    int used[IPT];
+    int s_end = 0;
+#pragma unroll
+    for (int it = 0; it < IPT; ++it) {
+      const int tb = ((SG > 1 ? tid % ITEMS : tid) + it * kThreads) / C4;
+      used[it] = used_s[tb];
+      s_end = max(s_end, used[it]);
+    }
+    reduce();
+    for (int s0 = 8 * SG; s0 < s_end; s0 += 8 * SG) {
+      load(s0, used);
+      reduce();
+    }
+    if constexpr (SG > 1) {  // merge the slot groups' partial reductions
+      const int item = tid % ITEMS;
+      merge_m[sg][item] = m[0];
+      merge_d[sg][item] = den[0];
+      merge_o[sg][item] = acc[0];
+      __syncthreads();
+      if (sg == 0) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SG; ++k) mx = fmaxf(mx, merge_m[k][item]);
+        float dd = 0.f;
+        floatx4 oo = {0.f, 0.f, 0.f, 0.f};
+        if (mx != -INFINITY) {
+#pragma unroll
+          for (int k = 0; k < SG; ++k) {
+            const float w = merge_m[k][item] == -INFINITY ? 0.f : __expf(merge_m[k][item] - mx);
+            dd += merge_d[k][item] * w;
+            oo += merge_o[k][item] * w;
+          }
+        }
+        m[0] = mx;
+        den[0] = dd;
+        acc[0] = oo;
+      }
     }
 #pragma unroll
     for (int it = 0; it < IPT; ++it) {
       const int item = tid + it * kThreads;
-      if (item >= TB * C4) continue;
+      if (item >= ITEMS) continue;  // slot groups past the first have merged into it
       const int tb = item / C4, c4 = item % C4;
       const floatx4 o = m[it] == -INFINITY ? floatx4{0.f, 0.f, 0.f, 0.f} : acc[it] * (1.0f / den[it]);
 #pragma unroll
@@ -784,14 +994,16 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
 
 template <int R>
 int launch_epilogue(const EpilogueParams& e, hipStream_t stream) {
-  hipLaunchKernelGGL(decode_epilogue<R>, dim3((unsigned)((e.T + kEpiTokens - 1) / kEpiTokens), kHeads), dim3(kThreads),
-                     0, stream, e);
+  if (e.T < 32 || e.S > kEpiSlots<4>)  // small steps: one token per workgroup, 16*T workgroups for the reduction
+    hipLaunchKernelGGL((decode_epilogue<R, 1>), dim3((unsigned)e.T, kHeads), dim3(kThreads), 0, stream, e);
+  else
+    hipLaunchKernelGGL((decode_epilogue<R, 4>), dim3((unsigned)((e.T + 3) / 4), kHeads), dim3(kThreads), 0, stream, e);
   return check_launch("decode_epilogue");
 }
 
 template <int R>
 int launch_combine(const HistoryParams& p, hipStream_t stream) {
-  hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(R / 4), 0, stream, p);
+  hipLaunchKernelGGL(history_combine<R>, dim3(p.T, kHeads), dim3(combine_threads<R>()), 0, stream, p);
   return check_launch("history_combine");
 }
 
@@ -802,7 +1014,7 @@ int launch(const HistoryParams& p, hipStream_t stream) {
     if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
-    const dim3 grid(p.T, p.num_splits);
+    const dim3 grid(split_workgroups(p.T, p.num_splits));
     if (p.shared_rows) hipLaunchKernelGGL((history_split<R, false>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_split<R, true>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   }
@@ -868,6 +1080,7 @@ int fill_history(HistoryParams& p, const void* q, int32_t num_tokens, int32_t nu
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
+  p.plan = nullptr;
   p.group = 1;
   p.shared_rows = false;
   p.direct = num_splits == 1 && !partials_only;
@@ -978,6 +1191,24 @@ extern "C" int hla_s6_history_reduce(const float* workspace, int64_t workspace_f
   return dispatch_combine(p, width, as_stream(stream));
 }
 
+extern "C" int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits) {
+  return num_tokens < 0 || num_splits < 1 ? -1 : hla::plan_ints(num_tokens, num_splits);
+}
+
+extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t cap, int32_t num_splits, int32_t* plan,
+                                 int64_t plan_len, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0 && num_splits >= 1 && num_splits <= kMaxSplits && cap >= 0, HLA_S6_EINVAL,
+              "split_plan: bad token count, slot count or key capacity");
+  if (num_tokens == 0) return HLA_S6_OK;
+  HLA_REQUIRE(ctx && plan, HLA_S6_EINVAL, "split_plan: null pointer argument");
+  HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL, "split_plan: %lld ints, need %lld",
+              (long long)plan_len, (long long)plan_ints(num_tokens, num_splits));
+  hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, as_stream(stream), ctx, num_tokens, cap, num_splits,
+                     plan);
+  return check_launch("split_plan");
+}
+
 extern "C" int hla_s6_attend_decode(
     const void* q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void* lat_k, const void* lat_v,
     int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size, int64_t lat_num_blocks,
@@ -987,8 +1218,8 @@ extern "C" int hla_s6_attend_decode(
     int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
     const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
     int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
-    int32_t num_splits, float* workspace, int64_t workspace_floats, void* o_hist,
-    float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+    int32_t num_splits, float* workspace, int64_t workspace_floats, const int32_t* plan, int64_t plan_len,
+    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
   using namespace hla;
   HistoryParams p;
   int rc = fill_history(p, q_lat, num_tokens, num_heads, width, ql_st, ql_sh, lat_k, lat_v, lat_page_stride,
@@ -1032,6 +1263,12 @@ extern "C" int hla_s6_attend_decode(
                   (reinterpret_cast<uintptr_t>(out) & 3u) == 0 && o_st % 2 == 0 && o_sh % 2 == 0,
               HLA_S6_EINVAL, "attend_decode: B and out need 4-byte aligned pairs");
   hipStream_t st = as_stream(stream);
+  if (plan && num_splits > 1) {
+    HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL,
+                "attend_decode: split plan of %lld ints, need %lld", (long long)plan_len,
+                (long long)plan_ints(num_tokens, num_splits));
+    p.plan = plan;
+  }
   p.combine = false;  // the epilogue reduces the splits
   rc = dispatch(p, width, st);
   if (rc != HLA_S6_OK) return rc;

@@ -105,12 +105,26 @@ class StepContext:
         self.invalid, self.empty = ~self.valid, self.ctx == 0
         self.empty_latent = self.ctx_latent == 0
         self._block_tables = {}
+        self._plans = {}
         if workspace is not None:
             workspace.ensure(device)
 
     def kv_splits(self, width):
         """History split count for a latent of ``width`` columns."""
         return int(self.kv_splits_by_width.get(width, self.num_kv_splits))
+
+    def split_plan(self, splits, cap):
+        """The step's split plan of the latent history (``hla_s6_split_plan``) for ``splits`` slots per row and
+        ``cap`` addressable rows: one small launch per distinct (splits, cap) per step, read by every layer."""
+        key = (int(splits), int(cap))
+        if key not in self._plans:
+            T = self.ctx_latent.shape[0]
+            n = _lib.load().hla_s6_split_plan_ints(T, key[0])
+            plan = torch.empty(max(int(n), 1), dtype=torch.int32, device=self.ctx_latent.device)
+            _lib.call('hla_s6_split_plan', _lib.ptr(self.ctx_latent), T, key[1], key[0], _lib.ptr(plan), plan.numel(),
+                      _lib.stream(plan.device))
+            self._plans[key] = plan
+        return self._plans[key]
 
     def block_table(self, table):
         """Per-token gather of a per-request block table, done once per distinct tensor per step."""
@@ -201,11 +215,12 @@ def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
     lse_win = torch.empty(H, T, dtype=torch.float32, device=dev)
     out = torch.empty(T, H, d, dtype=torch.bfloat16, device=dev)
     splits = ctx.kv_splits(w)
-    ws = None
+    ws = plan = None
     if splits > 1:
         if ctx.workspace is None:
             raise RuntimeError('history attention with num_kv_splits > 1 needs an S6Workspace')
         ws = ctx.workspace.attn_logits(T, H, splits, w, dev)
+        plan = ctx.split_plan(splits, block_table.shape[1] * cache.shape[2])
     _lib.call('hla_s6_attend_decode', _lib.ptr(q_lat), q_lat.stride(0), q_lat.stride(1), w, _lib.ptr(cache),
               _lib.ptr(cache[..., w:]), cache.stride(0), cache.stride(2), cache.shape[2], cache.shape[0],
               _lib.ptr(block_table), block_table.stride(0), block_table.shape[1], _lib.ptr(ctx.token_requests),
@@ -213,7 +228,8 @@ def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
               _lib.ptr(exact[..., d:]), exact.stride(0), exact.stride(2), exact.stride(1), exact.shape[2],
               exact.shape[0], _lib.ptr(ex_table), ex_table.stride(0), ex_table.shape[1], _lib.ptr(qsl), _lib.ptr(seq),
               R, int(ctx.window), _lib.ptr(B), B.stride(0), B.stride(1), _lib.ptr(ctx.invalid), T, H, float(ctx.scale),
-              splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(o_hist),
+              splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(plan), 0 if plan is None else plan.numel(),
+              _lib.ptr(o_hist),
               _lib.ptr(lse_hist), _lib.ptr(o_win), _lib.ptr(lse_win), _lib.ptr(out), out.stride(0), out.stride(1),
               _lib.stream(dev))
     return out

@@ -151,17 +151,18 @@ def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_bloc
 
 
 def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per_cu=8, min_keys_per_split=256):
-    """Split count of the history kernel on MI355X for a ``width``-wide latent. The kernel runs one wave per 128
-    latent columns, so a split of one row is a workgroup of ``width / 128`` waves; the policy aims at
-    ``waves_per_cu`` resident waves per compute unit over the step's rows (8 keeps enough loads in flight to stream
-    HBM on gfx950 for both the 512- and the 256-wide latent) and never cuts splits shorter than
-    ``min_keys_per_split`` keys (each split writes a 16 x width fp32 partial, so short splits turn into workspace
-    traffic). A function of constants and the row count only (graph-stable). The kernel partitions every row in
-    chunks sized from the longest row of the step, so rows of a ragged batch use a number of splits proportional
-    to their length."""
+    """Split slots per row of the history kernel on MI355X for a ``width``-wide latent. The kernel runs one wave per
+    128 latent columns, so a split is a workgroup of ``width / 128`` waves; about ``waves_per_cu`` resident waves per
+    compute unit (8 keeps enough loads in flight to stream HBM on gfx950) make ``W = waves_per_cu * CUs / (width /
+    128)`` busy workgroups. The kernel cuts every row in chunks sized so that about half of the ``num_tokens *
+    slots`` workgroups get equal work whatever the row lengths (short rows use few slots, long rows many), so this
+    returns ``2 * ceil(W / num_tokens)`` slots, never more than two per ``min_keys_per_split`` keys of the longest
+    row (so that filled slots hold at least that many keys) nor 1024. A function of constants and the row count only
+    (graph-stable)."""
     waves_per_split = max(1, width // 128)
-    by_occupancy = -(-waves_per_cu * cu_count // max(1, num_tokens * waves_per_split))
-    by_length = max(1, -(-max_seq_len // min_keys_per_split))
+    busy = -(-waves_per_cu * cu_count // waves_per_split)
+    by_occupancy = 2 * -(-busy // max(1, num_tokens))
+    by_length = max(1, 2 * -(-max_seq_len // min_keys_per_split))
     return max(1, min(by_occupancy, by_length, 1024))
 
 

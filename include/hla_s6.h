@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 1
+#define HLA_S6_ABI_VERSION 2
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -177,6 +177,17 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
                         int32_t num_tokens, int32_t num_heads, int32_t head_dim, int32_t mode, void *out,
                         int64_t o_st, int64_t o_sh, float *lse_out, void *stream);
 
+/* ---- split plan of a step (no reference counterpart: scheduling metadata of the split-KV kernels) -------
+ * The history kernels cut every row of a step in chunks of `chunk` 16-row tiles, one chunk per slot (num_splits
+ * slots per row), chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S))) with tiles = ceil(min(ctx[t],
+ * cap) / 16), and give the chunks to workgroups as one balanced list. hla_s6_split_plan computes that list once
+ * per step (one small launch) into `plan` (int32, hla_s6_split_plan_ints(T, S) entries; caller-owned) so that every
+ * fused decode call of the step reads it instead of deriving it per workgroup. It depends only on ctx, cap and S.
+ * cap = the latent table's columns * block_size. */
+int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits);
+int hla_s6_split_plan(const int32_t *ctx, int32_t num_tokens, int64_t cap, int32_t num_splits, int32_t *plan,
+                      int64_t plan_len, void *stream);
+
 /* ---- a9: fused decode attention of one layer x loop --------------------------------------------------
  * Replaces the decode branch of s6_layer.attend (hla/vllm_latent/s6_layer.py:97-100,110-115):
  * window_attention_fa + history_attention + the B_t einsum + merge_states, in two launches:
@@ -189,7 +200,9 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
  *      rows zeroed).
  * The intermediates o_hist [T, 16, width] bf16, lse_hist [16, T], o_win [T, 16, 128] bf16 and lse_win [16, T]
  * are caller-owned contiguous buffers (they hold the two partial attentions on return). B is [16, width, 128]
- * with strides (b_sh, b_sr, 1). Workspace as for hla_s6_history_attention. */
+ * with strides (b_sh, b_sr, 1). Workspace as for hla_s6_history_attention. `plan` (nullable, plan_len ints) is the
+ * step's hla_s6_split_plan for (ctx_latent, lat_bt_cols * block_size, num_splits); without it each workgroup derives
+ * its share itself. */
 int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void *lat_k,
                          const void *lat_v, int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size,
                          int64_t lat_num_blocks, const int32_t *lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols,
@@ -200,8 +213,9 @@ int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_
                          const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs, int32_t window,
                          const void *B, int64_t b_sh, int64_t b_sr, const uint8_t *invalid, int32_t num_tokens,
                          int32_t num_heads, float scale, int32_t num_splits, float *workspace,
-                         int64_t workspace_floats, void *o_hist, float *lse_hist, void *o_win,
-                         float *lse_win, void *out, int64_t o_st, int64_t o_sh, void *stream);
+                         int64_t workspace_floats, const int32_t *plan, int64_t plan_len, void *o_hist,
+                         float *lse_hist, void *o_win, float *lse_win, void *out, int64_t o_st, int64_t o_sh,
+                         void *stream);
 
 /* ---- a10 (slot-mapped row commit) -----------------------------------------------------------------
  * Slot of each token: block_table[token_requests[t], positions[t] / block_size] * block_size

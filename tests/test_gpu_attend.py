@@ -89,10 +89,12 @@ def test_config1_single_decode(ops, layer):
     assert_attention_close(host_f32(out), want)
 
 
-@pytest.mark.parametrize('splits', [1, 8])
-def test_ragged_batch_all_loops(ops, layer, splits):
-    rng = np.random.default_rng(1 + splits)
-    history = rng.integers(1024, 4096, 8)
+@pytest.mark.parametrize('rows,splits', [(8, 1), (8, 8), (8, 64), (8, 300), (40, 24)])
+def test_ragged_batch_all_loops(ops, layer, rows, splits):
+    """Ragged decode rows (one without history, one with history inside the window only, two padding tokens);
+    slot counts from one to more than the rows' chunks, with one and four tokens per epilogue workgroup."""
+    rng = np.random.default_rng(1 + splits + rows)
+    history = rng.integers(1024, 4096, rows)
     history[2], history[5] = 0, 20                       # no history at all; history inside the window only
     case = DecodeCase(rng, history, pad_tokens=2)
     ctx = case.context(layer, ops, splits)

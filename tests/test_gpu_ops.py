@@ -258,3 +258,49 @@ def test_merge_lse(ops):
     want, want_lse = O.merge_lse(bf16.to_f32(o1), l1, bf16.to_f32(o2), l2)
     assert_attention_close(host_f32(out), want, 'merge_lse')
     assert_lse_close(host_f32(lse), want_lse)
+
+
+def _plan_restated(ctx, cap, S):
+    """The split plan's documented formula in plain Python (an independent restatement for the integer check)."""
+    tiles = [-(-min(int(c), cap) // 16) for c in ctx]
+    T = len(ctx)
+    chunk = max(1, -(-max(tiles) // S), -(-2 * sum(tiles) // (T * S)))
+    used = [-(-t // chunk) for t in tiles]
+    ni = T if S == 1 else T * ((S + 1) // 2 + 1)
+    rows, slots = [-1] * ni, [None] * ni
+    k = 0
+    for r, u in enumerate(used):
+        for c in range(u):
+            rows[k], slots[k] = r, c
+            k += 1
+    return chunk, used, rows, slots
+
+
+@pytest.mark.parametrize('T,S', [(1, 2), (5, 7), (64, 16), (300, 32), (8, 1024), (700, 3)])
+def test_split_plan_is_the_documented_balanced_list(ops, T, S):
+    rng = np.random.default_rng(T * 1000 + S)
+    ctx = rng.integers(0, 20000, T).astype(np.int32)
+    ctx[::7] = 0                                            # rows without history
+    cap = 16 * 1000                                         # rows past the table's reach are not read
+    lib = ops._lib.load()
+    n = lib.hla_s6_split_plan_ints(T, S)
+    plan = torch.full((n,), -7, dtype=torch.int32, device='cuda')
+    ctx_d = dev_i32(ctx)
+    ops._lib.call('hla_s6_split_plan', ctx_d.data_ptr(), T, cap, S, plan.data_ptr(), n, ops._lib.stream())
+    got = plan.cpu().tolist()
+    chunk, used, rows, slots = _plan_restated(ctx, cap, S)
+    ni = len(rows)
+    assert n == 1 + T + 2 * ni
+    assert got[0] == chunk and got[1:1 + T] == used
+    assert got[1 + T:1 + T + ni] == rows
+    assert all(s is None or g == s for g, s in zip(got[1 + T + ni:], slots))
+    assert max(used) <= S                                  # every row fits its slots
+    tiles = [-(-min(int(c), cap) // 16) for c in ctx]
+    assert all(u * chunk >= t > (u - 1) * chunk for u, t in zip(used, tiles) if t)
+
+
+def test_split_plan_rejects_a_short_buffer(ops):
+    plan = torch.empty(3, dtype=torch.int32, device='cuda')
+    ctx = torch.ones(4, dtype=torch.int32, device='cuda')
+    with pytest.raises(ValueError, match='need'):
+        ops._lib.call('hla_s6_split_plan', ctx.data_ptr(), 4, 1024, 8, plan.data_ptr(), plan.numel(), ops._lib.stream())

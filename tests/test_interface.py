@@ -20,7 +20,7 @@ KNOWN = json.load(open(os.path.join(ROOT, 'tests', 'golden', 'known_answers.json
 def header_declarations():
     text = re.sub(r'/\*.*?\*/', '', open(HEADER).read(), flags=re.S)
     decls = {}
-    for m in re.finditer(r'^(?:int|const char \*)\s*(hla_s6_\w+)\s*\(([^)]*)\)\s*;', text, re.M):
+    for m in re.finditer(r'^(?:int|int64_t|const char \*)\s*(hla_s6_\w+)\s*\(([^)]*)\)\s*;', text, re.M):
         params = m.group(2).strip()
         decls[m.group(1)] = 0 if params in ('', 'void') else params.count(',') + 1
     return decls
@@ -60,13 +60,17 @@ def test_num_kv_splits_known_answers(ops, case):
 
 
 def test_mi355x_split_policy(ops):
-    # 8 resident waves per CU: a 512-wide split is a 4-wave workgroup, a 256-wide one 2 waves, a 128-wide one 1 wave
-    assert ops.mi355x_kv_splits(8192, 64, 256, width=512) == 8
-    assert ops.mi355x_kv_splits(8192, 64, 256, width=256) == 16
-    assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 32
-    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 32         # capped by 256-key splits
-    assert ops.mi355x_kv_splits(300, 1, 256) == 2
-    assert ops.mi355x_kv_splits(1, 4096, 256) == 1
+    # 8 resident waves per CU: a 512-wide split is a 4-wave workgroup, a 256-wide one 2 waves, a 128-wide one 1 wave;
+    # twice the busy workgroups in slots, of which the kernel's plan fills about half
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=512) == 16
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=256) == 32
+    assert ops.mi355x_kv_splits(8192, 32, 256, width=512) == 32
+    assert ops.mi355x_kv_splits(32768, 8, 256, width=512) == 128
+    assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 64
+    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 64         # capped by 256-key filled slots
+    assert ops.mi355x_kv_splits(32769, 8, 256, width=256) == 256
+    assert ops.mi355x_kv_splits(300, 1, 256) == 4
+    assert ops.mi355x_kv_splits(1, 4096, 256) == 2
     assert ops.mi355x_kv_splits(10 ** 6, 1, 256, width=128) == 1024    # the kernel's maximum
 
 
