@@ -223,35 +223,56 @@ def history_roofline(wl, iters=50, width=RANK):
     return us, us_reduce, nbytes
 
 
-def cpu_baseline(wl, tokens=8):
-    """The numpy oracle of one main loop and one loop-1 call of a layer on ``tokens`` rows of the same workload,
-    scaled to B rows x (1 + 3) loops: microseconds per layer on the host cores."""
-    from oracle import bf16, s6_oracle as O
+def cpu_baseline(wl, sample=8):
+    """The numpy oracle of one loop-1 call and one main-latent call of layer 0 on a sample of the step's query rows
+    (``sample`` decode rows, or the first ``sample`` query tokens of request 0 in a multi-query step), timed on the
+    host cores (median of 3 after a warm-up) and scaled to the whole step per layer (1 + 3 loops) by latent history
+    rows read, which dominate the oracle's time."""
+    from oracle import s6_oracle as O
     cores = len(os.sched_getaffinity(0))
-    B, n, seq_len = wl.B, wl.n_latent[0], wl.seq[0]      # the decode workload: every row has the same history
+    f32 = lambda t: t.float().cpu().numpy()
+    if wl.Q == 1:
+        rows = list(range(min(sample, wl.B)))
+        tokens = rows
+        qsl = np.arange(len(rows) + 1)
+    else:
+        rows = [0]
+        tokens = list(range(min(sample, wl.Q)))
+        qsl = np.array([0, len(tokens)])
+    n_rows = [wl.n_latent[r] for r in rows]
     timings = {}
     for w in (RANK, RANK1):
-        layer0 = wl.lat[0][w]
-        pages = wl.lat_table[w][:tokens, :-(-n // BLOCK)].long()
-        rows = layer0[pages.reshape(-1), 0].view(tokens, -1, 2 * w)[:, :n]       # [tokens, n, 2w] gathered on GPU
-        rows_h = rows.float().cpu().numpy().reshape(tokens * (rows.shape[1] // BLOCK), 1, BLOCK, 2 * w)
-        table = np.arange(tokens * (rows.shape[1] // BLOCK), dtype=np.int32).reshape(tokens, -1)
-        q = (torch.randn(tokens, HEADS, w, device=wl.device) * w ** -0.5).to(torch.bfloat16).float().cpu().numpy()
-        q_rope = wl.q_rope[1][:tokens].float().cpu().numpy()
         loop = 0 if w == RANK1 else 1
+        lat, table = wl.lat[0][w], wl.lat_table[w]
+        cols = max(1, -(-max(n_rows) // BLOCK))
+        pages = table[rows, :cols].long()                                   # [rows, cols]; 0 past a row's pages
+        lat_h = f32(lat[pages.reshape(-1)]).reshape(len(rows) * cols, 1, BLOCK, 2 * w)
+        lat_table = np.arange(len(rows) * cols, dtype=np.int32).reshape(len(rows), cols)
+        ex_h = f32(wl.exact[0][loop])
+        ex_table = wl.ex_table[loop][rows].cpu().numpy()
         _, Bw, _ = wl.readers[0].readers(loop)
-        Bw = Bw.float().cpu().numpy()
-        ex = wl.exact[0][loop]
-        ex_h = ex.float().cpu().numpy()
-        ex_table = wl.ex_table[loop][:tokens].cpu().numpy()
-        qsl = np.arange(tokens + 1)
-        seq = np.full(tokens, seq_len)
-        ctx_lat = np.full(tokens, n)
+        Bw = f32(Bw)
+        q = f32((torch.randn(len(tokens), HEADS, w, device=wl.device) * w ** -0.5).to(torch.bfloat16))
+        q_rope = f32(wl.q_rope[loop][tokens])
+        invalid = np.zeros(len(tokens), bool)
+        if wl.Q == 1:
+            seq = np.array([wl.seq[r] for r in rows])
 
-        def run():
-            return O.attend_decode(q, q_rope, Bw, rows_h[..., :w], rows_h[..., w:], table, ctx_lat, ex_h[..., :HEAD_DIM],
-                                   ex_h[..., HEAD_DIM:], ex_table, qsl, seq, WINDOW, HEAD_DIM ** -0.5,
-                                   np.zeros(tokens, bool))
+            def run():
+                return O.attend_decode(q, q_rope, Bw, lat_h[..., :w], lat_h[..., w:], lat_table, np.array(n_rows),
+                                       ex_h[..., :HEAD_DIM], ex_h[..., HEAD_DIM:], ex_table, qsl, seq, WINDOW,
+                                       HEAD_DIM ** -0.5, invalid)
+        else:
+            k_rope, v = f32(wl.k_rope[loop][tokens]), f32(wl.v[loop][tokens])
+            n_tok = len(tokens)
+            tabs = {'latent': np.repeat(lat_table, n_tok, 0), 'exact': np.repeat(ex_table, n_tok, 0)}
+            ctx = np.full(n_tok, wl.hist[0])
+            ctx_lat = np.full(n_tok, n_rows[0])
+
+            def run():
+                return O.attend_chunk(q, q_rope, k_rope, v, Bw, lat_h[..., :w], lat_h[..., w:], tabs, ctx, ctx_lat,
+                                      qsl, WINDOW, HEAD_DIM ** -0.5, invalid, ex_h[..., :HEAD_DIM],
+                                      ex_h[..., HEAD_DIM:])
         run()
         reps = []
         for _ in range(3):
@@ -259,12 +280,16 @@ def cpu_baseline(wl, tokens=8):
             run()
             reps.append(time.perf_counter() - t0)
         timings[w] = float(np.median(reps))
-        del rows, rows_h
-    per_layer_s = (timings[RANK1] + 3 * timings[RANK]) * B / tokens
+    sampled = sum(n_rows) * len(tokens) / len(rows)                    # (query row, latent row) pairs sampled
+    total = sum(n * wl.Q for n in wl.n_latent)
+    scale = total / max(sampled, 1)
+    per_layer_s = (timings[RANK1] + 3 * timings[RANK]) * scale
+    what = (f'{len(rows)} of the {wl.B} decode rows' if wl.Q == 1 else
+            f'the first {len(tokens)} query tokens of request 0 ({wl.B} requests x {wl.Q} tokens)')
     return {'value': per_layer_s * 1e6, 'unit': 'us/layer', 'cores': cores, 'kind': 'port',
-            'sample': f'numpy oracle of attend_decode (window + latent history + B_t + merge, fp32) on {tokens} of the '
-                      f'{B} rows, one loop-1 call and one main-latent call of layer 0 (median of 3 after 1 warm-up), '
-                      f'scaled x{B // tokens} rows x (1 + 3) loops; extrapolated'}
+            'sample': f'numpy oracle of s6_layer.attend (fp32 from bf16 inputs) on {what}: one loop-1 call and one '
+                      f'main-latent call of layer 0 (median of 3 after 1 warm-up), scaled x{scale:.1f} by latent '
+                      f'history rows read and x(1 + 3) loops; extrapolated'}
 
 
 def secondary(args, wl, B, context, layers, queries, splits):
@@ -279,7 +304,8 @@ def secondary(args, wl, B, context, layers, queries, splits):
            'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
            'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
            'history_tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
-           'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True}
+           'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True,
+           'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(wl)}
     print(json.dumps(out), flush=True)
 
 
