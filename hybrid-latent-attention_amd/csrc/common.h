@@ -49,6 +49,12 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast
 __device__ __forceinline__ floatx4 mfma16x16x32(u32x4 a, u32x4 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
+// 32x32x16 bf16: lane l supplies A[l%32][8*(l/32) .. +8] and B[8*(l/32) .. +8][l%32]; D[32][32] comes back as
+// d[4j + i] = D[8j + 4*(l/32) + i][l%32], j, i < 4.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ floatx16 mfma32x32x16(u32x4 a, u32x4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
 // 16x16x16 bf16: lane l supplies A[l%16][4*(l/16) .. +4] and B[4*(l/16) .. +4][l%16]; D as above.
 __device__ __forceinline__ floatx4 mfma16x16x16(short4v a, short4v b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);

@@ -690,6 +690,242 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
   }
 }
 
+// ---- multi-query history (chunked prefill) ------------------------------------------------------------------
+// history_mq: one workgroup per (group of 4 consecutive tokens, KV slot): the 64 query rows (4 tokens x 16 heads)
+// of tokens that share a block-table row read every K/V tile once. Four waves split the latent columns (QW = R/4
+// each). Per 32-key tile:
+//   * S^T[32 keys x 32 rows] partials per wave and row block (two blocks of 32 rows) on v_mfma_f32_32x32x16_bf16:
+//     the K fragment (A operand, lane: key l%32, 8 latent columns) comes straight from global memory through the
+//     caches (the rows are shared by the group's tokens and by the request's other groups); Q^T (B operand) stays
+//     in registers for the whole row;
+//   * the four partials meet in LDS; wave w owns 16 rows (token w's 16 heads): it sums their partials, runs the
+//     online softmax (the running maximum is only raised when a tile exceeds it by more than 2^8, so most tiles
+//     need no rescale) and writes P^T in the B-operand layout and the rows' rescale factors to LDS;
+//   * O^T[QW columns x 64 rows] += V^T P^T on v_mfma_f32_32x32x16_bf16: V goes through wave-private LDS and comes
+//     back transposed by ds_read_b64_tr_b16.
+constexpr int kMqTokens = 4;              // tokens per workgroup
+constexpr int kMqRows = 16 * kMqTokens;   // query rows per workgroup
+constexpr int kMqKeys = 32;               // keys per tile
+
+template <int R>
+struct MqGeo {
+  static constexpr int QW = R / 4;                 // latent columns per wave
+  static constexpr int KS = QW / 16;               // 16-column k-steps of S^T per tile
+  static constexpr int CB = QW / 32;               // 32-column blocks of O^T
+  static constexpr int CPR = QW / 8;               // 16-byte chunks per V row (the wave's columns)
+  static constexpr int VLD = kMqKeys * CPR / 64;   // 16-byte V loads per lane per tile
+  static constexpr int VS = QW + 32;               // LDS row stride of the V copy: conflict-free transposed reads
+};
+
+template <int R>
+__global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
+  using G = MqGeo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[4][kMqKeys * G::VS];
+  __shared__ __attribute__((aligned(16))) float sx[4][2][64][20];      // S^T partials (16 floats + pad per lane)
+  __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][2][64];        // P^T B operands [row block][k-step][lane]
+  __shared__ float alpha_s[kMqRows], l_s[kMqRows], m_s[kMqRows];
+  __shared__ int64_t red_lds[8];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hh = lane >> 5;            // MFMA lane coordinates
+  const int own_c = lane & 15, own_j = lane >> 4;       // softmax owner: row own_c of token `wave`, keys 8j..8j+7
+  const int S = a.num_splits, s = blockIdx.y;
+  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
+  const int col0 = wave * G::QW;
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int t_begin = blockIdx.x * kMqTokens, t_end = min(t_begin + kMqTokens, a.T);
+  uint16_t* vs = v_lds[wave];
+
+  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
+    const int64_t row = table_row(a, tp);
+    int te = tp + 1;
+    while (te < t_end && table_row(a, te) == row) ++te;
+    const int count = te - tp;
+    int n[kMqTokens];
+    int n_max = 0;
+#pragma unroll
+    for (int u = 0; u < kMqTokens; ++u) {
+      n[u] = u < count ? (int)min((int64_t)a.ctx[tp + u], cap) : 0;
+      n_max = max(n_max, n[u]);
+    }
+    const int tiles16 = (n_max + kTile - 1) / kTile;
+    const int j0 = S > 1 ? s * chunk : 0;
+    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
+    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);  // keys of this slot
+    const int own_n = min(k1, wave == 0 ? n[0] : wave == 1 ? n[1] : wave == 2 ? n[2] : n[3]);
+
+    float m_own = -INFINITY, l_own = 0.f;
+    floatx16 o[G::CB][2];
+#pragma unroll
+    for (int cb = 0; cb < G::CB; ++cb) o[cb][0] = o[cb][1] = floatx16{};
+    if (k0 < k1) {  // uniform over the workgroup
+      const int32_t* btr = a.bt + row * a.bt_stride;
+      u32x4 qf[2][G::KS];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int tq = tp + min(2 * qb + (l32 >> 4), count - 1);
+        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)(l32 & 15) * a.q_sh + col0 + 8 * hh;
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) qf[qb][ks] = ld16(qp + 16 * ks);
+      }
+      // K fragments of key kt + l32 and this lane's share of the V slice of tile kt; keys past the slot read row
+      // k1 - 1 (K: masked scores; V: zeroed).
+      u32x4 kf[G::KS], vr[G::VLD];
+      auto load_tile_mq = [&](int kt) {
+        {
+          const int key = min(kt + l32, k1 - 1);
+          const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
+          const uint16_t* kp = a.k + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 + 8 * hh;
+#pragma unroll
+          for (int ks = 0; ks < G::KS; ++ks) kf[ks] = ld16(kp + 16 * ks);
+        }
+#pragma unroll
+        for (int it = 0; it < G::VLD; ++it) {
+          const int c = it * 64 + lane, vrow = c / G::CPR;
+          const int key = min(kt + vrow, k1 - 1);
+          const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
+          const u32x4 x = ld16(a.v + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 +
+                               (c % G::CPR) * 8);
+          vr[it] = kt + vrow < k1 ? x : u32x4{0u, 0u, 0u, 0u};
+        }
+      };
+      for (int kt = k0; kt < k1; kt += kMqKeys) {
+        load_tile_mq(kt);
+        floatx16 sacc[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) {
+          sacc[0] = mfma32x32x16(kf[ks], qf[0][ks], sacc[0]);
+          sacc[1] = mfma32x32x16(kf[ks], qf[1][ks], sacc[1]);
+        }
+#pragma unroll
+        for (int it = 0; it < G::VLD; ++it) {
+          const int c = it * 64 + lane;
+          st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, vr[it]);
+        }
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4)
+            *reinterpret_cast<floatx4*>(&sx[wave][qb][lane][4 * q4]) =
+                floatx4{sacc[qb][4 * q4], sacc[qb][4 * q4 + 1], sacc[qb][4 * q4 + 2], sacc[qb][4 * q4 + 3]};
+        __syncthreads();
+        {  // owner softmax: rows 16*(wave&1) + own_c of block wave>>1, keys kt + 8*own_j + e
+          const int qb_o = wave >> 1, rl = 16 * (wave & 1) + own_c;
+          float sc[8];
+          {
+            floatx4 x0 = *reinterpret_cast<const floatx4*>(&sx[0][qb_o][rl][4 * own_j]);
+            floatx4 x1 = *reinterpret_cast<const floatx4*>(&sx[0][qb_o][rl + 32][4 * own_j]);
+#pragma unroll
+            for (int p = 1; p < 4; ++p) {
+              x0 += *reinterpret_cast<const floatx4*>(&sx[p][qb_o][rl][4 * own_j]);
+              x1 += *reinterpret_cast<const floatx4*>(&sx[p][qb_o][rl + 32][4 * own_j]);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              sc[e] = kt + 8 * own_j + e < own_n ? x0[e] * a.scale_log2 : -INFINITY;
+              sc[4 + e] = kt + 8 * own_j + 4 + e < own_n ? x1[e] * a.scale_log2 : -INFINITY;
+            }
+          }
+          float mx = sc[0];
+#pragma unroll
+          for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
+          mx = wave_max16x4(mx);
+          float alpha = 1.f;
+          const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
+          if (__any(raise)) {
+            const float m_new = raise ? mx : m_own;
+            alpha = fast_exp2(m_own - m_new);  // 0 on the first raise (m_own = -inf)
+            l_own *= alpha;
+            m_own = m_new;
+          }
+          const float m_use = m_own == -INFINITY ? 0.f : m_own;
+          float p[8], ps = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            p[e] = fast_exp2(sc[e] - m_use);
+            ps += p[e];
+          }
+          l_own += wave_sum16x4(ps);
+          p_lds[qb_o][own_j >> 1][rl + 32 * (own_j & 1)] =
+              u32x4{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
+          if (own_j == 0) alpha_s[16 * wave + own_c] = alpha;
+        }
+        __syncthreads();
+        {  // rescale O where a row's maximum was raised, then O^T += V^T P^T
+          const float al0 = alpha_s[l32], al1 = alpha_s[32 + l32];
+          if (__any(al0 != 1.f || al1 != 1.f)) {
+#pragma unroll
+            for (int cb = 0; cb < G::CB; ++cb) {
+              o[cb][0] = o[cb][0] * al0;
+              o[cb][1] = o[cb][1] * al1;
+            }
+          }
+          u32x4 pf[2][2];
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) pf[qb][ks] = p_lds[qb][ks][lane];
+          const int g = lane >> 4, i16 = lane & 15;
+#pragma unroll
+          for (int cb = 0; cb < G::CB; ++cb) {
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              // lane i16 of group g: column 32cb + 16(g%2) + i16, keys 16ks + 8(g/2) + e
+              const uint16_t* vp = vs + (16 * ks + 8 * (g >> 1) + (i16 >> 2)) * G::VS + 32 * cb + 16 * (g & 1) +
+                                   4 * (i16 & 3);
+              const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
+              const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                  (__attribute__((address_space(3))) short4v*)(vp + 4 * G::VS));
+              const u32x4 vt = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+                                (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+                                (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+                                (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+              o[cb][0] = mfma32x32x16(vt, pf[0][ks], o[cb][0]);
+              o[cb][1] = mfma32x32x16(vt, pf[1][ks], o[cb][1]);
+            }
+          }
+        }
+      }
+    }
+    if (own_j == 0) {  // owners publish their rows' softmax state
+      l_s[16 * wave + own_c] = l_own;
+      m_s[16 * wave + own_c] = m_own;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = 32 * qb + l32, u = r >> 4, h = r & 15;
+      if (u >= count) continue;
+      const int t = tp + u;
+      const float l = l_s[r];
+      const bool any = l > 0.f;
+      const float inv = any ? 1.0f / l : 0.f;
+      const float lse = any ? (m_s[r] + log2f(l)) * kLn2 : -INFINITY;
+#pragma unroll
+      for (int cb = 0; cb < G::CB; ++cb) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int col = col0 + 32 * cb + 8 * j + 4 * hh;
+          const floatx4 v = {o[cb][qb][4 * j] * inv, o[cb][qb][4 * j + 1] * inv, o[cb][qb][4 * j + 2] * inv,
+                             o[cb][qb][4 * j + 3] * inv};
+          if (a.direct) {
+            *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
+                uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+          } else {
+            *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
+          }
+        }
+      }
+      if (wave == 0 && hh == 0) {
+        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
+      }
+    }
+    __syncthreads();  // the next pass reuses the LDS exchange
+    tp = te;
+  }
+}
+
 // Split reduction: one workgroup per (token, head), thread i < R/4 owns output columns [4i, 4i+4).
 template <int R>
 constexpr int combine_threads() { return R / 4 < 64 ? 64 : R / 4; }
@@ -1011,7 +1247,8 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
+    if (p.group == 4 && R <= 512) hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(256), 0, stream, p);
+    else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
     const dim3 grid(split_workgroups(p.T, p.num_splits));

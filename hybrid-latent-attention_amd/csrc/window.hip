@@ -1,6 +1,6 @@
-// Exact (per-head K/V) attention over short key ranges: the decode sliding window over the exact paged
-// cache, the history-only window of prefill/mixed steps, and the causal current chunk. One wave per
-// (token, head) running exact_row (exact.h).
+// Exact (per-head K/V) attention: the decode sliding window over the exact paged cache and the history-only window
+// of prefill/mixed steps (short key ranges: one wave per (token, head) running exact_row, exact.h), and the causal
+// current chunk (chunk_mfma: sixteen tokens of one head per wave on MFMA).
 #include "exact.h"
 
 namespace hla {
@@ -65,6 +65,118 @@ int launch_exact(const ExactParams& p, hipStream_t stream, const char* what) {
   HLA_REQUIRE(pairs <= (int64_t)1 << 31, HLA_S6_EINVAL, "%s: too many rows", what);
   hipLaunchKernelGGL(exact_attention, dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, stream, p);
   return check_launch(what);
+}
+
+// Causal attention inside each request's chunk: one wave per (16 consecutive tokens, head). The tokens of a wave
+// that belong to one request read that request's keys once, in tiles of 16:
+//   S^T[16 keys x 16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows straight from memory as the A
+//   operand, Q^T in registers), causal mask key <= query, online softmax per query column, and
+//   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x16_bf16 with V^T from a wave-private LDS copy read by
+//   ds_read_b64_tr_b16.
+struct ChunkParams {
+  const uint16_t *q, *k, *v;
+  int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;
+  const int32_t* qsl;
+  int num_reqs, T;
+  float scale_log2;
+  uint16_t* out;
+  int64_t o_st, o_sh;
+  float* lse;  // [H, T]
+};
+
+constexpr int kChunkVS = kExactDim + 16;  // LDS row stride of the V tile (conflict-free transposed reads)
+
+__global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
+  __shared__ __attribute__((aligned(16))) uint16_t vs[16 * kChunkVS];
+  const int lane = threadIdx.x, hq = lane & 15, g = lane >> 4;
+  const int h = blockIdx.y, t_begin = blockIdx.x * 16, t_end = min(t_begin + 16, a.T);
+  const int valid_end = min(t_end, a.qsl[a.num_reqs]);
+  for (int tp = t_begin; tp < t_end;) {
+    int count, kb;
+    if (tp >= valid_end) {  // padding tokens: o = 0, lse = -inf
+      count = t_end - tp;
+      kb = 0;
+    } else {
+      const int r = request_of(a.qsl, a.num_reqs, tp);
+      count = min(valid_end, a.qsl[r + 1]) - tp;
+      kb = a.qsl[r];
+    }
+    const bool live = tp < valid_end;
+    const int ke = live ? tp + count : 0;  // keys [kb, ke): the request's tokens up to the pass's last query
+    const int tq = tp + min(hq, count - 1);   // query of this lane's column
+    u32x4 qb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qb[i] = ld16(a.q + (int64_t)tq * a.q_st + (int64_t)h * a.q_sh + 32 * i + 8 * g);
+    floatx4 oacc[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY, l = 0.f;
+    const int q_pos = tp + hq;  // this column's query token (keys <= q_pos are visible)
+    for (int k0 = kb; k0 < ke; k0 += 16) {
+      u32x4 kA[4], vr[4];
+      {
+        const int key = min(k0 + hq, ke - 1);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kA[i] = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + 32 * i + 8 * g);
+      }
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {  // V rows k0 .. k0+15: chunk c = it*64 + lane is row c/16, piece c%16
+        const int c = it * 64 + lane, row = c >> 4;
+        const int key = min(k0 + row, ke - 1);
+        const u32x4 x = ld16(a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + (c & 15) * 8);
+        vr[it] = k0 + row < ke ? x : u32x4{0u, 0u, 0u, 0u};
+      }
+      floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s = mfma16x16x32(kA[i], qb[i], s);
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int c = it * 64 + lane;
+        st16(vs + (c >> 4) * kChunkVS + (c & 15) * 8, vr[it]);
+      }
+      float sc[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = k0 + 4 * g + r;
+        sc[r] = (key < ke && key <= q_pos && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
+      }
+      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+      mx = wave_max16x4(mx);
+      const float m_new = fmaxf(m, mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a column with no visible key yet keeps its state
+      const float alpha = fast_exp2(m - m_use);
+      float p[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_use);
+      l = l * alpha + wave_sum16x4((p[0] + p[1]) + (p[2] + p[3]));
+      m = m_new;
+      short4v pb;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) pb[r] = (short)f2bf(p[r]);
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        // lane (g, hq) of the A operand: V[4g + e][16nt + hq]; the transposing read takes row 4g + hq/4,
+        // columns 16nt + 4(hq%4) .. +3 in each 16-lane group
+        const uint16_t* vp = vs + (4 * g + (hq >> 2)) * kChunkVS + 16 * nt + 4 * (hq & 3);
+        const short4v va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
+        oacc[nt] = oacc[nt] * alpha;
+        oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
+      }
+    }
+    if (hq < count) {
+      const int t = tp + hq;
+      const bool any = l > 0.f;
+      const float inv = any ? 1.0f / l : 0.f;
+      uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * g;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const floatx4 o = oacc[nt] * inv;
+        *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
+      }
+      if (g == 0) a.lse[(int64_t)h * a.T + t] = any ? (m + log2f(l)) * kLn2 : -INFINITY;
+    }
+    tp += count;
+  }
 }
 
 }  // namespace
@@ -144,27 +256,26 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
                   k_st % 8 == 0 && k_sh % 8 == 0 && v_st % 8 == 0 && v_sh % 8 == 0 && o_st % 8 == 0 &&
                   o_sh % 8 == 0,
               HLA_S6_EINVAL, "chunk_attention: rows must be 16-byte aligned");
-  ExactParams p = {};
+  HLA_REQUIRE((reinterpret_cast<uintptr_t>(out) & 7u) == 0 && o_st % 4 == 0 && o_sh % 4 == 0, HLA_S6_EINVAL,
+              "chunk_attention: output rows must be 8-byte aligned");
+  ChunkParams p = {};
   p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
   p.q_st = q_st;
   p.q_sh = q_sh;
-  p.src.k = static_cast<const uint16_t*>(k);
-  p.src.v = static_cast<const uint16_t*>(v);
-  p.src.paged = false;
-  p.src.k_st = k_st;
-  p.src.k_sh = k_sh;
-  p.src.v_st = v_st;
-  p.src.v_sh = v_sh;
-  p.src.block_size = 1;
-  p.mode = 2;
+  p.k_st = k_st;
+  p.k_sh = k_sh;
+  p.v_st = v_st;
+  p.v_sh = v_sh;
   p.qsl = query_start_loc;
   p.num_reqs = num_reqs;
-  p.scale_log2 = scale * kLog2e;
   p.T = num_tokens;
-  p.H = num_heads;
+  p.scale_log2 = scale * kLog2e;
   p.out = static_cast<uint16_t*>(out);
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
-  return launch_exact(p, as_stream(stream), "chunk_attention");
+  hipLaunchKernelGGL(chunk_mfma, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0, as_stream(stream), p);
+  return check_launch("chunk_attention");
 }

@@ -84,8 +84,10 @@ class StepContext:
         self.positions, self.tables, self.scale, self.backends = positions, tables, scale, backends
         self.workspace, self.num_kv_splits, self.rope_flat = workspace, num_kv_splits, rope_flat
         self.kv_splits_by_width = dict(kv_splits_by_width or {})
-        # query rows per workgroup of the history kernel in multi-query steps (1, 2 or 4)
-        self.history_group = 1
+        # query rows per workgroup of the history kernel: chunked-prefill steps with long chunks serve four tokens
+        # of a request per workgroup (the MFMA multi-query kernel); short chunks keep one token per workgroup, which
+        # gives the GPU more workgroups
+        self.history_group = 4 if (max_query_len or 1) >= 16 else 1
         self.history_needed = True
         self.md_present = query_start_loc is not None
         if not self.md_present:

@@ -136,12 +136,14 @@ def test_latent_query_then_attend_matches_fp32_reference(ops, layer):
         assert_attention_close(host_f32(out), want, f'loop {loop}')
 
 
-def test_prefill_and_mixed_branch(ops, layer):
-    """max_query_len > 1: causal chunk + exact window over history rows [ctx - W, ctx) + latent history."""
-    rng = np.random.default_rng(4)
+@pytest.mark.parametrize('lens,splits', [((6, 1, 3), 1), ((40, 1, 17), 1), ((40, 1, 17), 4)])
+def test_prefill_and_mixed_branch(ops, layer, lens, splits):
+    """max_query_len > 1: causal chunk + exact window over history rows [ctx - W, ctx) + latent history; chunks of
+    16 tokens or more take the multi-query history kernel (four tokens of a request per workgroup)."""
+    rng = np.random.default_rng(4 + sum(lens) + splits)
     w = 512
-    # request 0: prefill of 6 tokens after 900 history rows; request 1: decode after 40; request 2: fresh prompt of 3
-    lens, hist = np.array([6, 1, 3]), np.array([900, 40, 0])
+    # request 0: prefill after 900 history rows; request 1: decode after 40; request 2: fresh prompt
+    lens, hist = np.array(lens), np.array([900, 40, 0])
     qsl = np.concatenate(([0], np.cumsum(lens))).astype(np.int32)
     T = int(qsl[-1]) + 2
     seq = (hist + lens).astype(np.int32)
@@ -157,9 +159,10 @@ def test_prefill_and_mixed_branch(ops, layer):
                          dev_bf16(random_bits(rng, (3, H, D, w))), dev_bf16(np.stack([B] * 3)))
     q_lat = random_bits(rng, (T, H, w), 1 / math.sqrt(w))
     q_rope, k_rope, v = (random_bits(rng, (T, H, D)) for _ in range(3))
-    ws = ops.S6Workspace(H, w, T)
+    ws = ops.S6Workspace(H, w, T * splits)
     ctx = layer.StepContext(dev_i64(positions), dev_i32(qsl), dev_i32(seq), int(lens.max()), T, {}, SCALE,
-                            ops.HIP_BACKENDS, ws, 1, window=W, max_seqlen_k=int(seq.max()))
+                            ops.HIP_BACKENDS, ws, splits, window=W, max_seqlen_k=int(seq.max()))
+    assert ctx.history_group == (4 if lens.max() >= 16 else 1)
     out = layer.attend(sl, 1, dev_bf16(q_lat), dev_bf16(q_rope), dev_bf16(k_rope), dev_bf16(v), dev_bf16(lat),
                        dev_i32(lt), None, None, ctx, (dev_bf16(ex), dev_i32(et)))
     req, valid, c, cl = O.step_context(qsl, seq, T, W)

@@ -207,14 +207,15 @@ def test_window_history(ops, window):
     assert torch.equal(o, o2) and torch.equal(lse, lse2)
 
 
-def test_chunk_attention(ops):
-    rng = np.random.default_rng(9)
+@pytest.mark.parametrize('qsl,T', [((0, 5, 6, 20, 20, 20), 24),        # empty requests, four padding tokens
+                                   ((0, 100, 101, 400, 413), 420)])     # long chunks crossing 16-token blocks
+def test_chunk_attention(ops, qsl, T):
+    rng = np.random.default_rng(9 + T)
     H, d = 16, 128
-    qsl = np.array([0, 5, 6, 20, 20, 20], np.int32)   # mixed: two padded requests, four padding tokens
-    T = 24
+    qsl = np.array(qsl, np.int32)
     q, k, v = (random_bits(rng, (T, H, d)) for _ in range(3))
-    invalid = np.arange(T) >= 20
-    o, lse = ops.chunk_attention(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_i32(qsl), 14,
+    invalid = np.arange(T) >= qsl[-1]
+    o, lse = ops.chunk_attention(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_i32(qsl), int(np.diff(qsl).max()),
                                  torch.as_tensor(invalid, device=CUDA), 1 / math.sqrt(d), 'hip')
     want_o, want_lse = O.chunk_attention(bf16.to_f32(q), bf16.to_f32(k), bf16.to_f32(v), qsl, invalid, 1 / math.sqrt(d))
     assert o.is_contiguous() and lse.is_contiguous() and lse.shape == (H, T)
