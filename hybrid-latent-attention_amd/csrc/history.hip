@@ -692,16 +692,16 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
 
 // ---- multi-query history (chunked prefill) ------------------------------------------------------------------
 // history_mq: one workgroup per (group of 4 consecutive tokens, KV slot): the 64 query rows (4 tokens x 16 heads)
-// of tokens that share a block-table row read every K/V tile once. Four waves split the latent columns (QW = R/4
-// each). Per 32-key tile:
+// of tokens that share a block-table row read every K/V tile once. NW waves (8 from R = 256: two per SIMD) split
+// the latent columns (R/NW each). Per 32-key tile:
 //   * S^T[32 keys x 32 rows] partials per wave and row block (two blocks of 32 rows) on v_mfma_f32_32x32x16_bf16:
 //     the K fragment (A operand, lane: key l%32, 8 latent columns) comes straight from global memory through the
 //     caches (the rows are shared by the group's tokens and by the request's other groups); Q^T (B operand) stays
 //     in registers for the whole row;
-//   * the four partials meet in LDS; wave w owns 16 rows (token w's 16 heads): it sums their partials, runs the
-//     online softmax (the running maximum is only raised when a tile exceeds it by more than 2^8, so most tiles
-//     need no rescale) and writes P^T in the B-operand layout and the rows' rescale factors to LDS;
-//   * O^T[QW columns x 64 rows] += V^T P^T on v_mfma_f32_32x32x16_bf16: V goes through wave-private LDS and comes
+//   * the NW partials meet in LDS; wave w owns 64/NW rows: it sums their partials, runs the online softmax (the
+//     running maximum is only raised when a tile exceeds it by more than 2^8, so most tiles need no rescale) and
+//     writes P^T in the B-operand layout and the rows' rescale factors to LDS;
+//   * O^T[R/NW columns x 64 rows] += V^T P^T on v_mfma_f32_32x32x16_bf16: V goes through wave-private LDS and comes
 //     back transposed by ds_read_b64_tr_b16.
 constexpr int kMqTokens = 4;              // tokens per workgroup
 constexpr int kMqRows = 16 * kMqTokens;   // query rows per workgroup
@@ -709,26 +709,35 @@ constexpr int kMqKeys = 32;               // keys per tile
 
 template <int R>
 struct MqGeo {
-  static constexpr int QW = R / 4;                 // latent columns per wave
-  static constexpr int KS = QW / 16;               // 16-column k-steps of S^T per tile
-  static constexpr int CB = QW / 32;               // 32-column blocks of O^T
-  static constexpr int CPR = QW / 8;               // 16-byte chunks per V row (the wave's columns)
-  static constexpr int VLD = kMqKeys * CPR / 64;   // 16-byte V loads per lane per tile
-  static constexpr int VS = QW + 32;               // LDS row stride of the V copy: conflict-free transposed reads
+  static constexpr int NW = R >= 256 ? 8 : 4;         // waves (two per SIMD from R = 256)
+  static constexpr int QW = R / NW;                   // latent columns per wave
+  static constexpr int KS = QW / 16;                  // 16-column k-steps of S^T per tile
+  static constexpr int CB = QW / 32;                  // 32-column blocks of O^T
+  static constexpr int CPR = QW / 8;                  // 16-byte chunks per V row (the wave's columns)
+  static constexpr int VLD = kMqKeys * CPR / 64;      // 16-byte V loads per lane per tile
+  static constexpr int VS = QW + 32;                  // LDS row stride of the V copy (bf16)
+  static constexpr int KST = QW + 8;                  // LDS row stride of the K copy (conflict-free row reads)
+  static constexpr int RO = kMqRows / NW;             // softmax rows owned per wave
+  static constexpr int KG = 64 / RO;                  // key groups of an owned row (lanes sharing the row)
+  static constexpr int KPL = kMqKeys / KG;            // keys per owner lane (a multiple of 4)
 };
 
 template <int R>
-__global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
+__global__ __launch_bounds__(64 * MqGeo<R>::NW) void history_mq(HistoryParams a) {
   using G = MqGeo<R>;
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[4][kMqKeys * G::VS];
-  __shared__ __attribute__((aligned(16))) float sx[4][2][64][20];      // S^T partials (16 floats + pad per lane)
+  constexpr int NW = G::NW;
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[NW][kMqKeys * G::VS];
+  __shared__ __attribute__((aligned(16))) float sx[NW][2][64][20];     // S^T partials (16 floats + pad per lane)
+  static_assert(kMqKeys * G::KST * 2 <= 2 * 64 * 20 * 4, "the K copy must fit the wave's exchange buffer");
   __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][2][64];        // P^T B operands [row block][k-step][lane]
   __shared__ float alpha_s[kMqRows], l_s[kMqRows], m_s[kMqRows];
-  __shared__ int64_t red_lds[8];
+  __shared__ int64_t red_lds[2 * NW];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5;            // MFMA lane coordinates
-  const int own_c = lane & 15, own_j = lane >> 4;       // softmax owner: row own_c of token `wave`, keys 8j..8j+7
+  const int l32 = lane & 31, hh = lane >> 5;          // MFMA lane coordinates
+  const int own_c = lane % G::RO, own_j = lane / G::RO;  // softmax owner: row RO*wave + own_c, keys KPL*own_j ..
+  const int own_row = G::RO * wave + own_c;           // row of the workgroup (token own_row/16, head own_row%16)
+  const int qb_o = own_row >> 5, rb = own_row & 31;   // its row block and row within the block
   const int S = a.num_splits, s = blockIdx.y;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;
   const int col0 = wave * G::QW;
@@ -752,7 +761,8 @@ __global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
     const int j0 = S > 1 ? s * chunk : 0;
     const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
     const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);  // keys of this slot
-    const int own_n = min(k1, wave == 0 ? n[0] : wave == 1 ? n[1] : wave == 2 ? n[2] : n[3]);
+    const int own_u = own_row >> 4;
+    const int own_n = min(k1, own_u == 0 ? n[0] : own_u == 1 ? n[1] : own_u == 2 ? n[2] : n[3]);
 
     float m_own = -INFINITY, l_own = 0.f;
     floatx16 o[G::CB][2];
@@ -768,39 +778,42 @@ __global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) qf[qb][ks] = ld16(qp + 16 * ks);
       }
-      // K fragments of key kt + l32 and this lane's share of the V slice of tile kt; keys past the slot read row
-      // k1 - 1 (K: masked scores; V: zeroed).
-      u32x4 kf[G::KS], vr[G::VLD];
-      auto load_tile_mq = [&](int kt) {
-        {
-          const int key = min(kt + l32, k1 - 1);
-          const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
-          const uint16_t* kp = a.k + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 + 8 * hh;
-#pragma unroll
-          for (int ks = 0; ks < G::KS; ++ks) kf[ks] = ld16(kp + 16 * ks);
-        }
+      // This lane's share of the K and V slices of a tile, coalesced (chunk c = it*64 + lane: row c / CPR, 16-byte
+      // piece c % CPR); keys past the slot read row k1 - 1 (K: masked scores; V: zeroed). The next tile's slices
+      // are loaded as soon as the current ones are in LDS, so they are in flight during the whole tile. K goes
+      // through the wave's own partial-exchange buffer (free until the partials are written) and comes back in the
+      // A-operand layout (lane: key l32, 8 latent columns).
+      u32x4 kr[G::VLD], vr[G::VLD];
+      auto load_kv = [&](int kt) {
 #pragma unroll
         for (int it = 0; it < G::VLD; ++it) {
           const int c = it * 64 + lane, vrow = c / G::CPR;
           const int key = min(kt + vrow, k1 - 1);
           const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
-          const u32x4 x = ld16(a.v + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 +
-                               (c % G::CPR) * 8);
+          const int64_t off = page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 + (c % G::CPR) * 8;
+          kr[it] = ld16(a.k + off);
+          const u32x4 x = ld16(a.v + off);
           vr[it] = kt + vrow < k1 ? x : u32x4{0u, 0u, 0u, 0u};
         }
       };
+      load_kv(k0);
       for (int kt = k0; kt < k1; kt += kMqKeys) {
-        load_tile_mq(kt);
+        uint16_t* ks_lds = reinterpret_cast<uint16_t*>(&sx[wave][0][0][0]);
+#pragma unroll
+        for (int it = 0; it < G::VLD; ++it) {
+          const int c = it * 64 + lane;
+          st16(ks_lds + (c / G::CPR) * G::KST + (c % G::CPR) * 8, kr[it]);
+          st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, vr[it]);
+        }
+        if (kt + kMqKeys < k1) load_kv(kt + kMqKeys);
+        u32x4 kf[G::KS];
+#pragma unroll
+        for (int ks = 0; ks < G::KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(ks_lds + l32 * G::KST + 16 * ks + 8 * hh);
         floatx16 sacc[2] = {floatx16{}, floatx16{}};
 #pragma unroll
         for (int ks = 0; ks < G::KS; ++ks) {
           sacc[0] = mfma32x32x16(kf[ks], qf[0][ks], sacc[0]);
           sacc[1] = mfma32x32x16(kf[ks], qf[1][ks], sacc[1]);
-        }
-#pragma unroll
-        for (int it = 0; it < G::VLD; ++it) {
-          const int c = it * 64 + lane;
-          st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, vr[it]);
         }
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -809,27 +822,23 @@ __global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
             *reinterpret_cast<floatx4*>(&sx[wave][qb][lane][4 * q4]) =
                 floatx4{sacc[qb][4 * q4], sacc[qb][4 * q4 + 1], sacc[qb][4 * q4 + 2], sacc[qb][4 * q4 + 3]};
         __syncthreads();
-        {  // owner softmax: rows 16*(wave&1) + own_c of block wave>>1, keys kt + 8*own_j + e
-          const int qb_o = wave >> 1, rl = 16 * (wave & 1) + own_c;
-          float sc[8];
-          {
-            floatx4 x0 = *reinterpret_cast<const floatx4*>(&sx[0][qb_o][rl][4 * own_j]);
-            floatx4 x1 = *reinterpret_cast<const floatx4*>(&sx[0][qb_o][rl + 32][4 * own_j]);
+        {  // owner softmax: row rb of block qb_o, keys kt + KPL*own_j + e
+          float sc[G::KPL];
 #pragma unroll
-            for (int p = 1; p < 4; ++p) {
-              x0 += *reinterpret_cast<const floatx4*>(&sx[p][qb_o][rl][4 * own_j]);
-              x1 += *reinterpret_cast<const floatx4*>(&sx[p][qb_o][rl + 32][4 * own_j]);
-            }
+          for (int q = 0; q < G::KPL / 4; ++q) {
+            const int key = G::KPL * own_j + 4 * q;  // D layout: keys 8jj + 4h + i at lane rb + 32h, entries 4jj..
+            const float* src = &sx[0][qb_o][rb + 32 * ((key >> 2) & 1)][4 * (key >> 3)];
+            floatx4 x = *reinterpret_cast<const floatx4*>(src);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              sc[e] = kt + 8 * own_j + e < own_n ? x0[e] * a.scale_log2 : -INFINITY;
-              sc[4 + e] = kt + 8 * own_j + 4 + e < own_n ? x1[e] * a.scale_log2 : -INFINITY;
-            }
+            for (int p = 1; p < NW; ++p) x += *reinterpret_cast<const floatx4*>(src + p * (2 * 64 * 20));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sc[4 * q + e] = kt + key + e < own_n ? x[e] * a.scale_log2 : -INFINITY;
           }
           float mx = sc[0];
 #pragma unroll
-          for (int e = 1; e < 8; ++e) mx = fmaxf(mx, sc[e]);
-          mx = wave_max16x4(mx);
+          for (int e = 1; e < G::KPL; ++e) mx = fmaxf(mx, sc[e]);
+#pragma unroll
+          for (int off = G::RO; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
           float alpha = 1.f;
           const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
@@ -839,16 +848,22 @@ __global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
             m_own = m_new;
           }
           const float m_use = m_own == -INFINITY ? 0.f : m_own;
-          float p[8], ps = 0.f;
+          float p[G::KPL], ps = 0.f;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
+          for (int e = 0; e < G::KPL; ++e) {
             p[e] = fast_exp2(sc[e] - m_use);
             ps += p[e];
           }
-          l_own += wave_sum16x4(ps);
-          p_lds[qb_o][own_j >> 1][rl + 32 * (own_j & 1)] =
-              u32x4{pack2(p[0], p[1]), pack2(p[2], p[3]), pack2(p[4], p[5]), pack2(p[6], p[7])};
-          if (own_j == 0) alpha_s[16 * wave + own_c] = alpha;
+#pragma unroll
+          for (int off = G::RO; off < 64; off <<= 1) ps += __shfl_xor(ps, off);
+          l_own += ps;
+#pragma unroll
+          for (int q = 0; q < G::KPL / 4; ++q) {  // P^T B operand: lane rb + 32*(key/8 % 2), keys key%16 ..
+            const int key = G::KPL * own_j + 4 * q;
+            uint2* dst = reinterpret_cast<uint2*>(&p_lds[qb_o][key >> 4][rb + 32 * ((key >> 3) & 1)]) + ((key >> 2) & 1);
+            *dst = uint2{pack2(p[4 * q], p[4 * q + 1]), pack2(p[4 * q + 2], p[4 * q + 3])};
+          }
+          if (own_j == 0) alpha_s[own_row] = alpha;
         }
         __syncthreads();
         {  // rescale O where a row's maximum was raised, then O^T += V^T P^T
@@ -888,8 +903,8 @@ __global__ __launch_bounds__(256) void history_mq(HistoryParams a) {
       }
     }
     if (own_j == 0) {  // owners publish their rows' softmax state
-      l_s[16 * wave + own_c] = l_own;
-      m_s[16 * wave + own_c] = m_own;
+      l_s[own_row] = l_own;
+      m_s[own_row] = m_own;
     }
     __syncthreads();
 #pragma unroll
@@ -1247,7 +1262,8 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && R <= 512) hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(256), 0, stream, p);
+    if (p.group == 4 && R <= 512)
+      hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
     else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
