@@ -188,8 +188,9 @@ def measured_traffic(path=TRAFFIC_PROFILE):
 
 
 def history_roofline(wl, iters=50, width=RANK):
-    """The dominant kernel of the step, the split-KV history kernel (stage 1 of the history op), launched alone
-    over the main latent of every layer in turn: its average duration from HIP events on the stream it runs on,
+    """The dominant kernel of the step, the split-KV history kernel (stage 1 of the history op, with the step's
+    split plan as in the decode step), launched alone over the main latent of every layer in turn: its average
+    duration from HIP events on the stream it runs on,
     the average duration of the stage-2 reduction likewise, and the algorithmic bytes stage 1 reads (every latent
     K and V row of every token once)."""
     ops = wl.ops
@@ -197,11 +198,12 @@ def history_roofline(wl, iters=50, width=RANK):
     q = torch.randn(wl.B, HEADS, width, device=wl.device).to(torch.bfloat16) * (width ** -0.5)
     caches = [wl.lat[i][width] for i in range(wl.layers)]
     splits = wl.splits[width]
+    plan = ops.split_plan(ctx_lat, wl.lat_table[width].shape[1] * BLOCK, splits) if splits > 1 else None
 
     def stage1(i):
         c = caches[i % len(caches)]
         return ops.history_partials(q, c[..., :width], c[..., width:], wl.lat_table[width], ctx_lat, HEAD_DIM ** -0.5,
-                                    splits, wl.workspace)
+                                    splits, wl.workspace, plan=plan)
 
     def timed(fn):
         for i in range(5):

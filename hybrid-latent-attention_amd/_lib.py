@@ -33,7 +33,7 @@ SIGNATURES = {
     'hla_s6_history_attention_grouped': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I32, I64, P, I64, I32, P, P, F32,
                                          I32, P, I64, P, I64, I64, P, I32, I32, P],
     'hla_s6_history_partials': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I32, I64, P, I64, I32, P, P, F32, I32, P,
-                                I64, P],
+                                I64, P, I64, P],
     'hla_s6_history_reduce': [P, I64, I32, I32, I32, I32, P, I64, I64, P, P],
     'hla_s6_window_attention': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I64, I32, I64, P, I64, I32, P, I32, P, P,
                                 I32, P, I32, F32, P, I64, I64, P, P],

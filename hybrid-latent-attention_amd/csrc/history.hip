@@ -160,8 +160,11 @@ __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_
   return (int)max((int64_t)1, max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
 }
 
-// Workgroups of the split kernel: the plan puts at most T*S/2 + T (row, chunk) items in the list.
-__host__ __device__ inline unsigned split_workgroups(int T, int S) { return S == 1 ? (unsigned)T : (unsigned)T * ((S + 1) / 2 + 1); }
+// Workgroups of the split kernel: the plan puts at most T*S/2 + T (row, chunk) items in the list; a multiple of 8
+// (one share per XCD).
+__host__ __device__ inline unsigned split_workgroups(int T, int S) {
+  return S == 1 ? (unsigned)T : ((unsigned)T * ((S + 1) / 2 + 1) + 7u) / 8u * 8u;
+}
 
 // Work item b of the step's list of (row, slot) pairs, rows in order, each row contributing its used slots:
 // row = -1 past the end of the list. The split kernel gives item b to the workgroup dispatched b-th, so consecutive
@@ -206,7 +209,10 @@ __device__ void find_item(const int32_t* ctx, int T, int64_t cap, int chunk, int
 inline int64_t plan_ints(int T, int S) { return 1 + (int64_t)T + 2 * (int64_t)split_workgroups(T, S); }
 
 // The split plan of a step, computed once by one workgroup and read by every split kernel of the step (every layer
-// and loop with the same lengths and slot count) instead of being derived in each workgroup.
+// and loop with the same lengths and slot count) instead of being derived in each workgroup. The N items, rows in
+// order, are cut in 8 contiguous shares of q = ceil(N/8); item i goes to workgroup (i % q) * 8 + i / q, i.e. share
+// i / q lands on one XCD (workgroups are dealt to the XCDs round-robin), so every XCD gets the same number of
+// items and a row's chunks mostly share an XCD (its query is read from HBM once).
 __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, int S, int32_t* plan) {
   __shared__ int64_t red[8];
   __shared__ int wsum[4];
@@ -222,10 +228,21 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
     carry_s = 0;
   }
   for (int i = tid; i < ni; i += 256) rows[i] = -1;
+  int total = 0;  // items of the step
+  for (int r = tid; r < T; r += 256) {
+    const int u = used_slots(ctx[r], cap, chunk);
+    used[r] = u;
+    total += u;
+  }
+  for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
+  if (lane == 0) wsum[wave] = total;
+  __syncthreads();
+  total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  const int q = (total + 7) / 8;
   __syncthreads();
   for (int r0 = 0; r0 < T; r0 += 256) {  // rows in blocks of 256: exclusive prefix of the used slots
     const int r = r0 + tid;
-    const int u = r < T ? used_slots(ctx[r], cap, chunk) : 0;
+    const int u = r < T ? used[r] : 0;
     int x = u;
     for (int off = 1; off < 64; off <<= 1) {
       const int v = __shfl_up(x, off);
@@ -237,10 +254,10 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
     for (int w = 0; w < wave; ++w) base += wsum[w];
     const int first = base + x - u;
     if (r < T) {
-      used[r] = u;
       for (int c = 0; c < u; ++c) {
-        rows[first + c] = r;
-        slots[first + c] = c;
+        const int i = first + c, b = (i % q) * 8 + i / q;
+        rows[b] = r;
+        slots[b] = c;
       }
     }
     __syncthreads();
@@ -1245,7 +1262,7 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
 
 template <int R>
 int launch_epilogue(const EpilogueParams& e, hipStream_t stream) {
-  if (e.T < 32 || e.S > kEpiSlots<4>)  // small steps: one token per workgroup, 16*T workgroups for the reduction
+  if (e.T < 64 || e.S > kEpiSlots<4>)  // small steps: one token per workgroup, 16*T workgroups for the reduction
     hipLaunchKernelGGL((decode_epilogue<R, 1>), dim3((unsigned)e.T, kHeads), dim3(kThreads), 0, stream, e);
   else
     hipLaunchKernelGGL((decode_epilogue<R, 4>), dim3((unsigned)((e.T + 3) / 4), kHeads), dim3(kThreads), 0, stream, e);
@@ -1403,13 +1420,20 @@ extern "C" int hla_s6_history_partials(const void* q, int32_t num_tokens, int32_
                                        int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
                                        const int32_t* block_table, int64_t bt_stride, int32_t bt_cols,
                                        const int64_t* bt_rows, const int32_t* ctx, float scale, int32_t num_splits,
-                                       float* workspace, int64_t workspace_floats, void* stream) {
+                                       float* workspace, int64_t workspace_floats, const int32_t* plan,
+                                       int64_t plan_len, void* stream) {
   using namespace hla;
   HistoryParams p;
   int rc = fill_history(p, q, num_tokens, num_heads, width, q_st, q_sh, k_cache, v_cache, page_stride, row_stride,
                         block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
                         workspace, workspace_floats, nullptr, 0, 0, nullptr, true);
   if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  if (plan && num_splits > 1) {
+    HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL,
+                "history_partials: split plan of %lld ints, need %lld", (long long)plan_len,
+                (long long)plan_ints(num_tokens, num_splits));
+    p.plan = plan;
+  }
   return dispatch(p, width, as_stream(stream));
 }
 

@@ -120,12 +120,7 @@ class StepContext:
         ``cap`` addressable rows: one small launch per distinct (splits, cap) per step, read by every layer."""
         key = (int(splits), int(cap))
         if key not in self._plans:
-            T = self.ctx_latent.shape[0]
-            n = _lib.load().hla_s6_split_plan_ints(T, key[0])
-            plan = torch.empty(max(int(n), 1), dtype=torch.int32, device=self.ctx_latent.device)
-            _lib.call('hla_s6_split_plan', _lib.ptr(self.ctx_latent), T, key[1], key[0], _lib.ptr(plan), plan.numel(),
-                      _lib.stream(plan.device))
-            self._plans[key] = plan
+            self._plans[key] = s6_ops.split_plan(self.ctx_latent, key[1], key[0])
         return self._plans[key]
 
     def block_table(self, table):

@@ -250,11 +250,12 @@ def history_attention_kv(q, k, v, block_table, ctx, scale, num_kv_splits, worksp
     return o, lse
 
 
-def history_partials(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, bt_rows=None):
+def history_partials(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, bt_rows=None, plan=None):
     """Stage 1 of the history op alone, the split kernel (``hla/vllm_latent/s6_ops.py:186-196``): writes the
     normalized per-split partials and their lse to ``workspace`` for any ``num_kv_splits >= 1`` and returns the
     workspace view ``[T, H, splits, width + 1]`` (its layout is private to the HIP library). Operands and checks as
-    ``history_attention_kv``; ``history_reduce`` completes the op bitwise."""
+    ``history_attention_kv``; ``history_reduce`` completes the op bitwise. ``plan`` is an optional precomputed
+    split plan (``split_plan``)."""
     T, H, L, ctx, rows = _history_operands(q, k, v, block_table, ctx, False, bt_rows)
     splits = int(num_kv_splits)
     if workspace is None:
@@ -263,8 +264,22 @@ def history_partials(q, k, v, block_table, ctx, scale, num_kv_splits, workspace,
     _lib.call('hla_s6_history_partials', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k), _lib.ptr(v),
               k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table), block_table.stride(0),
               block_table.shape[1], _lib.ptr(rows), _lib.ptr(ctx), float(scale), splits, _lib.ptr(ws), ws.numel(),
-              _lib.stream(q.device))
+              _lib.ptr(plan), 0 if plan is None else plan.numel(), _lib.stream(q.device))
     return ws
+
+
+def split_plan(ctx, cap, num_kv_splits):
+    """The split plan of the history kernels for history lengths ``ctx[T]`` (int32), ``cap`` addressable rows per
+    token and ``num_kv_splits`` slots per row (``hla_s6_split_plan``): computed once on the GPU, reusable by every
+    history call of the step with the same lengths."""
+    _dev(ctx)
+    ctx = _int('ctx', ctx, I32)
+    T, splits = ctx.shape[0], int(num_kv_splits)
+    n = _lib.load().hla_s6_split_plan_ints(T, splits)
+    plan = torch.empty(max(int(n), 1), dtype=I32, device=ctx.device)
+    _lib.call('hla_s6_split_plan', _lib.ptr(ctx), T, int(cap), splits, _lib.ptr(plan), plan.numel(),
+              _lib.stream(ctx.device))
+    return plan
 
 
 def history_reduce(partials):

@@ -125,13 +125,14 @@ int hla_s6_history_attention_grouped(const void *q, int32_t num_tokens, int32_t 
  * per-split normalized partials and their lse to `workspace` for every num_splits >= 1 (same
  * arguments and checks as hla_s6_history_attention); hla_s6_history_reduce reads them back and writes
  * o and lse exactly as hla_s6_history_attention does (bitwise: the same kernels). The workspace layout
- * is private to the library: o partials [T][S][16][width] then lse [T][S][16], fp32. */
+ * is private to the library: o partials [T][S][16][width] then lse [T][S][16], fp32. `plan` (nullable) is the
+ * step's hla_s6_split_plan for (ctx, bt_cols * block_size, num_splits), as for hla_s6_attend_decode. */
 int hla_s6_history_partials(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
                             int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
                             int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
                             const int32_t *block_table, int64_t bt_stride, int32_t bt_cols, const int64_t *bt_rows,
                             const int32_t *ctx, float scale, int32_t num_splits, float *workspace,
-                            int64_t workspace_floats, void *stream);
+                            int64_t workspace_floats, const int32_t *plan, int64_t plan_len, void *stream);
 int hla_s6_history_reduce(const float *workspace, int64_t workspace_floats, int32_t num_tokens, int32_t num_heads,
                           int32_t width, int32_t num_splits, void *out, int64_t o_st, int64_t o_sh, float *lse,
                           void *stream);

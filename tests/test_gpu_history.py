@@ -146,6 +146,10 @@ def test_two_stage_history_is_bitwise_the_op(ops, width, splits):
     o, lse = ops.history_reduce(part)
     assert torch.equal(o.view(torch.int16), o_ref.view(torch.int16))
     assert torch.equal(lse, lse_ref)
+    if splits > 1:  # the same work split through a precomputed plan
+        plan = ops.split_plan(c, table.shape[1] * block, splits)
+        o2, lse2 = ops.history_reduce(ops.history_partials(q, k, v, bt, c, SCALE, splits, ws, plan=plan))
+        assert torch.equal(o2.view(torch.int16), o_ref.view(torch.int16)) and torch.equal(lse2, lse_ref)
     check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table, ctx), ctx)
     with pytest.raises(RuntimeError, match='S6Workspace'):
         ops.history_partials(q, k, v, bt, c, SCALE, splits, None)

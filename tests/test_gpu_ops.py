@@ -267,13 +267,15 @@ def _plan_restated(ctx, cap, S):
     T = len(ctx)
     chunk = max(1, -(-max(tiles) // S), -(-2 * sum(tiles) // (T * S)))
     used = [-(-t // chunk) for t in tiles]
-    ni = T if S == 1 else T * ((S + 1) // 2 + 1)
+    ni = T if S == 1 else -(-T * ((S + 1) // 2 + 1) // 8) * 8
     rows, slots = [-1] * ni, [None] * ni
-    k = 0
+    q = -(-sum(used) // 8)                                   # eight contiguous shares, one per XCD
+    i = 0
     for r, u in enumerate(used):
         for c in range(u):
-            rows[k], slots[k] = r, c
-            k += 1
+            b = (i % q) * 8 + i // q
+            rows[b], slots[b] = r, c
+            i += 1
     return chunk, used, rows, slots
 
 
