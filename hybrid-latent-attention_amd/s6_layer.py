@@ -108,6 +108,7 @@ class StepContext:
         self.empty_latent = self.ctx_latent == 0
         self._block_tables = {}
         self._plans = {}
+        self._slots = {}
         if workspace is not None:
             workspace.ensure(device)
 
@@ -122,6 +123,13 @@ class StepContext:
         if key not in self._plans:
             self._plans[key] = s6_ops.split_plan(self.ctx_latent, key[1], key[0])
         return self._plans[key]
+
+    def slots(self, table, block_size):
+        """Commit slot of every token for a per-request block table (``slot_mapping``), once per table per step."""
+        key = (table.data_ptr(), int(block_size))
+        if key not in self._slots:
+            self._slots[key] = slot_mapping(self, table, block_size)
+        return self._slots[key]
 
     def block_table(self, table):
         """Per-token gather of a per-request block table, done once per distinct tensor per step."""
@@ -238,12 +246,75 @@ class WriterState:
     first: torch.Tensor | None = None
 
 
+def _writer_weight(sl, loop):
+    """This loop's candidate projection: the ``[2w, hidden]`` nn.Linear weight and ``w`` (``cand1`` at loop 0,
+    ``cand_s[loop - 1]`` after; ``hla/latent/register.py:37-38``)."""
+    if loop == 0:
+        lin, width = sl.cand1, sl.rank1
+    else:
+        if getattr(sl, 'rank_v', sl.rank) != sl.rank:
+            raise ValueError(f'S6 rows need rank_v == rank (got {sl.rank_v} and {sl.rank})')
+        lin, width = sl.cand_s[loop - 1], sl.rank
+    weight = lin.weight
+    if weight.shape[0] != 2 * width:
+        raise ValueError(f'candidate projection has {weight.shape[0]} outputs, rows are 2 x {width} wide')
+    return weight, width
+
+
+def _write(h, weight, width, prev, reg, slots=None, positions=None, table=None, cache=None):
+    """One ``hla_s6_write_rows`` launch (projection, accumulation and, with ``cache``, the row commit)."""
+    s6_ops._dev(h, weight, prev, reg, cache)
+    s6_ops._bf16('h', h)
+    s6_ops._bf16('candidate weight', weight)
+    T, hidden = h.shape
+    if weight.shape[1] != hidden:
+        raise ValueError(f'candidate weight takes {weight.shape[1]} inputs, h has {hidden}')
+    if prev is not None:
+        s6_ops._bf16('previous register', prev)
+        if tuple(prev.shape) != (T, 2 * width):
+            raise ValueError(f'previous register is {tuple(prev.shape)}, expected {(T, 2 * width)}')
+    geo = (None, 0, 0, 0, 0)
+    if cache is not None:
+        s6_ops._bf16('cache', cache)
+        s6_ops._bf16('rope table', table)
+        if cache.shape[-1] != 2 * width or table.shape[1] != width:
+            raise ValueError(f'cache rows ({cache.shape[-1]}) / RoPE table ({table.shape[1]}) do not fit width {width}')
+        geo = (cache, cache.stride(0), cache.stride(2), cache.shape[2], cache.shape[0])
+        positions = s6_ops._int('positions', positions, torch.int64)
+        slots = s6_ops._int('slots', slots, torch.int64)
+    _lib.call('hla_s6_write_rows', _lib.ptr(h), T, hidden, h.stride(0), _lib.ptr(weight), width, weight.stride(0),
+              _lib.ptr(prev), 0 if prev is None else prev.stride(0), _lib.ptr(reg), 0 if reg is None else reg.stride(0),
+              _lib.ptr(slots), _lib.ptr(positions), _lib.ptr(table), 0 if table is None else table.shape[0],
+              0 if table is None else table.stride(0), _lib.ptr(geo[0]), geo[1], geo[2], geo[3], geo[4],
+              _lib.stream(h.device))
+    return reg
+
+
 def write_rows(sl, loop, h, state=None):
     """Writer accumulation on the attention input ``h[T, hidden]`` of this loop (``LatentLayer.write_step``/``write1``;
-    ``hla/vllm_latent/s6_layer.py:124-132``). Loop 0 produces the loop-1 row ``first``; later loops accumulate ``reg``."""
-    if loop == 0:
-        return WriterState(None, sl.write1(h))
-    return WriterState(sl.write_step(h, loop, state.reg), None)
+    ``hla/vllm_latent/s6_layer.py:124-132``). Loop 0 produces the loop-1 row ``first``; later loops accumulate ``reg``.
+
+    One HIP launch: the candidate projection on MFMA with the bf16 register update in its epilogue."""
+    weight, width = _writer_weight(sl, loop)
+    prev = None if loop == 0 or state is None else state.reg
+    reg = torch.empty(h.shape[0], 2 * width, dtype=h.dtype, device=h.device)
+    _write(h, weight, width, prev, reg)
+    return WriterState(None, reg) if loop == 0 else WriterState(reg, None)
+
+
+def write_commit(sl, loop, h, state, ctx, cache, block_table):
+    """``write_rows`` + ``committed_row`` + the slot-mapped store of ``hla/vllm_latent/ouro_latent.py:127-129`` in ONE
+    launch. At loop 0 and the last loop the committed row goes straight from the projection's epilogue into
+    ``cache`` (``[num_blocks, 1, block, 2w]``; K half latent-rotated, padding tokens skipped) and the returned state
+    holds no row, since nothing reads it again; other loops return the accumulated register as ``write_rows`` does.
+    ``block_table`` is the per-request table of ``cache``."""
+    if loop != 0 and loop != sl.loops - 1:
+        return write_rows(sl, loop, h, state)
+    weight, width = _writer_weight(sl, loop)
+    prev = None if loop == 0 or state is None else state.reg
+    slots = ctx.slots(block_table, cache.shape[2])
+    _write(h, weight, width, prev, None, slots, ctx.positions, ctx.tables[width], cache)
+    return WriterState(None, None)
 
 
 def committed_row(sl, loop, state, ctx):

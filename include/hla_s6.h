@@ -236,6 +236,22 @@ int hla_s6_store_rows(const void *key, int64_t k_st, const void *value, int64_t 
                       int32_t width, const int64_t *slots, void *cache, int64_t page_stride, int64_t row_stride,
                       int32_t block_size, int64_t num_blocks, void *stream);
 
+/* ---- writer (candidate projection, register accumulation, fused row commit) --------------------------
+ * Replaces LatentLayer.write_step / write1 (hla/latent/register.py:45-61) as called by write_rows
+ * (hla/vllm_latent/s6_layer.py:124-132), and, when `cache` is given, also committed_row
+ * (hla/vllm_latent/s6_layer.py:135-147) plus its store (hla/vllm_latent/ouro_latent.py:127-129):
+ *   u = bf16(h[t, :hidden] @ weight[n, :hidden]^T) for n < 2 * width   (nn.Linear, fp32 accumulation)
+ *   r = prev ? bf16(prev[t, n] + u) : u;  reg[t, n] = r  (when reg != NULL; all num_tokens rows)
+ *   cache row at slots[t] <- [RoPE_lat(r[:width]) by rope_table[positions[t]] | r[width:]]  (when cache != NULL;
+ *   negative slots and slots past num_blocks * block_size skipped; rotation per element as latent_rope).
+ * weight is the [2 * width, hidden] nn.Linear weight (w_st elements between rows); hidden must be a multiple
+ * of 512 and width of 16; h and weight rows 16-byte aligned with a unit last stride. One launch. */
+int hla_s6_write_rows(const void *h, int32_t num_tokens, int32_t hidden, int64_t h_st, const void *weight,
+                      int32_t width, int64_t w_st, const void *prev, int64_t prev_st, void *reg, int64_t reg_st,
+                      const int64_t *slots, const int64_t *positions, const void *rope_table, int32_t table_rows,
+                      int64_t table_stride, void *cache, int64_t page_stride, int64_t row_stride,
+                      int32_t block_size, int64_t num_blocks, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -153,6 +153,38 @@ def latent_query(q_pre_rope, A, positions, table, rounding=True):
 
 
 # ----------------------------------------------------------------------------------------------------------------
+# Writer (candidate projection, register accumulation, committed row)
+# ----------------------------------------------------------------------------------------------------------------
+
+def write_step(h, weight, prev=None, dtype=np.float64):
+    """One loop of the writer: ``update = h @ weight.T`` rounded to bf16 (an nn.Linear in bf16), then
+    ``previous + update`` rounded to bf16. Follows ``LatentLayer.write_step`` / ``write1``
+    (``hla/latent/register.py:45-49,60-61``) as ``write_rows`` calls them (``hla/vllm_latent/s6_layer.py:124-132``);
+    ``weight`` is the ``[2w, hidden]`` nn.Linear weight."""
+    update = round_bf16((h.astype(dtype) @ weight.astype(dtype).T).astype(np.float32))
+    return update if prev is None else round_bf16(prev + update)
+
+
+def write_trajectory(h_loops, weights):
+    """The register after every loop (loop 0 adds nothing: ``write_step`` returns zeros there); follows
+    ``LatentLayer.write`` (``hla/latent/register.py:51-58``). ``weights[l - 1]`` is ``cand_s[l - 1].weight``."""
+    reg, rows = None, []
+    for loop, h in enumerate(h_loops):
+        if loop == 0:
+            rows.append(np.zeros((h.shape[0], weights[0].shape[0]), np.float32))
+            continue
+        reg = write_step(h, weights[loop - 1], reg)
+        rows.append(reg)
+    return np.stack(rows)
+
+
+def committed_row(row, width, positions, table):
+    """``(RoPE_lat(row[:, :w]), row[:, w:])``: the key half rotated by the width's table, the value half as is;
+    follows ``hla/vllm_latent/s6_layer.py:135-147`` (rounding as ``latent_rope``)."""
+    return latent_rope(row[:, :width], positions, table), row[:, width:]
+
+
+# ----------------------------------------------------------------------------------------------------------------
 # Attention partials
 # ----------------------------------------------------------------------------------------------------------------
 

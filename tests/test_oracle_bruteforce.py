@@ -259,6 +259,79 @@ def test_absorb_is_batched_gemm():
             np.testing.assert_allclose(out[t, h], x[t, h].astype(np.float64) @ w[h].astype(np.float64), rtol=1e-12)
 
 
+# ---------------------------------------------------------------------------------------------- writer
+
+def test_write_step_is_rounded_linear_plus_rounded_sum():
+    """update[t, n] = bf16(sum_k h[t, k] W[n, k]) by explicit float64 loops; register = bf16(prev + update)."""
+    rng = np.random.default_rng(12)
+    T, hidden, out = 3, 8, 6                 # W is [out, hidden]: a transposed operand cannot even multiply
+    h = bf16.round_bf16(rng.standard_normal((T, hidden)).astype(np.float32))
+    W = bf16.round_bf16(rng.standard_normal((out, hidden)).astype(np.float32))
+    prev = bf16.round_bf16(rng.standard_normal((T, out)).astype(np.float32))
+    u = O.write_step(h, W)
+    r = O.write_step(h, W, prev)
+    for t in range(T):
+        for n in range(out):
+            dot = sum(float(h[t, k]) * float(W[n, k]) for k in range(hidden))
+            want_u = bf16.round_bf16(np.array([dot], np.float32))[0]
+            assert u[t, n] == want_u
+            assert r[t, n] == bf16.round_bf16(np.array([np.float32(prev[t, n]) + np.float32(want_u)], np.float32))[0]
+
+
+def test_write_step_with_a_permutation_weight_selects_columns():
+    rng = np.random.default_rng(13)
+    h = bf16.round_bf16(rng.standard_normal((5, 16)).astype(np.float32))
+    perm = rng.permutation(16)[:12]
+    W = np.zeros((12, 16), np.float32)
+    W[np.arange(12), perm] = 1.0
+    assert (O.write_step(h, W) == h[:, perm]).all()
+
+
+def _teacher_cos_sin(positions, inv):
+    """HF rotary layout: ``cos = cat(cos(p*f), cos(p*f))`` over the head dimension (float32 angle)."""
+    ang = np.asarray(positions, np.float32)[:, None] * inv[None, :]
+    return np.concatenate((np.cos(ang), np.cos(ang)), -1), np.concatenate((np.sin(ang), np.sin(ang)), -1)
+
+
+def _rope_latent(cos, sin, width):
+    idx = np.arange(width // 2) % (cos.shape[-1] // 2)
+    return np.concatenate((cos[..., idx], cos[..., idx]), -1), np.concatenate((sin[..., idx], sin[..., idx]), -1)
+
+
+def test_committed_rows_equal_the_training_pack():
+    """The rows committed at loop 0 and at the last loop equal the fields of the training writer's packed row,
+    whose rotation is built from the teacher's cos/sin, not from the latent table (hla/latent/register.py:23-25,
+    73-85; the equality is what hla/tests/test_s6_serving.py:80-83 asserts)."""
+    rng = np.random.default_rng(14)
+    T, hidden, head_dim, rank, rank1, loops = 4, 32, 16, 24, 12, 4
+    inv = O.latent_inv_freq(head_dim, 1e6)
+    pos = np.array([0, 3, 17, 40])
+    h = [bf16.round_bf16(rng.standard_normal((T, hidden)).astype(np.float32)) for _ in range(loops)]
+    cand = [bf16.round_bf16(rng.standard_normal((2 * rank, hidden)).astype(np.float32) / 6) for _ in range(loops - 1)]
+    cand1 = bf16.round_bf16(rng.standard_normal((2 * rank1, hidden)).astype(np.float32) / 6)
+    # serving order: write1 at loop 0, accumulate from loop 1, commit with the latent tables
+    first = O.write_step(h[0], cand1)
+    reg = O.write_trajectory(h, cand)[-1]
+    l1_key, l1_val = O.committed_row(first, rank1, pos, O.latent_rope_table(64, inv, rank1))
+    key, val = O.committed_row(reg, rank, pos, O.latent_rope_table(64, inv, rank))
+    # training pack (independent rotation tables)
+    cos, sin = _teacher_cos_sin(pos, inv)
+    c, s = _rope_latent(cos, sin, rank)
+    c1, s1 = _rope_latent(cos, sin, rank1)
+    r = bf16.round_bf16
+    packed = np.concatenate((r(r(reg[:, :rank] * c) + r(O.rotate_half(reg[:, :rank]) * s)), reg[:, rank:],
+                             r(r(first[:, :rank1] * c1) + r(O.rotate_half(first[:, :rank1]) * s1)), first[:, rank1:]), -1)
+    assert (np.concatenate((key, val), -1) == packed[:, :2 * rank]).all()
+    assert (np.concatenate((l1_key, l1_val), -1) == packed[:, 2 * rank:]).all()
+    assert (key[0] == reg[0, :rank]).all()             # position 0: cos = 1, sin = 0
+    # the register is the sum of the three loops' updates (loop 0 adds nothing)
+    total = sum(h[l].astype(np.float64) @ cand[l - 1].astype(np.float64).T for l in range(1, loops))
+    assert np.abs(reg - total).max() <= 2 ** -6 * np.abs(total).max()
+    # planted: rotating with the wrong half split fails the equality
+    wrong = O.latent_rope(reg[:, :rank], pos, O.latent_rope_table(64, inv, rank)[:, ::-1].copy())
+    assert not (wrong == packed[:, :rank]).all()
+
+
 def test_bf16_conversions():
     vals = np.array([1.0, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -2.5, 0.0, INF, -INF, 3.0e38], np.float32)
     bits = bf16.from_f32(vals)
