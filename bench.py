@@ -37,7 +37,7 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill'), default='decode',
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer'), default='decode',
                    help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
                         'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
                         'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
@@ -45,6 +45,7 @@ def parse():
     p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 32 / 8 / 4 by workload)')
     p.add_argument('--context', type=int, default=0, help='history tokens before the step (default by workload)')
     p.add_argument('--queries', type=int, default=512, help='new tokens per request of --workload prefill')
+    p.add_argument('--writer-queries', type=int, default=1, help='new tokens per request of --workload writer')
     p.add_argument('--layers', type=int, default=0, help='layers (default: 24 for decode/ragged, 1 otherwise)')
     p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
@@ -311,6 +312,88 @@ def secondary(args, wl, B, context, layers, queries, splits):
     print(json.dumps(out), flush=True)
 
 
+HIDDEN = 2048
+
+
+def writer_workload(args, layer, device):
+    """The writer of a step, per layer: loop 0 projects and commits the loop-1 row, loops 1-2 accumulate the register,
+    loop 3 accumulates and commits the main row (``write_commit``: one launch per loop). ``--batch`` requests of
+    ``--queries`` new tokens each (decode: 1), 24 layers, random-init nn.Linear weights; one JSON line."""
+    import types
+    B = args.batch or 64
+    Q = args.writer_queries
+    T, layers = B * Q, args.layers or LAYERS
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    bf = torch.bfloat16
+
+    def rnd(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=device) * std).to(bf)
+
+    sls = []
+    for _ in range(layers):
+        sl = types.SimpleNamespace(rank=RANK, rank_v=RANK, rank1=RANK1, loops=LOOPS, head_dim=HEAD_DIM)
+        sl.cand1 = types.SimpleNamespace(weight=rnd(2 * RANK1, HIDDEN, std=HIDDEN ** -0.5))
+        sl.cand_s = [types.SimpleNamespace(weight=rnd(2 * RANK, HIDDEN, std=HIDDEN ** -0.5)) for _ in range(LOOPS - 1)]
+        sls.append(sl)
+    hs = [rnd(T, HIDDEN) for _ in range(LOOPS)]
+    seq = torch.full((B,), 8192, dtype=torch.int32, device=device)
+    qsl = torch.arange(0, T + 1, Q, dtype=torch.int32, device=device)
+    positions = (seq.long()[:, None] - Q + torch.arange(Q, device=device)[None]).reshape(-1)
+    pages = (8192 + BLOCK - 1) // BLOCK
+    pool = B * pages + 1
+    table = (1 + torch.randperm(pool - 1, device=device)[:B * pages]).view(B, pages).to(torch.int32)
+    inv = layer.latent_inv_freq(HEAD_DIM, 1e6).to(device)
+    tables = {w: layer.latent_rope_table(MAX_POSITION, inv, w, bf) for w in (RANK, RANK1)}
+    caches = {w: torch.zeros(pool, 1, BLOCK, 2 * w, dtype=bf, device=device) for w in (RANK, RANK1)}
+    ctx = layer.StepContext(positions, qsl, seq, Q, T, tables, HEAD_DIM ** -0.5, layer.s6_ops.HIP_BACKENDS)
+    ctx.slots(table, BLOCK)                                   # the step's slots, computed outside the timed graph
+
+    def step():
+        for sl in sls:
+            state = None
+            for loop in range(LOOPS):
+                state = layer.write_commit(sl, loop, hs[loop], state, ctx, caches[RANK1 if loop == 0 else RANK], table)
+
+    ms = time_graph(step, args.steps, args.warmup)
+    us_layer = ms * 1000 / layers
+    weight_bytes = (2 * RANK1 + 3 * 2 * RANK) * HIDDEN * 2
+    act_bytes = 4 * T * HIDDEN * 2 + T * 2 * RANK * 2 * 4 + T * 2 * (RANK + RANK1) * 2   # h; register; rows
+    nbytes = weight_bytes + act_bytes
+    flops = 2 * T * HIDDEN * (2 * RANK1 + 3 * 2 * RANK)
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import s6_oracle as O
+        f32 = lambda t: t.float().cpu().numpy()
+        W = [f32(sls[0].cand1.weight)] + [f32(w.weight) for w in sls[0].cand_s]
+        H = [f32(h) for h in hs]
+        pos = positions.cpu().numpy()
+        tab_h = {w: f32(t) for w, t in tables.items()}
+
+        def run():
+            first = O.write_step(H[0], W[0], dtype=np.float32)
+            O.committed_row(first, RANK1, pos, tab_h[RANK1])
+            reg = None
+            for loop in range(1, LOOPS):
+                reg = O.write_step(H[loop], W[loop], reg, dtype=np.float32)
+            return O.committed_row(reg, RANK, pos, tab_h[RANK])
+        run()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        base = {'value': round(float(np.median(times)) * 1e6, 1), 'unit': 'us/layer',
+                'cores': len(os.sched_getaffinity(0)), 'kind': 'port',
+                'sample': f'one layer (4 loops) of the writer on all {T} tokens, numpy float32 GEMMs, median of 3'}
+    print(json.dumps({'workload': 'writer', 'value': round(us_layer, 2), 'unit': 'us/layer', 'tokens': T,
+                      'layers': layers, 'launches_per_layer': LOOPS, 'steps': args.steps, 'ms_per_step': round(ms, 4),
+                      'bytes_per_layer': nbytes, 'gbps': round(nbytes / (us_layer * 1e3), 1),
+                      'hbm_frac': round(nbytes / (us_layer * 1e3) / PEAK_HBM_GBPS, 4), 'flops_per_layer': flops,
+                      'tflops': round(flops / (us_layer * 1e6), 2),
+                      'data': 'synthetic (random-init nn.Linear weights and hidden states)', 'hip_graph': True,
+                      'cpu_baseline': base}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get('WORLD_SIZE', '1'))
@@ -333,6 +416,8 @@ def main():
         return
     pkg = importlib.import_module('hybrid-latent-attention_amd')
     ops, layer = pkg.s6_ops, pkg.s6_layer
+    if args.workload == 'writer':
+        return writer_workload(args, layer, device)
     cus = pkg._lib.device_cus(0)
     defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]

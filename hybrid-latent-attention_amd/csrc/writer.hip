@@ -8,9 +8,10 @@
 //
 // W is the nn.Linear weight [2w, hidden] (rows = output columns), so both MFMA operands are k-contiguous and
 // come straight from global memory with 16-byte loads: lane l takes A = h[row l%16][k + 8(l/16) ..] and
-// B = W[column l%16][k + 8(l/16) ..]. A workgroup computes 64 tokens x 16 output columns; its four waves take
-// one quarter of the hidden dimension each (v_mfma_f32_16x16x32_bf16), and the four fp32 partials are summed
-// in LDS in a fixed order. A key-half tile holds 8 rotation pairs (columns c and c + w/2), so each thread of
+// B = W[column l%16][k + 8(l/16) ..]. A workgroup computes 16 or 64 tokens x 16 output columns; its eight waves (four
+// when hidden is not a multiple of 1024) take one slice of the hidden dimension each, with two batches of four
+// v_mfma_f32_16x16x32_bf16 k steps in flight, so every operand byte of a decode step's workgroup is requested at
+// once (the kernel is latency-bound at decode sizes); the per-wave fp32 partials are summed in LDS in a fixed order. A key-half tile holds 8 rotation pairs (columns c and c + w/2), so each thread of
 // the epilogue has both partners of a RoPE pair; value-half tiles hold 16 consecutive columns.
 #include "common.h"
 
@@ -44,52 +45,70 @@ __device__ __forceinline__ int writer_col(int x, int j, int width) {
   return x < key_tiles ? 8 * x + (j & 7) + (j >> 3) * (width / 2) : width + 16 * (x - key_tiles) + j;
 }
 
-__global__ __launch_bounds__(256) void writer_kernel(WriterParams a) {
-  __shared__ float red[4][64][17];
+template <int WAVES, int MT>
+__global__ __launch_bounds__(WAVES * 64) void writer_kernel(WriterParams a) {
+  __shared__ float red[WAVES][16 * MT][17];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, g = lane >> 4;
-  const int x = blockIdx.x, t0 = blockIdx.y * 64;
-  const int kw = a.K / 4, k0 = wave * kw;
+  const int x = blockIdx.x, t0 = blockIdx.y * 16 * MT;
+  const int kw = a.K / WAVES, k0 = wave * kw;
+  const int msub = min(MT, (a.T - t0 + 15) / 16);  // row tiles holding tokens (wave-uniform)
 
   const uint16_t* wrow = a.w + (int64_t)writer_col(x, l16, a.width) * a.w_st + k0 + 8 * g;
-  const uint16_t* hrow[4];
+  const uint16_t* hrow[MT];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) hrow[m] = a.h + (int64_t)min(t0 + 16 * m + l16, a.T - 1) * a.h_st + k0 + 8 * g;
+  for (int m = 0; m < MT; ++m) hrow[m] = a.h + (int64_t)min(t0 + 16 * m + l16, a.T - 1) * a.h_st + k0 + 8 * g;
 
-  floatx4 acc[4];
+  floatx4 acc[MT];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // kw is a multiple of 128: batches of four 32-wide k steps, every load of a batch issued before its MFMAs
-  for (int k = 0; k < kw; k += 128) {
-    u32x4 bv[4], av[4][4];
+  for (int m = 0; m < MT; ++m) acc[m] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // kw is a multiple of 128: batches of four 32-wide k steps, two batches in flight (the second batch's loads
+  // are issued before the first batch's MFMAs)
+  u32x4 b0[4], a0[4][MT], b1[4], a1[4][MT];
+  auto issue = [&](u32x4(&bv)[4], u32x4(&av)[4][MT], int k) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       bv[i] = ld16(wrow + k + 32 * i);
 #pragma unroll
-      for (int m = 0; m < 4; ++m) av[i][m] = ld16(hrow[m] + k + 32 * i);
+      for (int m = 0; m < MT; ++m)
+        if (m < msub) av[i][m] = ld16(hrow[m] + k + 32 * i);
     }
+  };
+  auto compute = [&](const u32x4(&bv)[4], const u32x4(&av)[4][MT]) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) acc[m] = mfma16x16x32(av[i][m], bv[i], acc[m]);
+      for (int m = 0; m < MT; ++m)
+        if (m < msub) acc[m] = mfma16x16x32(av[i][m], bv[i], acc[m]);
+  };
+  issue(b0, a0, 0);
+  for (int k = 0; k < kw; k += 256) {
+    const bool second = k + 128 < kw;
+    if (second) issue(b1, a1, k + 128);
+    compute(b0, a0);
+    if (k + 256 < kw) issue(b0, a0, k + 256);
+    if (second) compute(b1, a1);
   }
   // lane holds D[4g + r][l16] of row tile m: token t0 + 16m + 4g + r, tile column l16
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][16 * m + 4 * g + r][l16] = acc[m][r];
   __syncthreads();
 
   // thread: token t0 + tid/4, tile columns q, q+4, q+8, q+12 (q = tid % 4): two rotation pairs in a key tile
   const int row = tid >> 2, q = tid & 3, t = t0 + row;
-  if (t >= a.T) return;
+  if (row >= 16 * MT || t >= a.T) return;
   float v[4];
   int col[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int j = q + 4 * i;
     col[i] = writer_col(x, j, a.width);
-    float u = rbf(((red[0][row][j] + red[1][row][j]) + red[2][row][j]) + red[3][row][j]);
+    float sum = red[0][row][j];
+#pragma unroll
+    for (int v2 = 1; v2 < WAVES; ++v2) sum += red[v2][row][j];
+    float u = rbf(sum);
     if (a.prev) u = rbf(bf2f(a.prev[(int64_t)t * a.prev_st + col[i]]) + u);
     v[i] = u;
     if (a.reg) a.reg[(int64_t)t * a.reg_st + col[i]] = f2bf(u);
@@ -170,7 +189,22 @@ extern "C" int hla_s6_write_rows(const void* h, int32_t num_tokens, int32_t hidd
   p.T = num_tokens;
   p.K = hidden;
   p.width = width;
-  const dim3 grid((unsigned)(width / 8), (unsigned)((num_tokens + 63) / 64));
-  hipLaunchKernelGGL(writer_kernel, grid, dim3(256), 0, as_stream(stream), p);
+  // up to 128 tokens a workgroup takes 16 of them (more workgroups, fewer operand bytes per CU: the kernel is
+  // latency-bound there); beyond, 64 (each weight tile is then read by fewer workgroups)
+  const bool small = num_tokens <= 128;
+  const int rows = small ? 16 : 64;
+  const dim3 grid((unsigned)(width / 8), (unsigned)((num_tokens + rows - 1) / rows));
+  hipStream_t st = as_stream(stream);
+  if (hidden % 1024 == 0) {
+    if (small)
+      hipLaunchKernelGGL((writer_kernel<8, 1>), grid, dim3(512), 0, st, p);
+    else
+      hipLaunchKernelGGL((writer_kernel<8, 4>), grid, dim3(512), 0, st, p);
+  } else {
+    if (small)
+      hipLaunchKernelGGL((writer_kernel<4, 1>), grid, dim3(256), 0, st, p);
+    else
+      hipLaunchKernelGGL((writer_kernel<4, 4>), grid, dim3(256), 0, st, p);
+  }
   return check_launch("write_rows");
 }

@@ -54,7 +54,7 @@ def assert_projection_close(got, want, update, what, steps=1, magnitude=None):
     assert same >= 0.99, f'{what}: only {same:.4f} of elements bit-identical'
 
 
-@pytest.mark.parametrize('T', [1, 5, 64, 130])
+@pytest.mark.parametrize('T', [1, 5, 64, 128, 130, 600])
 @pytest.mark.parametrize('loop', [0, 1, 2])
 def test_write_rows_matches_the_oracle(T, loop):
     rng = np.random.default_rng(100 + T + loop)
@@ -107,7 +107,7 @@ def test_permutation_weight_makes_the_writer_exact(width):
     assert (host_f32(cache_d).reshape(-1, 2 * width) == want_cache).all()
 
 
-@pytest.mark.parametrize('T', [3, 64, 97])
+@pytest.mark.parametrize('T', [3, 64, 97, 700])
 def test_fused_commit_equals_write_then_commit_then_store(T):
     """``write_commit`` at loop 0 and the last loop stores exactly what ``write_rows`` -> ``committed_row`` ->
     ``store_rows`` store (the reference's sequence in ouro_latent.forward), padding tokens included."""
@@ -120,9 +120,10 @@ def test_fused_commit_equals_write_then_commit_then_store(T):
     seq = rng.integers(20, 300, R).astype(np.int32)
     seq = np.maximum(seq, lens.astype(np.int32))
     positions = np.concatenate([np.arange(s - n, s) for s, n in zip(seq, lens)] + [np.zeros(T - qsl[-1], np.int64)])
-    num_blocks = 2 + R * 20
-    table = (1 + rng.permutation(num_blocks - 1)[:R * 20]).reshape(R, 20).astype(np.int32)
-    max_pos = 512
+    cols = int(-(-seq.max() // BLOCK))
+    num_blocks = 2 + R * cols
+    table = (1 + rng.permutation(num_blocks - 1)[:R * cols]).reshape(R, cols).astype(np.int32)
+    max_pos = 1024
     inv = O.latent_inv_freq(HEAD_DIM, 1e6)
     tables = {w: dev_bf16(bf16.from_f32(O.latent_rope_table(max_pos, inv, w))) for w in (256, 512)}
     ctx = layer.StepContext(dev_i64(positions), dev_i32(qsl), dev_i32(seq), int(lens.max()), T, tables, 1.0,
