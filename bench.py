@@ -37,7 +37,7 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer'), default='decode',
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export'), default='decode',
                    help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
                         'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
                         'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
@@ -394,6 +394,43 @@ def writer_workload(args, layer, device):
                       'cpu_baseline': base}), flush=True)
 
 
+def export_workload(args, pkg, device):
+    """The s6-rollout-cache-v1 export of one finished request of ``--context`` rows (default 8192): the one-launch
+    gather of all 24 layers' main and loop-1 rows through random block lists (timed in a HIP graph: value, GB/s of
+    read + write), then once the whole export (gather, one pinned device-to-host copy, torch.save) to a temporary
+    file, reported beside it. One JSON line."""
+    import tempfile
+    rc = pkg.rollout_cache
+    length, layers = args.context or 8192, args.layers or LAYERS
+    pages = -(-length // BLOCK)
+    pool = 4 * pages + 1
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    caches = [tuple((torch.randn(pool, 1, BLOCK, 2 * w, generator=g, device=device)).to(torch.bfloat16)
+                    for w in (RANK, RANK1)) for _ in range(layers)]
+    blocks = [torch.randperm(pool, generator=g, device=device)[:pages].to(torch.int32) for _ in range(2)]
+    gather = rc.PackedRowGather(caches)
+    rows = torch.empty(layers, length, 2 * (RANK + RANK1), dtype=torch.bfloat16, device=device)
+
+    def step():
+        gather(blocks[0], blocks[1], length, out=rows)
+    ms = time_graph(step, args.steps, args.warmup)
+    nbytes = 2 * layers * length * 2 * (2 * RANK + 2 * RANK1)
+    logits = torch.zeros(1, 1, 16)
+    with tempfile.TemporaryDirectory() as tmp:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        ref = rc.export_request(os.path.join(tmp, '0.pt'), gather, blocks[0], blocks[1], length, version=0,
+                                request_id='bench', cfg=dict(num_layers=layers, rank=RANK, rank_v=RANK, rank1=RANK1),
+                                prompt_ids=[0], first_response_logits=logits)
+        whole = time.perf_counter() - t0
+    print(json.dumps({'workload': 'export', 'value': round(ms * 1000, 2), 'unit': 'us/request (device gather)',
+                      'rows': length, 'layers': layers, 'row_bytes': 2 * (2 * RANK + 2 * RANK1),
+                      'bytes_moved': nbytes, 'gbps': round(nbytes / (ms * 1e6), 1),
+                      'hbm_frac': round(nbytes / (ms * 1e6) / PEAK_HBM_GBPS, 4), 'steps': args.steps,
+                      'whole_export_ms': round(whole * 1000, 1), 'file_bytes': ref['bytes'],
+                      'data': 'synthetic (random caches and block lists)', 'hip_graph': True}), flush=True)
+
+
 def main():
     args = parse()
     world = int(os.environ.get('WORLD_SIZE', '1'))
@@ -418,6 +455,8 @@ def main():
     ops, layer = pkg.s6_ops, pkg.s6_layer
     if args.workload == 'writer':
         return writer_workload(args, layer, device)
+    if args.workload == 'export':
+        return export_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
     defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]

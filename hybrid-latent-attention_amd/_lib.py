@@ -47,6 +47,8 @@ SIGNATURES = {
     'hla_s6_slot_mapping': [P, I64, I32, P, P, P, I32, I32, P, P],
     'hla_s6_store_rows': [P, I64, P, I64, I32, I32, P, P, I64, I64, I32, I64, P],
     'hla_s6_write_rows': [P, I32, I32, I64, P, I32, I64, P, I64, P, I64, P, P, P, I32, I64, P, I64, I64, I32, I64, P],
+    'hla_s6_gather_packed_rows': [P, I32, I64, I64, I32, I64, P, I32, I64, I64, I32, I64, P, I32, I32, P, I64, I64, I32,
+                                  P],
 }
 
 RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64}

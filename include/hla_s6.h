@@ -252,6 +252,22 @@ int hla_s6_write_rows(const void *h, int32_t num_tokens, int32_t hidden, int64_t
                       int64_t table_stride, void *cache, int64_t page_stride, int64_t row_stride,
                       int32_t block_size, int64_t num_blocks, void *stream);
 
+/* ---- rollout cache (s6-rollout-cache-v1 export) ------------------------------------------------------
+ * Replaces the per-layer gather of RolloutCacheExporter.export (hla/vllm_latent/cache_export.py:159-188):
+ * out[l, pos, :] = [main_l[block_main[pos / bs_main], 0, pos % bs_main, :2r] |
+ *                   l1_l[block_l1[pos / bs_l1], 0, pos % bs_l1, :2r1]]  for pos < length, every layer l,
+ * i.e. the packed row layout of hla/latent/register.py:73-79. cache_addrs is a DEVICE array of 2 * num_layers
+ * cache base addresses (main of layer l at 2l, loop-1 at 2l + 1); main_blocks / l1_blocks are the request's
+ * device block lists, at least ceil(length / block_size) long; a block id outside [0, num_blocks) yields a zero
+ * row. vector_ok != 0 promises 16-byte aligned cache bases (16-byte moves are then used when every row width and
+ * stride allows them). One launch. */
+int hla_s6_gather_packed_rows(const int64_t *cache_addrs, int32_t num_layers, int64_t main_page_stride,
+                              int64_t main_row_stride, int32_t main_width, int64_t main_num_blocks,
+                              const int32_t *main_blocks, int32_t main_block_size, int64_t l1_page_stride,
+                              int64_t l1_row_stride, int32_t l1_width, int64_t l1_num_blocks,
+                              const int32_t *l1_blocks, int32_t l1_block_size, int32_t length, void *out,
+                              int64_t out_layer_stride, int64_t out_row_stride, int32_t vector_ok, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
