@@ -37,7 +37,8 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export'), default='decode',
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop'),
+                   default='decode',
                    help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
                         'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
                         'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
@@ -49,7 +50,8 @@ def parse():
     p.add_argument('--layers', type=int, default=0, help='layers (default: 24 for decode/ragged, 1 otherwise)')
     p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
-    p.add_argument('--width', type=int, default=512, choices=(256, 512), help='latent width of --kernel-only')
+    p.add_argument('--width', type=int, default=512, choices=(256, 512),
+                   help='latent width of --kernel-only and --workload khop')
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device copy three times (scales the FETCH_SIZE / WRITE_SIZE counters '
                         'of a PMC profile to bytes)')
@@ -431,6 +433,61 @@ def export_workload(args, pkg, device):
                       'data': 'synthetic (random caches and block lists)', 'hip_graph': True}), flush=True)
 
 
+def khop_workload(args, pkg, device):
+    """Multi-query causal history attention with backward at the reference's operator benchmark shape
+    (hla/latent/benchmark_history_gemm.py:79-101): B = 4, 16 heads, L = 2880 queries and keys, latent width
+    ``--width`` (512 default), valid lengths L, 0.9 L, 0.8 L, 0.7 L, query i sees keys j < i. Times the forward and
+    the forward + backward (dq, dk, dv) in HIP graphs; reports TFLOP/s of the algorithmic work (2 GEMMs forward,
+    7 with the backward, over the visible pairs) against the 2.5 PFLOP/s bf16 peak. One JSON line."""
+    hg = pkg.history_gemm
+    B, L, R = args.batch or 4, args.context or 2880, args.width
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    q = torch.randn(B, L, HEADS, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    k = torch.randn(B, L, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    v = torch.randn(B, L, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    lengths = torch.tensor([max(2, int(L * (1 - 0.1 * i))) for i in range(B)], device=device)
+    valid = torch.arange(L, device=device)[None] < lengths[:, None]
+    order = torch.arange(L, device=device)[:, None] > torch.arange(L, device=device)[None]
+    mask = valid[:, :, None] & valid[:, None, :] & order[None]
+    pairs = int(mask.sum().item())
+    scale = 1 / math.sqrt(HEAD_DIM)
+    dz = torch.randn(B, L, HEADS, R, generator=g, device=device).to(torch.bfloat16)
+    dlse = torch.randn(B, HEADS, L, generator=g, device=device)
+
+    def fwd():
+        with torch.no_grad():
+            hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
+
+    def train():
+        z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
+        torch.autograd.backward([z, lse], [dz, dlse])
+
+    ms_f = time_graph(fwd, args.steps, args.warmup)
+    ms_t = time_eager(train, args.steps, args.warmup)
+    f_fwd, f_all = hg.flops(pairs, HEADS, R), hg.flops(pairs, HEADS, R, with_backward=True)
+    print(json.dumps({'workload': 'khop', 'value': round(ms_t, 3), 'unit': 'ms per forward+backward',
+                      'forward_ms': round(ms_f, 3), 'B': B, 'L': L, 'heads': HEADS, 'width': R,
+                      'visible_pairs': pairs, 'forward_tflops': round(f_fwd / (ms_f * 1e9), 1),
+                      'train_tflops': round(f_all / (ms_t * 1e9), 1),
+                      'forward_mfma_frac': round(f_fwd / (ms_f * 1e9) / PEAK_BF16_TFLOPS, 4),
+                      'train_mfma_frac': round(f_all / (ms_t * 1e9) / PEAK_BF16_TFLOPS, 4), 'steps': args.steps,
+                      'data': 'synthetic (randn q, k, v, cotangents)', 'forward_hip_graph': True}), flush=True)
+
+
+def time_eager(fn, steps, warmup):
+    """Events around ``steps`` eager calls after ``warmup`` (for work that allocates, e.g. autograd backward)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def main():
     args = parse()
     world = int(os.environ.get('WORLD_SIZE', '1'))
@@ -457,6 +514,8 @@ def main():
         return writer_workload(args, layer, device)
     if args.workload == 'export':
         return export_workload(args, pkg, device)
+    if args.workload == 'khop':
+        return khop_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
     defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]

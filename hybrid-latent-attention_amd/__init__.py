@@ -4,8 +4,9 @@
 ``hla/vllm_latent/s6_layer.py``; every op runs hand-written HIP kernels from ``libhla_s6.so`` through the C ABI of
 ``include/hla_s6.h``. The directory name is not a Python identifier: import it with
 ``importlib.import_module('hybrid-latent-attention_amd')`` with the repository root on ``sys.path``.
-``rollout_cache`` writes and reads the ``s6-rollout-cache-v1`` snapshot of a finished request.
+``rollout_cache`` writes and reads the ``s6-rollout-cache-v1`` snapshot of a finished request; ``history_gemm`` is
+the differentiable multi-query history attention of K-hop replay.
 """
-from . import _lib, rollout_cache, s6_layer, s6_ops
+from . import _lib, history_gemm, rollout_cache, s6_layer, s6_ops
 
-__all__ = ['_lib', 'rollout_cache', 's6_layer', 's6_ops']
+__all__ = ['_lib', 'history_gemm', 'rollout_cache', 's6_layer', 's6_ops']

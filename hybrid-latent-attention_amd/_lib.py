@@ -49,6 +49,12 @@ SIGNATURES = {
     'hla_s6_write_rows': [P, I32, I32, I64, P, I32, I64, P, I64, P, I64, P, P, P, I32, I64, P, I64, I64, I32, I64, P],
     'hla_s6_gather_packed_rows': [P, I32, I64, I64, I32, I64, P, I32, I64, I64, I32, I64, P, I32, I32, P, I64, I64, I32,
                                   P],
+    'hla_s6_khop_bounds': [P, I64, I64, I32, I32, I32, P, P],
+    'hla_s6_khop_forward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32, P,
+                            I64, I64, I64, P, P],
+    'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
+                             P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,
+                             I32, P, I64, P],
 }
 
 RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64}

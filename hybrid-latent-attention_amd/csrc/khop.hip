@@ -1,0 +1,685 @@
+// Multi-query latent history attention on contiguous rows with an arbitrary visibility mask, forward and backward
+// (the K-hop replay / training form: hla/latent/history_gemm.py:159-220, hla/latent/fused_history.py:126-153).
+//
+//   q [B, Lq, 16, R], k/v [B, N, R] (rows shared by the 16 heads), mask [B, Lq, N] (nonzero = visible)
+//   z[b,i,h] = softmax_j(scale q.k_j | visible) . v,  lse[b,h,i] (natural log; -inf and z = 0 with no visible key)
+//   backward (P = exp(s - lse), delta = dz.z):  dv = P^T dz,  dS = P (dz.v - delta + dlse) scale,
+//                                               dq = dS k,    dk = dS^T q
+//
+// Every kernel works on steps of 32 query rows (2 tokens x 16 heads) x 32 keys with 8 waves. The operand tiles sit
+// in LDS (row-major, rows padded by 8 elements): score blocks S = Q K^T and dP = dZ V^T are 16 x 16 blocks on
+// v_mfma_f32_16x16x32_bf16 with both operands read as 16-byte rows (k = latent column); the products over keys or
+// rows (P V, dS K, P^T dZ, dS^T Q) take their k-contiguous operand from a small bf16 LDS block and the other one
+// transposed by ds_read_b64_tr_b16, and split the R output columns over the 8 waves. P and dS enter the second
+// products rounded to bf16 (bf16 operands, fp32 accumulation, as the reference's bf16 mode).
+//
+// Each token's key bound (1 + its last visible key, from the mask) limits the key range, so a causal mask costs
+// half the work without a causality promise.
+#include "common.h"
+
+namespace hla {
+namespace {
+
+constexpr int kKhRows = 32;   // query rows per step (2 tokens x 16 heads)
+constexpr int kKhKeys = 32;   // keys per step
+constexpr int kKhThreads = 512;
+constexpr int kKhPS = kKhKeys + 8;  // LDS row stride of the bf16 P / dS blocks
+
+struct KhopParams {
+  const uint16_t* q;
+  int64_t q_sb, q_si, q_sh;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t k_sb, k_sn, v_sb, v_sn;
+  const uint8_t* mask;  // may be null (then every key below the bound is visible)
+  int64_t m_sb, m_si;
+  const int32_t* bound;  // [B * Lq] keys below this are candidates
+  int B, Lq, N;
+  float scale, scale_log2;
+  // forward outputs / backward inputs
+  uint16_t* z;
+  int64_t z_sb, z_si, z_sh;
+  float* lse;  // [B, 16, Lq]
+  const uint16_t* dz;
+  int64_t dz_sb, dz_si, dz_sh;
+  const float* dlse;   // [B, 16, Lq] or null
+  const float* delta;  // [B, 16, Lq]
+  // backward outputs (fp32)
+  float* dq;
+  int64_t dq_sb, dq_si, dq_sh;
+  float* dk;
+  float* dv;
+  int64_t dk_sb, dk_sn, dv_sb, dv_sn;
+  int key_splits;  // dkdv: row ranges per key tile (partials of split s go to dk + s * dk_ss)
+  int64_t dk_ss, dv_ss;
+};
+
+template <int R>
+struct KhGeo {
+  static constexpr int RS = R + 8;            // LDS row stride of the operand tiles (bf16)
+  static constexpr int CPR = R / 8;           // 16-byte pieces per row
+  static constexpr int TL = 32 * CPR / kKhThreads;  // pieces per thread per 32-row tile
+  static constexpr int QW = R / 8;            // output columns per wave
+  static constexpr int CB = QW / 16;          // 16-column blocks per wave
+  static_assert(TL >= 1 && QW >= 16, "R must be at least 128");
+};
+
+__device__ __forceinline__ bool kh_visible(const KhopParams& a, int64_t t, int key) {
+  if (key >= a.bound[t]) return false;
+  if (!a.mask) return true;
+  const int b = (int)(t / a.Lq), i = (int)(t % a.Lq);
+  return a.mask[(int64_t)b * a.m_sb + (int64_t)i * a.m_si + key] != 0;
+}
+
+// Load 32 rows x R of a row-major bf16 matrix into registers (coalesced: piece c = it * 512 + tid is row c / CPR,
+// 16-byte piece c % CPR); rows are addressed by `rowp(r)` (a clamped, in-bounds row pointer).
+template <int R, class RowP>
+__device__ __forceinline__ void kh_load(u32x4 (&reg)[KhGeo<R>::TL], RowP rowp) {
+  using G = KhGeo<R>;
+#pragma unroll
+  for (int it = 0; it < G::TL; ++it) {
+    const int c = it * kKhThreads + threadIdx.x;
+    reg[it] = ld16(rowp(c / G::CPR) + (c % G::CPR) * 8);
+  }
+}
+
+template <int R>
+__device__ __forceinline__ void kh_store(uint16_t* tile, const u32x4 (&reg)[KhGeo<R>::TL]) {
+  using G = KhGeo<R>;
+#pragma unroll
+  for (int it = 0; it < G::TL; ++it) {
+    const int c = it * kKhThreads + threadIdx.x;
+    st16(tile + (c / G::CPR) * G::RS + (c % G::CPR) * 8, reg[it]);
+  }
+}
+
+// 16 x 16 block D[m][n] = sum_c A[16 mb + m][c] * Bt[16 nb + n][c] over c in [c0, c1) of two row-major LDS tiles.
+// Lane l holds D[4 (l / 16) + r][l % 16], r < 4.
+template <int R>
+__device__ __forceinline__ floatx4 kh_block(const uint16_t* A, int mb, const uint16_t* Bt, int nb, int c0, int c1) {
+  using G = KhGeo<R>;
+  const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
+  const uint16_t* ap = A + (16 * mb + l16) * G::RS + 8 * g;
+  const uint16_t* bp = Bt + (16 * nb + l16) * G::RS + 8 * g;
+  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int c = c0; c < c1; c += 32)
+    acc = mfma16x16x32(*reinterpret_cast<const u32x4*>(ap + c), *reinterpret_cast<const u32x4*>(bp + c), acc);
+  return acc;
+}
+
+// Transposed B operand of a 16x16x32 product over 32 rows of a row-major LDS tile: lane (g, i) gets
+// tile[8g + e][c0 + i] for e < 8 (two ds_read_b64_tr_b16, each moving 4 rows of one column per lane).
+template <int R>
+__device__ __forceinline__ u32x4 kh_tr(const uint16_t* tile, int c0) {
+  using G = KhGeo<R>;
+  const int lane = threadIdx.x & 63, j = lane & 15, g = lane >> 4;
+  const uint16_t* p = tile + (8 * g + (j >> 2)) * G::RS + c0 + 4 * (j & 3);
+  const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
+  const short4v hi =
+      __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(p + 4 * G::RS));
+  return u32x4{(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
+               (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
+               (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
+               (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+}
+
+// out[16 mb .. +16][wave columns] += Pb[16 mb + m][k < 32] * T[k][col] (T a row-major LDS tile over 32 rows).
+template <int R>
+__device__ __forceinline__ void kh_accumulate(floatx4 (&acc)[2][KhGeo<R>::CB], const uint16_t* Pb,
+                                              const uint16_t* T) {
+  using G = KhGeo<R>;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
+  u32x4 pa[2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb) pa[mb] = *reinterpret_cast<const u32x4*>(Pb + (16 * mb + l16) * kKhPS + 8 * g);
+#pragma unroll
+  for (int cb = 0; cb < G::CB; ++cb) {
+    const u32x4 tb = kh_tr<R>(T, wave * G::QW + 16 * cb);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) acc[mb][cb] = mfma16x16x32(pa[mb], tb, acc[mb][cb]);
+  }
+}
+
+// ---- forward -------------------------------------------------------------------------------------------------
+// One workgroup per 2 consecutive tokens of a batch row: Q resident in LDS, K/V tiles of 32 keys streamed through
+// LDS (the next tile's loads in flight in registers), online softmax per query row (16 lanes per row).
+template <int R>
+__global__ __launch_bounds__(kKhThreads) void khop_fwd(KhopParams a) {
+  using G = KhGeo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kKhRows * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) floatx4 sx[8][64];
+  __shared__ __attribute__((aligned(16))) uint16_t ps[kKhRows * kKhPS];
+  __shared__ float alpha_s[kKhRows], l_s[kKhRows], m_s[kKhRows];
+  __shared__ int bound_s[2];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int b = blockIdx.y, i0 = blockIdx.x * 2;
+  const int64_t t0 = (int64_t)b * a.Lq + i0;
+  const int ntok = min(2, a.Lq - i0);
+  if (tid < 2) bound_s[tid] = tid < ntok ? min(a.bound[t0 + tid], a.N) : 0;
+  {
+    u32x4 qr[G::TL];
+    kh_load<R>(qr, [&](int r) {
+      const int tok = min(r >> 4, ntok - 1);
+      return a.q + (int64_t)b * a.q_sb + (int64_t)(i0 + tok) * a.q_si + (int64_t)(r & 15) * a.q_sh;
+    });
+    kh_store<R>(qs, qr);
+  }
+  __syncthreads();
+  const int nkeys = max(bound_s[0], bound_s[1]);
+  // softmax role: row sr (token sr / 16, head sr % 16), keys 2 kp, 2 kp + 1
+  const int sr = tid >> 4, kp = tid & 15;
+  const int64_t st = t0 + min(sr >> 4, ntok - 1);
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx4 acc[2][G::CB];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < G::CB; ++cb) acc[mb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 kr[G::TL], vr[G::TL];
+  auto load_kv = [&](int kt) {
+    kh_load<R>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
+    kh_load<R>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
+  };
+  if (nkeys > 0) load_kv(0);
+  for (int kt = 0; kt < nkeys; kt += kKhKeys) {
+    __syncthreads();  // the previous step's readers of ks / vs / ps are done
+    kh_store<R>(ks, kr);
+    kh_store<R>(vs, vr);
+    __syncthreads();
+    if (kt + kKhKeys < nkeys) load_kv(kt + kKhKeys);
+    {  // S partials: wave w -> block w % 4 (rows 16 (w/2 % 2).., keys 16 (w % 2)..), column half w / 4
+      const int blk = wave & 3, half = wave >> 2;
+      sx[wave][lane] = kh_block<R>(qs, blk >> 1, ks, blk & 1, half * (R / 2), (half + 1) * (R / 2));
+    }
+    __syncthreads();
+    {  // online softmax of row sr over keys kt + 2 kp, + 1
+      const int rb = sr >> 4, r4 = sr & 15;
+      float s2[2];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int key = 2 * kp + e, blk = 2 * rb + (key >> 4);
+        const int li = 16 * (r4 >> 2) + (key & 15);
+        const float s = sx[blk][li][r4 & 3] + sx[blk + 4][li][r4 & 3];
+        s2[e] = kh_visible(a, st, kt + key) && (sr >> 4) < ntok ? s * a.scale_log2 : -INFINITY;
+      }
+      float mx = fmaxf(s2[0], s2[1]);
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run - m_new);  // m_run = -inf: alpha = 0
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float p0 = fast_exp2(s2[0] - m_use), p1 = fast_exp2(s2[1] - m_use);
+      float ps_sum = p0 + p1;
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ps_sum += __shfl_xor(ps_sum, off);
+      l_run = l_run * alpha + ps_sum;
+      m_run = m_new;
+      *reinterpret_cast<uint32_t*>(ps + sr * kKhPS + 2 * kp) = pack2(p0, p1);
+      if (kp == 0) alpha_s[sr] = alpha;
+    }
+    __syncthreads();
+    {  // O = alpha O + P V over this wave's columns
+      const int g = lane >> 4;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const floatx4 al = {alpha_s[16 * mb + 4 * g], alpha_s[16 * mb + 4 * g + 1], alpha_s[16 * mb + 4 * g + 2],
+                            alpha_s[16 * mb + 4 * g + 3]};
+#pragma unroll
+        for (int cb = 0; cb < G::CB; ++cb) acc[mb][cb] *= al;
+      }
+      kh_accumulate<R>(acc, ps, vs);
+    }
+  }
+  if (kp == 0) {
+    l_s[sr] = l_run;
+    m_s[sr] = m_run;
+  }
+  __syncthreads();
+  {
+    const int l16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mb + 4 * g + r, tok = row >> 4, h = row & 15;
+        if (tok >= ntok) continue;
+        const float l = l_s[row];
+        const float inv = l > 0.f ? 1.f / l : 0.f;
+        uint16_t* zp = a.z + (int64_t)b * a.z_sb + (int64_t)(i0 + tok) * a.z_si + (int64_t)h * a.z_sh;
+#pragma unroll
+        for (int cb = 0; cb < G::CB; ++cb) zp[wave * G::QW + 16 * cb + l16] = f2bf(acc[mb][cb][r] * inv);
+      }
+    }
+    if (tid < kKhRows && (tid >> 4) < ntok) {
+      const float l = l_s[tid];
+      a.lse[((int64_t)b * 16 + (tid & 15)) * a.Lq + i0 + (tid >> 4)] =
+          l > 0.f ? (m_s[tid] + log2f(l)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+// ---- backward helpers ----------------------------------------------------------------------------------------
+// P and dS of a 32-row x 32-key step from the S blocks (waves 0-3) and dP blocks (waves 4-7) in sx, written as
+// bf16 to pb / dsb in [row][key] order (kTransposed: [key][row]). Row constants of row sr: lse2 (log2 domain),
+// delta - dlse in dd.
+template <bool kTransposed>
+__device__ __forceinline__ void kh_pds(const KhopParams& a, const floatx4 (*sx)[64], uint16_t* pb, uint16_t* dsb,
+                                       int64_t t_row, bool row_ok, int key0, float lse2, float dd) {
+  const int tid = threadIdx.x, sr = tid >> 4, kp = tid & 15;
+  const int rb = sr >> 4, r4 = sr & 15;
+  float p[2], ds[2];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int key = 2 * kp + e, blk = 2 * rb + (key >> 4);
+    const int li = 16 * (r4 >> 2) + (key & 15);
+    const float s = sx[blk][li][r4 & 3], dp = sx[blk + 4][li][r4 & 3];
+    const bool vis = row_ok && kh_visible(a, t_row, key0 + key);
+    p[e] = vis ? fast_exp2(s * a.scale_log2 - lse2) : 0.f;
+    ds[e] = p[e] * (dp - dd) * a.scale;
+  }
+  if (kTransposed) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      pb[(2 * kp + e) * kKhPS + sr] = f2bf(p[e]);
+      dsb[(2 * kp + e) * kKhPS + sr] = f2bf(ds[e]);
+    }
+  } else {
+    *reinterpret_cast<uint32_t*>(pb + sr * kKhPS + 2 * kp) = pack2(p[0], p[1]);
+    *reinterpret_cast<uint32_t*>(dsb + sr * kKhPS + 2 * kp) = pack2(ds[0], ds[1]);
+  }
+}
+
+// Row constants of a query row: lse in the log2 domain (0 for a row without history: all its P are 0 anyway) and
+// delta - dlse.
+__device__ __forceinline__ void kh_row_consts(const KhopParams& a, int b, int i, int h, float& lse2, float& dd) {
+  const int64_t idx = ((int64_t)b * 16 + h) * a.Lq + i;
+  const float lse = a.lse[idx];
+  const bool empty = !(lse > -INFINITY);
+  lse2 = empty ? 0.f : lse * kLog2e;
+  dd = a.delta[idx] - (a.dlse && !empty ? a.dlse[idx] : 0.f);
+}
+
+// ---- backward: dq ----------------------------------------------------------------------------------------------
+template <int R>
+__global__ __launch_bounds__(kKhThreads) void khop_dq(KhopParams a) {
+  using G = KhGeo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kKhRows * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t dzs[kKhRows * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) floatx4 sx[8][64];
+  __shared__ __attribute__((aligned(16))) uint16_t pb[kKhRows * kKhPS];
+  __shared__ __attribute__((aligned(16))) uint16_t dsb[kKhRows * kKhPS];
+  __shared__ int bound_s[2];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int b = blockIdx.y, i0 = blockIdx.x * 2;
+  const int64_t t0 = (int64_t)b * a.Lq + i0;
+  const int ntok = min(2, a.Lq - i0);
+  if (tid < 2) bound_s[tid] = tid < ntok ? min(a.bound[t0 + tid], a.N) : 0;
+  {
+    u32x4 r0[G::TL];
+    kh_load<R>(r0, [&](int r) {
+      const int tok = min(r >> 4, ntok - 1);
+      return a.q + (int64_t)b * a.q_sb + (int64_t)(i0 + tok) * a.q_si + (int64_t)(r & 15) * a.q_sh;
+    });
+    kh_store<R>(qs, r0);
+    kh_load<R>(r0, [&](int r) {
+      const int tok = min(r >> 4, ntok - 1);
+      return a.dz + (int64_t)b * a.dz_sb + (int64_t)(i0 + tok) * a.dz_si + (int64_t)(r & 15) * a.dz_sh;
+    });
+    kh_store<R>(dzs, r0);
+  }
+  __syncthreads();
+  const int nkeys = max(bound_s[0], bound_s[1]);
+  const int sr = tid >> 4;
+  const bool row_ok = (sr >> 4) < ntok;
+  const int64_t st = t0 + min(sr >> 4, ntok - 1);
+  float lse2, dd;
+  kh_row_consts(a, b, i0 + min(sr >> 4, ntok - 1), sr & 15, lse2, dd);
+  floatx4 acc[2][G::CB];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < G::CB; ++cb) acc[mb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  u32x4 kr[G::TL], vr[G::TL];
+  auto load_kv = [&](int kt) {
+    kh_load<R>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
+    kh_load<R>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
+  };
+  if (nkeys > 0) load_kv(0);
+  for (int kt = 0; kt < nkeys; kt += kKhKeys) {
+    __syncthreads();
+    kh_store<R>(ks, kr);
+    kh_store<R>(vs, vr);
+    __syncthreads();
+    if (kt + kKhKeys < nkeys) load_kv(kt + kKhKeys);
+    {  // waves 0-3: S block w; waves 4-7: dP block w - 4 (full R)
+      const int blk = wave & 3;
+      sx[wave][lane] = wave < 4 ? kh_block<R>(qs, blk >> 1, ks, blk & 1, 0, R)
+                                : kh_block<R>(dzs, blk >> 1, vs, blk & 1, 0, R);
+    }
+    __syncthreads();
+    kh_pds<false>(a, sx, pb, dsb, st, row_ok, kt, lse2, dd);
+    __syncthreads();
+    kh_accumulate<R>(acc, dsb, ks);  // dQ += dS K
+  }
+  {
+    const int l16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * mb + 4 * g + r, tok = row >> 4, h = row & 15;
+        if (tok >= ntok) continue;
+        float* dqp = a.dq + (int64_t)b * a.dq_sb + (int64_t)(i0 + tok) * a.dq_si + (int64_t)h * a.dq_sh;
+#pragma unroll
+        for (int cb = 0; cb < G::CB; ++cb) dqp[wave * G::QW + 16 * cb + l16] = acc[mb][cb][r];
+      }
+  }
+}
+
+// ---- backward: dk, dv ----------------------------------------------------------------------------------------
+// One workgroup per (32-key tile of a batch row, row split): K/V tile resident in LDS, the query rows of the split
+// streamed in steps of 2 tokens (Q and dZ through LDS, the next step's loads in flight in registers); steps whose
+// tokens cannot see the tile are skipped.
+template <int R>
+__global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
+  using G = KhGeo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t qs[kKhRows * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t dzs[kKhRows * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t ks[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[kKhKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) floatx4 sx[8][64];
+  __shared__ __attribute__((aligned(16))) uint16_t pt[kKhKeys * kKhPS];
+  __shared__ __attribute__((aligned(16))) uint16_t dst[kKhKeys * kKhPS];
+  __shared__ int skip_s;
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int b = blockIdx.y, kt = blockIdx.x * kKhKeys, split = blockIdx.z;
+  const int steps = (a.Lq + 1) / 2;
+  const int per = (steps + a.key_splits - 1) / a.key_splits;
+  const int s_begin = split * per, s_end = min(steps, s_begin + per);
+  {
+    u32x4 r0[G::TL];
+    kh_load<R>(r0, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
+    kh_store<R>(ks, r0);
+    kh_load<R>(r0, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
+    kh_store<R>(vs, r0);
+  }
+  floatx4 dk_acc[2][G::CB], dv_acc[2][G::CB];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int cb = 0; cb < G::CB; ++cb) dk_acc[mb][cb] = dv_acc[mb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int sr = tid >> 4;
+  u32x4 qr[G::TL], dzr[G::TL];
+  auto load_rows = [&](int step) {
+    const int i0 = 2 * step, ntok = min(2, a.Lq - i0);
+    kh_load<R>(qr, [&](int r) {
+      const int tok = min(r >> 4, ntok - 1);
+      return a.q + (int64_t)b * a.q_sb + (int64_t)(i0 + tok) * a.q_si + (int64_t)(r & 15) * a.q_sh;
+    });
+    kh_load<R>(dzr, [&](int r) {
+      const int tok = min(r >> 4, ntok - 1);
+      return a.dz + (int64_t)b * a.dz_sb + (int64_t)(i0 + tok) * a.dz_si + (int64_t)(r & 15) * a.dz_sh;
+    });
+  };
+  auto sees_tile = [&](int step) {  // either token of the step has candidate keys in this tile
+    const int i0 = 2 * step;
+    const int64_t t = (int64_t)b * a.Lq + i0;
+    return a.bound[t] > kt || (i0 + 1 < a.Lq && a.bound[t + 1] > kt);
+  };
+  int step = s_begin;
+  while (step < s_end && !sees_tile(step)) ++step;
+  if (step < s_end) load_rows(step);
+  while (step < s_end) {
+    const int i0 = 2 * step, ntok = min(2, a.Lq - i0);
+    __syncthreads();  // previous step's readers of qs / dzs / pt / dst are done
+    kh_store<R>(qs, qr);
+    kh_store<R>(dzs, dzr);
+    __syncthreads();
+    int next = step + 1;
+    while (next < s_end && !sees_tile(next)) ++next;
+    if (next < s_end) load_rows(next);
+    {
+      const int blk = wave & 3;
+      sx[wave][lane] = wave < 4 ? kh_block<R>(qs, blk >> 1, ks, blk & 1, 0, R)
+                                : kh_block<R>(dzs, blk >> 1, vs, blk & 1, 0, R);
+    }
+    __syncthreads();
+    {
+      const bool row_ok = (sr >> 4) < ntok;
+      const int tok = min(sr >> 4, ntok - 1);
+      float lse2, dd;
+      kh_row_consts(a, b, i0 + tok, sr & 15, lse2, dd);
+      kh_pds<true>(a, sx, pt, dst, (int64_t)b * a.Lq + i0 + tok, row_ok, kt, lse2, dd);
+    }
+    __syncthreads();
+    kh_accumulate<R>(dv_acc, pt, dzs);  // dV += P^T dZ
+    kh_accumulate<R>(dk_acc, dst, qs);  // dK += dS^T Q
+    step = next;
+  }
+  {
+    const int l16 = lane & 15, g = lane >> 4;
+    float* dkb = a.dk + split * a.dk_ss + (int64_t)b * a.dk_sb;
+    float* dvb = a.dv + split * a.dv_ss + (int64_t)b * a.dv_sb;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kt + 16 * mb + 4 * g + r;
+        if (key >= a.N) continue;
+#pragma unroll
+        for (int cb = 0; cb < G::CB; ++cb) {
+          const int col = wave * G::QW + 16 * cb + l16;
+          dkb[(int64_t)key * a.dk_sn + col] = dk_acc[mb][cb][r];
+          dvb[(int64_t)key * a.dv_sn + col] = dv_acc[mb][cb][r];
+        }
+      }
+  }
+}
+
+// ---- small kernels -------------------------------------------------------------------------------------------
+// bound[t] = 1 + the last key mask row t shows (0 when none; N without a mask). One wave per row.
+__global__ __launch_bounds__(256) void khop_bound_kernel(const uint8_t* mask, int64_t m_sb, int64_t m_si, int B,
+                                                          int Lq, int N, int32_t* bound) {
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (t >= (int64_t)B * Lq) return;
+  if (!mask) {
+    if (lane == 0) bound[t] = N;
+    return;
+  }
+  const uint8_t* row = mask + (t / Lq) * m_sb + (t % Lq) * m_si;
+  int last = -1;
+  for (int j = lane; j < N; j += 64)
+    if (row[j]) last = j;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off));
+  if (lane == 0) bound[t] = last + 1;
+}
+
+// delta[b, h, i] = sum_c dz[b, i, h, c] * z[b, i, h, c] (fp32 products of the bf16 values). One wave per row.
+__global__ __launch_bounds__(256) void khop_delta_kernel(const uint16_t* dz, int64_t dz_sb, int64_t dz_si,
+                                                          int64_t dz_sh, const uint16_t* z, int64_t z_sb, int64_t z_si,
+                                                          int64_t z_sh, int B, int Lq, int R, float* delta) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= (int64_t)B * Lq * 16) return;
+  const int h = (int)(row % 16);
+  const int64_t t = row / 16;
+  const int b = (int)(t / Lq), i = (int)(t % Lq);
+  const uint16_t* dzp = dz + b * dz_sb + i * dz_si + h * dz_sh;
+  const uint16_t* zp = z + b * z_sb + i * z_si + h * z_sh;
+  float s = 0.f;
+  for (int c = lane; c < R; c += 64) s = __builtin_fmaf(bf2f(dzp[c]), bf2f(zp[c]), s);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  if (lane == 0) delta[((int64_t)b * 16 + h) * Lq + i] = s;
+}
+
+// Sum of the per-split dk / dv partials (fixed order): out[n] = sum_s part[s][n], n < count.
+__global__ __launch_bounds__(256) void khop_split_sum_kernel(const float* part, int64_t split_stride, int splits,
+                                                              int64_t count, float* out) {
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= count) return;
+  float s = part[n];
+  for (int p = 1; p < splits; ++p) s += part[p * split_stride + n];
+  out[n] = s;
+}
+
+inline bool kh_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int kh_check(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_sn,
+             const void* v, int64_t v_sb, int64_t v_sn, int B, int Lq, int N, int R, int heads) {
+  HLA_REQUIRE(B >= 1 && B <= 65535 && Lq >= 0 && N >= 1, HLA_S6_EINVAL, "khop: bad sizes B=%d Lq=%d N=%d", B, Lq,
+              N);
+  HLA_REQUIRE(heads == 16, HLA_S6_EUNSUPPORTED, "khop: %d query heads (16 supported)", heads);
+  HLA_REQUIRE(R == 128 || R == 256 || R == 512, HLA_S6_EUNSUPPORTED, "khop: latent width %d not in {128, 256, 512}",
+              R);
+  HLA_REQUIRE(q && k && v, HLA_S6_EINVAL, "khop: null input");
+  HLA_REQUIRE(kh_aligned16(q) && kh_aligned16(k) && kh_aligned16(v) && q_sb % 8 == 0 && q_si % 8 == 0 &&
+                  q_sh % 8 == 0 && k_sb % 8 == 0 && k_sn % 8 == 0 && v_sb % 8 == 0 && v_sn % 8 == 0,
+              HLA_S6_EINVAL, "khop: q/k/v rows must be 16-byte aligned with a unit last stride");
+  return HLA_S6_OK;
+}
+
+}  // namespace
+}  // namespace hla
+
+#define HLA_KH_DISPATCH(KERNEL, R, GRID, P, ST)                                                  \
+  do {                                                                                           \
+    switch (R) {                                                                                 \
+      case 128: hipLaunchKernelGGL(KERNEL<128>, GRID, dim3(kKhThreads), 0, ST, P); break;        \
+      case 256: hipLaunchKernelGGL(KERNEL<256>, GRID, dim3(kKhThreads), 0, ST, P); break;        \
+      default: hipLaunchKernelGGL(KERNEL<512>, GRID, dim3(kKhThreads), 0, ST, P); break;         \
+    }                                                                                            \
+  } while (0)
+
+extern "C" int hla_s6_khop_bounds(const uint8_t* mask, int64_t m_sb, int64_t m_si, int32_t B, int32_t Lq, int32_t N,
+                                  int32_t* bound, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(B >= 1 && Lq >= 0 && N >= 1 && bound, HLA_S6_EINVAL, "khop_bounds: bad arguments");
+  const int64_t rows = (int64_t)B * Lq;
+  if (rows == 0) return HLA_S6_OK;
+  hipLaunchKernelGGL(khop_bound_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, as_stream(stream), mask,
+                     m_sb, m_si, B, Lq, N, bound);
+  return check_launch("khop_bounds");
+}
+
+extern "C" int hla_s6_khop_forward(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k,
+                                   int64_t k_sb, int64_t k_sn, const void* v, int64_t v_sb, int64_t v_sn,
+                                   const uint8_t* mask, int64_t m_sb, int64_t m_si, const int32_t* bound, int32_t B,
+                                   int32_t Lq, int32_t N, int32_t heads, int32_t width, float scale, void* z,
+                                   int64_t z_sb, int64_t z_si, int64_t z_sh, float* lse, void* stream) {
+  using namespace hla;
+  int rc = kh_check(q, q_sb, q_si, q_sh, k, k_sb, k_sn, v, v_sb, v_sn, B, Lq, N, width, heads);
+  if (rc != HLA_S6_OK) return rc;
+  if (Lq == 0) return HLA_S6_OK;
+  HLA_REQUIRE(bound && z && lse, HLA_S6_EINVAL, "khop_forward: null bound / output");
+  KhopParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_sb = q_sb; p.q_si = q_si; p.q_sh = q_sh;
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.k_sb = k_sb; p.k_sn = k_sn; p.v_sb = v_sb; p.v_sn = v_sn;
+  p.mask = mask; p.m_sb = m_sb; p.m_si = m_si;
+  p.bound = bound;
+  p.B = B; p.Lq = Lq; p.N = N;
+  p.scale = scale;
+  p.scale_log2 = scale * kLog2e;
+  p.z = static_cast<uint16_t*>(z);
+  p.z_sb = z_sb; p.z_si = z_si; p.z_sh = z_sh;
+  p.lse = lse;
+  const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
+  HLA_KH_DISPATCH(khop_fwd, width, grid, p, as_stream(stream));
+  return check_launch("khop_forward");
+}
+
+extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k,
+                                    int64_t k_sb, int64_t k_sn, const void* v, int64_t v_sb, int64_t v_sn,
+                                    const uint8_t* mask, int64_t m_sb, int64_t m_si, const int32_t* bound, int32_t B,
+                                    int32_t Lq, int32_t N, int32_t heads, int32_t width, float scale, const void* z,
+                                    int64_t z_sb, int64_t z_si, int64_t z_sh, const float* lse, const void* dz,
+                                    int64_t dz_sb, int64_t dz_si, int64_t dz_sh, const float* dlse, float* delta,
+                                    float* dq, int64_t dq_sb, int64_t dq_si, int64_t dq_sh, float* dk, int64_t dk_sb,
+                                    int64_t dk_sn, float* dv, int64_t dv_sb, int64_t dv_sn, int32_t key_splits,
+                                    float* workspace, int64_t workspace_floats, void* stream) {
+  using namespace hla;
+  int rc = kh_check(q, q_sb, q_si, q_sh, k, k_sb, k_sn, v, v_sb, v_sn, B, Lq, N, width, heads);
+  if (rc != HLA_S6_OK) return rc;
+  HLA_REQUIRE(bound && z && lse && dz && delta, HLA_S6_EINVAL, "khop_backward: null input");
+  HLA_REQUIRE(key_splits >= 1 && key_splits <= 64, HLA_S6_EINVAL, "khop_backward: key_splits %d not in [1, 64]",
+              key_splits);
+  HLA_REQUIRE(kh_aligned16(dz) && dz_sb % 8 == 0 && dz_si % 8 == 0 && dz_sh % 8 == 0, HLA_S6_EINVAL,
+              "khop_backward: dz rows must be 16-byte aligned with a unit last stride");
+  const bool need_q = dq != nullptr, need_kv = dk != nullptr || dv != nullptr;
+  HLA_REQUIRE(!need_kv || (dk && dv), HLA_S6_EINVAL, "khop_backward: dk and dv come together");
+  const int64_t part = (int64_t)B * N * width;  // floats of one dk (or dv) partial
+  if (need_kv && key_splits > 1) {
+    HLA_REQUIRE(workspace && workspace_floats >= 2 * key_splits * part, HLA_S6_EWORKSPACE,
+                "khop_backward: %d key splits need a workspace of %lld floats (got %lld)", key_splits,
+                (long long)(2 * key_splits * part), (long long)workspace_floats);
+  }
+  hipStream_t st = as_stream(stream);
+  KhopParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_sb = q_sb; p.q_si = q_si; p.q_sh = q_sh;
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.k_sb = k_sb; p.k_sn = k_sn; p.v_sb = v_sb; p.v_sn = v_sn;
+  p.mask = mask; p.m_sb = m_sb; p.m_si = m_si;
+  p.bound = bound;
+  p.B = B; p.Lq = Lq; p.N = N;
+  p.scale = scale;
+  p.scale_log2 = scale * kLog2e;
+  p.lse = const_cast<float*>(lse);
+  p.dz = static_cast<const uint16_t*>(dz);
+  p.dz_sb = dz_sb; p.dz_si = dz_si; p.dz_sh = dz_sh;
+  p.dlse = dlse;
+  p.delta = delta;
+  if (Lq > 0) {
+    const int64_t rows = (int64_t)B * Lq * 16;
+    hipLaunchKernelGGL(khop_delta_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(dz), dz_sb, dz_si, dz_sh, static_cast<const uint16_t*>(z), z_sb,
+                       z_si, z_sh, B, Lq, width, delta);
+    if ((rc = check_launch("khop_delta")) != HLA_S6_OK) return rc;
+  }
+  if (need_q && Lq > 0) {
+    p.dq = dq;
+    p.dq_sb = dq_sb; p.dq_si = dq_si; p.dq_sh = dq_sh;
+    const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
+    HLA_KH_DISPATCH(khop_dq, width, grid, p, st);
+    if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
+  }
+  if (need_kv) {
+    const bool split = key_splits > 1;
+    HLA_REQUIRE(!split || (dk_sb == (int64_t)N * width && dk_sn == width && dv_sb == (int64_t)N * width &&
+                           dv_sn == width),
+                HLA_S6_EINVAL, "khop_backward: with key splits dk / dv must be contiguous [B, N, width]");
+    p.key_splits = key_splits;
+    p.dk = split ? workspace : dk;
+    p.dv = split ? workspace + key_splits * part : dv;
+    p.dk_sb = split ? (int64_t)N * width : dk_sb;
+    p.dk_sn = split ? width : dk_sn;
+    p.dv_sb = split ? (int64_t)N * width : dv_sb;
+    p.dv_sn = split ? width : dv_sn;
+    p.dk_ss = p.dv_ss = part;
+    const dim3 grid((unsigned)((N + kKhKeys - 1) / kKhKeys), (unsigned)B, (unsigned)key_splits);
+    HLA_KH_DISPATCH(khop_dkdv, width, grid, p, st);
+    if ((rc = check_launch("khop_dkdv")) != HLA_S6_OK) return rc;
+    if (split) {
+      hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part + 255) / 256)), dim3(256), 0, st, workspace,
+                         part, key_splits, part, dk);
+      hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part + 255) / 256)), dim3(256), 0, st,
+                         workspace + key_splits * part, part, key_splits, part, dv);
+      if ((rc = check_launch("khop_split_sum")) != HLA_S6_OK) return rc;
+    }
+  }
+  return HLA_S6_OK;
+}

@@ -1,0 +1,176 @@
+"""Multi-query causal history attention with backward on MI355X: the interface of ``hla/latent/history_gemm.py``
+(``causal_history_gemm``) and of ``hla/latent/fused_history.py:126-153`` (``causal_history_attention``) over the HIP
+kernels of ``khop.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward``, ``hla_s6_khop_backward``).
+
+Every query row ``(b, i, h)`` attends over the latent rows ``k[b, j], v[b, j]`` that ``mask[b, i, j]`` shows (all
+heads share the rows). The kernels compute with bf16 GEMM operands and fp32 accumulation and softmax (the
+reference's ``precision='bf16'`` mode); they derive each query's key bound from the mask, so ``causal`` needs no
+promise and only documents intent. No ``[B, H, Lq, N]`` tensor is ever formed.
+"""
+from __future__ import annotations
+
+import torch
+from torch.autograd.function import once_differentiable
+
+from . import _lib, s6_ops
+
+PRECISIONS = ('bf16',)
+DEFAULT_CHUNK = 128
+DEFAULT_MAX_ELEMENTS = 1 << 26
+KEY_ALIGN = 16
+HEADS = 16
+WIDTHS = (128, 256, 512)
+
+
+def bf16_fp32_output_supported(device) -> bool:
+    """The HIP kernels always accumulate bf16 products in fp32 (``history_gemm.py:84-98`` probes torch for this)."""
+    return True
+
+
+def _round_up(value: int, multiple: int) -> int:
+    return -(-value // multiple) * multiple
+
+
+def chunk_plan(Lq: int, N: int, batch: int, heads: int, *, causal: bool, chunk: int,
+               max_elements: int = DEFAULT_MAX_ELEMENTS, padded_keys: int | None = None, align: int = 1):
+    """``(start, end, key_end)`` query chunks of the reference's chunked GEMM (``history_gemm.py:109-130``): with
+    ``causal`` a chunk ending at ``end`` needs keys ``< end - 1 + N - Lq`` rounded up to ``align``. The HIP kernels
+    do not chunk (each query's bound comes from the mask); the plan is kept for callers that size work with it."""
+    total = N if padded_keys is None else padded_keys
+    shift = N - Lq
+    rows = max(1, min(chunk, max_elements // max(1, batch * heads * total)))
+    for start in range(0, Lq, rows):
+        end = min(Lq, start + rows)
+        if causal:
+            needed = end - 1 + shift
+            key_end = min(total, _round_up(needed, align)) if needed > 0 else 0
+        else:
+            key_end = total
+        yield start, end, key_end
+
+
+def causal_mask_is_consistent(mask: torch.Tensor) -> bool:
+    """True when ``mask [B, Lq, N]`` shows no key at or after the query position ``i + N - Lq``."""
+    B, Lq, N = mask.shape
+    shift = N - Lq
+    forbidden = (torch.arange(N, device=mask.device)[None, :]
+                 >= torch.arange(Lq, device=mask.device)[:, None] + shift)
+    return not bool((mask.bool() & forbidden[None]).any())
+
+
+def _bf16_rows(name, t):
+    t = t.to(torch.bfloat16)
+    if t.stride(-1) != 1 or any(s % 8 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _key_splits(tiles: int, device) -> int:
+    """Row ranges per 32-key tile of the dk/dv kernel: enough workgroups for four per CU."""
+    cus = _lib.device_cus(device.index or 0)
+    return max(1, min(16, -(-4 * cus // max(1, tiles))))
+
+
+class _CausalHistory(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale):
+        B, Lq, H, R = q.shape
+        N = k.shape[1]
+        dev = q.device
+        qb, kb, vb = _bf16_rows('q', q), _bf16_rows('k', k), _bf16_rows('v', v)
+        m = mask if mask.dtype == torch.bool else mask.bool()
+        if m.stride(-1) != 1:
+            m = m.contiguous()
+        m8 = m.view(torch.uint8)
+        bound = torch.empty(B * Lq, dtype=torch.int32, device=dev)
+        st = _lib.stream(dev)
+        _lib.call('hla_s6_khop_bounds', _lib.ptr(m8), m8.stride(0), m8.stride(1), B, Lq, N, _lib.ptr(bound), st)
+        z = torch.empty(B, Lq, H, R, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+        _lib.call('hla_s6_khop_forward', _lib.ptr(qb), qb.stride(0), qb.stride(1), qb.stride(2), _lib.ptr(kb),
+                  kb.stride(0), kb.stride(1), _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(m8), m8.stride(0),
+                  m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, float(scale), _lib.ptr(z), z.stride(0), z.stride(1),
+                  z.stride(2), _lib.ptr(lse), st)
+        ctx.save_for_backward(qb, kb, vb, m8, bound, lse, z)
+        ctx.settings = (float(scale), q.dtype, k.dtype, v.dtype)
+        return z.to(q.dtype), lse
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dz, dlse):
+        qb, kb, vb, m8, bound, lse, z = ctx.saved_tensors
+        scale, q_dtype, k_dtype, v_dtype = ctx.settings
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        B, Lq, H, R = qb.shape
+        N = kb.shape[1]
+        dev = qb.device
+        dzb = _bf16_rows('dz', dz if dz is not None else torch.zeros_like(z))
+        dl = None if dlse is None else dlse.to(torch.float32).contiguous()
+        delta = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+        dq = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev) if need_q else None
+        need_kv = need_k or need_v
+        dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+        dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+        splits = _key_splits(-(-N // 32) * B, dev) if need_kv else 1
+        ws = torch.empty(2 * splits * B * N * R, dtype=torch.float32, device=dev) if splits > 1 else None
+        _lib.call('hla_s6_khop_backward', _lib.ptr(qb), qb.stride(0), qb.stride(1), qb.stride(2), _lib.ptr(kb),
+                  kb.stride(0), kb.stride(1), _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(m8), m8.stride(0),
+                  m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, scale, _lib.ptr(z), z.stride(0), z.stride(1),
+                  z.stride(2), _lib.ptr(lse), _lib.ptr(dzb), dzb.stride(0), dzb.stride(1), dzb.stride(2), _lib.ptr(dl),
+                  _lib.ptr(delta), _lib.ptr(dq), 0 if dq is None else dq.stride(0), 0 if dq is None else dq.stride(1),
+                  0 if dq is None else dq.stride(2), _lib.ptr(dk), 0 if dk is None else dk.stride(0),
+                  0 if dk is None else dk.stride(1), _lib.ptr(dv), 0 if dv is None else dv.stride(0),
+                  0 if dv is None else dv.stride(1), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+                  _lib.stream(dev))
+        return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
+                dv.to(v_dtype) if need_v else None, None, None)
+
+
+def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHUNK, precision='bf16',
+                        max_elements=DEFAULT_MAX_ELEMENTS):
+    """Causal history attention (``hla/latent/history_gemm.py:270-294``).
+
+    q: [B, Lq, 16, R], k: [B, N, R], v: [B, N, R], mask: [B, Lq, N] (True = visible). Returns z [B, Lq, 16, R] in
+    q.dtype and lse [B, 16, Lq] (fp32, -inf on rows with no visible history, where z is 0); differentiable in q, k
+    and v. ``causal`` asks for the reference's promise check only; ``chunk`` and ``max_elements`` are accepted for
+    signature parity (the kernels do not chunk).
+    """
+    if q.ndim != 4 or k.ndim != 3 or v.ndim != 3 or mask.ndim != 3:
+        raise ValueError(f'Expected Q[B,Lq,H,R], K[B,N,R], V[B,N,Rv], mask[B,Lq,N], got '
+                         f'{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}, {tuple(mask.shape)}')
+    B, Lq, H, Rk = q.shape
+    N = k.shape[1]
+    if (k.shape[0] != B or k.shape[-1] != Rk or v.shape[:2] != k.shape[:2]
+            or tuple(mask.shape) != (B, Lq, N)):
+        raise ValueError('Inconsistent history attention shapes')
+    if causal and N < Lq:
+        raise ValueError('Causal history requires at least as many keys as queries')
+    if precision not in PRECISIONS:
+        raise ValueError(f'Unsupported precision {precision!r}: the MI355X kernels compute with bf16 operands and '
+                         f'fp32 accumulation (precision="bf16")')
+    if chunk < 1 or max_elements < 1:
+        raise ValueError('chunk and max_elements must be positive')
+    if H != HEADS or v.shape[-1] != Rk or Rk not in WIDTHS:
+        raise ValueError(f'the HIP kernels take {HEADS} heads and equal K/V widths in {WIDTHS} '
+                         f'(got H={H}, Rk={Rk}, Rv={v.shape[-1]})')
+    s6_ops._dev(q, k, v, mask)
+    return _CausalHistory.apply(q, k, v, mask, float(scale))
+
+
+HISTORY_BACKENDS = ('triton', 'gemm', 'hip')
+
+
+def causal_history_attention(q, k, v, mask, scale, reference_forward=False, *, backend='gemm', precision='bf16',
+                             chunk=None, causal=False):
+    """``hla/latent/fused_history.py:126-153`` with every backend name served by the one HIP path (``'reference'``,
+    the dense torch autograd form, belongs to the tests)."""
+    if backend not in HISTORY_BACKENDS:
+        raise ValueError(f'Unknown causal history backend {backend!r}; expected one of {HISTORY_BACKENDS}')
+    return causal_history_gemm(q, k, v, mask, scale, causal=causal, chunk=chunk or DEFAULT_CHUNK,
+                               precision=precision)
+
+
+def flops(visible_pairs: int, heads: int, width: int, with_backward: bool = False) -> float:
+    """Algorithmic FLOPs for ``visible_pairs`` visible (query, key) pairs, ``2 * heads * width`` per pair and GEMM:
+    2 GEMMs forward (S, P V); the backward adds 5 (S again, dP, dV, dQ, dK)."""
+    return 2.0 * heads * width * visible_pairs * (7 if with_backward else 2)

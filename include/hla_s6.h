@@ -268,6 +268,35 @@ int hla_s6_gather_packed_rows(const int64_t *cache_addrs, int32_t num_layers, in
                               const int32_t *l1_blocks, int32_t l1_block_size, int32_t length, void *out,
                               int64_t out_layer_stride, int64_t out_row_stride, int32_t vector_ok, void *stream);
 
+/* ---- multi-query causal history attention with backward (K-hop replay / training) ---------------------------
+ * Replaces causal_history_gemm (hla/latent/history_gemm.py:159-220,270-294) for bf16 GEMM operands with fp32
+ * accumulation: q [B, Lq, 16, width] (strides q_sb, q_si, q_sh), k / v [B, N, width] (strides *_sb, *_sn), mask
+ * [B, Lq, N] bytes (nonzero = visible; strides m_sb, m_si, unit last stride; NULL = all keys below the bound),
+ * width in {128, 256, 512}, bf16 rows 16-byte aligned with unit last stride.
+ * hla_s6_khop_bounds: bound[b * Lq + i] = 1 + the last key mask row (b, i) shows (0 if none; N without a mask).
+ * hla_s6_khop_forward: z [B, Lq, 16, width] bf16 and lse [B, 16, Lq] fp32 (natural log; -inf and z = 0 for a row
+ *   without visible keys); one launch.
+ * hla_s6_khop_backward: from dz [B, Lq, 16, width] bf16 and dlse [B, 16, Lq] (NULL = 0): delta = dz.z into
+ *   `delta` [B, 16, Lq], then dq [B, Lq, 16, width] (NULL: skipped) and dk / dv [B, N, width] fp32 (both NULL:
+ *   skipped). key_splits > 1 splits each key tile's query rows over that many workgroups, with fp32 partials in
+ *   `workspace` (at least 2 * key_splits * B * N * width floats; dk / dv then contiguous) summed in a fixed order,
+ *   so results are deterministic for a given key_splits. Up to 5 launches. */
+int hla_s6_khop_bounds(const uint8_t *mask, int64_t m_sb, int64_t m_si, int32_t B, int32_t Lq, int32_t N,
+                       int32_t *bound, void *stream);
+int hla_s6_khop_forward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void *k, int64_t k_sb,
+                        int64_t k_sn, const void *v, int64_t v_sb, int64_t v_sn, const uint8_t *mask, int64_t m_sb,
+                        int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N, int32_t heads,
+                        int32_t width, float scale, void *z, int64_t z_sb, int64_t z_si, int64_t z_sh, float *lse,
+                        void *stream);
+int hla_s6_khop_backward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void *k, int64_t k_sb,
+                         int64_t k_sn, const void *v, int64_t v_sb, int64_t v_sn, const uint8_t *mask, int64_t m_sb,
+                         int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N, int32_t heads,
+                         int32_t width, float scale, const void *z, int64_t z_sb, int64_t z_si, int64_t z_sh,
+                         const float *lse, const void *dz, int64_t dz_sb, int64_t dz_si, int64_t dz_sh,
+                         const float *dlse, float *delta, float *dq, int64_t dq_sb, int64_t dq_si, int64_t dq_sh,
+                         float *dk, int64_t dk_sb, int64_t dk_sn, float *dv, int64_t dv_sb, int64_t dv_sn,
+                         int32_t key_splits, float *workspace, int64_t workspace_floats, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

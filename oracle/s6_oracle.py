@@ -376,6 +376,58 @@ def attend_chunk(q_lat, q_rope, k_rope, v, B, lat_k, lat_v, token_table, ctx, ct
     return merge_states(o_h, lse_h, o_c, lse_c, invalid, rounding)
 
 
+# ----------------------------------------------------------------------------------------------------------------
+# Multi-query causal history attention with backward (K-hop replay / chunked prefill on contiguous rows)
+# ----------------------------------------------------------------------------------------------------------------
+
+def _masked_scores(q, k, mask, scale, dtype):
+    s = np.einsum('bihr,bjr->bihj', q.astype(dtype), k.astype(dtype)) * dtype(scale)
+    vis = np.asarray(mask, bool)[:, :, None, :]
+    return np.where(vis, s, -np.inf), vis
+
+
+def causal_history(q, k, v, mask, scale, dtype=np.float64):
+    """``z [B, Lq, H, Rv]`` and ``lse [B, H, Lq]`` of every query row (i, h) over the keys ``mask[b, i, :]``
+    shows; rows without a visible key give ``z = 0``, ``lse = -inf``. Follows ``_forward``
+    (``hla/latent/history_gemm.py:159-177``): peak-shifted exponentials, ``lse = log(den) + peak``,
+    ``z = (prob @ v) / den``."""
+    s, vis = _masked_scores(q, k, mask, scale, dtype)
+    peak = s.max(-1, keepdims=True)
+    peak = np.where(np.isfinite(peak), peak, 0.0)
+    prob = np.where(vis, np.exp(s - peak), 0.0)
+    den = prob.sum(-1, keepdims=True)
+    with np.errstate(divide='ignore'):
+        lse = (np.log(den) + peak)[..., 0]
+    z = np.einsum('bihj,bjr->bihr', prob, v.astype(dtype)) / np.where(den == 0, 1.0, den)
+    return z, lse.transpose(0, 2, 1)
+
+
+def causal_history_backward(q, k, v, mask, scale, lse, dz, dlse=None, z=None, dtype=np.float64):
+    """``(dq, dk, dv)`` of ``causal_history`` for output cotangents ``dz [B, Lq, H, Rv]`` and
+    ``dlse [B, H, Lq]``. Follows ``_backward`` (``hla/latent/history_gemm.py:180-220``):
+    ``P = exp(s - lse)`` (0 on rows without history), ``dv = P^T dz``, ``dP = dz v^T``,
+    ``delta = sum(dz * z)`` when ``z`` is given, else ``sum(P * dP)``,
+    ``dS = P (dP - delta + dlse) scale``, ``dq = dS k``, ``dk = dS^T q``."""
+    s, vis = _masked_scores(q, k, mask, scale, dtype)
+    lse_t = np.asarray(lse, dtype).transpose(0, 2, 1)[..., None]            # [B, Lq, H, 1]
+    empty = ~np.isfinite(lse_t)
+    prob = np.where(vis & ~empty, np.exp(s - np.where(empty, 0.0, lse_t)), 0.0)
+    dz = np.asarray(dz, dtype)
+    dv = np.einsum('bihj,bihr->bjr', prob, dz)
+    dp = np.einsum('bihr,bjr->bihj', dz, v.astype(dtype))
+    if z is not None:
+        delta = (dz * np.asarray(z, dtype)).sum(-1, keepdims=True)
+    else:
+        delta = (dp * prob).sum(-1, keepdims=True)
+    ds = dp - delta
+    if dlse is not None:
+        ds = ds + np.where(empty, 0.0, np.asarray(dlse, dtype).transpose(0, 2, 1)[..., None])
+    ds = ds * prob * dtype(scale)
+    dq = np.einsum('bihj,bjr->bihr', ds, k.astype(dtype))
+    dk = np.einsum('bihj,bihr->bjr', ds, q.astype(dtype))
+    return dq, dk, dv
+
+
 def rel_l2(a, b):
     """Relative L2 error ``||a - b|| / ||b||`` in float64."""
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)

@@ -1,0 +1,156 @@
+"""Multi-query causal history attention with backward (``history_gemm.causal_history_gemm`` over khop.hip) against
+the float64 oracle (``oracle.s6_oracle.causal_history`` / ``causal_history_backward``, restating
+hla/latent/history_gemm.py:159-220) on bf16-rounded inputs.
+
+Bars: z within the attention tolerance (max-abs 2e-2, rel-L2 5e-3) and lse within 1e-3 of the oracle. Gradients
+(bf16 GEMM operands, including the bf16-rounded P and dS that enter the second products, as the reference's bf16
+mode) within relative L2 1e-2 per tensor and max-abs 2e-2 of its largest magnitude; empty rows give exactly
+z = 0, lse = -inf and no gradient; results are bitwise repeatable.
+"""
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import bf16
+from oracle import s6_oracle as O
+from s6util import assert_attention_close, assert_lse_close, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+hg = importlib.import_module('hybrid-latent-attention_amd.history_gemm')
+
+GRAD_REL = 1e-2
+
+
+def benchmark_mask(lengths, L):
+    """The mask of hla/latent/benchmark_history_gemm.py:72-76: valid rows and keys, query i sees keys j < i."""
+    lengths = np.asarray(lengths)
+    valid = np.arange(L)[None] < lengths[:, None]
+    order = np.arange(L)[:, None] > np.arange(L)[None]
+    return valid[:, :, None] & valid[:, None, :] & order[None]
+
+
+def case(seed, B, Lq, N, R, kind):
+    rng = np.random.default_rng(seed)
+    q = bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32))
+    k = bf16.round_bf16(rng.standard_normal((B, N, R)).astype(np.float32))
+    v = bf16.round_bf16(rng.standard_normal((B, N, R)).astype(np.float32))
+    if kind == 'benchmark':
+        assert Lq == N
+        mask = benchmark_mask([max(2, int(Lq * (1 - 0.1 * b))) for b in range(B)], Lq)
+    elif kind == 'khop':                       # prompt P, window W: query i sees j < P + i - W (khop_replay.py:105)
+        P, W = N - Lq, 3
+        mask = np.broadcast_to(np.arange(N)[None] < P + np.arange(Lq)[:, None] - W, (B, Lq, N)).copy()
+    else:                                      # arbitrary
+        mask = rng.random((B, Lq, N)) < 0.3
+        mask[:, 1] = False                     # rows without history
+    return q, k, v, mask
+
+
+def run(q, k, v, mask, scale, need_grad=True, dz=None, dlse=None):
+    dev = lambda x, grad: torch.tensor(x, device='cuda').to(torch.bfloat16).requires_grad_(grad)
+    qt, kt, vt = dev(q, need_grad), dev(k, need_grad), dev(v, need_grad)
+    mt = torch.tensor(mask, device='cuda')
+    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale, causal=True)
+    out = {'z': z.detach().float().cpu().numpy(), 'lse': lse.detach().cpu().numpy()}
+    if need_grad:
+        dzt = torch.tensor(dz, device='cuda').to(torch.bfloat16)
+        dlt = torch.tensor(dlse, device='cuda', dtype=torch.float32)
+        obj = (z.float() * dzt.float()).sum() + torch.where(torch.isfinite(lse), lse * dlt, 0.).sum()
+        g = torch.autograd.grad(obj, [qt, kt, vt])
+        out.update(dq=g[0].float().cpu().numpy(), dk=g[1].float().cpu().numpy(), dv=g[2].float().cpu().numpy())
+    return out
+
+
+def assert_grad_close(got, want, what):
+    assert np.isfinite(got).all(), f'{what}: non-finite'
+    r = rel_l2(got, want)
+    err = float(np.abs(got - want).max())
+    assert r <= GRAD_REL, f'{what}: rel-L2 {r:.3e} > {GRAD_REL}'
+    assert err <= 2e-2 * max(1.0, float(np.abs(want).max())), f'{what}: max-abs {err:.3e}'
+
+
+@pytest.mark.parametrize('R', [128, 256, 512])
+@pytest.mark.parametrize('kind,B,Lq,N', [('benchmark', 3, 45, 45), ('khop', 2, 21, 70), ('any', 2, 37, 50)])
+def test_forward_and_backward_match_the_oracle(R, kind, B, Lq, N):
+    q, k, v, mask = case(7 * R + Lq, B, Lq, N, R, kind)
+    scale = 1 / math.sqrt(128)
+    rng = np.random.default_rng(R + N)
+    dz = bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32))
+    dlse = rng.standard_normal((B, 16, Lq)).astype(np.float32)
+    got = run(q, k, v, mask, scale, dz=dz, dlse=dlse)
+    z, lse = O.causal_history(q, k, v, mask, scale)
+    assert_attention_close(got['z'], z, 'z')
+    assert_lse_close(got['lse'], lse)
+    empty = ~mask.any(-1)                                          # [B, Lq]
+    assert (got['z'][empty] == 0).all() and np.isneginf(got['lse'].transpose(0, 2, 1)[empty]).all()
+    dq, dk, dv = O.causal_history_backward(q, k, v, mask, scale, lse, dz, dlse)
+    assert_grad_close(got['dq'], dq, 'dq')
+    assert_grad_close(got['dk'], dk, 'dk')
+    assert_grad_close(got['dv'], dv, 'dv')
+    assert (got['dq'][empty] == 0).all()
+
+
+def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
+    q, k, v, mask = case(3, 2, 30, 30, 256, 'benchmark')
+    rng = np.random.default_rng(4)
+    dz = bf16.round_bf16(rng.standard_normal(q.shape).astype(np.float32))
+    dlse = rng.standard_normal((2, 16, 30)).astype(np.float32)
+    a = run(q, k, v, mask, 0.1, dz=dz, dlse=dlse)
+    b = run(q, k, v, mask, 0.1, dz=dz, dlse=dlse)
+    for key in ('z', 'lse', 'dq', 'dk', 'dv'):
+        assert np.array_equal(a[key], b[key]), key
+    qt = torch.tensor(q, device='cuda').to(torch.bfloat16).requires_grad_(True)
+    kt = torch.tensor(k, device='cuda').to(torch.bfloat16)
+    vt = torch.tensor(v, device='cuda').to(torch.bfloat16)
+    z, lse = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), 0.1)
+    (gq,) = torch.autograd.grad((z.float() * torch.tensor(dz, device='cuda')).sum()
+                                + torch.where(torch.isfinite(lse), lse * torch.tensor(dlse, device='cuda'), 0.).sum(),
+                                [qt])
+    assert np.array_equal(gq.float().cpu().numpy(), a['dq'])
+
+
+def test_unsplit_key_tiles_match_the_oracle(monkeypatch):
+    """dk / dv accumulated by one workgroup per key tile (no row splits, no partial sums)."""
+    monkeypatch.setattr(hg, '_key_splits', lambda tiles, device: 1)
+    q, k, v, mask = case(11, 2, 40, 40, 512, 'benchmark')
+    rng = np.random.default_rng(12)
+    dz = bf16.round_bf16(rng.standard_normal(q.shape).astype(np.float32))
+    dlse = rng.standard_normal((2, 16, 40)).astype(np.float32)
+    got = run(q, k, v, mask, 0.09, dz=dz, dlse=dlse)
+    z, lse = O.causal_history(q, k, v, mask, 0.09)
+    dq, dk, dv = O.causal_history_backward(q, k, v, mask, 0.09, lse, dz, dlse)
+    assert_grad_close(got['dk'], dk, 'dk')
+    assert_grad_close(got['dv'], dv, 'dv')
+    assert_grad_close(got['dq'], dq, 'dq')
+
+
+def test_fp32_inputs_and_transposed_query_view():
+    """fp32 leaves (as in the reference benchmark) are rounded to bf16 operands; a [B,H,L,R] -> [B,L,H,R] view works."""
+    rng = np.random.default_rng(9)
+    B, L, R = 2, 33, 256
+    q = torch.randn(B, 16, L, R, device='cuda').transpose(1, 2)
+    k, v = torch.randn(B, L, R, device='cuda'), torch.randn(B, L, R, device='cuda')
+    mask = torch.tensor(benchmark_mask([L, 20], L), device='cuda')
+    z, lse = hg.causal_history_gemm(q, k, v, mask, 0.125, causal=True)
+    assert z.dtype == torch.float32 and lse.shape == (B, 16, L)
+    qn, kn, vn = (bf16.round_bf16(t.contiguous().cpu().numpy()) for t in (q, k, v))
+    zo, lo = O.causal_history(qn, kn, vn, mask.cpu().numpy(), 0.125)
+    assert_attention_close(z.detach().cpu().numpy(), zo, 'z')
+    assert_lse_close(lse.detach().cpu().numpy(), lo)
+    del rng
+
+
+def test_rejects_unsupported_shapes_and_precision():
+    q = torch.zeros(1, 4, 16, 1024, device='cuda', dtype=torch.bfloat16)
+    k = torch.zeros(1, 4, 1024, device='cuda', dtype=torch.bfloat16)
+    m = torch.ones(1, 4, 4, dtype=torch.bool, device='cuda')
+    with pytest.raises(ValueError, match='widths'):
+        hg.causal_history_gemm(q, k, k, m, 1.0)
+    with pytest.raises(ValueError, match='precision'):
+        hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0, precision='fp32')
+    with pytest.raises(ValueError, match='Inconsistent'):
+        hg.causal_history_gemm(q[..., :256], k[..., :256], k[:, :3, :256], m, 1.0)

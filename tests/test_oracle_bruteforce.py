@@ -400,3 +400,77 @@ def test_planted_mistakes_fail_the_pins():
     wrong = x * np.concatenate((table_r[pos, :4], table_r[pos, :4]), -1)[:, None] - \
         O.rotate_half(x) * np.concatenate((table_r[pos, 4:], table_r[pos, 4:]), -1)[:, None]
     assert not np.allclose(wrong, O.latent_rope(x, pos, table_r, rounding=False), atol=1e-3)
+
+
+# ---------------------------------------------------------------------------------------------- multi-query history
+
+def _khop_case(seed, B=2, Lq=5, N=7, H=3, R=4, causal=True):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, Lq, H, R))
+    k = rng.standard_normal((B, N, R))
+    v = rng.standard_normal((B, N, R))
+    i = np.arange(Lq)[:, None]
+    j = np.arange(N)[None, :]
+    mask = np.broadcast_to(j < i + N - Lq, (B, Lq, N)).copy() if causal else rng.random((B, Lq, N)) < 0.6
+    mask[0, 0] = False                          # one query row without history
+    if B > 1:
+        mask[1, :, N - 1] = False               # a padded key
+    return q, k, v, mask
+
+
+def test_causal_history_matches_per_row_softmax():
+    q, k, v, mask = _khop_case(20, causal=False)
+    scale = 0.37
+    z, lse = O.causal_history(q, k, v, mask, scale)
+    B, Lq, H, _ = q.shape
+    for b in range(B):
+        for i in range(Lq):
+            for h in range(H):
+                keys = np.flatnonzero(mask[b, i])
+                if keys.size == 0:
+                    assert (z[b, i, h] == 0).all() and lse[b, h, i] == -np.inf
+                    continue
+                out, l = _softmax64(k[b, keys] @ q[b, i, h] * scale, v[b, keys])
+                np.testing.assert_allclose(z[b, i, h], out, rtol=1e-12, atol=1e-12)
+                np.testing.assert_allclose(lse[b, h, i], l, rtol=1e-12)
+
+
+@pytest.mark.parametrize('use_z', [False, True])
+def test_causal_history_backward_is_the_gradient(use_z):
+    """Central finite differences of L = sum(z * dz) + sum(lse * dlse) (finite lse only) in float64."""
+    q, k, v, mask = _khop_case(21, B=2, Lq=4, N=6, H=2, R=3)
+    rng = np.random.default_rng(22)
+    scale = 0.6
+    z, lse = O.causal_history(q, k, v, mask, scale)
+    dz = rng.standard_normal(z.shape)
+    dlse = rng.standard_normal(lse.shape)
+
+    def objective(q_, k_, v_):
+        z_, l_ = O.causal_history(q_, k_, v_, mask, scale)
+        return float((z_ * dz).sum() + np.where(np.isfinite(l_), l_ * dlse, 0.0).sum())
+
+    dq, dk, dv = O.causal_history_backward(q, k, v, mask, scale, lse, dz, dlse, z=z if use_z else None)
+    eps = 1e-6
+    for name, x, g in (('q', q, dq), ('k', k, dk), ('v', v, dv)):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            args = {'q': (xp, k, v), 'k': (q, xp, v), 'v': (q, k, xp)}[name]
+            argm = {'q': (xm, k, v), 'k': (q, xm, v), 'v': (q, k, xm)}[name]
+            num[idx] = (objective(*args) - objective(*argm)) / (2 * eps)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7, err_msg=name)
+
+
+def test_causal_history_planted_mistakes_fail():
+    """A dropped dlse term or a transposed key/query in dk fails the finite-difference pin."""
+    q, k, v, mask = _khop_case(23, B=1, Lq=3, N=4, H=2, R=2)
+    rng = np.random.default_rng(24)
+    z, lse = O.causal_history(q, k, v, mask, 0.5)
+    dz, dlse = rng.standard_normal(z.shape), rng.standard_normal(lse.shape)
+    dq, dk, dv = O.causal_history_backward(q, k, v, mask, 0.5, lse, dz, dlse)
+    dq0, _, _ = O.causal_history_backward(q, k, v, mask, 0.5, lse, dz, None)
+    assert np.abs(dq - dq0).max() > 1e-3
+    _, dkv, _ = O.causal_history_backward(q, v, k, mask, 0.5, lse, dz, dlse)
+    assert np.abs(dk - dkv).max() > 1e-3
