@@ -43,6 +43,13 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// The 8 bf16 of two ds_read_b64_tr_b16 results as one 16-byte MFMA operand (lo first; a pure register view).
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ u32x4 join_tr(short4v lo, short4v hi) {
+  const u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
 // ---- MFMA wrappers ----------------------------------------------------------------------------------
 // 16x16x32 bf16: lane l supplies A[l%16][8*(l/16) .. +8] and B[8*(l/16) .. +8][l%16];
 // D: lane l holds D[4*(l/16) + r][l%16], r = 0..3.

@@ -46,6 +46,9 @@ namespace {
 #ifndef HLA_HIST_WCOLS
 #define HLA_HIST_WCOLS 128
 #endif
+#ifndef HLA_MQ_V2
+#define HLA_MQ_V2 1  // multi-query steps: history_mq2 (token-per-wave-pair) instead of history_mq
+#endif
 #ifndef HLA_HIST_VTR
 #define HLA_HIST_VTR 1  // V^T operands by ds_read_b64_tr_b16 (else four 16-bit LDS reads)
 #endif
@@ -908,10 +911,7 @@ __global__ __launch_bounds__(64 * MqGeo<R>::NW) void history_mq(HistoryParams a)
               const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
               const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                   (__attribute__((address_space(3))) short4v*)(vp + 4 * G::VS));
-              const u32x4 vt = {(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
-                                (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
-                                (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
-                                (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+              const u32x4 vt = join_tr(lo, hi);
               o[cb][0] = mfma32x32x16(vt, pf[0][ks], o[cb][0]);
               o[cb][1] = mfma32x32x16(vt, pf[1][ks], o[cb][1]);
             }
@@ -954,6 +954,232 @@ __global__ __launch_bounds__(64 * MqGeo<R>::NW) void history_mq(HistoryParams a)
       }
     }
     __syncthreads();  // the next pass reuses the LDS exchange
+    tp = te;
+  }
+}
+
+// history_mq2: one workgroup per (group of 4 consecutive tokens, KV slot) with 8 waves; wave w owns token w / 2 (its
+// 16 heads are the 16 query rows) and latent column half w % 2. Per 32-key tile:
+//   * S^T[32 keys x 16 rows] partial over the wave's R/2 columns on v_mfma_f32_16x16x32_bf16: K rows (A operand)
+//     from LDS, Q^T (B operand) in registers for the whole pass;
+//   * the two halves of a token swap partials through LDS (one barrier); both waves then hold the full scores and
+//     run the same online softmax (a row's 32 keys sit in 4 lanes; the running maximum is raised lazily, only when
+//     a tile exceeds it by more than 2^8);
+//   * O^T[R/2 columns x 16 rows] += V^T P^T: P^T stays in registers (the score layout is the B-operand layout under
+//     a fixed permutation of the 32 keys over the MFMA k index, which V^T follows: two ds_read_b64_tr_b16 per
+//     operand, keys 4g.. and 16 + 4g..).
+// K tiles are double-buffered in LDS, V single-buffered (a second barrier before its refill); each K and V tile is
+// requested about one tile ahead of its LDS store, through registers.
+constexpr int kMq2Pages = 2048;  // block-table entries of a pass kept in LDS (longer passes read them from memory)
+
+template <int R>
+struct Mq2Geo {
+  static constexpr int C = R / 2;                 // latent columns per wave
+  static constexpr int KS = C / 32;               // 32-column k-steps of S^T
+  static constexpr int CB = C / 16;               // 16-column blocks of O^T
+  static constexpr int CPR = R / 8;               // 16-byte pieces per K / V row
+  static constexpr int TL = kMqKeys * CPR / 512;  // pieces per thread per tile (K and V each)
+  static constexpr int RS = R + 16;               // LDS row stride (bf16): rows 8 banks apart, so the K row reads
+                                                  // (8 lanes a cycle) and the transposing V reads are conflict-free
+  static_assert(TL >= 1 && KS >= 1, "R must be at least 128");
+};
+
+template <int R>
+__global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
+  using G = Mq2Geo<R>;
+  __shared__ __attribute__((aligned(16))) uint16_t ks_lds[2][kMqKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_lds[kMqKeys * G::RS];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[2][8][2][64];  // S^T partials [tile parity][wave][key block]
+  __shared__ int32_t pg_lds[kMq2Pages];                              // the pass's pages (block-table entries)
+  __shared__ int64_t red_lds[16];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, g = lane >> 4;
+  const int u = wave >> 1, half = wave & 1, col0 = half * G::C;
+  const int S = a.num_splits, s = blockIdx.y;
+  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int t_begin = blockIdx.x * kMqTokens, t_end = min(t_begin + kMqTokens, a.T);
+  int par = 0;  // parity of the partial exchange buffer, continued across passes
+
+  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
+    const int64_t row = table_row(a, tp);
+    int te = tp + 1;
+    while (te < t_end && table_row(a, te) == row) ++te;
+    const int count = te - tp;
+    int n_max = 0, n_own = 0;
+#pragma unroll
+    for (int v = 0; v < kMqTokens; ++v) {
+      const int n = v < count ? (int)min((int64_t)a.ctx[tp + v], cap) : 0;
+      n_max = max(n_max, n);
+      if (v == u) n_own = n;
+    }
+    const int tiles16 = (n_max + kTile - 1) / kTile;
+    const int j0 = S > 1 ? s * chunk : 0;
+    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
+    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);
+    const int own_n = min(k1, n_own);
+    float m_own = -INFINITY, l_own = 0.f;
+    floatx4 o[G::CB];
+#pragma unroll
+    for (int cb = 0; cb < G::CB; ++cb) o[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (k0 < k1) {  // uniform over the workgroup
+      const int32_t* btr = a.bt + row * a.bt_stride;
+      const int tq = tp + min(u, count - 1);
+      u32x4 qf[G::KS];
+      {
+        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + col0 + 8 * g;
+#pragma unroll
+        for (int k = 0; k < G::KS; ++k) qf[k] = ld16(qp + 32 * k);
+      }
+      // the pass's block-table entries go to LDS once, so no K / V load waits on a dependent table load
+      const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
+      const bool pg_local = np <= kMq2Pages;
+      __syncthreads();  // the previous pass's readers of the tiles and pages are done
+      if (pg_local)
+        for (int i = tid; i < np; i += 512)
+          pg_lds[i] = (int32_t)min(max((int64_t)btr[p0 + i], (int64_t)0), a.num_blocks - 1);
+      __syncthreads();
+      auto page_of = [&](int key) -> int64_t {
+        const int p = key / a.block_size;
+        return pg_local ? (int64_t)pg_lds[p - p0] : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+      };
+      u32x4 kr[G::TL], vr[G::TL];
+      // piece c = it * 512 + tid of a tile: key kt + c / CPR, 16-byte piece c % CPR. With 16-row pages (tiles start
+      // on a page) the page is entry kt / 16 + (c / CPR) / 16 and the row (c / CPR) % 16: fixed offsets per thread.
+      const bool page16 = a.block_size == kTile;
+      auto load = [&](u32x4(&r)[G::TL], const uint16_t* base, int kt) {
+#pragma unroll
+        for (int it = 0; it < G::TL; ++it) {
+          const int c = it * 512 + tid, kr_ = c / G::CPR;
+          const int key = min(kt + kr_, k1 - 1);
+          int64_t off;
+          if (page16 && pg_local && kt + kMqKeys <= k1)
+            off = (int64_t)pg_lds[(kt >> 4) - p0 + (kr_ >> 4)] * a.page_stride + (int64_t)(kr_ & 15) * a.row_stride;
+          else
+            off = page_of(key) * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride;
+          r[it] = ld16(base + off + (c % G::CPR) * 8);
+        }
+      };
+      auto store = [&](uint16_t* tile, const u32x4(&r)[G::TL]) {
+#pragma unroll
+        for (int it = 0; it < G::TL; ++it) {
+          const int c = it * 512 + tid;
+          st16(tile + (c / G::CPR) * G::RS + (c % G::CPR) * 8, r[it]);
+        }
+      };
+      load(kr, a.k, k0);
+      load(vr, a.v, k0);
+      store(ks_lds[0], kr);
+      store(vs_lds, vr);
+      __syncthreads();
+      if (k0 + kMqKeys < k1) {
+        load(kr, a.k, k0 + kMqKeys);
+        load(vr, a.v, k0 + kMqKeys);
+      }
+      int buf = 0;
+      // tile i: K(i + 1) goes to the other K buffer before the exchange barrier and K(i + 2) is requested right
+      // after it; V(i + 1) replaces V(i) after the P V barrier and V(i + 2) is requested then: every load has about
+      // one tile of time before it is needed
+      for (int kt = k0; kt < k1; kt += kMqKeys) {
+        const bool more = kt + kMqKeys < k1, more2 = kt + 2 * kMqKeys < k1;
+        {  // S^T partials over this wave's columns
+          const uint16_t* kp = ks_lds[buf] + l16 * G::RS + col0 + 8 * g;
+          floatx4 sp[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+          for (int k = 0; k < G::KS; ++k) {
+            sp[0] = mfma16x16x32(*reinterpret_cast<const u32x4*>(kp + 32 * k), qf[k], sp[0]);
+            sp[1] = mfma16x16x32(*reinterpret_cast<const u32x4*>(kp + 16 * G::RS + 32 * k), qf[k], sp[1]);
+          }
+          xs[par][wave][0][lane] = sp[0];
+          xs[par][wave][1][lane] = sp[1];
+        }
+        if (more) store(ks_lds[buf ^ 1], kr);  // every wave finished reading that buffer before the last barrier
+        __syncthreads();
+        if (more2) load(kr, a.k, kt + 2 * kMqKeys);
+        float p[2][4];
+        {  // full scores (own + partner partial), online softmax of row l16 (keys 16kb + 4g + r in this lane)
+          const floatx4 mine0 = xs[par][wave][0][lane], mine1 = xs[par][wave][1][lane];
+          const floatx4 other0 = xs[par][wave ^ 1][0][lane], other1 = xs[par][wave ^ 1][1][lane];
+          float sc[2][4];
+          const bool full = kt + kMqKeys <= own_n;  // wave-uniform: no key of the tile is past the row's history
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float s0 = (half == 0 ? mine0[r] + other0[r] : other0[r] + mine0[r]) * a.scale_log2;
+            const float s1 = (half == 0 ? mine1[r] + other1[r] : other1[r] + mine1[r]) * a.scale_log2;
+            sc[0][r] = full || kt + 4 * g + r < own_n ? s0 : -INFINITY;
+            sc[1][r] = full || kt + 16 + 4 * g + r < own_n ? s1 : -INFINITY;
+          }
+          float mx = sc[0][0];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+          mx = fmaxf(mx, __shfl_xor(mx, 16));
+          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
+          if (__any(raise)) {
+            const float m_new = raise ? mx : m_own;
+            const float alpha = fast_exp2(m_own - m_new);  // 0 on the first raise (m_own = -inf)
+            l_own *= alpha;
+            m_own = m_new;
+#pragma unroll
+            for (int cb = 0; cb < G::CB; ++cb) o[cb] *= alpha;
+          }
+          const float m_use = m_own == -INFINITY ? 0.f : m_own;
+          float ps = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              p[kb][r] = fast_exp2(sc[kb][r] - m_use);
+              ps += p[kb][r];
+            }
+          ps += __shfl_xor(ps, 16);
+          ps += __shfl_xor(ps, 32);
+          l_own += ps;
+        }
+        {  // O^T += V^T P^T (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
+          const u32x4 pb = {pack2(p[0][0], p[0][1]), pack2(p[0][2], p[0][3]), pack2(p[1][0], p[1][1]),
+                            pack2(p[1][2], p[1][3])};
+          const uint16_t* vp = vs_lds + (4 * g + (l16 >> 2)) * G::RS + col0 + 4 * (l16 & 3);
+#pragma unroll
+          for (int cb = 0; cb < G::CB; ++cb) {
+            const short4v lo =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
+            const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v*)(vp + 16 * G::RS + 16 * cb));
+            const u32x4 vt = join_tr(lo, hi);
+            o[cb] = mfma16x16x32(vt, pb, o[cb]);
+          }
+        }
+        par ^= 1;
+        if (more) {
+          __syncthreads();  // every wave's P V of this tile is done with the V buffer
+          store(vs_lds, vr);
+          if (more2) load(vr, a.v, kt + 2 * kMqKeys);
+          buf ^= 1;
+        }
+      }
+    }
+    if (u < count) {  // lane holds O^T[col 16cb + 4g + r][head l16] of token tp + u
+      const int t = tp + u, h = l16;
+      const bool any = l_own > 0.f;
+      const float inv = any ? 1.0f / l_own : 0.f;
+#pragma unroll
+      for (int cb = 0; cb < G::CB; ++cb) {
+        const int col = col0 + 16 * cb + 4 * g;
+        const floatx4 v = o[cb] * inv;
+        if (a.direct)
+          *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
+              uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+        else
+          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
+      }
+      if (half == 0 && g == 0) {
+        const float lse = any ? (m_own + log2f(l_own)) * kLn2 : -INFINITY;
+        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
+      }
+    }
     tp = te;
   }
 }
@@ -1279,7 +1505,9 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && R <= 512)
+    if (p.group == 4 && R <= 512 && HLA_MQ_V2)
+      hipLaunchKernelGGL(history_mq2<R <= 512 ? R : 512>, grid, dim3(512), 0, stream, p);
+    else if (p.group == 4 && R <= 512)
       hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
     else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);

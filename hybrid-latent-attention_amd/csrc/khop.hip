@@ -7,7 +7,7 @@
 //                                               dq = dS k,    dk = dS^T q
 //
 // Every kernel works on steps of 32 query rows (2 tokens x 16 heads) x 32 keys with 8 waves. The operand tiles sit
-// in LDS (row-major, rows padded by 8 elements): score blocks S = Q K^T and dP = dZ V^T are 16 x 16 blocks on
+// in LDS (row-major, rows padded by 16 elements): score blocks S = Q K^T and dP = dZ V^T are 16 x 16 blocks on
 // v_mfma_f32_16x16x32_bf16 with both operands read as 16-byte rows (k = latent column); the products over keys or
 // rows (P V, dS K, P^T dZ, dS^T Q) take their k-contiguous operand from a small bf16 LDS block and the other one
 // transposed by ds_read_b64_tr_b16, and split the R output columns over the 8 waves. P and dS enter the second
@@ -56,7 +56,8 @@ struct KhopParams {
 
 template <int R>
 struct KhGeo {
-  static constexpr int RS = R + 8;            // LDS row stride of the operand tiles (bf16)
+  static constexpr int RS = R + 16;           // LDS row stride of the operand tiles (bf16): rows 8 banks apart, so
+                                              // 16-byte row reads and the transposing reads are conflict-free
   static constexpr int CPR = R / 8;           // 16-byte pieces per row
   static constexpr int TL = 32 * CPR / kKhThreads;  // pieces per thread per 32-row tile
   static constexpr int QW = R / 8;            // output columns per wave
@@ -117,10 +118,7 @@ __device__ __forceinline__ u32x4 kh_tr(const uint16_t* tile, int c0) {
   const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
   const short4v hi =
       __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(p + 4 * G::RS));
-  return u32x4{(uint32_t)(uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16),
-               (uint32_t)(uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16),
-               (uint32_t)(uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16),
-               (uint32_t)(uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16)};
+  return join_tr(lo, hi);
 }
 
 // out[16 mb .. +16][wave columns] += Pb[16 mb + m][k < 32] * T[k][col] (T a row-major LDS tile over 32 rows).
