@@ -102,6 +102,12 @@ struct HistoryParams {
   bool direct;   // one split writing the final output and lse (else split partials to the workspace)
   bool combine;  // launch history_combine after the split kernel (with more than one split)
   WindowPart win;
+  // contiguous-row form (history_mq2 only): with bt == null, token t reads table row t / tok_per_row whose page p
+  // is row * bt_cols + p; lse then goes to [rows, 16, tok_per_row]; mask (when set) hides key j of token t where
+  // mask[t * mask_st + j] == 0
+  int tok_per_row;
+  const uint8_t* mask;
+  int64_t mask_st;
 };
 
 template <int R>
@@ -602,7 +608,7 @@ __device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4
 }
 
 __device__ __forceinline__ int64_t table_row(const HistoryParams& a, int t) {
-  return a.bt_rows ? a.bt_rows[t] : (int64_t)t;
+  return a.bt_rows ? a.bt_rows[t] : a.tok_per_row > 0 ? (int64_t)(t / a.tok_per_row) : (int64_t)t;
 }
 
 // Writes token t's result of split s: the normalized output and lse (one split) or the split partial.
@@ -984,7 +990,7 @@ struct Mq2Geo {
   static_assert(TL >= 1 && KS >= 1, "R must be at least 128");
 };
 
-template <int R>
+template <int R, bool kContig>
 __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
   using G = Mq2Geo<R>;
   __shared__ __attribute__((aligned(16))) uint16_t ks_lds[2][kMqKeys * G::RS];
@@ -1024,8 +1030,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 #pragma unroll
     for (int cb = 0; cb < G::CB; ++cb) o[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (k0 < k1) {  // uniform over the workgroup
-      const int32_t* btr = a.bt + row * a.bt_stride;
+      const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
       const int tq = tp + min(u, count - 1);
+      const uint8_t* mrow = kContig && a.mask ? a.mask + (int64_t)tq * a.mask_st : nullptr;
       u32x4 qf[G::KS];
       {
         const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + col0 + 8 * g;
@@ -1036,13 +1043,15 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
       const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
       const bool pg_local = np <= kMq2Pages;
       __syncthreads();  // the previous pass's readers of the tiles and pages are done
+      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row (identity pages: contiguous rows)
+        return kContig ? row * a.bt_cols + p : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+      };
       if (pg_local)
-        for (int i = tid; i < np; i += 512)
-          pg_lds[i] = (int32_t)min(max((int64_t)btr[p0 + i], (int64_t)0), a.num_blocks - 1);
+        for (int i = tid; i < np; i += 512) pg_lds[i] = (int32_t)table_page(p0 + i);
       __syncthreads();
       auto page_of = [&](int key) -> int64_t {
         const int p = key / a.block_size;
-        return pg_local ? (int64_t)pg_lds[p - p0] : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+        return pg_local ? (int64_t)pg_lds[p - p0] : table_page(p);
       };
       u32x4 kr[G::TL], vr[G::TL];
       // piece c = it * 512 + tid of a tile: key kt + c / CPR, 16-byte piece c % CPR. With 16-row pages (tiles start
@@ -1102,13 +1111,15 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
           const floatx4 mine0 = xs[par][wave][0][lane], mine1 = xs[par][wave][1][lane];
           const floatx4 other0 = xs[par][wave ^ 1][0][lane], other1 = xs[par][wave ^ 1][1][lane];
           float sc[2][4];
-          const bool full = kt + kMqKeys <= own_n;  // wave-uniform: no key of the tile is past the row's history
+          // wave-uniform: no key of the tile is past the row's history and no mask applies
+          const bool full = kt + kMqKeys <= own_n && (!kContig || !mrow);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float s0 = (half == 0 ? mine0[r] + other0[r] : other0[r] + mine0[r]) * a.scale_log2;
             const float s1 = (half == 0 ? mine1[r] + other1[r] : other1[r] + mine1[r]) * a.scale_log2;
-            sc[0][r] = full || kt + 4 * g + r < own_n ? s0 : -INFINITY;
-            sc[1][r] = full || kt + 16 + 4 * g + r < own_n ? s1 : -INFINITY;
+            const int j0 = kt + 4 * g + r, j1 = kt + 16 + 4 * g + r;
+            sc[0][r] = full || (j0 < own_n && (!kContig || !mrow || mrow[j0])) ? s0 : -INFINITY;
+            sc[1][r] = full || (j1 < own_n && (!kContig || !mrow || mrow[j1])) ? s1 : -INFINITY;
           }
           float mx = sc[0][0];
 #pragma unroll
@@ -1176,7 +1187,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
       }
       if (half == 0 && g == 0) {
         const float lse = any ? (m_own + log2f(l_own)) * kLn2 : -INFINITY;
-        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        if (kContig)
+          a.lse[((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row] = lse;
+        else if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
         else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
       }
     }
@@ -1506,7 +1519,7 @@ int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
     if (p.group == 4 && R <= 512 && HLA_MQ_V2)
-      hipLaunchKernelGGL(history_mq2<R <= 512 ? R : 512>, grid, dim3(512), 0, stream, p);
+      hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512)
       hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
     else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
@@ -1605,6 +1618,51 @@ int dispatch_combine(const HistoryParams& p, int width, hipStream_t st) {
 }
 
 }  // namespace
+}  // namespace hla
+
+namespace hla {
+// Multi-query forward over contiguous rows for the K-hop op (hla_s6_khop_forward): q / z [B * Lq, 16, width]
+// (token strides q_st / z_st), k / v [B, N, width] with row stride k_sn (batch stride N * k_sn, N a multiple of
+// 16), mask [B * Lq, N] bytes (row stride mask_st) or null, bound [B * Lq]. Returns HLA_S6_EUNSUPPORTED when the
+// shapes do not fit this kernel (the caller then uses its own).
+int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
+                    int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
+                    void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream) {
+  if (!HLA_MQ_V2 || N % kTile != 0 || (width != 128 && width != 256 && width != 512)) return HLA_S6_EUNSUPPORTED;
+  HistoryParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_st = q_st;
+  p.q_sh = q_sh;
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.page_stride = kTile * k_sn;
+  p.row_stride = k_sn;
+  p.block_size = kTile;
+  p.num_blocks = (int64_t)B * (N / kTile);
+  p.bt = nullptr;
+  p.bt_cols = N / kTile;
+  p.tok_per_row = Lq;
+  p.ctx = bound;
+  p.scale_log2 = scale * kLog2e;
+  p.num_splits = 1;
+  p.T = B * Lq;
+  p.out = static_cast<uint16_t*>(z);
+  p.o_st = z_st;
+  p.o_sh = z_sh;
+  p.lse = lse;
+  p.group = kMqTokens;
+  p.shared_rows = true;
+  p.direct = true;
+  p.mask = mask;
+  p.mask_st = mask_st;
+  const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
+  switch (width) {
+    case 128: hipLaunchKernelGGL((history_mq2<128, true>), grid, dim3(512), 0, stream, p); break;
+    case 256: hipLaunchKernelGGL((history_mq2<256, true>), grid, dim3(512), 0, stream, p); break;
+    default: hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p); break;
+  }
+  return check_launch("khop_forward");
+}
 }  // namespace hla
 
 extern "C" int hla_s6_history_attention(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,

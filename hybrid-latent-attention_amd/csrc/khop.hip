@@ -580,6 +580,13 @@ extern "C" int hla_s6_khop_forward(const void* q, int64_t q_sb, int64_t q_si, in
   if (rc != HLA_S6_OK) return rc;
   if (Lq == 0) return HLA_S6_OK;
   HLA_REQUIRE(bound && z && lse, HLA_S6_EINVAL, "khop_forward: null bound / output");
+  // rows linear in the token index (t = b * Lq + i): the multi-query history kernel of the serving path runs it
+  if (q_sb == (int64_t)Lq * q_si && z_sb == (int64_t)Lq * z_si && k_sn == v_sn && k_sb == (int64_t)N * k_sn &&
+      v_sb == (int64_t)N * v_sn && (!mask || m_sb == (int64_t)Lq * m_si)) {
+    rc = khop_forward_mq(q, q_si, q_sh, k, v, k_sn, B, Lq, N, width, mask, m_si, bound, scale, z, z_si, z_sh, lse,
+                         as_stream(stream));
+    if (rc != HLA_S6_EUNSUPPORTED) return rc;
+  }
   KhopParams p = {};
   p.q = static_cast<const uint16_t*>(q);
   p.q_sb = q_sb; p.q_si = q_si; p.q_sh = q_sh;
