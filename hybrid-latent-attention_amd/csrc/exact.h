@@ -145,10 +145,17 @@ __device__ __forceinline__ bool decode_window_range(const int32_t* qsl, const in
                                                     int window, int& req, int& lo, int& hi) {
   lo = hi = 0;
   req = 0;
-  if (t >= qsl[R]) return false;
-  req = request_of(qsl, R, t);
-  const int lq = qsl[req + 1] - qsl[req];
-  const int p = seq_lens[req] - lq + (t - qsl[req]);
+  // one query per request up to token t (a decode batch): token t is request t, found with two independent loads
+  // instead of a dependent binary search
+  const bool direct = t < R && qsl[t] == t && qsl[t + 1] == t + 1;
+  if (!direct) {
+    if (t >= qsl[R]) return false;
+    req = request_of(qsl, R, t);
+  } else {
+    req = t;
+  }
+  const int lq = direct ? 1 : qsl[req + 1] - qsl[req];
+  const int p = seq_lens[req] - lq + (direct ? 0 : t - qsl[req]);
   if (p >= 0) {
     lo = max(0, p - window);
     hi = p + 1;
