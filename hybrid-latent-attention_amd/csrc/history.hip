@@ -1624,11 +1624,13 @@ namespace hla {
 // Multi-query forward over contiguous rows for the K-hop op (hla_s6_khop_forward): q / z [B * Lq, 16, width]
 // (token strides q_st / z_st), k / v [B, N, width] with row stride k_sn (batch stride N * k_sn, N a multiple of
 // 16), mask [B * Lq, N] bytes (row stride mask_st) or null, bound [B * Lq]. Returns HLA_S6_EUNSUPPORTED when the
-// shapes do not fit this kernel (the caller then uses its own).
+// shapes do not fit this kernel or another kernel is faster for them (the caller then uses its own).
 int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
                     int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
                     void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream) {
-  if (!HLA_MQ_V2 || N % kTile != 0 || (width != 128 && width != 256 && width != 512)) return HLA_S6_EUNSUPPORTED;
+  // measured at B=4, L=2880: width 512 runs faster here than in khop_fwd (1.67 vs 2.1 ms), width 256 slower
+  // (1.26 vs 1.08 ms)
+  if (!HLA_MQ_V2 || N % kTile != 0 || width != 512) return HLA_S6_EUNSUPPORTED;
   HistoryParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
