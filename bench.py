@@ -492,8 +492,8 @@ def main():
     args = parse()
     world = int(os.environ.get('WORLD_SIZE', '1'))
     if args.gpus != 1 or world != 1:
-        print('bench.py measures one GPU: the S6 decode path shards by sequence with no exchange, and this build has '
-              'no multi-GPU path; run with --gpus 1', file=sys.stderr)
+        print('bench.py measures one GPU: the S6 decode path shards by sequence with no exchange, and this '
+              'implementation has no multi-GPU path; run with --gpus 1', file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print('bench.py needs an MI355X GPU', file=sys.stderr)
