@@ -3,8 +3,9 @@
 // One workgroup computes 64 tokens x 64 output columns of one head: 4 waves, each 16 tokens x 4 column
 // tiles of 16, on v_mfma_f32_16x16x32_bf16. Every global load of the workgroup is issued before the first
 // barrier: the whole weight slab w[h, :, 64 columns] (K x 128 bytes) and each wave's x rows (the A operand,
-// k contiguous, straight into MFMA layout). The slab is written to LDS transposed (column-major) so that the
-// B operand is one 16-byte LDS read per lane. Epilogues:
+// k contiguous, straight into MFMA layout). The slab goes to LDS row-major with 16-byte stores (rows 72 elements
+// apart: conflict-free) and the B operand (8 consecutive k of one column) comes back by two ds_read_b64_tr_b16.
+// Epilogues:
 //   * STORE: bf16 result;
 //   * ROPE: latent RoPE of the bf16-rounded product (fused latent_query); the four column tiles are then
 //     {c, c+16, c+N/2, c+N/2+16}, so every lane holds both rotation partners of its outputs.
@@ -32,7 +33,7 @@ struct AbsorbParams {
 
 template <int K, int EPI>
 __global__ __launch_bounds__(256) void absorb_kernel(AbsorbParams a) {
-  constexpr int LS = K + 8;             // LDS row stride (one output column per row), bf16
+  constexpr int LS = 72;                // LDS row stride of the slab (one k per row, 64 columns + 8), bf16
   constexpr int CH = K / 32;            // 16-byte slab pieces per thread (K * 8 pieces / 256 threads)
   extern __shared__ __attribute__((aligned(16))) uint16_t wt[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -83,29 +84,30 @@ __global__ __launch_bounds__(256) void absorb_kernel(AbsorbParams a) {
       }
     }
   }
-  // transpose the slab into LDS: wt[col][k]
+  // the slab into LDS row-major: wt[k][local column], local column 16 i + j is column ct[i] + j
 #pragma unroll
   for (int i = 0; i < CH; ++i) {
     const int c = i * 256 + tid;
     const int kr = c >> 3, cchunk = c & 7;
-    uint16_t* dst = wt + ((cchunk >> 1) * 16 + (cchunk & 1) * 8) * LS + kr;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      dst[(2 * e) * LS] = (uint16_t)(slab[i][e] & 0xffffu);
-      dst[(2 * e + 1) * LS] = (uint16_t)(slab[i][e] >> 16);
-    }
+    st16(wt + kr * LS + cchunk * 8, slab[i]);
   }
   __syncthreads();
 
   floatx4 acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+  // B operand of lane (g, l16): wt[32 kk + 8 g + e][16 i + l16], e < 8 (lane j of a 16-lane group addresses row
+  // 32 kk + 8 g + j / 4, columns 16 i + 4 (j % 4) ..; the transposing read hands lane l16 its column)
+  const uint16_t* tp = wt + (8 * g + (l16 >> 2)) * LS + 4 * (l16 & 3);
 #pragma unroll
   for (int kk = 0; kk < CH; ++kk) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x4 bv = *reinterpret_cast<const u32x4*>(wt + (i * 16 + l16) * LS + 32 * kk + 8 * g);
-      acc[i] = mfma16x16x32(xa[kk], bv, acc[i]);
+      const uint16_t* p = tp + 32 * kk * LS + 16 * i;
+      const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
+      const short4v hi =
+          __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(p + 4 * LS));
+      acc[i] = mfma16x16x32(xa[kk], join_tr(lo, hi), acc[i]);
     }
   }
 
@@ -140,7 +142,7 @@ int launch_k(const AbsorbParams& p, int K, int H, hipStream_t st) {
   switch (K) {
 #define HLA_ABSORB_CASE(KK)                                                                             \
   case KK: {                                                                                            \
-    constexpr int lds = 64 * (KK + 8) * 2;                                                              \
+    constexpr int lds = KK * 72 * 2;                                                                    \
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&absorb_kernel<KK, EPI>), \
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds); \
     if (attr != hipSuccess) return fail(HLA_S6_ELAUNCH, "absorb: LDS size %d rejected", lds);          \
