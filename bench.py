@@ -425,12 +425,32 @@ def export_workload(args, pkg, device):
                                 request_id='bench', cfg=dict(num_layers=layers, rank=RANK, rank_v=RANK, rank1=RANK1),
                                 prompt_ids=[0], first_response_logits=logits)
         whole = time.perf_counter() - t0
+    base = None
+    if not args.no_cpu_baseline:
+        # the same gather on host copies of layer 0's caches (numpy fancy indexing), scaled by the layers
+        main_h, l1_h = (c.view(torch.int16).cpu().numpy() for c in caches[0])
+        bl = [b.long().cpu().numpy() for b in blocks]
+        pos = np.arange(length)
+
+        def run():
+            return np.concatenate((main_h[bl[0][pos // BLOCK], 0, pos % BLOCK], l1_h[bl[1][pos // BLOCK], 0, pos % BLOCK]),
+                                  -1)
+        run()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        base = {'value': round(float(np.median(times)) * 1e6 * layers, 1), 'unit': 'us/request', 'cores': 1,
+                'kind': 'port', 'sample': f'numpy gather of layer 0 ({length} rows of both caches) on host copies, '
+                                          f'median of 3, x{layers} layers; extrapolated'}
     print(json.dumps({'workload': 'export', 'value': round(ms * 1000, 2), 'unit': 'us/request (device gather)',
                       'rows': length, 'layers': layers, 'row_bytes': 2 * (2 * RANK + 2 * RANK1),
                       'bytes_moved': nbytes, 'gbps': round(nbytes / (ms * 1e6), 1),
                       'hbm_frac': round(nbytes / (ms * 1e6) / PEAK_HBM_GBPS, 4), 'steps': args.steps,
                       'whole_export_ms': round(whole * 1000, 1), 'file_bytes': ref['bytes'],
-                      'data': 'synthetic (random caches and block lists)', 'hip_graph': True}), flush=True)
+                      'data': 'synthetic (random caches and block lists)', 'hip_graph': True,
+                      'cpu_baseline': base}), flush=True)
 
 
 def khop_workload(args, pkg, device):
@@ -465,13 +485,40 @@ def khop_workload(args, pkg, device):
     ms_f = time_graph(fwd, args.steps, args.warmup)
     ms_t = time_eager(train, args.steps, args.warmup)
     f_fwd, f_all = hg.flops(pairs, HEADS, R), hg.flops(pairs, HEADS, R, with_backward=True)
+    base = None
+    if not args.no_cpu_baseline:
+        # the oracle's forward + backward (numpy float32) on the last 64 queries of request 0 over all its keys,
+        # scaled by visible (query, key) pairs
+        from oracle import s6_oracle as O
+        f32 = lambda t: t.detach().float().cpu().numpy()
+        n_q = 64
+        qs, ks, vs = f32(q[:1, L - n_q:]), f32(k[:1]), f32(v[:1])
+        ms_ = mask[:1, L - n_q:].cpu().numpy()
+        dzs, dls = f32(dz[:1, L - n_q:]), f32(dlse[:1, :, L - n_q:])
+
+        def run():
+            z_, l_ = O.causal_history(qs, ks, vs, ms_, scale, dtype=np.float32)
+            return O.causal_history_backward(qs, ks, vs, ms_, scale, l_, dzs, dls, dtype=np.float32)
+        run()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        sample_pairs = int(ms_.sum())
+        base = {'value': round(float(np.median(times)) * 1e3 * pairs / sample_pairs, 1),
+                'unit': 'ms per forward+backward', 'cores': len(os.sched_getaffinity(0)), 'kind': 'port',
+                'sample': f'numpy oracle forward + backward (float32) on the last {n_q} queries of request 0 '
+                          f'({sample_pairs} visible pairs), median of 3, scaled by visible pairs ({pairs}); '
+                          f'extrapolated'}
     print(json.dumps({'workload': 'khop', 'value': round(ms_t, 3), 'unit': 'ms per forward+backward',
                       'forward_ms': round(ms_f, 3), 'B': B, 'L': L, 'heads': HEADS, 'width': R,
                       'visible_pairs': pairs, 'forward_tflops': round(f_fwd / (ms_f * 1e9), 1),
                       'train_tflops': round(f_all / (ms_t * 1e9), 1),
                       'forward_mfma_frac': round(f_fwd / (ms_f * 1e9) / PEAK_BF16_TFLOPS, 4),
                       'train_mfma_frac': round(f_all / (ms_t * 1e9) / PEAK_BF16_TFLOPS, 4), 'steps': args.steps,
-                      'data': 'synthetic (randn q, k, v, cotangents)', 'forward_hip_graph': True}), flush=True)
+                      'data': 'synthetic (randn q, k, v, cotangents)', 'forward_hip_graph': True,
+                      'cpu_baseline': base}), flush=True)
 
 
 def time_eager(fn, steps, warmup):
