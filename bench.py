@@ -574,7 +574,9 @@ def main():
         hist = [context + WINDOW] * B                          # `context` latent rows + the exact window
     else:
         hist = [context] * B
-    splits = {w: args.splits or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w)
+    group = 4 if queries >= 16 else 1                        # the step's history_group (StepContext)
+    splits = {w: args.splits or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w,
+                                                     tokens_per_group=group)
               for w in (RANK, RANK1)}
     print(f'bench: building workload {args.workload} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
           f'splits={splits} cus={cus}', file=sys.stderr, flush=True)
