@@ -38,6 +38,8 @@ SIGNATURES = {
     'hla_s6_window_attention': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I64, I32, I64, P, I64, I32, P, I32, P, P,
                                 I32, P, I32, F32, P, I64, I64, P, P],
     'hla_s6_chunk_attention': [P, P, P, I32, I32, I32, I64, I64, I64, I64, I64, I64, P, I32, F32, P, I64, I64, P, P],
+    'hla_s6_chunk_window_attention': [P, P, P, I32, I32, I32, I64, I64, I64, I64, I64, I64, P, P, I32, P, P, I64, I64,
+                                      I64, I32, I64, P, I64, I32, I32, F32, P, I64, I64, P, P],
     'hla_s6_merge_states': [P, I64, I64, P, P, I64, I64, P, P, I32, I32, I32, I32, P, I64, I64, P, P],
     'hla_s6_attend_decode': [P, I64, I64, I32, P, P, I64, I64, I32, I64, P, I64, I32, P, P, P, I64, I64, P, P, I64, I64,
                              I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32, F32, I32, P, I64, P,

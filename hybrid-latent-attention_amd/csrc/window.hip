@@ -82,10 +82,18 @@ struct ChunkParams {
   uint16_t* out;
   int64_t o_st, o_sh;
   float* lse;  // [H, T]
+  // the exact window over the request's history rows [ctx - window, ctx), ctx = seq_len - query_len (chunk_window)
+  ExactSource win;
+  const int32_t* bt;  // per-request block table of the exact cache
+  int64_t bt_stride;
+  int bt_cols;
+  const int32_t* seq_lens;
+  int window;
 };
 
 constexpr int kChunkVS = kExactDim + 16;  // LDS row stride of the V tile (conflict-free transposed reads)
 
+template <bool kWin>
 __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
   __shared__ __attribute__((aligned(16))) uint16_t vs[16 * kChunkVS];
   const int lane = threadIdx.x, hq = lane & 15, g = lane >> 4;
@@ -103,6 +111,16 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
     }
     const bool live = tp < valid_end;
     const int ke = live ? tp + count : 0;  // keys [kb, ke): the request's tokens up to the pass's last query
+    // window keys (history rows [w_lo, w_hi) of the exact cache, visible to every query of the request)
+    int w_lo = 0, w_hi = 0;
+    ExactSource src = a.win;
+    if (kWin && live) {
+      const int r = request_of(a.qsl, a.num_reqs, tp);
+      w_hi = a.seq_lens[r] - (a.qsl[r + 1] - a.qsl[r]);
+      w_lo = max(0, w_hi - a.window);
+      w_hi = max(min(w_hi, a.bt_cols * src.block_size), w_lo);  // never negative: the chunk tiles follow
+      src.table_row = a.bt + (int64_t)r * a.bt_stride;
+    }
     const int tq = tp + min(hq, count - 1);   // query of this lane's column
     u32x4 qb[4];
 #pragma unroll
@@ -112,19 +130,36 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
     for (int nt = 0; nt < 8; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
     const int q_pos = tp + hq;  // this column's query token (keys <= q_pos are visible)
-    for (int k0 = kb; k0 < ke; k0 += 16) {
+    const int nwt = (w_hi - w_lo + 15) / 16;  // window tiles, taken before the chunk's (one online softmax)
+    const int nct = ke > kb ? (ke - kb + 15) / 16 : 0;
+    for (int ti = 0; ti < nwt + nct; ++ti) {
+      const bool wt = kWin && ti < nwt;
+      const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
+      const int kend = wt ? w_hi : ke;
       u32x4 kA[4], vr[4];
-      {
+      if (wt) {
+        const uint16_t *kp, *vp;
+        src.rows(min(k0 + hq, kend - 1), h, 8 * g, kp, vp);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kA[i] = ld16(kp + 32 * i);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const int c = it * 64 + lane, row = c >> 4;
+          src.rows(min(k0 + row, kend - 1), h, (c & 15) * 8, kp, vp);
+          const u32x4 x = ld16(vp);
+          vr[it] = k0 + row < kend ? x : u32x4{0u, 0u, 0u, 0u};
+        }
+      } else {
         const int key = min(k0 + hq, ke - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) kA[i] = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + 32 * i + 8 * g);
-      }
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {  // V rows k0 .. k0+15: chunk c = it*64 + lane is row c/16, piece c%16
-        const int c = it * 64 + lane, row = c >> 4;
-        const int key = min(k0 + row, ke - 1);
-        const u32x4 x = ld16(a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + (c & 15) * 8);
-        vr[it] = k0 + row < ke ? x : u32x4{0u, 0u, 0u, 0u};
+        for (int it = 0; it < 4; ++it) {  // V rows k0 .. k0+15: chunk c = it*64 + lane is row c/16, piece c%16
+          const int c = it * 64 + lane, row = c >> 4;
+          const int key2 = min(k0 + row, ke - 1);
+          const u32x4 x = ld16(a.v + (int64_t)key2 * a.v_st + (int64_t)h * a.v_sh + (c & 15) * 8);
+          vr[it] = k0 + row < ke ? x : u32x4{0u, 0u, 0u, 0u};
+        }
       }
       floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -138,7 +173,8 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int key = k0 + 4 * g + r;
-        sc[r] = (key < ke && key <= q_pos && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
+        const bool vis = wt ? key < kend : key < ke && key <= q_pos;
+        sc[r] = (vis && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
       }
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = wave_max16x4(mx);
@@ -276,6 +312,67 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
-  hipLaunchKernelGGL(chunk_mfma, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0, as_stream(stream), p);
+  hipLaunchKernelGGL(chunk_mfma<false>, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0,
+                     as_stream(stream), p);
   return check_launch("chunk_attention");
+}
+
+extern "C" int hla_s6_chunk_window_attention(const void* q, const void* k, const void* v, int32_t num_tokens,
+                                             int32_t num_heads, int32_t head_dim, int64_t q_st, int64_t q_sh,
+                                             int64_t k_st, int64_t k_sh, int64_t v_st, int64_t v_sh,
+                                             const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs,
+                                             const void* k_cache, const void* v_cache, int64_t page_stride,
+                                             int64_t row_stride, int64_t head_stride, int32_t block_size,
+                                             int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                                             int32_t bt_cols, int32_t window, float scale, void* out, int64_t o_st,
+                                             int64_t o_sh, float* lse, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0 && num_heads > 0, HLA_S6_EINVAL, "chunk_window_attention: bad token/head count");
+  HLA_REQUIRE(head_dim == kExactDim, HLA_S6_EUNSUPPORTED,
+              "chunk_window_attention: head_dim %d (the kernel is built for 128)", head_dim);
+  HLA_REQUIRE(window >= 0 && block_size > 0 && num_blocks >= 1 && bt_cols >= 0, HLA_S6_EINVAL,
+              "chunk_window_attention: bad window, block size, cache size or table width");
+  if (num_tokens == 0) return HLA_S6_OK;
+  HLA_REQUIRE(q && k && v && query_start_loc && seq_lens && num_reqs >= 1 && k_cache && v_cache && block_table &&
+                  out && lse,
+              HLA_S6_EINVAL, "chunk_window_attention: null pointer or no request");
+  HLA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out) && aligned16(k_cache) &&
+                  aligned16(v_cache) && q_st % 8 == 0 && q_sh % 8 == 0 && k_st % 8 == 0 && k_sh % 8 == 0 &&
+                  v_st % 8 == 0 && v_sh % 8 == 0 && o_st % 8 == 0 && o_sh % 8 == 0 && page_stride % 8 == 0 &&
+                  row_stride % 8 == 0 && head_stride % 8 == 0,
+              HLA_S6_EINVAL, "chunk_window_attention: rows must be 16-byte aligned");
+  ChunkParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.q_st = q_st;
+  p.q_sh = q_sh;
+  p.k_st = k_st;
+  p.k_sh = k_sh;
+  p.v_st = v_st;
+  p.v_sh = v_sh;
+  p.qsl = query_start_loc;
+  p.num_reqs = num_reqs;
+  p.T = num_tokens;
+  p.scale_log2 = scale * kLog2e;
+  p.out = static_cast<uint16_t*>(out);
+  p.o_st = o_st;
+  p.o_sh = o_sh;
+  p.lse = lse;
+  p.win.k = static_cast<const uint16_t*>(k_cache);
+  p.win.v = static_cast<const uint16_t*>(v_cache);
+  p.win.paged = true;
+  p.win.page_stride = page_stride;
+  p.win.row_stride = row_stride;
+  p.win.head_stride = head_stride;
+  p.win.num_blocks = num_blocks;
+  p.win.block_size = block_size;
+  p.bt = block_table;
+  p.bt_stride = bt_stride;
+  p.bt_cols = bt_cols;
+  p.seq_lens = seq_lens;
+  p.window = window;
+  hipLaunchKernelGGL(chunk_mfma<true>, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0,
+                     as_stream(stream), p);
+  return check_launch("chunk_window_attention");
 }

@@ -167,15 +167,15 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     if fused:
         o_chunk, lse_chunk = s6_ops.window_attention_fa(q_rope, window[0], window[1], ctx.query_start_loc, ctx.seq_lens,
                                                         ctx.window, ctx.scale, ctx.max_seqlen_k, ctx.invalid)
+    elif window is not None and has_history:  # the chunk and its exact window history in one softmax
+        o_chunk, lse_chunk = s6_ops.chunk_window_attention(q_rope, k_rope, v, ctx.query_start_loc, ctx.seq_lens,
+                                                           window[0], window[1], ctx.window, ctx.scale,
+                                                           ctx.backends.chunk)
     else:
         o_chunk, lse_chunk = s6_ops.chunk_attention(q_rope, k_rope, v, ctx.query_start_loc, ctx.max_query_len,
                                                     ctx.invalid, ctx.scale, ctx.backends.chunk)
     if not has_history:
         return o_chunk.masked_fill_(ctx.invalid[:, None, None], 0)
-    if window is not None:
-        o_win, lse_win = s6_ops.window_history_fa(q_rope, window[0], ctx.block_table(window[1]), ctx.ctx, ctx.window,
-                                                  ctx.scale, ctx.max_seqlen_k, ctx.empty)
-        o_chunk, lse_chunk = s6_ops.merge_lse(o_chunk, lse_chunk, o_win, lse_win)
     _, B, _ = sl.readers(loop)
     w = q_lat.shape[-1]
     o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,

@@ -356,6 +356,38 @@ def chunk_attention(q, k, v, query_start_loc, max_query_len, invalid, scale, bac
     return o, lse
 
 
+def chunk_window_attention(q, k, v, query_start_loc, seq_lens, cache, block_table, window, scale, backend):
+    """``chunk_attention`` merged with ``window_history_fa`` in one softmax: every token of request ``r`` attends to
+    the exact-cache history rows ``[ctx_r - window, ctx_r)`` (``ctx_r = seq_lens[r] - query length``, read through
+    the per-request ``block_table``) and to its request's chunk tokens up to itself.
+
+    Same outputs as ``merge_lse(chunk_attention(...), window_history_fa(...))`` up to the bf16 rounding of the two
+    partial outputs, which the one-pass form does not make; ``cache`` is ``[num_blocks, H, block, 2d]`` (K then V).
+    """
+    _backend('chunk', backend)
+    _dev(q, k, v, query_start_loc, seq_lens, cache, block_table)
+    for name, t in (('q', q), ('k', k), ('v', v), ('cache', cache)):
+        _bf16(name, t)
+    qsl = _int('query_start_loc', query_start_loc, I32)
+    sl = _int('seq_lens', seq_lens, I32)
+    T, H, d = q.shape
+    R = qsl.shape[0] - 1
+    if cache.dim() != 4 or cache.shape[1] != H or cache.shape[-1] != 2 * d:
+        raise ValueError(f'exact cache must be [num_blocks, {H}, block, {2 * d}], got {tuple(cache.shape)}')
+    if block_table.dtype != I32 or block_table.stride(-1) != 1:
+        raise ValueError('block_table must be int32 with a unit last stride')
+    if block_table.shape[0] < R or sl.shape[0] < R:
+        raise ValueError(f'per-request block_table / seq_lens need {R} rows')
+    o = torch.empty(T, H, d, dtype=BF16, device=q.device)
+    lse = torch.empty(H, T, dtype=torch.float32, device=q.device)
+    _lib.call('hla_s6_chunk_window_attention', _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), T, H, d, q.stride(0),
+              q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1), _lib.ptr(qsl), _lib.ptr(sl), R,
+              _lib.ptr(cache), _lib.ptr(cache[..., d:]), cache.stride(0), cache.stride(2), cache.stride(1),
+              cache.shape[2], cache.shape[0], _lib.ptr(block_table), block_table.stride(0), block_table.shape[1],
+              int(window), float(scale), _lib.ptr(o), o.stride(0), o.stride(1), _lib.ptr(lse), _lib.stream(q.device))
+    return o, lse
+
+
 def merge_states(o_hist, lse_hist, o_chunk, lse_chunk, invalid, backend):
     """LSE merge of two partial softmaxes; ``[T,H,D]`` outputs, ``[H,T]`` fp32 lse; ``invalid`` rows are zeroed.
 

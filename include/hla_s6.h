@@ -167,6 +167,22 @@ int hla_s6_chunk_attention(const void *q, const void *k, const void *v, int32_t 
                            int64_t v_st, int64_t v_sh, const int32_t *query_start_loc, int32_t num_reqs,
                            float scale, void *out, int64_t o_st, int64_t o_sh, float *lse, void *stream);
 
+/* ---- a7+a6: causal current chunk and its exact window history in one softmax ----------------------
+ * Replaces the prefill / mixed-step sequence of hla/vllm_latent/s6_layer.py:101-110: chunk_attention
+ * (s6_ops.py:234-259), window_history_fa (s6_ops.py:334-350) and merge_lse (s6_ops.py:353-361). Every token of
+ * request r attends to the exact-cache rows [ctx_r - window, ctx_r), ctx_r = seq_lens[r] - (query_start_loc[r+1] -
+ * query_start_loc[r]), read through the per-request block_table (rows >= bt_cols * block_size are not read), and
+ * causally to its own chunk tokens. Cache geometry as hla_s6_window_attention (K at k_cache, V at v_cache, same
+ * strides). Tokens >= query_start_loc[num_reqs] get o = 0, lse = -inf. */
+int hla_s6_chunk_window_attention(const void *q, const void *k, const void *v, int32_t num_tokens,
+                                  int32_t num_heads, int32_t head_dim, int64_t q_st, int64_t q_sh, int64_t k_st,
+                                  int64_t k_sh, int64_t v_st, int64_t v_sh, const int32_t *query_start_loc,
+                                  const int32_t *seq_lens, int32_t num_reqs, const void *k_cache, const void *v_cache,
+                                  int64_t page_stride, int64_t row_stride, int64_t head_stride, int32_t block_size,
+                                  int64_t num_blocks, const int32_t *block_table, int64_t bt_stride, int32_t bt_cols,
+                                  int32_t window, float scale, void *out, int64_t o_st, int64_t o_sh, float *lse,
+                                  void *stream);
+
 /* ---- a8: LSE merge of two partial attentions -----------------------------------------------------
  * mode 0 replaces s6_ops.merge_states (hla/vllm_latent/s6_ops.py:262-284): +inf lse counts as empty,
  *   both empty -> 0, rows with invalid[t] != 0 -> 0 (invalid nullable); lse_out must be NULL.

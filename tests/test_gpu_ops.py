@@ -223,6 +223,37 @@ def test_chunk_attention(ops, qsl, T):
     assert_lse_close(host_f32(lse), want_lse)
 
 
+@pytest.mark.parametrize('lens,hist,pad', [((5, 1, 14, 0, 0), (0, 40, 7, 3, 0), 4),   # no history, short history,
+                                           ((100, 1, 299, 13), (33, 90, 0, 17), 7)])  # empty requests, padding
+def test_chunk_window_attention(ops, lens, hist, pad):
+    """The one-softmax chunk + exact window against the oracle's chunk, window history and LSE merge."""
+    rng = np.random.default_rng(sum(lens) + pad)
+    H, d, W, block = 16, 128, 32, 16
+    lens, hist = np.array(lens, np.int64), np.array(hist, np.int64)
+    R = len(lens)
+    qsl = np.concatenate(([0], np.cumsum(lens))).astype(np.int32)
+    T = int(qsl[-1]) + pad
+    seq = (hist + lens).astype(np.int32)
+    cols = int(-(-max(hist.max(), 1) // block))
+    nb = R * cols + 3
+    table = (1 + rng.permutation(nb - 1)[:R * cols]).reshape(R, cols).astype(np.int32)
+    cache = random_bits(rng, (nb, H, block, 2 * d))
+    q, k, v = (random_bits(rng, (T, H, d)) for _ in range(3))
+    req, valid, ctx, _ = O.step_context(qsl, seq, T, W)
+    invalid = ~valid
+    scale = 1 / math.sqrt(d)
+    o, lse = ops.chunk_window_attention(dev_bf16(q), dev_bf16(k), dev_bf16(v), dev_i32(qsl), dev_i32(seq),
+                                        dev_bf16(cache), dev_i32(table), W, scale, 'hip')
+    cf = bf16.to_f32(cache)
+    o_c, l_c = O.chunk_attention(bf16.to_f32(q), bf16.to_f32(k), bf16.to_f32(v), qsl, invalid, scale)
+    o_w, l_w = O.window_history(bf16.to_f32(q), cf[..., :d], cf[..., d:], table[req], ctx, W, scale)
+    want_o, want_lse = O.merge_lse(o_c, l_c, o_w, l_w)
+    assert o.shape == (T, H, d) and lse.shape == (H, T)
+    assert_attention_close(host_f32(o), want_o, 'chunk+window o')
+    assert_lse_close(host_f32(lse), want_lse)
+    assert (host_f32(o)[invalid] == 0).all() and np.isneginf(host_f32(lse)[:, invalid]).all()
+
+
 # ------------------------------------------------------------------------------------------------ merges
 
 def test_merge_states_edge_cases(ops):
