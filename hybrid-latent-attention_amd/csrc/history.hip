@@ -1197,6 +1197,269 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
   }
 }
 
+// history_mq4 (the 512-wide latent): one workgroup per (group of 8 consecutive tokens, KV slot) with 8 waves; wave w
+// owns tokens 2(w/2) and 2(w/2) + 1 of the pass (32 query rows, so every K and V operand read from LDS feeds two
+// MFMAs) and latent column half w % 2. The per-tile phases are those of history_mq2 (S^T partials over the wave's
+// columns, swap of partials with the partner half, online softmax, O^T += V^T P^T with P^T in registers); the K and
+// V tiles go global -> LDS by direct loads (global_load_lds_dwordx4: 64 lanes x 16 bytes, one 1 KB row per
+// instruction, wave w copying rows 4w .. 4w+3) into three rotating tile buffers. At tile i the buffers hold K(i),
+// V(i) and K(i+1); after the exchange barrier V(i+1) replaces K(i), after the P V barrier K(i+2) replaces V(i), so
+// every copy is requested about one tile ahead. The copies are waited for explicitly (s_waitcnt vmcnt counting the
+// copies issued after the awaited one) and the tile loop synchronizes with plain s_barrier behind those waits: a
+// copy still in flight for a later tile is never waited for at a barrier.
+#ifndef HLA_MQ4
+#define HLA_MQ4 1  // 512-wide multi-query steps: history_mq4 (8 tokens per workgroup) instead of history_mq2
+#endif
+constexpr int kMq4Tokens = 8;           // tokens per workgroup
+constexpr int kMq4Keys = 32;            // keys per tile
+constexpr int kMq4RS = 512 + 16;        // LDS row stride (bf16): rows 8 banks apart, as in history_mq2
+constexpr int kMq4Buf = kMq4Keys * kMq4RS;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
+
+// One direct global -> LDS copy of 16 bytes per lane: lane i reads 16 bytes at row + voff (row wave-uniform, voff
+// the lane's byte offset) and writes them to LDS address lds + 16 i (lds wave-uniform). Issued as inline assembly
+// so that the compiler neither waits for it before unrelated LDS reads (it cannot tell which tile buffer a copy
+// writes) nor counts it: the caller waits for it with an explicit s_waitcnt.
+__device__ __forceinline__ void copy16_to_lds(const void* row, uint32_t voff, const void* lds) {
+  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(row)
+               : "memory", "m0");
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// A workgroup barrier that waits for nothing by itself: the caller has already waited for what other waves read
+// after it. The empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
+  constexpr int C = 256, KS = C / 32, CB = C / 16, RS = kMq4RS;
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[3][kMq4Buf];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][2][64];  // S^T partials [wave][token][key block][lane]
+  __shared__ int32_t pg_lds[kMq2Pages];
+  __shared__ int64_t red_lds[16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int pair = wave >> 1, half = wave & 1, col0 = half * C;
+  const int S = a.num_splits, s = blockIdx.y;
+  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int t_begin = blockIdx.x * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
+
+  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
+    const int64_t row = table_row(a, tp);
+    int te = tp + 1;
+    while (te < t_end && table_row(a, te) == row) ++te;
+    const int count = te - tp;
+    int n_max = 0, n_tok[2] = {0, 0};
+#pragma unroll
+    for (int v = 0; v < kMq4Tokens; ++v) {
+      const int n = v < count ? (int)min((int64_t)a.ctx[tp + v], cap) : 0;
+      n_max = max(n_max, n);
+      if (v == 2 * pair) n_tok[0] = n;
+      if (v == 2 * pair + 1) n_tok[1] = n;
+    }
+    const int tiles16 = (n_max + kTile - 1) / kTile;
+    const int j0 = S > 1 ? s * chunk : 0;
+    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
+    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);
+    const int own_n[2] = {min(k1, n_tok[0]), min(k1, n_tok[1])};
+    float m_own[2] = {-INFINITY, -INFINITY}, l_own[2] = {0.f, 0.f};
+    floatx4 o[2][CB];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) o[x][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (k0 < k1) {  // uniform over the workgroup
+      const int32_t* btr = a.bt + row * a.bt_stride;
+      u32x4 qf[2][KS];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int tq = tp + min(2 * pair + x, count - 1);
+        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + col0 + 8 * g;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qf[x][k] = ld16(qp + 32 * k);
+      }
+      const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
+      const bool pg_local = np <= kMq2Pages;
+      __syncthreads();  // the previous pass's readers of the tiles and pages are done
+      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row
+        return min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+      };
+      if (pg_local)
+        for (int i = tid; i < np; i += 512) pg_lds[i] = (int32_t)table_page(p0 + i);
+      __syncthreads();
+      // the query loads are complete before the first copy: the compiler does not see the copies, so no wait it
+      // places for an earlier load may end up counting them
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+      const bool page16 = a.block_size == kTile;
+      // rows 4 * wave .. + 3 of the tile at key kt into buffer b (keys past the slot's range read its last row). With
+      // 16-row pages and a whole tile the four rows sit in one page (entry kt / 16 + wave / 4, rows 4 * wave % 16 ..).
+      const uint32_t voff = 16u * lane;
+      auto copy = [&](int b, const uint16_t* base, int kt) {
+        if (page16 && pg_local && kt + kMq4Keys <= k1) {
+          const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 2)]);
+          const uint16_t* src = base + page * a.page_stride + (int64_t)((4 * wave) & 15) * a.row_stride;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) copy16_to_lds(src + i * a.row_stride, voff, &tiles[b][(4 * wave + i) * RS]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = min(kt + 4 * wave + i, k1 - 1), p = key / a.block_size;
+            const int64_t page = uniform64(pg_local ? (int64_t)pg_lds[p - p0] : table_page(p));
+            copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
+                          &tiles[b][(4 * wave + i) * RS]);
+          }
+        }
+      };
+      const int ntiles = (k1 - k0 + kMq4Keys - 1) / kMq4Keys;
+      int kb = 0, vb = 1, nk = 2;
+      copy(kb, a.k, k0);
+      copy(vb, a.v, k0);
+      if (ntiles > 1) {
+        copy(nk, a.k, k0 + kMq4Keys);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 15));  // K(0) landed; V(0) and K(1) may be in flight
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 15));
+      }
+      plain_barrier();
+      for (int i = 0; i < ntiles; ++i) {
+        const int kt = k0 + i * kMq4Keys;
+        const bool more = i + 1 < ntiles, more2 = i + 2 < ntiles;
+        {  // S^T partials of both tokens over this wave's columns
+          const uint16_t* kp = &tiles[kb][l16 * RS + col0 + 8 * g];
+          floatx4 sp[2][2];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k = 0; k < KS; ++k) {
+            const u32x4 ka = *reinterpret_cast<const u32x4*>(kp + 32 * k);
+            const u32x4 kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * k);
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              sp[x][0] = mfma16x16x32(ka, qf[x][k], sp[x][0]);
+              sp[x][1] = mfma16x16x32(kc, qf[x][k], sp[x][1]);
+            }
+          }
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            xs[wave][x][0][lane] = sp[x][0];
+            xs[wave][x][1][lane] = sp[x][1];
+          }
+        }
+        // V(i) landed (only K(i+1) may still be in flight) and the partials are in LDS
+        if (more) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+        plain_barrier();
+        if (more) copy(kb, a.v, kt + kMq4Keys);  // V(i+1) into K(i)'s buffer: every wave is past its S^T
+        u32x4 pb[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {  // full scores, online softmax of row l16 of token x
+          const floatx4 mine0 = xs[wave][x][0][lane], mine1 = xs[wave][x][1][lane];
+          const floatx4 other0 = xs[wave ^ 1][x][0][lane], other1 = xs[wave ^ 1][x][1][lane];
+          const int n = own_n[x];
+          float sc[2][4];
+          const bool full = kt + kMq4Keys <= n;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float s0 = (half == 0 ? mine0[r] + other0[r] : other0[r] + mine0[r]) * a.scale_log2;
+            const float s1 = (half == 0 ? mine1[r] + other1[r] : other1[r] + mine1[r]) * a.scale_log2;
+            const int j0k = kt + 4 * g + r, j1k = kt + 16 + 4 * g + r;
+            sc[0][r] = full || j0k < n ? s0 : -INFINITY;
+            sc[1][r] = full || j1k < n ? s1 : -INFINITY;
+          }
+          float mx = sc[0][0];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+          mx = fmaxf(mx, __shfl_xor(mx, 16));
+          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
+          if (__any(raise)) {
+            const float m_new = raise ? mx : m_own[x];
+            const float alpha = fast_exp2(m_own[x] - m_new);  // 0 on the first raise (m_own = -inf)
+            l_own[x] *= alpha;
+            m_own[x] = m_new;
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) o[x][cb] *= alpha;
+          }
+          const float m_use = m_own[x] == -INFINITY ? 0.f : m_own[x];
+          float p[2][4], ps = 0.f;
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              p[kb2][r] = fast_exp2(sc[kb2][r] - m_use);
+              ps += p[kb2][r];
+            }
+          ps += __shfl_xor(ps, 16);
+          ps += __shfl_xor(ps, 32);
+          l_own[x] += ps;
+          pb[x] = u32x4{pack2(p[0][0], p[0][1]), pack2(p[0][2], p[0][3]), pack2(p[1][0], p[1][1]),
+                        pack2(p[1][2], p[1][3])};
+        }
+        {  // O^T += V^T P^T for both tokens (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
+          const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) {
+            const short4v lo =
+                __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
+            const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
+            const u32x4 vt = join_tr(lo, hi);
+            o[0][cb] = mfma16x16x32(vt, pb[0], o[0][cb]);
+            o[1][cb] = mfma16x16x32(vt, pb[1], o[1][cb]);
+          }
+        }
+        if (more) {
+          // K(i+1) landed (only V(i+1) may still be in flight); every wave is done with V(i) and the partials
+          __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+          plain_barrier();
+          if (more2) copy(vb, a.k, kt + 2 * kMq4Keys);  // K(i+2) into V(i)'s buffer
+          const int freed = kb;
+          kb = nk;
+          nk = vb;
+          vb = freed;
+        }
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      if (2 * pair + x >= count) continue;
+      const int t = tp + 2 * pair + x, h = l16;  // lane holds O^T[col 16cb + 4g + r][head l16] of token t
+      const bool any = l_own[x] > 0.f;
+      const float inv = any ? 1.0f / l_own[x] : 0.f;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int col = col0 + 16 * cb + 4 * g;
+        const floatx4 v = o[x][cb] * inv;
+        if (a.direct)
+          *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
+              uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+        else
+          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * 512 + col) = v;
+      }
+      if (half == 0 && g == 0) {
+        const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
+        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
+      }
+    }
+    tp = te;
+  }
+}
+
 // Split reduction: one workgroup per (token, head), thread i < R/4 owns output columns [4i, 4i+4).
 template <int R>
 constexpr int combine_threads() { return R / 4 < 64 ? 64 : R / 4; }
@@ -1518,7 +1781,10 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && R <= 512 && HLA_MQ_V2)
+    if (p.group == 4 && R == 512 && HLA_MQ4)
+      hipLaunchKernelGGL(history_mq4, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+                         dim3(512), 0, stream, p);
+    else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
       hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512)
       hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
@@ -1658,11 +1924,7 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.mask = mask;
   p.mask_st = mask_st;
   const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
-  switch (width) {
-    case 128: hipLaunchKernelGGL((history_mq2<128, true>), grid, dim3(512), 0, stream, p); break;
-    case 256: hipLaunchKernelGGL((history_mq2<256, true>), grid, dim3(512), 0, stream, p); break;
-    default: hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p); break;
-  }
+  hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p);
   return check_launch("khop_forward");
 }
 }  // namespace hla

@@ -161,9 +161,9 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per
     row (so that filled slots hold at least that many keys) nor 1024. A function of constants and the row count only
     (graph-stable).
 
-    Multi-query steps (``tokens_per_group`` 4: one 8-wave workgroup per group of four tokens and slot, one per CU
-    for its LDS) want two such workgroups per CU: ``ceil(2 * CUs / groups)`` slots, at least 1 (with 512-token chunks
-    of four requests, one slot: no split reduction at all)."""
+    Multi-query steps (``tokens_per_group`` 4) want about one 8-wave workgroup of eight tokens per CU for the
+    512-wide latent (two of four tokens for narrower ones): ``ceil(2 * CUs / groups)`` slots for ``groups`` four-token
+    groups, at least 1 (with 512-token chunks of four requests, one slot: no split reduction at all)."""
     if tokens_per_group > 1:
         groups = -(-max(1, num_tokens) // tokens_per_group)
         by_length = max(1, 2 * -(-max_seq_len // min_keys_per_split))

@@ -184,6 +184,35 @@ def test_grouped_history_matches_oracle(ops, width, splits, group):
     assert_lse_close(lse, lse1)
 
 
+@pytest.mark.parametrize('block,long_ctx,splits', [(16, 33000, 1),   # more pages than the LDS page list holds
+                                                   (16, 33000, 3),
+                                                   (32, 5003, 1),    # pages of 32 rows
+                                                   (32, 5003, 4)])
+def test_grouped_history_page_geometry(ops, block, long_ctx, splits):
+    """Four-token groups of the 512-wide latent over long rows and other page sizes: request 0 (11 rows) sees
+    ``long_ctx`` rows, request 1 (6 rows) ragged lengths ending inside a tile, request 2 (3 rows) rows of 1-40."""
+    rng = np.random.default_rng(block + long_ctx + splits)
+    width, num_blocks = 512, -(-long_ctx // block) + 64
+    lens = [11, 6, 3]
+    req = np.repeat(np.arange(len(lens)), lens)
+    ctx = np.concatenate([np.full(11, long_ctx), 517 + 5 * np.arange(6), [1, 17, 40]]).astype(np.int32)
+    per_req = np.array([ctx[req == r].max() for r in range(len(lens))])
+    cols = -(-long_ctx // block)
+    table = np.zeros((len(lens), cols), np.int32)
+    for r, n in enumerate(per_req):  # request 0 walks the whole pool in a random order, the others share pages
+        need = -(-int(n) // block)
+        table[r, :need] = rng.permutation(np.arange(1, num_blocks))[:need] if r == 0 else \
+            rng.integers(1, num_blocks, need)
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    q_bits = random_bits(rng, (len(ctx), 16, width))
+    q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    ws = ops.S6Workspace(16, width, len(ctx) * splits)
+    o, lse = ops.history_attention_kv(q, cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx), SCALE,
+                                      splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=4,
+                                      shared_rows=True)
+    check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
+
+
 def test_grouped_history_rejects_unsupported_group(ops):
     q = torch.zeros(2, 16, 512, dtype=torch.bfloat16, device='cuda')
     cache = torch.zeros(4, 1, 16, 1024, dtype=torch.bfloat16, device='cuda')
