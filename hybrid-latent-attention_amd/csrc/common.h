@@ -69,14 +69,28 @@ __device__ __forceinline__ floatx4 mfma16x16x16(short4v a, short4v b, floatx4 c)
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-__device__ __forceinline__ float wave_max16x4(float v) {  // max across lanes l, l^16, l^32, l^48
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
+// Reductions across lanes l, l^16, l^32, l^48 (every lane of the four gets the same value). v_permlane16_swap with
+// both operands v leaves (row 0, row 0, row 2, row 2) in one result and (row 1, row 1, row 3, row 3) in the other,
+// so combining the two pairs each lane with lane l^16; v_permlane32_swap does the same for l^32. VALU only, no LDS
+// round trip; the additions are the ones of the shuffle form, (v_l + v_l^16) + (v_l^32 + v_l^48).
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-__device__ __forceinline__ float wave_sum16x4(float v) {
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float wave_max16x4(float v) { return xor32_max(xor16_max(v)); }
+__device__ __forceinline__ float wave_sum16x4(float v) { return xor32_sum(xor16_sum(v)); }
 
 }  // namespace hla
 

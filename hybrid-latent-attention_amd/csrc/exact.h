@@ -101,8 +101,7 @@ __device__ __forceinline__ void exact_row(const ExactSource& src, const uint16_t
     }
   }
 
-  float M = fmaxf(m, __shfl_xor(m, 16));
-  M = fmaxf(M, __shfl_xor(M, 32));
+  const float M = wave_max16x4(m);
   uint16_t* op = out + d0;
   if (M == -INFINITY) {
     if (grp == 0) st16(op, u32x4{0u, 0u, 0u, 0u});
@@ -110,15 +109,10 @@ __device__ __forceinline__ void exact_row(const ExactSource& src, const uint16_t
     return;
   }
   const float sc = (m == -INFINITY) ? 0.f : fast_exp2(m - M);
-  float L = l * sc;
-  L += __shfl_xor(L, 16);
-  L += __shfl_xor(L, 32);
+  const float L = wave_sum16x4(l * sc);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float x = o[e] * sc;
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
-    o[e] = x;
+    o[e] = wave_sum16x4(o[e] * sc);
   }
   if (grp == 0) {
     const float inv = 1.0f / L;

@@ -1124,8 +1124,7 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
           float mx = sc[0][0];
 #pragma unroll
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-          mx = fmaxf(mx, __shfl_xor(mx, 16));
-          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          mx = wave_max16x4(mx);
           const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own;
@@ -1144,8 +1143,7 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
               p[kb][r] = fast_exp2(sc[kb][r] - m_use);
               ps += p[kb][r];
             }
-          ps += __shfl_xor(ps, 16);
-          ps += __shfl_xor(ps, 32);
+          ps = wave_sum16x4(ps);
           l_own += ps;
         }
         {  // O^T += V^T P^T (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
@@ -1343,14 +1341,18 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           floatx4 sp[2][2];
 #pragma unroll
           for (int x = 0; x < 2; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+          u32x4 ka = *reinterpret_cast<const u32x4*>(kp), kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS);
 #pragma unroll
-          for (int k = 0; k < KS; ++k) {
-            const u32x4 ka = *reinterpret_cast<const u32x4*>(kp + 32 * k);
-            const u32x4 kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * k);
+          for (int k = 0; k < KS; ++k) {  // the next k-step's fragments are requested before this one's MFMAs
+            const u32x4 ca = ka, cc = kc;
+            if (k + 1 < KS) {
+              ka = *reinterpret_cast<const u32x4*>(kp + 32 * (k + 1));
+              kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * (k + 1));
+            }
 #pragma unroll
             for (int x = 0; x < 2; ++x) {
-              sp[x][0] = mfma16x16x32(ka, qf[x][k], sp[x][0]);
-              sp[x][1] = mfma16x16x32(kc, qf[x][k], sp[x][1]);
+              sp[x][0] = mfma16x16x32(ca, qf[x][k], sp[x][0]);
+              sp[x][1] = mfma16x16x32(cc, qf[x][k], sp[x][1]);
             }
           }
 #pragma unroll
@@ -1383,8 +1385,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           float mx = sc[0][0];
 #pragma unroll
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-          mx = fmaxf(mx, __shfl_xor(mx, 16));
-          mx = fmaxf(mx, __shfl_xor(mx, 32));
+          mx = wave_max16x4(mx);
           const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own[x];
@@ -1403,23 +1404,27 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
               p[kb2][r] = fast_exp2(sc[kb2][r] - m_use);
               ps += p[kb2][r];
             }
-          ps += __shfl_xor(ps, 16);
-          ps += __shfl_xor(ps, 32);
+          ps = wave_sum16x4(ps);
           l_own[x] += ps;
           pb[x] = u32x4{pack2(p[0][0], p[0][1]), pack2(p[0][2], p[0][3]), pack2(p[1][0], p[1][1]),
                         pack2(p[1][2], p[1][3])};
         }
         {  // O^T += V^T P^T for both tokens (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
           const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
-#pragma unroll
-          for (int cb = 0; cb < CB; ++cb) {
+          auto vfrag = [&](int cb) {
             const short4v lo =
                 __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
             const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                 (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
-            const u32x4 vt = join_tr(lo, hi);
-            o[0][cb] = mfma16x16x32(vt, pb[0], o[0][cb]);
-            o[1][cb] = mfma16x16x32(vt, pb[1], o[1][cb]);
+            return join_tr(lo, hi);
+          };
+          u32x4 vt = vfrag(0);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs
+            const u32x4 cur = vt;
+            if (cb + 1 < CB) vt = vfrag(cb + 1);
+            o[0][cb] = mfma16x16x32(cur, pb[0], o[0][cb]);
+            o[1][cb] = mfma16x16x32(cur, pb[1], o[1][cb]);
           }
         }
         if (more) {
