@@ -1195,23 +1195,22 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
   }
 }
 
-// history_mq4 (the 512-wide latent): one workgroup per (group of 8 consecutive tokens, KV slot) with 8 waves; wave w
-// owns tokens 2(w/2) and 2(w/2) + 1 of the pass (32 query rows, so every K and V operand read from LDS feeds two
-// MFMAs) and latent column half w % 2. The per-tile phases are those of history_mq2 (S^T partials over the wave's
-// columns, swap of partials with the partner half, online softmax, O^T += V^T P^T with P^T in registers); the K and
-// V tiles go global -> LDS by direct loads (global_load_lds_dwordx4: 64 lanes x 16 bytes, one 1 KB row per
-// instruction, wave w copying rows 4w .. 4w+3) into three rotating tile buffers. At tile i the buffers hold K(i),
-// V(i) and K(i+1); after the exchange barrier V(i+1) replaces K(i), after the P V barrier K(i+2) replaces V(i), so
-// every copy is requested about one tile ahead. The copies are waited for explicitly (s_waitcnt vmcnt counting the
-// copies issued after the awaited one) and the tile loop synchronizes with plain s_barrier behind those waits: a
-// copy still in flight for a later tile is never waited for at a barrier.
+// history_mq4 (the 512- and 256-wide latents): one workgroup per (group of 8 consecutive tokens, KV slot) with 8
+// waves; wave w owns tokens 2(w/2) and 2(w/2) + 1 of the pass (32 query rows, so every K and V operand read from LDS
+// feeds two MFMAs) and latent column half w % 2. The per-tile phases are those of history_mq2 (S^T partials over the
+// wave's columns, swap of partials with the partner half, online softmax, O^T += V^T P^T with P^T in registers); the
+// K and V tiles go global -> LDS by direct loads (global_load_lds_dwordx4: 16 bytes per lane, one row per
+// instruction: all 64 lanes for a 1 KB row, lanes 0-31 for a 512 B one; wave w copies rows 4w .. 4w+3) into three
+// rotating tile buffers. At tile i the buffers hold K(i), V(i) and K(i+1); after the exchange barrier V(i+1) replaces
+// K(i), after the P V barrier K(i+2) replaces V(i), so every copy is requested about one tile ahead. The copies are
+// waited for explicitly (s_waitcnt vmcnt counting the copies issued after the awaited one) and the tile loop
+// synchronizes with plain s_barrier behind those waits: a copy still in flight for a later tile is never waited for
+// at a barrier.
 #ifndef HLA_MQ4
 #define HLA_MQ4 1  // 512-wide multi-query steps: history_mq4 (8 tokens per workgroup) instead of history_mq2
 #endif
 constexpr int kMq4Tokens = 8;           // tokens per workgroup
 constexpr int kMq4Keys = 32;            // keys per tile
-constexpr int kMq4RS = 512 + 16;        // LDS row stride (bf16): rows 8 banks apart, as in history_mq2
-constexpr int kMq4Buf = kMq4Keys * kMq4RS;
 
 // s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
 constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
@@ -1240,9 +1239,12 @@ __device__ __forceinline__ void plain_barrier() {
   asm volatile("" ::: "memory");
 }
 
+template <int R>
 __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
-  constexpr int C = 256, KS = C / 32, CB = C / 16, RS = kMq4RS;
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[3][kMq4Buf];
+  static_assert(R == 512 || R == 256, "rows of 1 KB (one copy instruction) or 512 B (half of one)");
+  // C latent columns per wave; LDS row stride R + 16 keeps rows 8 banks apart, as in history_mq2
+  constexpr int C = R / 2, KS = C / 32, CB = C / 16, RS = R + 16;
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[3][kMq4Keys * RS];
   __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][2][64];  // S^T partials [wave][token][key block][lane]
   __shared__ int32_t pg_lds[kMq2Pages];
   __shared__ int64_t red_lds[16];
@@ -1311,14 +1313,16 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 2)]);
           const uint16_t* src = base + page * a.page_stride + (int64_t)((4 * wave) & 15) * a.row_stride;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) copy16_to_lds(src + i * a.row_stride, voff, &tiles[b][(4 * wave + i) * RS]);
+          for (int i = 0; i < 4; ++i)
+            if (R == 512 || lane < 32) copy16_to_lds(src + i * a.row_stride, voff, &tiles[b][(4 * wave + i) * RS]);
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = min(kt + 4 * wave + i, k1 - 1), p = key / a.block_size;
             const int64_t page = uniform64(pg_local ? (int64_t)pg_lds[p - p0] : table_page(p));
-            copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
-                          &tiles[b][(4 * wave + i) * RS]);
+            if (R == 512 || lane < 32)
+              copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
+                            &tiles[b][(4 * wave + i) * RS]);
           }
         }
       };
@@ -1453,7 +1457,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
               uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
         else
-          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * 512 + col) = v;
+          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
       }
       if (half == 0 && g == 0) {
         const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
@@ -1786,8 +1790,8 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && R == 512 && HLA_MQ4)
-      hipLaunchKernelGGL(history_mq4, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+    if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4)
+      hipLaunchKernelGGL(history_mq4<R == 256 ? 256 : 512>, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
       hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);

@@ -184,15 +184,17 @@ def test_grouped_history_matches_oracle(ops, width, splits, group):
     assert_lse_close(lse, lse1)
 
 
-@pytest.mark.parametrize('block,long_ctx,splits', [(16, 33000, 1),   # more pages than the LDS page list holds
-                                                   (16, 33000, 3),
-                                                   (32, 5003, 1),    # pages of 32 rows
-                                                   (32, 5003, 4)])
-def test_grouped_history_page_geometry(ops, block, long_ctx, splits):
-    """Four-token groups of the 512-wide latent over long rows and other page sizes: request 0 (11 rows) sees
-    ``long_ctx`` rows, request 1 (6 rows) ragged lengths ending inside a tile, request 2 (3 rows) rows of 1-40."""
-    rng = np.random.default_rng(block + long_ctx + splits)
-    width, num_blocks = 512, -(-long_ctx // block) + 64
+@pytest.mark.parametrize('width,block,long_ctx,splits', [(512, 16, 33000, 1),  # more pages than the LDS list holds
+                                                         (512, 16, 33000, 3),
+                                                         (512, 32, 5003, 1),   # pages of 32 rows
+                                                         (512, 32, 5003, 4),
+                                                         (256, 16, 33000, 1),
+                                                         (256, 32, 5003, 4)])
+def test_grouped_history_page_geometry(ops, width, block, long_ctx, splits):
+    """Four-token groups over long rows and other page sizes: request 0 (11 rows) sees ``long_ctx`` rows, request 1
+    (6 rows) ragged lengths ending inside a tile, request 2 (3 rows) rows of 1-40."""
+    rng = np.random.default_rng(width + block + long_ctx + splits)
+    num_blocks = -(-long_ctx // block) + 64
     lens = [11, 6, 3]
     req = np.repeat(np.arange(len(lens)), lens)
     ctx = np.concatenate([np.full(11, long_ctx), 517 + 5 * np.arange(6), [1, 17, 40]]).astype(np.int32)
