@@ -34,6 +34,14 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
 }
 
+// Pack two finite fp32 values into one dword of two bf16 with the hardware conversion (v_cvt_pk_bf16_f32, round to
+// nearest even). Used for softmax probabilities, where it equals pack2 (NaN and denormal inputs do not occur).
+__device__ __forceinline__ uint32_t pack2_hw(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float float2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){a, b}, bf16x2_t));
+}
+
 __device__ __forceinline__ float lo_bf(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_bf(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 

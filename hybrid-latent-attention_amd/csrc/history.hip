@@ -1376,20 +1376,25 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           const floatx4 mine0 = xs[wave][x][0][lane], mine1 = xs[wave][x][1][lane];
           const floatx4 other0 = xs[wave ^ 1][x][0][lane], other1 = xs[wave ^ 1][x][1][lane];
           const int n = own_n[x];
+          // unscaled scores; IEEE addition commutes, so both column halves hold the same values
           float sc[2][4];
-          const bool full = kt + kMq4Keys <= n;
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float s0 = (half == 0 ? mine0[r] + other0[r] : other0[r] + mine0[r]) * a.scale_log2;
-            const float s1 = (half == 0 ? mine1[r] + other1[r] : other1[r] + mine1[r]) * a.scale_log2;
-            const int j0k = kt + 4 * g + r, j1k = kt + 16 + 4 * g + r;
-            sc[0][r] = full || j0k < n ? s0 : -INFINITY;
-            sc[1][r] = full || j1k < n ? s1 : -INFINITY;
+            sc[0][r] = mine0[r] + other0[r];
+            sc[1][r] = mine1[r] + other1[r];
+          }
+          if (kt + kMq4Keys > n) {  // wave-uniform: the tile runs past the row's history
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (kt + 4 * g + r >= n) sc[0][r] = -INFINITY;
+              if (kt + 16 + 4 * g + r >= n) sc[1][r] = -INFINITY;
+            }
           }
           float mx = sc[0][0];
 #pragma unroll
           for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
-          mx = wave_max16x4(mx);
+          // the scale is positive, so the maximum of the scaled scores is the scaled maximum (log2 units)
+          mx = wave_max16x4(mx) * a.scale_log2;
           const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own[x];
@@ -1405,13 +1410,13 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-              p[kb2][r] = fast_exp2(sc[kb2][r] - m_use);
+              p[kb2][r] = fast_exp2(__builtin_fmaf(sc[kb2][r], a.scale_log2, -m_use));
               ps += p[kb2][r];
             }
           ps = wave_sum16x4(ps);
           l_own[x] += ps;
-          pb[x] = u32x4{pack2(p[0][0], p[0][1]), pack2(p[0][2], p[0][3]), pack2(p[1][0], p[1][1]),
-                        pack2(p[1][2], p[1][3])};
+          pb[x] = u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
+                        pack2_hw(p[1][2], p[1][3])};
         }
         {  // O^T += V^T P^T for both tokens (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
           const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
@@ -1790,7 +1795,7 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4)
+    if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)  // mq4 folds a positive scale
       hipLaunchKernelGGL(history_mq4<R == 256 ? 256 : 512>, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
