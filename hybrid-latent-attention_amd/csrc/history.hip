@@ -1390,16 +1390,16 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
               if (kt + 16 + 4 * g + r >= n) sc[1][r] = -INFINITY;
             }
           }
-          float mx = sc[0][0];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) mx = fmaxf(mx, fmaxf(sc[0][r], sc[1][r]));
+          // (scores are finite or -inf: rows past the history are masked before any NaN they hold is used)
+          float mx = max3_nn(max3_nn(sc[0][0], sc[0][1], sc[0][2]), max3_nn(sc[0][3], sc[1][0], sc[1][1]),
+                             max_nn(sc[1][2], sc[1][3]));
           // the scale is positive, so the maximum of the scaled scores is the scaled maximum (log2 units)
-          mx = wave_max16x4(mx) * a.scale_log2;
+          mx = wave_max16x4_nn(mx) * a.scale_log2;
           const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own[x];
             const float alpha = fast_exp2(m_own[x] - m_new);  // 0 on the first raise (m_own = -inf)
-            l_own[x] *= alpha;
+            l_own[x] *= alpha;  // this lane's share of the row sum
             m_own[x] = m_new;
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb) o[x][cb] *= alpha;
@@ -1413,8 +1413,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
               p[kb2][r] = fast_exp2(__builtin_fmaf(sc[kb2][r], a.scale_log2, -m_use));
               ps += p[kb2][r];
             }
-          ps = wave_sum16x4(ps);
-          l_own[x] += ps;
+          l_own[x] += ps;  // the four lanes of a row are summed once, after the last tile
           pb[x] = u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
                         pack2_hw(p[1][2], p[1][3])};
         }
@@ -1448,6 +1447,8 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
         }
       }
     }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) l_own[x] = wave_sum16x4(l_own[x]);
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
       if (2 * pair + x >= count) continue;
