@@ -65,13 +65,6 @@ struct KhGeo {
   static_assert(TL >= 1 && QW >= 16, "R must be at least 128");
 };
 
-__device__ __forceinline__ bool kh_visible(const KhopParams& a, int64_t t, int key) {
-  if (key >= a.bound[t]) return false;
-  if (!a.mask) return true;
-  const int b = (int)(t / a.Lq), i = (int)(t % a.Lq);
-  return a.mask[(int64_t)b * a.m_sb + (int64_t)i * a.m_si + key] != 0;
-}
-
 // Load 32 rows x R of a row-major bf16 matrix into registers (coalesced: piece c = it * 512 + tid is row c / CPR,
 // 16-byte piece c % CPR); rows are addressed by `rowp(r)` (a clamped, in-bounds row pointer).
 template <int R, class RowP>
@@ -138,6 +131,42 @@ __device__ __forceinline__ void kh_accumulate(floatx4 (&acc)[2][KhGeo<R>::CB], c
   }
 }
 
+// ---- row data loaded one step ahead ---------------------------------------------------------------------------
+// What the P / dS role of thread (row sr, keys 2 kp, 2 kp + 1) needs from memory for one step: the row's lse,
+// delta, dlse and key bound, and the mask bytes of its two keys. Loaded one step ahead (plain register loads, used
+// after the next barrier), so their latency is not on the step's critical path.
+struct KhRow {
+  float lse, delta, dlse;
+  int bound;
+  uint8_t m[2];
+};
+
+__device__ __forceinline__ KhRow kh_row_load(const KhopParams& a, int b, int i, int h, int key0, int kp) {
+  KhRow r;
+  const int64_t idx = ((int64_t)b * 16 + h) * a.Lq + i, t = (int64_t)b * a.Lq + i;
+  r.lse = a.lse[idx];
+  r.delta = a.delta[idx];
+  r.dlse = a.dlse ? a.dlse[idx] : 0.f;
+  r.bound = a.bound[t];
+  r.m[0] = r.m[1] = 1;
+  if (a.mask) {
+    const uint8_t* mr = a.mask + (int64_t)b * a.m_sb + (int64_t)i * a.m_si;
+    r.m[0] = mr[min(key0 + 2 * kp, a.N - 1)];
+    r.m[1] = mr[min(key0 + 2 * kp + 1, a.N - 1)];
+  }
+  return r;
+}
+
+// Mask bytes only (the dq kernel keeps its rows for the whole pass).
+__device__ __forceinline__ void kh_mask_load(const KhopParams& a, int b, int i, int key0, int kp, uint8_t (&m)[2]) {
+  m[0] = m[1] = 1;
+  if (a.mask) {
+    const uint8_t* mr = a.mask + (int64_t)b * a.m_sb + (int64_t)i * a.m_si;
+    m[0] = mr[min(key0 + 2 * kp, a.N - 1)];
+    m[1] = mr[min(key0 + 2 * kp + 1, a.N - 1)];
+  }
+}
+
 // ---- forward -------------------------------------------------------------------------------------------------
 // One workgroup per 2 consecutive tokens of a batch row: Q resident in LDS, K/V tiles of 32 keys streamed through
 // LDS (the next tile's loads in flight in registers), online softmax per query row (16 lanes per row).
@@ -169,7 +198,9 @@ __global__ __launch_bounds__(kKhThreads) void khop_fwd(KhopParams a) {
   const int nkeys = max(bound_s[0], bound_s[1]);
   // softmax role: row sr (token sr / 16, head sr % 16), keys 2 kp, 2 kp + 1
   const int sr = tid >> 4, kp = tid & 15;
-  const int64_t st = t0 + min(sr >> 4, ntok - 1);
+  const int row_i = i0 + min(sr >> 4, ntok - 1);
+  const int row_bound = a.bound[t0 + min(sr >> 4, ntok - 1)];
+  uint8_t m_cur[2], m_next[2] = {1, 1};
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[2][G::CB];
 #pragma unroll
@@ -182,13 +213,21 @@ __global__ __launch_bounds__(kKhThreads) void khop_fwd(KhopParams a) {
     kh_load<R>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
     kh_load<R>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
   };
-  if (nkeys > 0) load_kv(0);
+  if (nkeys > 0) {
+    load_kv(0);
+    kh_mask_load(a, b, row_i, 0, kp, m_next);
+  }
   for (int kt = 0; kt < nkeys; kt += kKhKeys) {
     __syncthreads();  // the previous step's readers of ks / vs / ps are done
     kh_store<R>(ks, kr);
     kh_store<R>(vs, vr);
+    m_cur[0] = m_next[0];
+    m_cur[1] = m_next[1];
     __syncthreads();
-    if (kt + kKhKeys < nkeys) load_kv(kt + kKhKeys);
+    if (kt + kKhKeys < nkeys) {
+      load_kv(kt + kKhKeys);
+      kh_mask_load(a, b, row_i, kt + kKhKeys, kp, m_next);
+    }
     {  // S partials: wave w -> block w % 4 (rows 16 (w/2 % 2).., keys 16 (w % 2)..), column half w / 4
       const int blk = wave & 3, half = wave >> 2;
       sx[wave][lane] = kh_block<R>(qs, blk >> 1, ks, blk & 1, half * (R / 2), (half + 1) * (R / 2));
@@ -202,7 +241,7 @@ __global__ __launch_bounds__(kKhThreads) void khop_fwd(KhopParams a) {
         const int key = 2 * kp + e, blk = 2 * rb + (key >> 4);
         const int li = 16 * (r4 >> 2) + (key & 15);
         const float s = sx[blk][li][r4 & 3] + sx[blk + 4][li][r4 & 3];
-        s2[e] = kh_visible(a, st, kt + key) && (sr >> 4) < ntok ? s * a.scale_log2 : -INFINITY;
+        s2[e] = kt + key < row_bound && m_cur[e] && (sr >> 4) < ntok ? s * a.scale_log2 : -INFINITY;
       }
       float mx = fmaxf(s2[0], s2[1]);
 #pragma unroll
@@ -261,12 +300,24 @@ __global__ __launch_bounds__(kKhThreads) void khop_fwd(KhopParams a) {
 }
 
 // ---- backward helpers ----------------------------------------------------------------------------------------
+// Row constants of a query row: lse in the log2 domain (0 for a row without history: all its P are 0 anyway) and
+// delta - dlse.
+__device__ __forceinline__ void kh_row_consts(const KhRow& r, float& lse2, float& dd) {
+  const bool empty = !(r.lse > -INFINITY);
+  lse2 = empty ? 0.f : r.lse * kLog2e;
+  dd = r.delta - (empty ? 0.f : r.dlse);
+}
+
+// bf16 of one finite fp32 value by the hardware conversion (round to nearest even)
+__device__ __forceinline__ uint16_t f2bf_hw(float x) { return (uint16_t)pack2_hw(x, 0.f); }
+
 // P and dS of a 32-row x 32-key step from the S blocks (waves 0-3) and dP blocks (waves 4-7) in sx, written as
 // bf16 to pb / dsb in [row][key] order (kTransposed: [key][row]). Row constants of row sr: lse2 (log2 domain),
-// delta - dlse in dd.
+// delta - dlse in dd; key key0 + 2 kp + e is visible when row_ok, below the row's bound and its mask byte is set.
 template <bool kTransposed>
 __device__ __forceinline__ void kh_pds(const KhopParams& a, const floatx4 (*sx)[64], uint16_t* pb, uint16_t* dsb,
-                                       int64_t t_row, bool row_ok, int key0, float lse2, float dd) {
+                                       int bound, const uint8_t (&m)[2], bool row_ok, int key0, float lse2,
+                                       float dd) {
   const int tid = threadIdx.x, sr = tid >> 4, kp = tid & 15;
   const int rb = sr >> 4, r4 = sr & 15;
   float p[2], ds[2];
@@ -275,30 +326,20 @@ __device__ __forceinline__ void kh_pds(const KhopParams& a, const floatx4 (*sx)[
     const int key = 2 * kp + e, blk = 2 * rb + (key >> 4);
     const int li = 16 * (r4 >> 2) + (key & 15);
     const float s = sx[blk][li][r4 & 3], dp = sx[blk + 4][li][r4 & 3];
-    const bool vis = row_ok && kh_visible(a, t_row, key0 + key);
+    const bool vis = row_ok && key0 + key < bound && m[e] != 0;
     p[e] = vis ? fast_exp2(s * a.scale_log2 - lse2) : 0.f;
     ds[e] = p[e] * (dp - dd) * a.scale;
   }
   if (kTransposed) {
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      pb[(2 * kp + e) * kKhPS + sr] = f2bf(p[e]);
-      dsb[(2 * kp + e) * kKhPS + sr] = f2bf(ds[e]);
+      pb[(2 * kp + e) * kKhPS + sr] = f2bf_hw(p[e]);
+      dsb[(2 * kp + e) * kKhPS + sr] = f2bf_hw(ds[e]);
     }
   } else {
-    *reinterpret_cast<uint32_t*>(pb + sr * kKhPS + 2 * kp) = pack2(p[0], p[1]);
-    *reinterpret_cast<uint32_t*>(dsb + sr * kKhPS + 2 * kp) = pack2(ds[0], ds[1]);
+    *reinterpret_cast<uint32_t*>(pb + sr * kKhPS + 2 * kp) = pack2_hw(p[0], p[1]);
+    *reinterpret_cast<uint32_t*>(dsb + sr * kKhPS + 2 * kp) = pack2_hw(ds[0], ds[1]);
   }
-}
-
-// Row constants of a query row: lse in the log2 domain (0 for a row without history: all its P are 0 anyway) and
-// delta - dlse.
-__device__ __forceinline__ void kh_row_consts(const KhopParams& a, int b, int i, int h, float& lse2, float& dd) {
-  const int64_t idx = ((int64_t)b * 16 + h) * a.Lq + i;
-  const float lse = a.lse[idx];
-  const bool empty = !(lse > -INFINITY);
-  lse2 = empty ? 0.f : lse * kLog2e;
-  dd = a.delta[idx] - (a.dlse && !empty ? a.dlse[idx] : 0.f);
 }
 
 // ---- backward: dq ----------------------------------------------------------------------------------------------
@@ -334,11 +375,13 @@ __global__ __launch_bounds__(kKhThreads) void khop_dq(KhopParams a) {
   }
   __syncthreads();
   const int nkeys = max(bound_s[0], bound_s[1]);
-  const int sr = tid >> 4;
+  const int sr = tid >> 4, kp = tid & 15;
   const bool row_ok = (sr >> 4) < ntok;
-  const int64_t st = t0 + min(sr >> 4, ntok - 1);
+  const int row_i = i0 + min(sr >> 4, ntok - 1);
+  const KhRow row = kh_row_load(a, b, row_i, sr & 15, 0, kp);
   float lse2, dd;
-  kh_row_consts(a, b, i0 + min(sr >> 4, ntok - 1), sr & 15, lse2, dd);
+  kh_row_consts(row, lse2, dd);
+  uint8_t m_cur[2] = {row.m[0], row.m[1]}, m_next[2] = {1, 1};
   floatx4 acc[2][G::CB];
 #pragma unroll
   for (int mb = 0; mb < 2; ++mb)
@@ -355,14 +398,19 @@ __global__ __launch_bounds__(kKhThreads) void khop_dq(KhopParams a) {
     kh_store<R>(ks, kr);
     kh_store<R>(vs, vr);
     __syncthreads();
-    if (kt + kKhKeys < nkeys) load_kv(kt + kKhKeys);
+    if (kt + kKhKeys < nkeys) {
+      load_kv(kt + kKhKeys);
+      kh_mask_load(a, b, row_i, kt + kKhKeys, kp, m_next);
+    }
     {  // waves 0-3: S block w; waves 4-7: dP block w - 4 (full R)
       const int blk = wave & 3;
       sx[wave][lane] = wave < 4 ? kh_block<R>(qs, blk >> 1, ks, blk & 1, 0, R)
                                 : kh_block<R>(dzs, blk >> 1, vs, blk & 1, 0, R);
     }
     __syncthreads();
-    kh_pds<false>(a, sx, pb, dsb, st, row_ok, kt, lse2, dd);
+    kh_pds<false>(a, sx, pb, dsb, row.bound, m_cur, row_ok, kt, lse2, dd);
+    m_cur[0] = m_next[0];
+    m_cur[1] = m_next[1];
     __syncthreads();
     kh_accumulate<R>(acc, dsb, ks);  // dQ += dS K
   }
@@ -414,8 +462,9 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
   for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
     for (int cb = 0; cb < G::CB; ++cb) dk_acc[mb][cb] = dv_acc[mb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int sr = tid >> 4;
+  const int sr = tid >> 4, kp = tid & 15;
   u32x4 qr[G::TL], dzr[G::TL];
+  KhRow row_next;
   auto load_rows = [&](int step) {
     const int i0 = 2 * step, ntok = min(2, a.Lq - i0);
     kh_load<R>(qr, [&](int r) {
@@ -426,6 +475,7 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
       const int tok = min(r >> 4, ntok - 1);
       return a.dz + (int64_t)b * a.dz_sb + (int64_t)(i0 + tok) * a.dz_si + (int64_t)(r & 15) * a.dz_sh;
     });
+    row_next = kh_row_load(a, b, i0 + min(sr >> 4, ntok - 1), sr & 15, kt, kp);
   };
   auto sees_tile = [&](int step) {  // either token of the step has candidate keys in this tile
     const int i0 = 2 * step;
@@ -440,6 +490,7 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
     __syncthreads();  // previous step's readers of qs / dzs / pt / dst are done
     kh_store<R>(qs, qr);
     kh_store<R>(dzs, dzr);
+    const KhRow row = row_next;
     __syncthreads();
     int next = step + 1;
     while (next < s_end && !sees_tile(next)) ++next;
@@ -451,11 +502,9 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
     }
     __syncthreads();
     {
-      const bool row_ok = (sr >> 4) < ntok;
-      const int tok = min(sr >> 4, ntok - 1);
       float lse2, dd;
-      kh_row_consts(a, b, i0 + tok, sr & 15, lse2, dd);
-      kh_pds<true>(a, sx, pt, dst, (int64_t)b * a.Lq + i0 + tok, row_ok, kt, lse2, dd);
+      kh_row_consts(row, lse2, dd);
+      kh_pds<true>(a, sx, pt, dst, row.bound, row.m, (sr >> 4) < ntok, kt, lse2, dd);
     }
     __syncthreads();
     kh_accumulate<R>(dv_acc, pt, dzs);  // dV += P^T dZ
