@@ -1225,6 +1225,12 @@ __device__ __forceinline__ void copy16_to_lds(const void* row, uint32_t voff, co
                : "memory", "m0");
 }
 
+// The same with a per-lane source address (64-bit, in VGPRs).
+__device__ __forceinline__ void copy16_to_lds_v(const void* src, const void* lds) {
+  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
+}
+
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
@@ -1239,13 +1245,21 @@ __device__ __forceinline__ void plain_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int R>
+// kMode 0: paged rows; 1: contiguous rows (identity pages: row t / tok_per_row, lse [rows, 16, tok_per_row]);
+// 2: contiguous rows with a visibility mask (key j of token t visible where mask[t * mask_st + j] != 0; the mask
+// bytes of a tile travel with its K copy into LDS, 32 per token, so the loop issues no other global load).
+template <int R, int kMode>
 __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
   static_assert(R == 512 || R == 256, "rows of 1 KB (one copy instruction) or 512 B (half of one)");
+  constexpr bool kContig = kMode != 0, kMask = kMode == 2;
+  constexpr int KOPS = kMask ? 5 : 4;  // copy instructions per wave for a K tile (4 rows, and its mask bytes)
   // C latent columns per wave; LDS row stride R + 16 keeps rows 8 banks apart, as in history_mq2
   constexpr int C = R / 2, KS = C / 32, CB = C / 16, RS = R + 16;
   __shared__ __attribute__((aligned(16))) uint16_t tiles[3][kMq4Keys * RS];
   __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][2][64];  // S^T partials [wave][token][key block][lane]
+  // mask bytes [tile parity][column half][pair][token of the pair * 32 + key] (one copy per column half, each
+  // written by its own wave)
+  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[kMask ? 2 : 1][2][4][64];
   __shared__ int32_t pg_lds[kMq2Pages];
   __shared__ int64_t red_lds[16];
 
@@ -1283,7 +1297,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) o[x][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (k0 < k1) {  // uniform over the workgroup
-      const int32_t* btr = a.bt + row * a.bt_stride;
+      const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
       u32x4 qf[2][KS];
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
@@ -1295,8 +1309,8 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
       const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
       const bool pg_local = np <= kMq2Pages;
       __syncthreads();  // the previous pass's readers of the tiles and pages are done
-      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row
-        return min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row (identity pages: contiguous rows)
+        return kContig ? row * a.bt_cols + p : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
       };
       if (pg_local)
         for (int i = tid; i < np; i += 512) pg_lds[i] = (int32_t)table_page(p0 + i);
@@ -1308,7 +1322,17 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
       // rows 4 * wave .. + 3 of the tile at key kt into buffer b (keys past the slot's range read its last row). With
       // 16-row pages and a whole tile the four rows sit in one page (entry kt / 16 + wave / 4, rows 4 * wave % 16 ..).
       const uint32_t voff = 16u * lane;
+      // mask bytes of this wave's two tokens for the tile at key kt: lanes 0-3, token l / 2, bytes 16 (l % 2) ..
+      // (a chunk past the row's end is read from its last 16 bytes instead: those keys are past every bound)
+      auto copy_mask = [&](int kt) {
+        if (lane < 4) {
+          const int tq = tp + min(2 * pair + (lane >> 1), count - 1);
+          const int c0 = min(kt + 16 * (lane & 1), (int)cap - 16);
+          copy16_to_lds_v(a.mask + (int64_t)tq * a.mask_st + c0, &mk_lds[((kt - k0) / kMq4Keys) & 1][half][pair][0]);
+        }
+      };
       auto copy = [&](int b, const uint16_t* base, int kt) {
+        if (kMask && base == a.k) copy_mask(kt);
         if (page16 && pg_local && kt + kMq4Keys <= k1) {
           const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 2)]);
           const uint16_t* src = base + page * a.page_stride + (int64_t)((4 * wave) & 15) * a.row_stride;
@@ -1332,7 +1356,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
       copy(vb, a.v, k0);
       if (ntiles > 1) {
         copy(nk, a.k, k0 + kMq4Keys);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(8, 15));  // K(0) landed; V(0) and K(1) may be in flight
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(4 + KOPS, 15));  // K(0) landed; V(0) and K(1) may be in flight
       } else {
         __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 15));
       }
@@ -1366,7 +1390,7 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           }
         }
         // V(i) landed (only K(i+1) may still be in flight) and the partials are in LDS
-        if (more) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+        if (more) __builtin_amdgcn_s_waitcnt(waitcnt_imm(KOPS, 0));
         else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
         plain_barrier();
         if (more) copy(kb, a.v, kt + kMq4Keys);  // V(i+1) into K(i)'s buffer: every wave is past its S^T
@@ -1383,7 +1407,15 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
             sc[0][r] = mine0[r] + other0[r];
             sc[1][r] = mine1[r] + other1[r];
           }
-          if (kt + kMq4Keys > n) {  // wave-uniform: the tile runs past the row's history
+          if (kMask) {  // mask bytes of keys 4g + r and 16 + 4g + r of token x
+            const uint8_t* mb = &mk_lds[i & 1][half][pair][32 * x + 4 * g];
+            const uint32_t m0 = *reinterpret_cast<const uint32_t*>(mb), m1 = *reinterpret_cast<const uint32_t*>(mb + 16);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (kt + 4 * g + r >= n || ((m0 >> (8 * r)) & 255u) == 0) sc[0][r] = -INFINITY;
+              if (kt + 16 + 4 * g + r >= n || ((m1 >> (8 * r)) & 255u) == 0) sc[1][r] = -INFINITY;
+            }
+          } else if (kt + kMq4Keys > n) {  // wave-uniform: the tile runs past the row's history
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               if (kt + 4 * g + r >= n) sc[0][r] = -INFINITY;
@@ -1467,7 +1499,9 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
       }
       if (half == 0 && g == 0) {
         const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
-        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        if (kContig)
+          a.lse[((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row] = lse;
+        else if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
         else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
       }
     }
@@ -1797,7 +1831,7 @@ int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
     if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)  // mq4 folds a positive scale
-      hipLaunchKernelGGL(history_mq4<R == 256 ? 256 : 512>, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+      hipLaunchKernelGGL((history_mq4<R == 256 ? 256 : 512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
       hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
@@ -1909,9 +1943,11 @@ namespace hla {
 int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
                     int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
                     void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream) {
-  // measured at B=4, L=2880: width 512 runs faster here than in khop_fwd (1.67 vs 2.1 ms), width 256 slower
-  // (1.26 vs 1.08 ms)
-  if (!HLA_MQ_V2 || N % kTile != 0 || width != 512) return HLA_S6_EUNSUPPORTED;
+  // widths 512 and 256 run faster here than in khop_fwd; history_mq4 takes a positive scale and a mask whose rows
+  // start on 16-byte boundaries (its bytes are copied in 16-byte pieces), history_mq2 (width 512) anything else
+  const bool mq4 = HLA_MQ4 && (width == 512 || width == 256) && scale > 0.f &&
+                   (!mask || (((uintptr_t)mask & 15u) == 0 && mask_st % 16 == 0));
+  if (!HLA_MQ_V2 || N % kTile != 0 || !(mq4 || width == 512)) return HLA_S6_EUNSUPPORTED;
   HistoryParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
@@ -1938,8 +1974,16 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.direct = true;
   p.mask = mask;
   p.mask_st = mask_st;
-  const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
-  hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p);
+  if (mq4) {
+    const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
+    if (width == 512 && mask) hipLaunchKernelGGL((history_mq4<512, 2>), grid4, dim3(512), 0, stream, p);
+    else if (width == 512) hipLaunchKernelGGL((history_mq4<512, 1>), grid4, dim3(512), 0, stream, p);
+    else if (mask) hipLaunchKernelGGL((history_mq4<256, 2>), grid4, dim3(512), 0, stream, p);
+    else hipLaunchKernelGGL((history_mq4<256, 1>), grid4, dim3(512), 0, stream, p);
+  } else {
+    const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
+    hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p);
+  }
   return check_launch("khop_forward");
 }
 }  // namespace hla
