@@ -381,25 +381,36 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   const int hq = lane & 15, g = lane >> 4;
   const int kb = key0 + 4 * g;
   float sc[4];
+  if (key0 + kTile <= n) {  // wave-uniform: every key of the tile is history
 #pragma unroll
-  for (int r = 0; r < 4; ++r) sc[r] = (kb + r < n) ? s[r] * scale_log2 : -INFINITY;
-  float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  mx = wave_max16x4(mx);
-  const float m_new = fmaxf(m, mx);
-  const float alpha = fast_exp2(m - m_new);
+    for (int r = 0; r < 4; ++r) sc[r] = s[r] * scale_log2;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = (kb + r < n) ? s[r] * scale_log2 : -INFINITY;
+  }
+  // (scores are finite or -inf: rows past the history are masked before any NaN they hold is used)
+  const float mx = wave_max16x4_nn(max_nn(max_nn(sc[0], sc[1]), max_nn(sc[2], sc[3])));
+  // the running maximum is raised lazily, only when a tile exceeds it by more than 2^8 (the exponentials stay
+  // below 2^8), which skips the rescale of the accumulators on most tiles
+  const bool raise = mx > m + 8.f;  // false while the row has no key yet (mx = -inf)
+  if (__any(raise)) {
+    const float m_new = raise ? mx : m;
+    const float alpha = fast_exp2(m - m_new);  // 0 on the first raise (m = -inf)
+    l *= alpha;
+    m = m_new;
+#pragma unroll
+    for (int nt = 0; nt < G::NT; ++nt) oacc[nt] = oacc[nt] * alpha;
+  }
+  const float m_use = m == -INFINITY ? 0.f : m;
   float p[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_new);
-  const float ps = wave_sum16x4((p[0] + p[1]) + (p[2] + p[3]));
-  l = l * alpha + ps;
-  m = m_new;
-  short4v pb;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) pb[r] = (short)f2bf(p[r]);
+  for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_use);
+  l += (p[0] + p[1]) + (p[2] + p[3]);  // this lane's share of the row sum (the 4 lanes are summed at the end)
+  const uint32_t p01 = pack2_hw(p[0], p[1]), p23 = pack2_hw(p[2], p[3]);
+  const short4v pb = {(short)(p01 & 0xffffu), (short)(p01 >> 16), (short)(p23 & 0xffffu), (short)(p23 >> 16)};
 #pragma unroll
   for (int nt = 0; nt < G::NT; ++nt) {
     const short4v va = vt_operand<R>(vs, nt, g, hq);
-    oacc[nt] = oacc[nt] * alpha;
     oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
   }
 }
@@ -508,6 +519,7 @@ void history_split(HistoryParams a) {
       }
     }
 
+    l = wave_sum16x4(l);
     const float inv = 1.0f / l;
     const float lse = (m + log2f(l)) * kLn2;
     if (a.direct) {
