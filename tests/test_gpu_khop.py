@@ -94,6 +94,59 @@ def test_forward_and_backward_match_the_oracle(R, kind, B, Lq, N):
     assert (got['dq'][empty] == 0).all()
 
 
+@pytest.mark.parametrize('R', [256, 512])
+@pytest.mark.parametrize('kind,B,Lq,N', [('benchmark', 2, 48, 48), ('khop', 2, 19, 64), ('any', 3, 29, 96)])
+def test_key_counts_of_whole_pages_match_the_oracle(R, kind, B, Lq, N):
+    """N a multiple of 16: the forward runs on the multi-query history kernel (eight tokens per workgroup, the mask
+    bytes copied to LDS with each K tile); token counts that do not fill the last workgroup, rows without history."""
+    q, k, v, mask = case(5 * R + N, B, Lq, N, R, kind)
+    scale = 1 / math.sqrt(128)
+    rng = np.random.default_rng(R * N)
+    dz = bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32))
+    dlse = rng.standard_normal((B, 16, Lq)).astype(np.float32)
+    got = run(q, k, v, mask, scale, dz=dz, dlse=dlse)
+    z, lse = O.causal_history(q, k, v, mask, scale)
+    assert_attention_close(got['z'], z, 'z')
+    assert_lse_close(got['lse'], lse)
+    empty = ~mask.any(-1)
+    assert (got['z'][empty] == 0).all() and np.isneginf(got['lse'].transpose(0, 2, 1)[empty]).all()
+    dq, dk, dv = O.causal_history_backward(q, k, v, mask, scale, lse, dz, dlse)
+    assert_grad_close(got['dq'], dq, 'dq')
+    assert_grad_close(got['dk'], dk, 'dk')
+    assert_grad_close(got['dv'], dv, 'dv')
+
+
+@pytest.mark.parametrize('R', [256, 512])
+def test_mask_rows_off_16_byte_boundaries_and_no_mask(R):
+    """A mask view whose rows do not start on 16-byte boundaries takes the other forward kernels; the C ABI without a
+    mask (every key below the bound visible) takes the multi-query kernel's unmasked form. Same results as the
+    oracle."""
+    B, Lq, N = 2, 21, 64
+    q, k, v, mask = case(17 + R, B, Lq, N, R, 'any')
+    scale = 0.11
+    wide = np.zeros((B, Lq, N + 8), bool)
+    wide[..., :N] = mask
+    qt, kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (q, k, v))
+    mt = torch.tensor(wide, device='cuda')[..., :N]
+    assert mt.stride(1) % 16 != 0
+    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale)
+    zo, lo = O.causal_history(q, k, v, mask, scale)
+    assert_attention_close(z.float().cpu().numpy(), zo, 'z (strided mask)')
+    assert_lse_close(lse.cpu().numpy(), lo)
+    lib = hg._lib
+    bound = torch.empty(B * Lq, dtype=torch.int32, device='cuda')
+    st = lib.stream(qt.device)
+    lib.call('hla_s6_khop_bounds', None, 0, 0, B, Lq, N, lib.ptr(bound), st)
+    z2 = torch.empty(B, Lq, 16, R, dtype=torch.bfloat16, device='cuda')
+    lse2 = torch.empty(B, 16, Lq, dtype=torch.float32, device='cuda')
+    lib.call('hla_s6_khop_forward', lib.ptr(qt), qt.stride(0), qt.stride(1), qt.stride(2), lib.ptr(kt), kt.stride(0),
+             kt.stride(1), lib.ptr(vt), vt.stride(0), vt.stride(1), None, 0, 0, lib.ptr(bound), B, Lq, N, 16, R,
+             scale, lib.ptr(z2), z2.stride(0), z2.stride(1), z2.stride(2), lib.ptr(lse2), st)
+    zo2, lo2 = O.causal_history(q, k, v, np.ones((B, Lq, N), bool), scale)
+    assert_attention_close(z2.float().cpu().numpy(), zo2, 'z (no mask)')
+    assert_lse_close(lse2.cpu().numpy(), lo2)
+
+
 def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
     q, k, v, mask = case(3, 2, 30, 30, 256, 'benchmark')
     rng = np.random.default_rng(4)
