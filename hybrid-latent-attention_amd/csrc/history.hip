@@ -1406,9 +1406,8 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
         else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
         plain_barrier();
         if (more) copy(kb, a.v, kt + kMq4Keys);  // V(i+1) into K(i)'s buffer: every wave is past its S^T
-        u32x4 pb[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {  // full scores, online softmax of row l16 of token x
+        // online softmax of row l16 of token x over the full scores; returns P^T packed as the B operand
+        auto softmax_tok = [&](int x) -> u32x4 {
           const floatx4 mine0 = xs[wave][x][0][lane], mine1 = xs[wave][x][1][lane];
           const floatx4 other0 = xs[wave ^ 1][x][0][lane], other1 = xs[wave ^ 1][x][1][lane];
           const int n = own_n[x];
@@ -1458,25 +1457,27 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
               ps += p[kb2][r];
             }
           l_own[x] += ps;  // the four lanes of a row are summed once, after the last tile
-          pb[x] = u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
-                        pack2_hw(p[1][2], p[1][3])};
-        }
-        {  // O^T += V^T P^T for both tokens (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
-          const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
-          auto vfrag = [&](int cb) {
-            const short4v lo =
-                __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
-            const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
-            return join_tr(lo, hi);
-          };
+          return u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
+                       pack2_hw(p[1][2], p[1][3])};
+        };
+        // O^T += V^T P^T (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
+        const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
+        auto vfrag = [&](int cb) {
+          const short4v lo =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
+          return join_tr(lo, hi);
+        };
+        {
+          const u32x4 pb0 = softmax_tok(0), pb1 = softmax_tok(1);
           u32x4 vt = vfrag(0);
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs
-            const u32x4 cur = vt;
+          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs; it feeds both
+            const u32x4 cur = vt;           // tokens' MFMAs
             if (cb + 1 < CB) vt = vfrag(cb + 1);
-            o[0][cb] = mfma16x16x32(cur, pb[0], o[0][cb]);
-            o[1][cb] = mfma16x16x32(cur, pb[1], o[1][cb]);
+            o[0][cb] = mfma16x16x32(cur, pb0, o[0][cb]);
+            o[1][cb] = mfma16x16x32(cur, pb1, o[1][cb]);
           }
         }
         if (more) {
