@@ -120,6 +120,41 @@ __device__ __forceinline__ float wave_max16x4_nn(float v) {
 }
 __device__ __forceinline__ float wave_sum16x4(float v) { return xor32_sum(xor16_sum(v)); }
 
+
+// ---- direct global -> LDS copies and the waits that go with them -----------------------------------------------
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
+
+// One direct global -> LDS copy of 16 bytes per lane: lane i reads 16 bytes at row + voff (row wave-uniform, voff
+// the lane's byte offset) and writes them to LDS address lds + 16 i (lds wave-uniform). Issued as inline assembly
+// so that the compiler neither waits for it before unrelated LDS reads (it cannot tell which tile buffer a copy
+// writes) nor counts it: the caller waits for it with an explicit s_waitcnt.
+__device__ __forceinline__ void copy16_to_lds(const void* row, uint32_t voff, const void* lds) {
+  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(row)
+               : "memory", "m0");
+}
+
+// The same with a per-lane source address (64-bit, in VGPRs).
+__device__ __forceinline__ void copy16_to_lds_v(const void* src, const void* lds) {
+  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
+}
+
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// A workgroup barrier that waits for nothing by itself: the caller has already waited for what other waves read
+// after it. The empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 }  // namespace hla
 
 // ---- host-side error plumbing (api.hip) ----------------------------------------------------------

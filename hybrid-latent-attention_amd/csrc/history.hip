@@ -1224,39 +1224,6 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 constexpr int kMq4Tokens = 8;           // tokens per workgroup
 constexpr int kMq4Keys = 32;            // keys per tile
 
-// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
-constexpr int waitcnt_imm(int vm, int lgkm) { return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | ((lgkm & 15) << 8); }
-
-// One direct global -> LDS copy of 16 bytes per lane: lane i reads 16 bytes at row + voff (row wave-uniform, voff
-// the lane's byte offset) and writes them to LDS address lds + 16 i (lds wave-uniform). Issued as inline assembly
-// so that the compiler neither waits for it before unrelated LDS reads (it cannot tell which tile buffer a copy
-// writes) nor counts it: the caller waits for it with an explicit s_waitcnt.
-__device__ __forceinline__ void copy16_to_lds(const void* row, uint32_t voff, const void* lds) {
-  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(row)
-               : "memory", "m0");
-}
-
-// The same with a per-lane source address (64-bit, in VGPRs).
-__device__ __forceinline__ void copy16_to_lds_v(const void* src, const void* lds) {
-  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
-}
-
-__device__ __forceinline__ int64_t uniform64(int64_t v) {
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
-  return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-
-// A workgroup barrier that waits for nothing by itself: the caller has already waited for what other waves read
-// after it. The empty asm statements keep the compiler from moving memory accesses across it.
-__device__ __forceinline__ void plain_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // kMode 0: paged rows; 1: contiguous rows (identity pages: row t / tok_per_row, lse [rows, 16, tok_per_row]);
 // 2: contiguous rows with a visibility mask (key j of token t visible where mask[t * mask_st + j] != 0; the mask
 // bytes of a tile travel with its K copy into LDS, 32 per token, so the loop issues no other global load).

@@ -20,6 +20,10 @@
 namespace hla {
 namespace {
 
+#ifndef HLA_KH_DQ4
+#define HLA_KH_DQ4 1  // dq on khop_dq4 (4 tokens per workgroup, direct tile copies) where the shapes allow
+#endif
+
 constexpr int kKhRows = 32;   // query rows per step (2 tokens x 16 heads)
 constexpr int kKhKeys = 32;   // keys per step
 constexpr int kKhThreads = 512;
@@ -429,6 +433,169 @@ __global__ __launch_bounds__(kKhThreads) void khop_dq(KhopParams a) {
   }
 }
 
+// ---- backward: dq on the multi-query layout ---------------------------------------------------------------
+// khop_dq4: one workgroup per 4 consecutive tokens of a batch row, 8 waves; wave w serves token w / 2 and, for the
+// score blocks, role w % 2: role 0 computes S^T = K Q^T and role 1 dP^T = V dZ^T over all R columns (the token's
+// Q^T or dZ^T in registers as the MFMA B operand, the 16-byte K or V rows of the tile as the A operand). The pair
+// swaps the two 32-key x 16-row blocks through LDS; both waves then form P = exp(S scale - lse) and
+// dS = P (dP - delta + dlse) scale for the row of lane l % 16, keep dS^T in registers as the B operand (the score
+// layout is that operand's layout under a fixed permutation of the 32 keys over the MFMA k index, which the two
+// transposing reads of K^T follow) and accumulate dQ^T over their column half (R / 2) from K^T fragments.
+// K and V tiles of 32 keys go global -> LDS by direct copies into four buffers (K and V of tiles i and i + 1):
+// after the swap barrier V(i+2) replaces V(i), after the dQ barrier K(i+2) replaces K(i), so every copy has about
+// a tile of time; the copies are waited for by explicit s_waitcnt behind plain barriers. With a mask the 32 bytes of
+// the wave's token for the tile travel with the K copy.
+template <int R, bool kMask>
+__global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
+  constexpr int C = R / 2, KF = R / 32, CB = C / 16, RS = R + 16;
+  constexpr int KOPS = kMask ? 5 : 4;  // copy instructions per wave for a K tile (4 rows, and the mask bytes)
+  __shared__ __attribute__((aligned(16))) uint16_t kt_lds[2][32 * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][32 * RS];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][64];      // [wave][key block][lane]
+  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[2][8][32];  // [tile parity][wave][key]
+  __shared__ int bound_s[4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int u = wave >> 1, role = wave & 1, col0 = role * C;
+  const int b = blockIdx.y, i0 = blockIdx.x * 4;
+  const int ntok = min(4, a.Lq - i0);
+  const int iu = i0 + min(u, ntok - 1);  // this wave's token (clamped: waves past the last token store nothing)
+  if (tid < 4) bound_s[tid] = tid < ntok ? min(a.bound[(int64_t)b * a.Lq + i0 + tid], a.N) : 0;
+  // row constants of row (token iu, head l16): lse in the log2 domain (0 without history) and delta - dlse
+  const int64_t ridx = ((int64_t)b * 16 + l16) * a.Lq + iu;
+  const float lse = a.lse[ridx];
+  const bool empty = !(lse > -INFINITY);
+  const float lse2 = empty ? 0.f : lse * kLog2e;
+  const float dd = a.delta[ridx] - (a.dlse && !empty ? a.dlse[ridx] : 0.f);
+  u32x4 rf[KF];  // Q^T (role 0) or dZ^T (role 1) of the token: B operand, 8 consecutive columns per lane and k-step
+  {
+    const uint16_t* rp = role == 0
+                             ? a.q + (int64_t)b * a.q_sb + (int64_t)iu * a.q_si + (int64_t)l16 * a.q_sh + 8 * g
+                             : a.dz + (int64_t)b * a.dz_sb + (int64_t)iu * a.dz_si + (int64_t)l16 * a.dz_sh + 8 * g;
+#pragma unroll
+    for (int k = 0; k < KF; ++k) rf[k] = ld16(rp + 32 * k);
+  }
+  __syncthreads();
+  const int nkeys = max(max(bound_s[0], bound_s[1]), max(bound_s[2], bound_s[3]));
+  const int own_bound = bound_s[min(u, ntok - 1)];
+  // every earlier load is complete before the first copy: the compiler does not see the copies, so no wait it
+  // places for an earlier load may end up counting them
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+  floatx4 acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) acc[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t voff = 16u * lane;
+  // rows 4 * wave .. + 3 of the tile at key kt (keys past N read row N - 1)
+  auto copy_rows = [&](uint16_t* buf, const uint16_t* base, int64_t bst, int64_t rst, int kt) {
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int r = 4 * wave + r4;
+      const uint16_t* row = base + (int64_t)b * bst + (int64_t)min(kt + r, a.N - 1) * rst;
+      if (R == 512 || lane < 32) copy16_to_lds(row, voff, &buf[r * RS]);
+    }
+  };
+  auto copy_k = [&](int j) {  // K tile j, and the mask bytes of this wave's token for it (lanes 0-1)
+    const int kt = j * 32;
+    if (kMask && lane < 2) {
+      const int c0 = min(kt + 16 * lane, a.N - 16);  // N is a multiple of 16; keys past N are past every bound
+      copy16_to_lds_v(a.mask + (int64_t)b * a.m_sb + (int64_t)iu * a.m_si + c0, &mk_lds[j & 1][wave][0]);
+    }
+    copy_rows(kt_lds[j & 1], a.k, a.k_sb, a.k_sn, kt);
+  };
+  auto copy_v = [&](int j) { copy_rows(vt_lds[j & 1], a.v, a.v_sb, a.v_sn, j * 32); };
+
+  const int ntiles = (nkeys + 31) / 32;
+  if (ntiles > 0) {
+    copy_k(0);
+    copy_v(0);
+    if (ntiles > 1) {
+      copy_k(1);
+      copy_v(1);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(KOPS + 4, 15));  // tile 0 landed; tile 1 may be in flight
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    }
+    plain_barrier();
+  }
+  for (int i = 0; i < ntiles; ++i) {
+    const int kt = i * 32, par = i & 1;
+    const bool more = i + 1 < ntiles, more2 = i + 2 < ntiles;
+    floatx4 sb[2];  // this wave's block: S^T (role 0) or dP^T (role 1), keys kt + 16 kb + 4g + r, row l16
+    {
+      const uint16_t* ap = (role == 0 ? kt_lds[par] : vt_lds[par]) + l16 * RS + 8 * g;
+      sb[0] = sb[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+      u32x4 fa = *reinterpret_cast<const u32x4*>(ap), fc = *reinterpret_cast<const u32x4*>(ap + 16 * RS);
+#pragma unroll
+      for (int k = 0; k < KF; ++k) {  // the next k-step's fragments are requested before this one's MFMAs
+        const u32x4 ca = fa, cc = fc;
+        if (k + 1 < KF) {
+          fa = *reinterpret_cast<const u32x4*>(ap + 32 * (k + 1));
+          fc = *reinterpret_cast<const u32x4*>(ap + 16 * RS + 32 * (k + 1));
+        }
+        sb[0] = mfma16x16x32(ca, rf[k], sb[0]);
+        sb[1] = mfma16x16x32(cc, rf[k], sb[1]);
+      }
+    }
+    xs[wave][0][lane] = sb[0];
+    xs[wave][1][lane] = sb[1];
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));  // the block is in LDS
+    plain_barrier();
+    if (more2) copy_v(i + 2);  // V(i+2) into V(i)'s buffer: every wave is past its score block
+    const floatx4 ob0 = xs[wave ^ 1][0][lane], ob1 = xs[wave ^ 1][1][lane];
+    const floatx4 s0 = role == 0 ? sb[0] : ob0, s1 = role == 0 ? sb[1] : ob1;
+    const floatx4 d0 = role == 0 ? ob0 : sb[0], d1 = role == 0 ? ob1 : sb[1];
+    uint32_t m0 = ~0u, m1 = ~0u;
+    if (kMask) {
+      const uint8_t* mb = &mk_lds[par][wave][4 * g];
+      m0 = *reinterpret_cast<const uint32_t*>(mb);
+      m1 = *reinterpret_cast<const uint32_t*>(mb + 16);
+    }
+    float ds[2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool v0 = kt + 4 * g + r < own_bound && ((m0 >> (8 * r)) & 255u) != 0;
+      const bool v1 = kt + 16 + 4 * g + r < own_bound && ((m1 >> (8 * r)) & 255u) != 0;
+      const float p0 = v0 ? fast_exp2(s0[r] * a.scale_log2 - lse2) : 0.f;
+      const float p1 = v1 ? fast_exp2(s1[r] * a.scale_log2 - lse2) : 0.f;
+      ds[0][r] = p0 * (d0[r] - dd) * a.scale;
+      ds[1][r] = p1 * (d1[r] - dd) * a.scale;
+    }
+    const u32x4 dsb = {pack2_hw(ds[0][0], ds[0][1]), pack2_hw(ds[0][2], ds[0][3]), pack2_hw(ds[1][0], ds[1][1]),
+                       pack2_hw(ds[1][2], ds[1][3])};
+    {  // dQ^T += K^T dS^T over this wave's columns (k slot 8g + e <-> key 4g + e, e < 4; 16 + 4g + e - 4, e >= 4)
+      const uint16_t* kp = &kt_lds[par][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
+      auto kfrag = [&](int cb) {
+        const short4v lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(kp + 16 * cb));
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) short4v*)(kp + 16 * RS + 16 * cb));
+        return join_tr(lo, hi);
+      };
+      u32x4 kf = kfrag(0);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const u32x4 cur = kf;
+        if (cb + 1 < CB) kf = kfrag(cb + 1);
+        acc[cb] = mfma16x16x32(cur, dsb, acc[cb]);
+      }
+    }
+    if (more) {
+      // tile i+1 landed (only V(i+2) may still be in flight); every wave is done with K(i) and the blocks
+      if (more2) __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+      plain_barrier();
+      if (more2) copy_k(i + 2);  // K(i+2) into K(i)'s buffer
+    }
+  }
+  if (u < ntok) {  // lane holds dQ^T[col 16cb + 4g + r][head l16] of token i0 + u
+    float* dqp = a.dq + (int64_t)b * a.dq_sb + (int64_t)(i0 + u) * a.dq_si + (int64_t)l16 * a.dq_sh + col0 + 4 * g;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) *reinterpret_cast<floatx4*>(dqp + 16 * cb) = acc[cb];
+  }
+}
+
 // ---- backward: dk, dv ----------------------------------------------------------------------------------------
 // One workgroup per (32-key tile of a batch row, row split): K/V tile resident in LDS, the query rows of the split
 // streamed in steps of 2 tokens (Q and dZ through LDS, the next step's loads in flight in registers); steps whose
@@ -707,8 +874,20 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
   if (need_q && Lq > 0) {
     p.dq = dq;
     p.dq_sb = dq_sb; p.dq_si = dq_si; p.dq_sh = dq_sh;
-    const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
-    HLA_KH_DISPATCH(khop_dq, width, grid, p, st);
+    // the multi-query form: widths 512 / 256, whole 16-key groups, 16-byte aligned fp32 dq rows and mask rows
+    const bool dq4 = HLA_KH_DQ4 && (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(dq) &&
+                     dq_sb % 4 == 0 && dq_si % 4 == 0 && dq_sh % 4 == 0 &&
+                     (!mask || (kh_aligned16(mask) && m_sb % 16 == 0 && m_si % 16 == 0));
+    if (dq4) {
+      const dim3 grid4((unsigned)((Lq + 3) / 4), (unsigned)B);
+      if (width == 512 && mask) hipLaunchKernelGGL((khop_dq4<512, true>), grid4, dim3(kKhThreads), 0, st, p);
+      else if (width == 512) hipLaunchKernelGGL((khop_dq4<512, false>), grid4, dim3(kKhThreads), 0, st, p);
+      else if (mask) hipLaunchKernelGGL((khop_dq4<256, true>), grid4, dim3(kKhThreads), 0, st, p);
+      else hipLaunchKernelGGL((khop_dq4<256, false>), grid4, dim3(kKhThreads), 0, st, p);
+    } else {
+      const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
+      HLA_KH_DISPATCH(khop_dq, width, grid, p, st);
+    }
     if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
   }
   if (need_kv) {

@@ -145,6 +145,20 @@ def test_mask_rows_off_16_byte_boundaries_and_no_mask(R):
     zo2, lo2 = O.causal_history(q, k, v, np.ones((B, Lq, N), bool), scale)
     assert_attention_close(z2.float().cpu().numpy(), zo2, 'z (no mask)')
     assert_lse_close(lse2.cpu().numpy(), lo2)
+    # dq alone through the C ABI without a mask (dk, dv not asked for)
+    rng = np.random.default_rng(R)
+    dz = bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32))
+    dzt = torch.tensor(dz, device='cuda').to(torch.bfloat16)
+    delta = torch.empty(B, 16, Lq, dtype=torch.float32, device='cuda')
+    dq = torch.empty(B, Lq, 16, R, dtype=torch.float32, device='cuda')
+    lib.call('hla_s6_khop_backward', lib.ptr(qt), qt.stride(0), qt.stride(1), qt.stride(2), lib.ptr(kt), kt.stride(0),
+             kt.stride(1), lib.ptr(vt), vt.stride(0), vt.stride(1), None, 0, 0, lib.ptr(bound), B, Lq, N, 16, R, scale,
+             lib.ptr(z2), z2.stride(0), z2.stride(1), z2.stride(2), lib.ptr(lse2), lib.ptr(dzt), dzt.stride(0),
+             dzt.stride(1), dzt.stride(2), None, lib.ptr(delta), lib.ptr(dq), dq.stride(0), dq.stride(1), dq.stride(2),
+             None, 0, 0, None, 0, 0, 1, None, 0, st)
+    dqo, _, _ = O.causal_history_backward(q, k, v, np.ones((B, Lq, N), bool), scale, lo2, dz, None,
+                                          z=bf16.round_bf16(zo2.astype(np.float32)))
+    assert_grad_close(dq.cpu().numpy(), dqo, 'dq (no mask)')
 
 
 def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
