@@ -141,6 +141,12 @@ __device__ __forceinline__ void copy16_to_lds_v(const void* src, const void* lds
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
 }
 
+// 4 bytes per lane from a per-lane source address to LDS address lds + 4 i (a gather of scattered words).
+__device__ __forceinline__ void copy4_to_lds_v(const void* src, const void* lds) {
+  const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(dst), "v"(src) : "memory", "m0");
+}
+
 __device__ __forceinline__ int64_t uniform64(int64_t v) {
   const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
   const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));

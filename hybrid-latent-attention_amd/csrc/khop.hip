@@ -23,6 +23,9 @@ namespace {
 #ifndef HLA_KH_DQ4
 #define HLA_KH_DQ4 1  // dq on khop_dq4 (4 tokens per workgroup, direct tile copies) where the shapes allow
 #endif
+#ifndef HLA_KH_DKDV4
+#define HLA_KH_DKDV4 1  // dk / dv on khop_dkdv4 (64-key tiles, tokens streamed by direct copies) where shapes allow
+#endif
 
 constexpr int kKhRows = 32;   // query rows per step (2 tokens x 16 heads)
 constexpr int kKhKeys = 32;   // keys per step
@@ -698,6 +701,180 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
   }
 }
 
+// ---- backward: dk, dv on the multi-query layout ----------------------------------------------------------
+// khop_dkdv4: one workgroup per (64-key tile of a batch row, row split), 8 waves; wave w serves the 16 keys
+// 16 (w / 2) .. of the tile and role w % 2: role 0 computes the score blocks S = Q K^T and accumulates dK^T, role 1
+// the blocks dP = dZ V^T and dV^T. The wave's K^T or V^T (all R columns) stays in registers as the MFMA B operand;
+// the query tokens of the split stream through LDS two at a time (32 rows): per step the pair swaps its two
+// 32-row x 16-key blocks through LDS, both waves form P = exp(S scale - lse) and dS = P (dP - delta + dlse) scale
+// (lane l holds rows 4 (l / 16) .. + 3 of each token for key l % 16: the B-operand layout of a 16x16x32 MFMA over
+// the 32 rows under a fixed permutation of k, which the two transposing reads of the A operand follow), and role 0
+// adds Q^T dS, role 1 dZ^T P over all R columns. Every step's Q and dZ rows, its rows' lse / delta / dlse and the
+// tokens' key bounds (gathers of words) and the wave's mask bytes go global -> LDS by direct copies into two
+// buffers, requested one step ahead. Tokens of the split before the first one whose bound reaches the tile are
+// skipped; later tokens that see no key of the tile add zeros.
+template <int R, bool kMask>
+__global__ __launch_bounds__(kKhThreads, 1) void khop_dkdv4(KhopParams a) {
+  constexpr int KF = R / 32, CBO = R / 16, RS = R + 16;
+  constexpr int OPS = kMask ? 11 : 10;  // copies per wave per step: 8 rows, 2 gathers, the mask bytes
+  __shared__ __attribute__((aligned(16))) uint16_t rows_lds[2][2][32 * RS];  // [buffer][Q, dZ][token * 16 + head]
+  __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][64];             // score blocks [wave][token][lane]
+  // [buffer][wave][lse t0 | lse t1 | delta t0 | delta t1 | dlse t0 | dlse t1 | bound t0, t1]
+  __shared__ __attribute__((aligned(16))) float rc_lds[2][8][128];
+  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[2][8][32];  // [buffer][wave][token * 16 + key of block]
+  __shared__ int first_s;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int kb = wave >> 1, role = wave & 1;
+  const int b = blockIdx.y, kt0 = blockIdx.x * 64, split = blockIdx.z;
+  const int key = kt0 + 16 * kb + l16;  // this lane's key (clamped below for reads)
+  const int keyc = min(key, a.N - 1);
+  const int per = (a.Lq + a.key_splits - 1) / a.key_splits;
+  const int s_begin = split * per, s_end = min(a.Lq, s_begin + per);
+  // first token of the split whose key bound reaches the tile (bounds are arbitrary: every thread scans a share)
+  if (tid == 0) first_s = s_end;
+  __syncthreads();
+  for (int i = s_begin + tid; i < s_end; i += kKhThreads)
+    if (a.bound[(int64_t)b * a.Lq + i] > kt0) {
+      atomicMin(&first_s, i);
+      break;
+    }
+  u32x4 rf[KF];  // K^T (role 0) or V^T (role 1) of the wave's 16 keys: B operand
+  {
+    const uint16_t* rp = role == 0 ? a.k + (int64_t)b * a.k_sb + (int64_t)keyc * a.k_sn + 8 * g
+                                   : a.v + (int64_t)b * a.v_sb + (int64_t)keyc * a.v_sn + 8 * g;
+#pragma unroll
+    for (int k = 0; k < KF; ++k) rf[k] = ld16(rp + 32 * k);
+  }
+  __syncthreads();
+  const int first = __builtin_amdgcn_readfirstlane(first_s);
+  // every earlier load is complete before the first copy: the compiler does not see the copies, so no wait it
+  // places for an earlier load may end up counting them
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+  floatx4 acc[CBO];
+#pragma unroll
+  for (int cb = 0; cb < CBO; ++cb) acc[cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t voff = 16u * lane;
+  auto copy_step = [&](int i, int c) {  // tokens i, i + 1 (clamped to the split) into buffer c
+    {  // 8 rows: waves 0-3 Q rows 8 (w % 4) .. + 7 of the step, waves 4-7 the dZ rows
+      const int half = wave >> 2;
+#pragma unroll
+      for (int r8 = 0; r8 < 8; ++r8) {
+        const int r = 8 * (wave & 3) + r8, tok = min(i + (r >> 4), s_end - 1), h = r & 15;
+        const uint16_t* row = reinterpret_cast<const uint16_t*>(uniform64(
+            half == 0 ? (int64_t)(a.q + (int64_t)b * a.q_sb + (int64_t)tok * a.q_si + (int64_t)h * a.q_sh)
+                      : (int64_t)(a.dz + (int64_t)b * a.dz_sb + (int64_t)tok * a.dz_si + (int64_t)h * a.dz_sh)));
+        if (R == 512 || lane < 32) copy16_to_lds(row, voff, &rows_lds[c][half][r * RS]);
+      }
+    }
+    const int t1 = min(i + 1, s_end - 1);
+    {  // lanes 0-15 / 16-31: lse of the two tokens, 32-47 / 48-63: their delta
+      const int tok = (lane & 16) ? t1 : i, h = l16;
+      const int64_t ridx = ((int64_t)b * 16 + h) * a.Lq + tok;
+      copy4_to_lds_v(lane < 32 ? (const void*)(a.lse + ridx) : (const void*)(a.delta + ridx), &rc_lds[c][wave][0]);
+    }
+    if (lane < 34) {  // lanes 0-31: dlse of the two tokens (lse again without one), 32-33: their key bounds
+      const int tok = (lane < 32 ? (lane & 16) : (lane & 1)) ? t1 : i, h = l16;
+      const int64_t ridx = ((int64_t)b * 16 + h) * a.Lq + tok;
+      copy4_to_lds_v(lane < 32 ? (const void*)(a.dlse ? a.dlse + ridx : a.lse + ridx)
+                               : (const void*)(a.bound + (int64_t)b * a.Lq + tok),
+                     &rc_lds[c][wave][64]);
+    }
+    if (kMask && lane < 2)
+      copy16_to_lds_v(a.mask + (int64_t)b * a.m_sb + (int64_t)(lane ? t1 : i) * a.m_si +
+                          min(kt0 + 16 * kb, a.N - 16),
+                      &mk_lds[c][wave][0]);
+  };
+  const int nsteps = s_end > first ? (s_end - first + 1) / 2 : 0;
+  if (nsteps > 0) {
+    copy_step(first, 0);
+    if (nsteps > 1) {
+      copy_step(first + 2, 1);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(OPS, 15));  // step 0 landed; step 1 may be in flight
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    }
+    plain_barrier();
+  }
+  for (int j = 0; j < nsteps; ++j) {
+    const int i = first + 2 * j, c = j & 1;
+    const bool tok1 = i + 1 < s_end;  // the step's second token exists
+    floatx4 sblk[2];  // S (role 0) or dP (role 1) of token x: rows 4g + r of key l16
+    {
+      const uint16_t* ap = &rows_lds[c][role][l16 * RS + 8 * g];  // A operand: Q or dZ rows l16, 16 + l16
+      sblk[0] = sblk[1] = floatx4{0.f, 0.f, 0.f, 0.f};
+      u32x4 fa = *reinterpret_cast<const u32x4*>(ap), fc = *reinterpret_cast<const u32x4*>(ap + 16 * RS);
+#pragma unroll
+      for (int k = 0; k < KF; ++k) {  // the next fragments are requested before this k-step's MFMAs
+        const u32x4 ca = fa, cc = fc;
+        if (k + 1 < KF) {
+          fa = *reinterpret_cast<const u32x4*>(ap + 32 * (k + 1));
+          fc = *reinterpret_cast<const u32x4*>(ap + 16 * RS + 32 * (k + 1));
+        }
+        sblk[0] = mfma16x16x32(ca, rf[k], sblk[0]);
+        sblk[1] = mfma16x16x32(cc, rf[k], sblk[1]);
+      }
+    }
+    xs[wave][0][lane] = sblk[0];
+    xs[wave][1][lane] = sblk[1];
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(63, 0));  // the blocks are in LDS
+    plain_barrier();
+    const float* rc = rc_lds[c][wave];
+    float pq[2][4];  // P (role 1) or dS (role 0) of rows 4g + r of token x
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const floatx4 ob = xs[wave ^ 1][x][lane];
+      const floatx4 sv = role == 0 ? sblk[x] : ob, dpv = role == 0 ? ob : sblk[x];
+      const floatx4 lse4 = *reinterpret_cast<const floatx4*>(rc + 16 * x + 4 * g);
+      const floatx4 del4 = *reinterpret_cast<const floatx4*>(rc + 32 + 16 * x + 4 * g);
+      const floatx4 dl4 = *reinterpret_cast<const floatx4*>(rc + 64 + 16 * x + 4 * g);
+      const int bnd = __float_as_int(rc[96 + x]);
+      const bool vis = (x == 0 || tok1) && key < bnd && (!kMask || mk_lds[c][wave][16 * x + l16] != 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool emp = !(lse4[r] > -INFINITY);
+        const float p = vis && !emp ? fast_exp2(sv[r] * a.scale_log2 - lse4[r] * kLog2e) : 0.f;
+        const float dd = del4[r] - (a.dlse && !emp ? dl4[r] : 0.f);
+        pq[x][r] = role == 0 ? p * (dpv[r] - dd) * a.scale : p;
+      }
+    }
+    const u32x4 bq = {pack2_hw(pq[0][0], pq[0][1]), pack2_hw(pq[0][2], pq[0][3]), pack2_hw(pq[1][0], pq[1][1]),
+                      pack2_hw(pq[1][2], pq[1][3])};
+    {  // role 0: dK^T += Q^T dS; role 1: dV^T += dZ^T P (k slot 8g + e <-> row 4g + e of token 0, e < 4; of
+       // token 1, e >= 4)
+      const uint16_t* tp = &rows_lds[c][role][(4 * g + (l16 >> 2)) * RS + 4 * (l16 & 3)];
+      auto afrag = [&](int cb) {
+        const short4v lo =
+            __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(tp + 16 * cb));
+        const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) short4v*)(tp + 16 * RS + 16 * cb));
+        return join_tr(lo, hi);
+      };
+      u32x4 af = afrag(0);
+#pragma unroll
+      for (int cb = 0; cb < CBO; ++cb) {
+        const u32x4 cur = af;
+        if (cb + 1 < CBO) af = afrag(cb + 1);
+        acc[cb] = mfma16x16x32(cur, bq, acc[cb]);
+      }
+    }
+    if (j + 1 < nsteps) {
+      // step j+1 landed (nothing newer is in flight); every wave is done with buffer c
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+      plain_barrier();
+      if (j + 2 < nsteps) copy_step(i + 4, c);  // step j+2 into step j's buffer
+    }
+  }
+  if (key < a.N) {  // lane holds dK^T (role 0) or dV^T (role 1) [col 16 cb + 4g + r][key]
+    float* out = role == 0 ? a.dk + split * a.dk_ss + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_sn
+                           : a.dv + split * a.dv_ss + (int64_t)b * a.dv_sb + (int64_t)key * a.dv_sn;
+#pragma unroll
+    for (int cb = 0; cb < CBO; ++cb) *reinterpret_cast<floatx4*>(out + 16 * cb + 4 * g) = acc[cb];
+  }
+}
+
 // ---- small kernels -------------------------------------------------------------------------------------------
 // bound[t] = 1 + the last key mask row t shows (0 when none; N without a mask). One wave per row.
 __global__ __launch_bounds__(256) void khop_bound_kernel(const uint8_t* mask, int64_t m_sb, int64_t m_si, int B,
@@ -903,8 +1080,20 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
     p.dv_sb = split ? (int64_t)N * width : dv_sb;
     p.dv_sn = split ? width : dv_sn;
     p.dk_ss = p.dv_ss = part;
-    const dim3 grid((unsigned)((N + kKhKeys - 1) / kKhKeys), (unsigned)B, (unsigned)key_splits);
-    HLA_KH_DISPATCH(khop_dkdv, width, grid, p, st);
+    // the multi-query form: widths 512 / 256, whole 16-key groups, 16-byte aligned fp32 dk / dv rows and mask rows
+    const bool kv4 = HLA_KH_DKDV4 && (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(p.dk) &&
+                     kh_aligned16(p.dv) && p.dk_sb % 4 == 0 && p.dk_sn % 4 == 0 && p.dv_sb % 4 == 0 &&
+                     p.dv_sn % 4 == 0 && (!mask || (kh_aligned16(mask) && m_sb % 16 == 0 && m_si % 16 == 0));
+    if (kv4) {
+      const dim3 grid4((unsigned)((N + 63) / 64), (unsigned)B, (unsigned)key_splits);
+      if (width == 512 && mask) hipLaunchKernelGGL((khop_dkdv4<512, true>), grid4, dim3(kKhThreads), 0, st, p);
+      else if (width == 512) hipLaunchKernelGGL((khop_dkdv4<512, false>), grid4, dim3(kKhThreads), 0, st, p);
+      else if (mask) hipLaunchKernelGGL((khop_dkdv4<256, true>), grid4, dim3(kKhThreads), 0, st, p);
+      else hipLaunchKernelGGL((khop_dkdv4<256, false>), grid4, dim3(kKhThreads), 0, st, p);
+    } else {
+      const dim3 grid((unsigned)((N + kKhKeys - 1) / kKhKeys), (unsigned)B, (unsigned)key_splits);
+      HLA_KH_DISPATCH(khop_dkdv, width, grid, p, st);
+    }
     if ((rc = check_launch("khop_dkdv")) != HLA_S6_OK) return rc;
     if (split) {
       hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part + 255) / 256)), dim3(256), 0, st, workspace,

@@ -111,7 +111,9 @@ class _CausalHistory(torch.autograd.Function):
         need_kv = need_k or need_v
         dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
         dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
-        splits = _key_splits(-(-N // 32) * B, dev) if need_kv else 1
+        # key tiles of the dk / dv kernel: 64 keys on the multi-query form (widths 512 / 256, N a multiple of 16)
+        tile = 64 if R in (256, 512) and N % 16 == 0 else 32
+        splits = _key_splits(-(-N // tile) * B, dev) if need_kv else 1
         ws = torch.empty(2 * splits * B * N * R, dtype=torch.float32, device=dev) if splits > 1 else None
         _lib.call('hla_s6_khop_backward', _lib.ptr(qb), qb.stride(0), qb.stride(1), qb.stride(2), _lib.ptr(kb),
                   kb.stride(0), kb.stride(1), _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(m8), m8.stride(0),
