@@ -182,7 +182,7 @@ def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
 
 def test_unsplit_key_tiles_match_the_oracle(monkeypatch):
     """dk / dv accumulated by one workgroup per key tile (no row splits, no partial sums)."""
-    monkeypatch.setattr(hg, '_key_splits', lambda tiles, device: 1)
+    monkeypatch.setattr(hg, '_key_splits', lambda tiles, device, per_cu=4: 1)
     q, k, v, mask = case(11, 2, 40, 40, 512, 'benchmark')
     rng = np.random.default_rng(12)
     dz = bf16.round_bf16(rng.standard_normal(q.shape).astype(np.float32))
