@@ -170,35 +170,50 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
         st16(vs + (c >> 4) * kChunkVS + (c & 15) * 8, vr[it]);
       }
       float sc[4];
+      // wave-uniform: every key of the tile is visible to every query of the pass (a window tile inside the
+      // window, or a chunk tile wholly before the pass's first query)
+      const bool full = wt ? k0 + 16 <= kend : k0 + 16 <= ke && k0 + 15 <= tp;
+      if (full) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = k0 + 4 * g + r;
-        const bool vis = wt ? key < kend : key < ke && key <= q_pos;
-        sc[r] = (vis && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
+        for (int r = 0; r < 4; ++r) sc[r] = hq < count ? s[r] * a.scale_log2 : -INFINITY;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 4 * g + r;
+          const bool vis = wt ? key < kend : key < ke && key <= q_pos;
+          sc[r] = (vis && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
+        }
       }
-      float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-      mx = wave_max16x4(mx);
-      const float m_new = fmaxf(m, mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a column with no visible key yet keeps its state
-      const float alpha = fast_exp2(m - m_use);
+      // (scores are finite or -inf: masked keys never reach a maximum); the running maximum is raised lazily, only
+      // when a tile exceeds it by more than 2^8 (the exponentials stay below 2^8), which skips the rescale of the
+      // accumulators on most tiles
+      const float mx = wave_max16x4_nn(max_nn(max_nn(sc[0], sc[1]), max_nn(sc[2], sc[3])));
+      const bool raise = mx > m + 8.f;  // false while the column has no visible key (mx = -inf)
+      if (__any(raise)) {
+        const float m_new = raise ? mx : m;
+        const float alpha = fast_exp2(m - m_new);  // 0 on the first raise (m = -inf)
+        l *= alpha;
+        m = m_new;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) oacc[nt] = oacc[nt] * alpha;
+      }
+      const float m_use = m == -INFINITY ? 0.f : m;
       float p[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_use);
-      l = l * alpha + wave_sum16x4((p[0] + p[1]) + (p[2] + p[3]));
-      m = m_new;
-      short4v pb;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) pb[r] = (short)f2bf(p[r]);
+      l += (p[0] + p[1]) + (p[2] + p[3]);  // this lane's share of the column sum (summed over the 4 lanes at the end)
+      const uint32_t p01 = pack2_hw(p[0], p[1]), p23 = pack2_hw(p[2], p[3]);
+      const short4v pb = {(short)(p01 & 0xffffu), (short)(p01 >> 16), (short)(p23 & 0xffffu), (short)(p23 >> 16)};
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
         // lane (g, hq) of the A operand: V[4g + e][16nt + hq]; the transposing read takes row 4g + hq/4,
         // columns 16nt + 4(hq%4) .. +3 in each 16-lane group
         const uint16_t* vp = vs + (4 * g + (hq >> 2)) * kChunkVS + 16 * nt + 4 * (hq & 3);
         const short4v va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
-        oacc[nt] = oacc[nt] * alpha;
         oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
       }
     }
+    l = wave_sum16x4(l);
     if (hq < count) {
       const int t = tp + hq;
       const bool any = l > 0.f;
