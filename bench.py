@@ -456,9 +456,10 @@ def export_workload(args, pkg, device):
 def khop_workload(args, pkg, device):
     """Multi-query causal history attention with backward at the reference's operator benchmark shape
     (hla/latent/benchmark_history_gemm.py:79-101): B = 4, 16 heads, L = 2880 queries and keys, latent width
-    ``--width`` (512 default), valid lengths L, 0.9 L, 0.8 L, 0.7 L, query i sees keys j < i. Times the forward and
-    the forward + backward (dq, dk, dv) in HIP graphs; reports TFLOP/s of the algorithmic work (2 GEMMs forward,
-    7 with the backward, over the visible pairs) against the 2.5 PFLOP/s bf16 peak. One JSON line."""
+    ``--width`` (512 default), valid lengths L, 0.9 L, 0.8 L, 0.7 L, query i sees keys j < i. Times the forward (in
+    a HIP graph) and the forward + backward (dq, dk, dv through autograd, returned as the reference's benchmark does
+    with torch.autograd.grad; bf16 leaves here, fp32 there); reports TFLOP/s of the algorithmic work (2 GEMMs
+    forward, 7 with the backward, over the visible pairs) against the 2.5 PFLOP/s bf16 peak. One JSON line."""
     hg = pkg.history_gemm
     B, L, R = args.batch or 4, args.context or 2880, args.width
     g = torch.Generator(device=device).manual_seed(args.seed)
@@ -478,9 +479,9 @@ def khop_workload(args, pkg, device):
         with torch.no_grad():
             hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
 
-    def train():
+    def train():  # gradients returned, not accumulated into .grad (as the reference's operator benchmark does)
         z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
-        torch.autograd.backward([z, lse], [dz, dlse])
+        torch.autograd.grad([z, lse], [q, k, v], [dz, dlse])
 
     ms_f = time_graph(fwd, args.steps, args.warmup)
     ms_t = time_eager(train, args.steps, args.warmup)
