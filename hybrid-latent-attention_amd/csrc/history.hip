@@ -1221,6 +1221,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 #ifndef HLA_MQ4
 #define HLA_MQ4 1  // 512-wide multi-query steps: history_mq4 (8 tokens per workgroup) instead of history_mq2
 #endif
+#ifndef HLA_MQ5
+#define HLA_MQ5 1  // 256-wide multi-query steps: history_mq5 (4 waves, no score exchange) instead of history_mq4
+#endif
 constexpr int kMq4Tokens = 8;           // tokens per workgroup
 constexpr int kMq4Keys = 32;            // keys per tile
 
@@ -1478,6 +1481,251 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
           *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
       }
       if (half == 0 && g == 0) {
+        const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
+        if (kContig)
+          a.lse[((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row] = lse;
+        else if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
+        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
+      }
+    }
+    tp = te;
+  }
+}
+
+// history_mq5 (the 256-wide latent): one workgroup per (group of 8 consecutive tokens, KV slot) with 4 waves; wave w
+// owns tokens 2w and 2w + 1 of the pass (32 query rows) and all 256 latent columns, so its scores need no exchange
+// with another wave: per 32-key tile it computes S^T for both tokens (every K fragment read from LDS feeds both
+// tokens' MFMAs), runs the online softmax of history_mq4 and adds V^T P^T. K and V tiles go global -> LDS by direct
+// copies (one 512-byte row per half-wave instruction, wave w copying rows 8w .. 8w+7) into four buffers (K and V of
+// tiles i and i+1); one barrier per tile, after which tile i+2 replaces tile i, so every copy has a tile of time.
+// 74 KB of LDS: two workgroups per CU, whose tiles run out of step, so one's softmax overlaps the other's MFMAs.
+constexpr int kMq5Pages = 1024;  // block-table entries of a pass kept in LDS (longer passes read them from memory)
+
+template <int kMode>
+__global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
+  constexpr int R = 256;
+  constexpr bool kContig = kMode != 0, kMask = kMode == 2;
+  constexpr int TOPS = kMask ? 17 : 16;  // copy instructions per wave for a tile (8 K rows, 8 V rows, mask bytes)
+  constexpr int KS = R / 32, CB = R / 16, RS = R + 16;
+  __shared__ __attribute__((aligned(16))) uint16_t kt_lds[2][kMq4Keys * RS];
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][kMq4Keys * RS];
+  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[kMask ? 2 : 1][4][64];  // [tile parity][wave][token*32+key]
+  __shared__ int32_t pg_lds[kMq5Pages];
+  __shared__ int64_t red_lds[8];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, g = lane >> 4;
+  const int S = a.num_splits, s = blockIdx.y;
+  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int t_begin = blockIdx.x * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
+
+  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
+    const int64_t row = table_row(a, tp);
+    int te = tp + 1;
+    while (te < t_end && table_row(a, te) == row) ++te;
+    const int count = te - tp;
+    int n_max = 0, n_tok[2] = {0, 0};
+#pragma unroll
+    for (int v = 0; v < kMq4Tokens; ++v) {
+      const int n = v < count ? (int)min((int64_t)a.ctx[tp + v], cap) : 0;
+      n_max = max(n_max, n);
+      if (v == 2 * wave) n_tok[0] = n;
+      if (v == 2 * wave + 1) n_tok[1] = n;
+    }
+    const int tiles16 = (n_max + kTile - 1) / kTile;
+    const int j0 = S > 1 ? s * chunk : 0;
+    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
+    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);
+    const int own_n[2] = {min(k1, n_tok[0]), min(k1, n_tok[1])};
+    float m_own[2] = {-INFINITY, -INFINITY}, l_own[2] = {0.f, 0.f};
+    floatx4 o[2][CB];
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) o[x][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (k0 < k1) {  // uniform over the workgroup
+      const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
+      u32x4 qf[2][KS];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int tq = tp + min(2 * wave + x, count - 1);
+        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + 8 * g;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) qf[x][k] = ld16(qp + 32 * k);
+      }
+      const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
+      const bool pg_local = np <= kMq5Pages;
+      __syncthreads();  // the previous pass's readers of the tiles and pages are done
+      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row (identity pages: contiguous rows)
+        return kContig ? row * a.bt_cols + p : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
+      };
+      if (pg_local)
+        for (int i = tid; i < np; i += 256) pg_lds[i] = (int32_t)table_page(p0 + i);
+      __syncthreads();
+      // the query loads are complete before the first copy: the compiler does not see the copies, so no wait it
+      // places for an earlier load may end up counting them
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+      const bool page16 = a.block_size == kTile;
+      const uint32_t voff = 16u * lane;
+      // rows 8 * wave .. + 7 of the tile at key kt into buffer buf (keys past the slot's range read its last row)
+      auto copy_rows = [&](uint16_t* buf, const uint16_t* base, int kt) {
+        if (page16 && pg_local && kt + kMq4Keys <= k1) {  // the 8 rows sit in page kt / 16 + wave / 2
+          const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 1)]);
+          const uint16_t* src = base + page * a.page_stride + (int64_t)((8 * wave) & 15) * a.row_stride;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (lane < 32) copy16_to_lds(src + i * a.row_stride, voff, &buf[(8 * wave + i) * RS]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int key = min(kt + 8 * wave + i, k1 - 1), p = key / a.block_size;
+            const int64_t page = uniform64(pg_local ? (int64_t)pg_lds[p - p0] : table_page(p));
+            if (lane < 32)
+              copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
+                            &buf[(8 * wave + i) * RS]);
+          }
+        }
+      };
+      auto copy_tile = [&](int j) {  // tile j (K, V and this wave's mask bytes) into the buffers of parity j & 1
+        const int kt = k0 + j * kMq4Keys;
+        if (kMask && lane < 4) {  // lanes 0-3: token l / 2, bytes 16 (l % 2) .. (chunks past the row: its end)
+          const int tq = tp + min(2 * wave + (lane >> 1), count - 1);
+          const int c0 = min(kt + 16 * (lane & 1), (int)cap - 16);
+          copy16_to_lds_v(a.mask + (int64_t)tq * a.mask_st + c0, &mk_lds[j & 1][wave][0]);
+        }
+        copy_rows(kt_lds[j & 1], a.k, kt);
+        copy_rows(vt_lds[j & 1], a.v, kt);
+      };
+      const int ntiles = (k1 - k0 + kMq4Keys - 1) / kMq4Keys;
+      copy_tile(0);
+      if (ntiles > 1) {
+        copy_tile(1);
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(TOPS, 15));  // tile 0 landed; tile 1 may be in flight
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+      }
+      plain_barrier();
+      for (int i = 0; i < ntiles; ++i) {
+        const int kt = k0 + i * kMq4Keys, par = i & 1;
+        floatx4 sp[2][2];  // S^T of both tokens: keys 16 kb + 4g + r, row l16
+        {
+          const uint16_t* kp = &kt_lds[par][l16 * RS + 8 * g];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+          u32x4 ka = *reinterpret_cast<const u32x4*>(kp), kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS);
+#pragma unroll
+          for (int k = 0; k < KS; ++k) {  // the next k-step's fragments are requested before this one's MFMAs
+            const u32x4 ca = ka, cc = kc;
+            if (k + 1 < KS) {
+              ka = *reinterpret_cast<const u32x4*>(kp + 32 * (k + 1));
+              kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * (k + 1));
+            }
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+              sp[x][0] = mfma16x16x32(ca, qf[x][k], sp[x][0]);
+              sp[x][1] = mfma16x16x32(cc, qf[x][k], sp[x][1]);
+            }
+          }
+        }
+        auto softmax_tok = [&](int x) -> u32x4 {  // online softmax of row l16 of token x; P^T as the B operand
+          const int n = own_n[x];
+          float sc[2][4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sc[0][r] = sp[x][0][r];
+            sc[1][r] = sp[x][1][r];
+          }
+          if (kMask) {  // mask bytes of keys 4g + r and 16 + 4g + r of token x
+            const uint8_t* mb = &mk_lds[par][wave][32 * x + 4 * g];
+            const uint32_t m0 = *reinterpret_cast<const uint32_t*>(mb), m1 = *reinterpret_cast<const uint32_t*>(mb + 16);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (kt + 4 * g + r >= n || ((m0 >> (8 * r)) & 255u) == 0) sc[0][r] = -INFINITY;
+              if (kt + 16 + 4 * g + r >= n || ((m1 >> (8 * r)) & 255u) == 0) sc[1][r] = -INFINITY;
+            }
+          } else if (kt + kMq4Keys > n) {  // wave-uniform: the tile runs past the row's history
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              if (kt + 4 * g + r >= n) sc[0][r] = -INFINITY;
+              if (kt + 16 + 4 * g + r >= n) sc[1][r] = -INFINITY;
+            }
+          }
+          // (scores are finite or -inf: rows past the history are masked before any NaN they hold is used)
+          float mx = max3_nn(max3_nn(sc[0][0], sc[0][1], sc[0][2]), max3_nn(sc[0][3], sc[1][0], sc[1][1]),
+                             max_nn(sc[1][2], sc[1][3]));
+          // the scale is positive, so the maximum of the scaled scores is the scaled maximum (log2 units)
+          mx = wave_max16x4_nn(mx) * a.scale_log2;
+          const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
+          if (__any(raise)) {
+            const float m_new = raise ? mx : m_own[x];
+            const float alpha = fast_exp2(m_own[x] - m_new);  // 0 on the first raise (m_own = -inf)
+            l_own[x] *= alpha;  // this lane's share of the row sum
+            m_own[x] = m_new;
+#pragma unroll
+            for (int cb = 0; cb < CB; ++cb) o[x][cb] *= alpha;
+          }
+          const float m_use = m_own[x] == -INFINITY ? 0.f : m_own[x];
+          float p[2][4], ps = 0.f;
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              p[kb2][r] = fast_exp2(__builtin_fmaf(sc[kb2][r], a.scale_log2, -m_use));
+              ps += p[kb2][r];
+            }
+          l_own[x] += ps;  // the four lanes of a row are summed once, after the last tile
+          return u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
+                       pack2_hw(p[1][2], p[1][3])};
+        };
+        // O^T += V^T P^T (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
+        const uint16_t* vp = &vt_lds[par][(4 * g + (l16 >> 2)) * RS + 4 * (l16 & 3)];
+        auto vfrag = [&](int cb) {
+          const short4v lo =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
+          return join_tr(lo, hi);
+        };
+        {
+          const u32x4 pb0 = softmax_tok(0), pb1 = softmax_tok(1);
+          u32x4 vt = vfrag(0);
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs; it feeds both
+            const u32x4 cur = vt;           // tokens' MFMAs
+            if (cb + 1 < CB) vt = vfrag(cb + 1);
+            o[0][cb] = mfma16x16x32(cur, pb0, o[0][cb]);
+            o[1][cb] = mfma16x16x32(cur, pb1, o[1][cb]);
+          }
+        }
+        if (i + 1 < ntiles) {
+          // tile i+1 landed (nothing newer is in flight); every wave is done with tile i's buffers
+          __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
+          plain_barrier();
+          if (i + 2 < ntiles) copy_tile(i + 2);  // tile i+2 into tile i's buffers
+        }
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) l_own[x] = wave_sum16x4(l_own[x]);
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      if (2 * wave + x >= count) continue;
+      const int t = tp + 2 * wave + x, h = l16;  // lane holds O^T[col 16cb + 4g + r][head l16] of token t
+      const bool any = l_own[x] > 0.f;
+      const float inv = any ? 1.0f / l_own[x] : 0.f;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int col = 16 * cb + 4 * g;
+        const floatx4 v = o[x][cb] * inv;
+        if (a.direct)
+          *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
+              uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+        else
+          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
+      }
+      if (g == 0) {
         const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
         if (kContig)
           a.lse[((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row] = lse;
@@ -1810,7 +2058,10 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)  // mq4 folds a positive scale
+    if (p.group == 4 && R == 256 && HLA_MQ5 && p.scale_log2 > 0.f)  // mq5 and mq4 fold a positive scale
+      hipLaunchKernelGGL(history_mq5<0>, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+                         dim3(256), 0, stream, p);
+    else if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)
       hipLaunchKernelGGL((history_mq4<R == 256 ? 256 : 512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
@@ -1958,6 +2209,8 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
     const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
     if (width == 512 && mask) hipLaunchKernelGGL((history_mq4<512, 2>), grid4, dim3(512), 0, stream, p);
     else if (width == 512) hipLaunchKernelGGL((history_mq4<512, 1>), grid4, dim3(512), 0, stream, p);
+    else if (HLA_MQ5 && mask) hipLaunchKernelGGL(history_mq5<2>, grid4, dim3(256), 0, stream, p);
+    else if (HLA_MQ5) hipLaunchKernelGGL(history_mq5<1>, grid4, dim3(256), 0, stream, p);
     else if (mask) hipLaunchKernelGGL((history_mq4<256, 2>), grid4, dim3(512), 0, stream, p);
     else hipLaunchKernelGGL((history_mq4<256, 1>), grid4, dim3(512), 0, stream, p);
   } else {
