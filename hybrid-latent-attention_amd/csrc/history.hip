@@ -1224,6 +1224,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 #ifndef HLA_MQ5
 #define HLA_MQ5 1  // 256-wide multi-query steps: history_mq5 (4 waves, no score exchange) instead of history_mq4
 #endif
+#ifndef HLA_MQ5_512
+#define HLA_MQ5_512 1  // 512-wide multi-query steps: history_mq5 (8 waves of one token) instead of history_mq4
+#endif
 constexpr int kMq4Tokens = 8;           // tokens per workgroup
 constexpr int kMq4Keys = 32;            // keys per tile
 
@@ -1492,24 +1495,34 @@ __global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
   }
 }
 
-// history_mq5 (the 256-wide latent): one workgroup per (group of 8 consecutive tokens, KV slot) with 4 waves; wave w
-// owns tokens 2w and 2w + 1 of the pass (32 query rows) and all 256 latent columns, so its scores need no exchange
-// with another wave: per 32-key tile it computes S^T for both tokens (every K fragment read from LDS feeds both
-// tokens' MFMAs), runs the online softmax of history_mq4 and adds V^T P^T. K and V tiles go global -> LDS by direct
-// copies (one 512-byte row per half-wave instruction, wave w copying rows 8w .. 8w+7) into four buffers (K and V of
-// tiles i and i+1); one barrier per tile, after which tile i+2 replaces tile i, so every copy has a tile of time.
-// 74 KB of LDS: two workgroups per CU, whose tiles run out of step, so one's softmax overlaps the other's MFMAs.
+// history_mq5: one workgroup per (group of 8 consecutive tokens, KV slot); each wave owns TPW tokens of the pass
+// and all R latent columns, so its scores need no exchange with another wave: per 32-key tile it computes S^T for
+// its tokens (every K fragment read from LDS feeds their MFMAs), runs the online softmax of history_mq4 and adds
+// V^T P^T. K and V tiles go global -> LDS by direct copies (one row per instruction: half a wave for a 512-byte row,
+// the whole wave for a 1 KB one; wave w copying rows 32 / NW * w ..) into four buffers (K and V of tiles i and i+1);
+// one barrier per tile, after which tile i+2 replaces tile i, so every copy has a tile of time.
+//   R = 256: 4 waves of 2 tokens, 74 KB of LDS: two workgroups per CU, whose tiles run out of step;
+//   R = 512: 8 waves of 1 token (the registers hold 16 query rows x 512 columns), 139 KB of LDS.
 constexpr int kMq5Pages = 1024;  // block-table entries of a pass kept in LDS (longer passes read them from memory)
 
-template <int kMode>
-__global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
-  constexpr int R = 256;
+template <int R>
+struct Mq5Geo {
+  static constexpr int TPW = R == 256 ? 2 : 1;  // tokens per wave
+  static constexpr int NW = kMq4Tokens / TPW;   // waves per workgroup
+  static constexpr int RPW = kMq4Keys / NW;     // tile rows each wave copies (K and V each)
+};
+
+template <int R, int kMode>
+__global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_mq5(HistoryParams a) {
+  static_assert(R == 256 || R == 512, "rows of 512 B (half a copy instruction) or 1 KB");
+  using G = Mq5Geo<R>;
+  constexpr int TPW = G::TPW, NW = G::NW, RPW = G::RPW;
   constexpr bool kContig = kMode != 0, kMask = kMode == 2;
-  constexpr int TOPS = kMask ? 17 : 16;  // copy instructions per wave for a tile (8 K rows, 8 V rows, mask bytes)
+  constexpr int TOPS = 2 * RPW + (kMask ? 1 : 0);  // copy instructions per wave for a tile (K, V rows, mask)
   constexpr int KS = R / 32, CB = R / 16, RS = R + 16;
   __shared__ __attribute__((aligned(16))) uint16_t kt_lds[2][kMq4Keys * RS];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[2][kMq4Keys * RS];
-  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[kMask ? 2 : 1][4][64];  // [tile parity][wave][token*32+key]
+  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[kMask ? 2 : 1][NW][32 * TPW];  // [parity][wave][token*32+key]
   __shared__ int32_t pg_lds[kMq5Pages];
   __shared__ int64_t red_lds[8];
 
@@ -1526,31 +1539,38 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
     int te = tp + 1;
     while (te < t_end && table_row(a, te) == row) ++te;
     const int count = te - tp;
-    int n_max = 0, n_tok[2] = {0, 0};
+    int n_max = 0, n_tok[TPW];
+#pragma unroll
+    for (int x = 0; x < TPW; ++x) n_tok[x] = 0;
 #pragma unroll
     for (int v = 0; v < kMq4Tokens; ++v) {
       const int n = v < count ? (int)min((int64_t)a.ctx[tp + v], cap) : 0;
       n_max = max(n_max, n);
-      if (v == 2 * wave) n_tok[0] = n;
-      if (v == 2 * wave + 1) n_tok[1] = n;
+#pragma unroll
+      for (int x = 0; x < TPW; ++x)
+        if (v == TPW * wave + x) n_tok[x] = n;
     }
     const int tiles16 = (n_max + kTile - 1) / kTile;
     const int j0 = S > 1 ? s * chunk : 0;
     const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
     const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);
-    const int own_n[2] = {min(k1, n_tok[0]), min(k1, n_tok[1])};
-    float m_own[2] = {-INFINITY, -INFINITY}, l_own[2] = {0.f, 0.f};
-    floatx4 o[2][CB];
+    int own_n[TPW];
+    float m_own[TPW], l_own[TPW];
+    floatx4 o[TPW][CB];
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int x = 0; x < TPW; ++x) {
+      own_n[x] = min(k1, n_tok[x]);
+      m_own[x] = -INFINITY;
+      l_own[x] = 0.f;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) o[x][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
     if (k0 < k1) {  // uniform over the workgroup
       const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
-      u32x4 qf[2][KS];
+      u32x4 qf[TPW][KS];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int tq = tp + min(2 * wave + x, count - 1);
+      for (int x = 0; x < TPW; ++x) {
+        const int tq = tp + min(TPW * wave + x, count - 1);
         const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + 8 * g;
 #pragma unroll
         for (int k = 0; k < KS; ++k) qf[x][k] = ld16(qp + 32 * k);
@@ -1562,36 +1582,37 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
         return kContig ? row * a.bt_cols + p : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
       };
       if (pg_local)
-        for (int i = tid; i < np; i += 256) pg_lds[i] = (int32_t)table_page(p0 + i);
+        for (int i = tid; i < np; i += 64 * NW) pg_lds[i] = (int32_t)table_page(p0 + i);
       __syncthreads();
       // the query loads are complete before the first copy: the compiler does not see the copies, so no wait it
       // places for an earlier load may end up counting them
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
       const bool page16 = a.block_size == kTile;
       const uint32_t voff = 16u * lane;
-      // rows 8 * wave .. + 7 of the tile at key kt into buffer buf (keys past the slot's range read its last row)
+      // rows RPW * wave .. of the tile at key kt into buffer buf (keys past the slot's range read its last row)
       auto copy_rows = [&](uint16_t* buf, const uint16_t* base, int kt) {
-        if (page16 && pg_local && kt + kMq4Keys <= k1) {  // the 8 rows sit in page kt / 16 + wave / 2
-          const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 1)]);
-          const uint16_t* src = base + page * a.page_stride + (int64_t)((8 * wave) & 15) * a.row_stride;
+        const int r0 = RPW * wave;
+        if (page16 && pg_local && kt + kMq4Keys <= k1) {  // the RPW rows sit in page kt / 16 + r0 / 16
+          const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (r0 >> 4)]);
+          const uint16_t* src = base + page * a.page_stride + (int64_t)(r0 & 15) * a.row_stride;
 #pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (lane < 32) copy16_to_lds(src + i * a.row_stride, voff, &buf[(8 * wave + i) * RS]);
+          for (int i = 0; i < RPW; ++i)
+            if (R == 512 || lane < 32) copy16_to_lds(src + i * a.row_stride, voff, &buf[(r0 + i) * RS]);
         } else {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int key = min(kt + 8 * wave + i, k1 - 1), p = key / a.block_size;
+          for (int i = 0; i < RPW; ++i) {
+            const int key = min(kt + r0 + i, k1 - 1), p = key / a.block_size;
             const int64_t page = uniform64(pg_local ? (int64_t)pg_lds[p - p0] : table_page(p));
-            if (lane < 32)
+            if (R == 512 || lane < 32)
               copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
-                            &buf[(8 * wave + i) * RS]);
+                            &buf[(r0 + i) * RS]);
           }
         }
       };
       auto copy_tile = [&](int j) {  // tile j (K, V and this wave's mask bytes) into the buffers of parity j & 1
         const int kt = k0 + j * kMq4Keys;
-        if (kMask && lane < 4) {  // lanes 0-3: token l / 2, bytes 16 (l % 2) .. (chunks past the row: its end)
-          const int tq = tp + min(2 * wave + (lane >> 1), count - 1);
+        if (kMask && lane < 2 * TPW) {  // token l / 2, bytes 16 (l % 2) .. (chunks past the row: its end)
+          const int tq = tp + min(TPW * wave + (lane >> 1), count - 1);
           const int c0 = min(kt + 16 * (lane & 1), (int)cap - 16);
           copy16_to_lds_v(a.mask + (int64_t)tq * a.mask_st + c0, &mk_lds[j & 1][wave][0]);
         }
@@ -1609,11 +1630,11 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
       plain_barrier();
       for (int i = 0; i < ntiles; ++i) {
         const int kt = k0 + i * kMq4Keys, par = i & 1;
-        floatx4 sp[2][2];  // S^T of both tokens: keys 16 kb + 4g + r, row l16
+        floatx4 sp[TPW][2];  // S^T of the wave's tokens: keys 16 kb + 4g + r, row l16
         {
           const uint16_t* kp = &kt_lds[par][l16 * RS + 8 * g];
 #pragma unroll
-          for (int x = 0; x < 2; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+          for (int x = 0; x < TPW; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
           u32x4 ka = *reinterpret_cast<const u32x4*>(kp), kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS);
 #pragma unroll
           for (int k = 0; k < KS; ++k) {  // the next k-step's fragments are requested before this one's MFMAs
@@ -1623,7 +1644,7 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
               kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * (k + 1));
             }
 #pragma unroll
-            for (int x = 0; x < 2; ++x) {
+            for (int x = 0; x < TPW; ++x) {
               sp[x][0] = mfma16x16x32(ca, qf[x][k], sp[x][0]);
               sp[x][1] = mfma16x16x32(cc, qf[x][k], sp[x][1]);
             }
@@ -1689,14 +1710,16 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
           return join_tr(lo, hi);
         };
         {
-          const u32x4 pb0 = softmax_tok(0), pb1 = softmax_tok(1);
+          u32x4 pb[TPW];
+#pragma unroll
+          for (int x = 0; x < TPW; ++x) pb[x] = softmax_tok(x);
           u32x4 vt = vfrag(0);
 #pragma unroll
-          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs; it feeds both
-            const u32x4 cur = vt;           // tokens' MFMAs
+          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs; it feeds
+            const u32x4 cur = vt;           // every token's MFMA
             if (cb + 1 < CB) vt = vfrag(cb + 1);
-            o[0][cb] = mfma16x16x32(cur, pb0, o[0][cb]);
-            o[1][cb] = mfma16x16x32(cur, pb1, o[1][cb]);
+#pragma unroll
+            for (int x = 0; x < TPW; ++x) o[x][cb] = mfma16x16x32(cur, pb[x], o[x][cb]);
           }
         }
         if (i + 1 < ntiles) {
@@ -1708,11 +1731,11 @@ __global__ __launch_bounds__(256, 2) void history_mq5(HistoryParams a) {
       }
     }
 #pragma unroll
-    for (int x = 0; x < 2; ++x) l_own[x] = wave_sum16x4(l_own[x]);
+    for (int x = 0; x < TPW; ++x) l_own[x] = wave_sum16x4(l_own[x]);
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      if (2 * wave + x >= count) continue;
-      const int t = tp + 2 * wave + x, h = l16;  // lane holds O^T[col 16cb + 4g + r][head l16] of token t
+    for (int x = 0; x < TPW; ++x) {
+      if (TPW * wave + x >= count) continue;
+      const int t = tp + TPW * wave + x, h = l16;  // lane holds O^T[col 16cb + 4g + r][head l16] of token t
       const bool any = l_own[x] > 0.f;
       const float inv = any ? 1.0f / l_own[x] : 0.f;
 #pragma unroll
@@ -2059,8 +2082,11 @@ int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
     if (p.group == 4 && R == 256 && HLA_MQ5 && p.scale_log2 > 0.f)  // mq5 and mq4 fold a positive scale
-      hipLaunchKernelGGL(history_mq5<0>, dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+      hipLaunchKernelGGL((history_mq5<256, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(256), 0, stream, p);
+    else if (p.group == 4 && R == 512 && HLA_MQ5_512 && p.scale_log2 > 0.f)
+      hipLaunchKernelGGL((history_mq5<512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
+                         dim3(512), 0, stream, p);
     else if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)
       hipLaunchKernelGGL((history_mq4<R == 256 ? 256 : 512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
                          dim3(512), 0, stream, p);
@@ -2207,10 +2233,12 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.mask_st = mask_st;
   if (mq4) {
     const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
-    if (width == 512 && mask) hipLaunchKernelGGL((history_mq4<512, 2>), grid4, dim3(512), 0, stream, p);
+    if (width == 512 && HLA_MQ5_512 && mask) hipLaunchKernelGGL((history_mq5<512, 2>), grid4, dim3(512), 0, stream, p);
+    else if (width == 512 && HLA_MQ5_512) hipLaunchKernelGGL((history_mq5<512, 1>), grid4, dim3(512), 0, stream, p);
+    else if (width == 512 && mask) hipLaunchKernelGGL((history_mq4<512, 2>), grid4, dim3(512), 0, stream, p);
     else if (width == 512) hipLaunchKernelGGL((history_mq4<512, 1>), grid4, dim3(512), 0, stream, p);
-    else if (HLA_MQ5 && mask) hipLaunchKernelGGL(history_mq5<2>, grid4, dim3(256), 0, stream, p);
-    else if (HLA_MQ5) hipLaunchKernelGGL(history_mq5<1>, grid4, dim3(256), 0, stream, p);
+    else if (HLA_MQ5 && mask) hipLaunchKernelGGL((history_mq5<256, 2>), grid4, dim3(256), 0, stream, p);
+    else if (HLA_MQ5) hipLaunchKernelGGL((history_mq5<256, 1>), grid4, dim3(256), 0, stream, p);
     else if (mask) hipLaunchKernelGGL((history_mq4<256, 2>), grid4, dim3(512), 0, stream, p);
     else hipLaunchKernelGGL((history_mq4<256, 1>), grid4, dim3(512), 0, stream, p);
   } else {
