@@ -37,12 +37,14 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop'),
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop', 'rows'),
                    default='decode',
                    help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
                         'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
                         'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
-                        'history, one layer x 4 loops. Only decode prints the headline line.')
+                        'history, one layer x 4 loops; writer: the row writer and commit; export: the rollout-cache '
+                        'gather; khop: multi-query history with backward (B=4, L=2880); rows: single-query history '
+                        'over contiguous rows with a key mask (B=8, 8192 rows). Only decode prints the headline line.')
     p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 32 / 8 / 4 by workload)')
     p.add_argument('--context', type=int, default=0, help='history tokens before the step (default by workload)')
     p.add_argument('--queries', type=int, default=512, help='new tokens per request of --workload prefill')
@@ -51,7 +53,7 @@ def parse():
     p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
     p.add_argument('--width', type=int, default=512, choices=(256, 512),
-                   help='latent width of --kernel-only and --workload khop')
+                   help='latent width of --kernel-only and --workload khop / rows')
     p.add_argument('--copy-calibration', action='store_true',
                    help='only run a plain 1 GiB device copy three times (scales the FETCH_SIZE / WRITE_SIZE counters '
                         'of a PMC profile to bytes)')
@@ -522,6 +524,62 @@ def khop_workload(args, pkg, device):
                       'cpu_baseline': base}), flush=True)
 
 
+def rows_workload(args, pkg, device):
+    """Single-query history attention over contiguous rows with a key mask: the HF rolling engine's history call
+    (``hla/latent/fused_history.py:49-54``) at its decode shape, B = 8 rows of ``--context`` (8192) latent rows of
+    width ``--width`` (512), padding masks (valid lengths N, 0.95 N, ..., and every 7th key of row 1 hidden). Times
+    the forward (bounds, split kernel and reduction in a HIP graph; HBM GB/s of the rows up to each row's last
+    visible key plus the mask) and the forward + backward through autograd (dq, dk, dv). One JSON line."""
+    hg = pkg.history_gemm
+    B, N, R = args.batch or 8, args.context or 8192, args.width
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    q = (torch.randn(B, HEADS, R, generator=g, device=device) * R ** -0.5).to(torch.bfloat16).requires_grad_(True)
+    k = torch.randn(B, N, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    v = torch.randn(B, N, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    lengths = torch.tensor([max(1, int(N * (1 - 0.05 * i))) for i in range(B)], device=device)
+    mask = torch.arange(N, device=device)[None] < lengths[:, None]
+    if B > 1:
+        mask[1, ::7] = False
+    scale = 1 / math.sqrt(HEAD_DIM)
+    dz = torch.randn(B, HEADS, R, generator=g, device=device).to(torch.bfloat16)
+    dlse = torch.randn(B, HEADS, generator=g, device=device)
+
+    def fwd():
+        with torch.no_grad():
+            hg.history_attention(q, k, v, mask, scale)
+
+    def train():
+        z, lse = hg.history_attention(q, k, v, mask, scale)
+        torch.autograd.grad([z, lse], [q, k, v], [dz, dlse])
+
+    ms_f = time_graph(fwd, args.steps, args.warmup)
+    ms_t = time_eager(train, args.steps, args.warmup)
+    rows = int(lengths.sum().item())                       # rows up to each row's last visible key
+    nbytes = rows * 2 * R * 2 + B * N
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import s6_oracle as O
+        f32 = lambda t: t.detach().float().cpu().numpy()
+        qs, ks, vs, ms_ = f32(q[:1]), f32(k[:1]), f32(v[:1]), mask[:1].cpu().numpy()
+        run = lambda: O.single_history(qs, ks, vs, ms_, scale, dtype=np.float32)
+        run()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        base = {'value': round(float(np.median(times)) * 1e6 * rows / int(lengths[0].item()), 1),
+                'unit': 'us per forward', 'cores': len(os.sched_getaffinity(0)), 'kind': 'port',
+                'sample': f'numpy oracle forward (float32) of row 0 ({int(lengths[0].item())} keys), median of 3, '
+                          f'scaled by rows read ({rows}); extrapolated'}
+    gbps = nbytes / (ms_f * 1e6)
+    print(json.dumps({'workload': 'rows', 'value': round(ms_f * 1000, 2), 'unit': 'us per forward', 'B': B, 'N': N,
+                      'heads': HEADS, 'width': R, 'rows_read': rows, 'bytes': nbytes, 'gbps': round(gbps, 1),
+                      'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'train_ms': round(ms_t, 3), 'steps': args.steps,
+                      'data': 'synthetic (randn q, k, v, cotangents; padding masks)', 'forward_hip_graph': True,
+                      'cpu_baseline': base}), flush=True)
+
+
 def time_eager(fn, steps, warmup):
     """Events around ``steps`` eager calls after ``warmup`` (for work that allocates, e.g. autograd backward)."""
     for _ in range(warmup):
@@ -564,6 +622,8 @@ def main():
         return export_workload(args, pkg, device)
     if args.workload == 'khop':
         return khop_workload(args, pkg, device)
+    if args.workload == 'rows':
+        return rows_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
     defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]

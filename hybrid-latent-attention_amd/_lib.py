@@ -54,12 +54,16 @@ SIGNATURES = {
     'hla_s6_khop_bounds': [P, I64, I64, I32, I32, I32, P, P],
     'hla_s6_khop_forward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32, P,
                             I64, I64, I64, P, P],
+    'hla_s6_masked_history': [P, I64, I64, P, P, I64, I64, P, I64, P, I32, I32, I32, I32, F32, I32, P, I64, P, I64,
+                              I64, P, P],
+    'hla_s6_khop_backward_workspace': [I32, I32, I32, I32, I32],
     'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
                              P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,
                              I32, P, I64, P],
 }
 
-RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64}
+RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64,
+            'hla_s6_khop_backward_workspace': ctypes.c_int64}
 
 _LIB = None
 

@@ -135,6 +135,15 @@ __device__ __forceinline__ void copy16_to_lds(const void* row, uint32_t voff, co
                : "memory", "m0");
 }
 
+// The same for callers whose LDS address the compiler may hold in a VGPR (a uniform value): it goes through
+// readfirstlane into the SGPR the copy needs.
+__device__ __forceinline__ void copy16_to_lds_rfl(const void* row, uint32_t voff, const void* lds) {
+  const uint32_t dst =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(voff), "s"(row)
+               : "memory", "m0");
+}
+
 // The same with a per-lane source address (64-bit, in VGPRs).
 __device__ __forceinline__ void copy16_to_lds_v(const void* src, const void* lds) {
   const uint32_t dst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;

@@ -108,6 +108,7 @@ struct HistoryParams {
   int tok_per_row;
   const uint8_t* mask;
   int64_t mask_st;
+  bool lse_rows;  // lse of history_split / history_combine in [rows][16][tok_per_row] instead of [16][T]
 };
 
 template <int R>
@@ -279,6 +280,15 @@ template <int R>
 struct TileRegs {
   u32x4 k[Geo<R>::KI];
   u32x4 v[Geo<R>::VC];
+  uint32_t mk;  // contiguous rows with a key mask: mask bytes of keys 4g .. 4g+3 of the tile (lane group g)
+};
+
+// Where history_split's token t finds its rows: a block-table row (paged caches), or the contiguous rows
+// [t / tok_per_row] (rows at page_stride, keys at row_stride) with an optional byte mask per (token, key).
+struct RowSource {
+  const int32_t* btr;    // paged: the token's block-table row
+  int64_t base;          // contiguous: element offset of the token's first row
+  const uint8_t* mrow;   // contiguous: the token's mask row, or null (every key visible)
 };
 
 // K/V row loads: non-temporal when every row is read once (decode), cached when several tokens read the same rows
@@ -289,13 +299,33 @@ __device__ __forceinline__ u32x4 ld_stream(const uint16_t* p) {
   else return ld16(p);
 }
 
-template <int R, bool NT>
-__device__ __forceinline__ void load_tile(const HistoryParams& a, const int32_t* btr, int n, int j, int col0,
+template <int R, bool NT, bool kRows = false>
+__device__ __forceinline__ void load_tile(const HistoryParams& a, const RowSource& src, int n, int j, int col0,
                                           int lane, TileRegs<R>& r) {
   using G = Geo<R>;
   const int key0 = j * kTile;
-  const int64_t page = min(max((int64_t)btr[key0 / a.block_size], (int64_t)0), a.num_blocks - 1);
-  const int64_t base = page * a.page_stride + (int64_t)(key0 % a.block_size) * a.row_stride + col0;
+  int64_t base;
+  if constexpr (kRows) {
+    base = src.base + (int64_t)key0 * a.row_stride + col0;
+    // mask bytes of keys kb .. kb+3 (one 4-byte load when they are all below the bound and the row is 4-byte
+    // aligned; keys at or past the bound are hidden by the bound itself and their bytes are not read)
+    const int kb = key0 + 4 * (lane >> 4);
+    uint32_t mk = 0xffffffffu;
+    if (src.mrow) {
+      if (kb + 4 <= n && (reinterpret_cast<uintptr_t>(src.mrow) & 3u) == 0) {
+        mk = *reinterpret_cast<const uint32_t*>(src.mrow + kb);
+      } else {
+        mk = 0u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (kb + e < n) mk |= (uint32_t)src.mrow[kb + e] << (8 * e);
+      }
+    }
+    r.mk = mk;
+  } else {
+    const int64_t page = min(max((int64_t)src.btr[key0 / a.block_size], (int64_t)0), a.num_blocks - 1);
+    base = page * a.page_stride + (int64_t)(key0 % a.block_size) * a.row_stride + col0;
+  }
   const int hq = lane & 15, g = lane >> 4;
 #if HLA_HIST_KLDS
   (void)hq;
@@ -368,10 +398,12 @@ __device__ __forceinline__ short4v vt_operand(const uint16_t* vs, int nt, int g,
 #endif
 }
 
-// Stage B: exchange S partials, online softmax, O^T += V^T P^T.
-template <int R>
+// Stage B: exchange S partials, online softmax, O^T += V^T P^T. With kMask, byte r of mk hides key 4g + r of the
+// tile when zero.
+template <int R, bool kMask = false>
 __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_t* vs, int key0, int n, float scale_log2,
-                                        int wave, int lane, floatx4 (&oacc)[Geo<R>::NT], float& m, float& l) {
+                                        int wave, int lane, floatx4 (&oacc)[Geo<R>::NT], float& m, float& l,
+                                        uint32_t mk = 0xffffffffu) {
   using G = Geo<R>;
   sx[wave * 64 + lane] = sacc;
   __syncthreads();
@@ -381,7 +413,10 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   const int hq = lane & 15, g = lane >> 4;
   const int kb = key0 + 4 * g;
   float sc[4];
-  if (key0 + kTile <= n) {  // wave-uniform: every key of the tile is history
+  if (kMask) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = (kb + r < n && ((mk >> (8 * r)) & 255u) != 0) ? s[r] * scale_log2 : -INFINITY;
+  } else if (key0 + kTile <= n) {  // wave-uniform: every key of the tile is history
 #pragma unroll
     for (int r = 0; r < 4; ++r) sc[r] = s[r] * scale_log2;
   } else {
@@ -430,7 +465,15 @@ __device__ void window_jobs(const WindowPart& w, int T, float scale_log2, int v,
   }
 }
 
-template <int R, bool NT>
+// lse index of (token t, head h): [16][T], or [rows][16][tok_per_row] with lse_rows (contiguous rows)
+__device__ __forceinline__ int64_t lse_index(const HistoryParams& a, int t, int h) {
+  if (!a.lse_rows) return (int64_t)h * a.T + t;
+  return ((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row;
+}
+
+// kRows: contiguous rows (bt == null; token t reads rows [t / tok_per_row]) with an optional key mask, whose
+// partials may then see no key at all (a zero output and lse = -inf)
+template <int R, bool NT, bool kRows = false>
 __global__ __launch_bounds__(Geo<R>::THREADS)
 #if HLA_HIST_WPE
 __attribute__((amdgpu_waves_per_eu(HLA_HIST_WPE, HLA_HIST_WPE)))
@@ -482,12 +525,18 @@ void history_split(HistoryParams a) {
       uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
 #pragma unroll
       for (int nt = 0; nt < G::NT; ++nt) *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{0u, 0u};
-      if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = -INFINITY;
+      if (wave == 0 && g == 0) a.lse[kRows ? lse_index(a, t, hq) : (int64_t)hq * a.T + t] = -INFINITY;
       return;
     }
     if (wave == 0 && g == 0) a.ws_lse[part_row] = -INFINITY;
   } else {
-    const int32_t* btr = a.bt + (a.bt_rows ? a.bt_rows[t] : (int64_t)t) * a.bt_stride;
+    RowSource src{};
+    if constexpr (kRows) {
+      src.base = (int64_t)(t / a.tok_per_row) * a.page_stride;
+      src.mrow = a.mask ? a.mask + (int64_t)t * a.mask_st : nullptr;
+    } else {
+      src.btr = a.bt + (a.bt_rows ? a.bt_rows[t] : (int64_t)t) * a.bt_stride;
+    }
     u32x4 qreg[G::KI];
     {
       const uint16_t* qp = a.q + (int64_t)t * a.q_st + (int64_t)hq * a.q_sh + col0 + 8 * g;
@@ -505,7 +554,7 @@ void history_split(HistoryParams a) {
     TileRegs<R> regs[DEPTH];
 #pragma unroll
     for (int u = 0; u < DEPTH; ++u)
-      if (j_begin + u < j_end) load_tile<R, NT>(a, btr, n, j_begin + u, col0, lane, regs[u]);
+      if (j_begin + u < j_end) load_tile<R, NT, kRows>(a, src, n, j_begin + u, col0, lane, regs[u]);
     for (int j = j_begin; j < j_end; j += DEPTH) {
 #pragma unroll
       for (int u = 0; u < DEPTH; ++u) {
@@ -513,15 +562,17 @@ void history_split(HistoryParams a) {
         if (jt < j_end) {
           uint16_t* vs = v_lds[wave][jt % NVB];
           floatx4 sa = stage_a<R>(regs[u], qreg, vs, k_lds[wave], lane);
-          if (jt + DEPTH < j_end) load_tile<R, NT>(a, btr, n, jt + DEPTH, col0, lane, regs[u]);
-          stage_b<R>(sa, s_lds[jt & 1], vs, jt * kTile, n, a.scale_log2, wave, lane, oacc, m, l);
+          const uint32_t mk = regs[u].mk;
+          if (jt + DEPTH < j_end) load_tile<R, NT, kRows>(a, src, n, jt + DEPTH, col0, lane, regs[u]);
+          stage_b<R, kRows>(sa, s_lds[jt & 1], vs, jt * kTile, n, a.scale_log2, wave, lane, oacc, m, l, mk);
         }
       }
     }
 
     l = wave_sum16x4(l);
-    const float inv = 1.0f / l;
-    const float lse = (m + log2f(l)) * kLn2;
+    // (with a key mask a split may see no key: l = 0 gives a zero partial with lse = -inf)
+    const float inv = kRows ? (l > 0.f ? 1.0f / l : 0.f) : 1.0f / l;
+    const float lse = kRows && !(l > 0.f) ? -INFINITY : (m + log2f(l)) * kLn2;
     if (a.direct) {
       uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)hq * a.o_sh + col0 + 4 * g;
 #pragma unroll
@@ -529,7 +580,7 @@ void history_split(HistoryParams a) {
         const floatx4 o = oacc[nt] * inv;
         *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
       }
-      if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = lse;
+      if (wave == 0 && g == 0) a.lse[kRows ? lse_index(a, t, hq) : (int64_t)hq * a.T + t] = lse;
       return;
     }
     float* wp = a.ws_o + part_row * R + col0 + 4 * g;
@@ -699,7 +750,8 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
       for (int nt = 0; nt < G::NT; ++nt) oacc[u][nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     if (j_begin < j_end) {  // uniform over the workgroup
-      const int32_t* btr = a.bt + row * a.bt_stride;
+      RowSource src{};
+      src.btr = a.bt + row * a.bt_stride;
       u32x4 qreg[NQ][G::KI];
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
@@ -712,11 +764,11 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
       // a slower wave may still be reading (the barrier in between orders them); the wave-private K/V copies may
       // be rewritten by the next tile because a wave's own LDS accesses stay in order.
       TileRegs<R> regs;
-      load_tile<R, false>(a, btr, n_max, j_begin, col0, lane, regs);
+      load_tile<R, false>(a, src, n_max, j_begin, col0, lane, regs);
       for (int jt = j_begin; jt < j_end; ++jt) {
         floatx4 sa[NQ];
         group_stage_a<R, NQ>(regs, qreg, v_lds[wave], k_lds[wave], lane, count, sa);
-        if (jt + 1 < j_end) load_tile<R, false>(a, btr, n_max, jt + 1, col0, lane, regs);
+        if (jt + 1 < j_end) load_tile<R, false>(a, src, n_max, jt + 1, col0, lane, regs);
         group_stage_b<R, NQ>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane, oacc, m, l);
         par ^= 1;
       }
@@ -1782,7 +1834,7 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
   uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * i;
   if (mx == -INFINITY) {
     *reinterpret_cast<uint2*>(op) = uint2{0u, 0u};
-    if (i == 0) a.lse[(int64_t)h * a.T + t] = -INFINITY;
+    if (i == 0) a.lse[lse_index(a, t, h)] = -INFINITY;
     return;
   }
   const float* base = a.ws_o + ((int64_t)t * S_all * kHeads + h) * R + 4 * i;
@@ -1810,7 +1862,7 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
   }
   acc = acc * (1.0f / den);
   *reinterpret_cast<uint2*>(op) = uint2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
-  if (i == 0) a.lse[(int64_t)h * a.T + t] = mx + logf(den);
+  if (i == 0) a.lse[lse_index(a, t, h)] = mx + logf(den);
 }
 
 // ---- decode epilogue --------------------------------------------------------------------------------------------
@@ -2283,6 +2335,76 @@ extern "C" int hla_s6_history_attention_grouped(
   p.group = group;
   p.shared_rows = shared_rows != 0 || group > 1;
   return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_masked_history(const void* q, int64_t q_sb, int64_t q_sh, const void* k, const void* v,
+                                     int64_t kv_sb, int64_t kv_sn, const uint8_t* mask, int64_t m_sb,
+                                     const int32_t* bound, int32_t B, int32_t N, int32_t num_heads, int32_t width,
+                                     float scale, int32_t num_splits, float* workspace, int64_t workspace_floats,
+                                     void* z, int64_t z_sb, int64_t z_sh, float* lse, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(B >= 0 && N >= 1, HLA_S6_EINVAL, "masked_history: need B >= 0 and at least one storage row");
+  HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED, "masked_history: %d heads (the kernel is built for 16)",
+              num_heads);
+  HLA_REQUIRE(width == 128 || width == 256 || width == 512 || width == 1024, HLA_S6_EUNSUPPORTED,
+              "masked_history: latent width %d not in {128, 256, 512, 1024}", width);
+  HLA_REQUIRE(num_splits >= 1 && num_splits <= kMaxSplits, HLA_S6_EINVAL,
+              "masked_history: num_splits must be in [1, %d]", kMaxSplits);
+  if (B == 0) return HLA_S6_OK;
+  HLA_REQUIRE(q && k && v && bound && z && lse, HLA_S6_EINVAL, "masked_history: null pointer argument");
+  HLA_REQUIRE(aligned16(q) && q_sb % 8 == 0 && q_sh % 8 == 0, HLA_S6_EINVAL,
+              "masked_history: q needs 16-byte aligned rows (unit last stride, strides multiple of 8)");
+  HLA_REQUIRE(aligned16(k) && aligned16(v) && kv_sb % 8 == 0 && kv_sn % 8 == 0, HLA_S6_EINVAL,
+              "masked_history: k / v rows must be 16-byte aligned (strides multiple of 8 elements)");
+  HLA_REQUIRE((reinterpret_cast<uintptr_t>(z) & 7u) == 0 && z_sb % 4 == 0 && z_sh % 4 == 0, HLA_S6_EINVAL,
+              "masked_history: z rows must be 8-byte aligned");
+  HLA_REQUIRE(!mask || m_sb >= N, HLA_S6_EINVAL, "masked_history: mask row stride below N");
+  if (num_splits > 1) {
+    const int64_t need = (int64_t)B * num_splits * kHeads * (width + 1);
+    HLA_REQUIRE(workspace != nullptr && workspace_floats >= need, HLA_S6_EWORKSPACE,
+                "S6 workspace overflow: need %lld floats, have %lld", (long long)need, (long long)workspace_floats);
+    HLA_REQUIRE(aligned16(workspace), HLA_S6_EINVAL, "masked_history: workspace must be 16-byte aligned");
+  }
+  HistoryParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_st = q_sb;
+  p.q_sh = q_sh;
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.page_stride = kv_sb;  // one "page" per batch row holding its N rows
+  p.row_stride = kv_sn;
+  p.block_size = N;
+  p.num_blocks = B;
+  p.bt = nullptr;
+  p.bt_cols = 1;
+  p.tok_per_row = 1;
+  p.lse_rows = true;
+  p.ctx = bound;
+  p.mask = mask;
+  p.mask_st = m_sb;
+  p.scale_log2 = scale * kLog2e;
+  p.num_splits = num_splits;
+  p.T = B;
+  p.ws_o = num_splits > 1 ? workspace : nullptr;
+  p.ws_lse = num_splits > 1 ? workspace + (int64_t)B * num_splits * kHeads * width : nullptr;
+  p.out = static_cast<uint16_t*>(z);
+  p.o_st = z_sb;
+  p.o_sh = z_sh;
+  p.lse = lse;
+  p.group = 1;
+  p.direct = num_splits == 1;
+  p.combine = true;
+  const hipStream_t st = as_stream(stream);
+  const dim3 grid(split_workgroups(B, num_splits));
+  switch (width) {
+    case 128: hipLaunchKernelGGL((history_split<128, true, true>), grid, dim3(Geo<128>::THREADS), 0, st, p); break;
+    case 256: hipLaunchKernelGGL((history_split<256, true, true>), grid, dim3(Geo<256>::THREADS), 0, st, p); break;
+    case 512: hipLaunchKernelGGL((history_split<512, true, true>), grid, dim3(Geo<512>::THREADS), 0, st, p); break;
+    default: hipLaunchKernelGGL((history_split<1024, true, true>), grid, dim3(Geo<1024>::THREADS), 0, st, p); break;
+  }
+  int rc = check_launch("masked_history");
+  if (rc == HLA_S6_OK && num_splits > 1) rc = dispatch_combine(p, width, st);
+  return rc;
 }
 
 extern "C" int hla_s6_history_partials(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,

@@ -59,6 +59,7 @@ struct KhopParams {
   int64_t dk_sb, dk_sn, dv_sb, dv_sn;
   int key_splits;  // dkdv: row ranges per key tile (partials of split s go to dk + s * dk_ss)
   int64_t dk_ss, dv_ss;
+  int64_t dq_ss;   // dq4 with key ranges (gridDim.z > 1): the partial of range z goes to dq + z * dq_ss
 };
 
 template <int R>
@@ -483,6 +484,13 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
   __syncthreads();
   const int nkeys = max(max(bound_s[0], bound_s[1]), max(bound_s[2], bound_s[3]));
   const int own_bound = bound_s[min(u, ntok - 1)];
+  // key range z of gridDim.z: tiles [tb, te) of the workgroup's 32-key tiles (dq is linear in the keys, so each
+  // range writes a partial and the partials are summed afterwards)
+  // (uniform, and kept in SGPRs: the copy instructions take the tile's row address and LDS buffer from them)
+  const int tiles_all = (nkeys + 31) / 32;
+  const int per = (tiles_all + (int)gridDim.z - 1) / (int)gridDim.z;
+  const int tb = __builtin_amdgcn_readfirstlane(min(tiles_all, (int)blockIdx.z * per));
+  const int te = __builtin_amdgcn_readfirstlane(min(tiles_all, tb + per));
   // every earlier load is complete before the first copy: the compiler does not see the copies, so no wait it
   // places for an earlier load may end up counting them
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -496,7 +504,7 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
     for (int r4 = 0; r4 < 4; ++r4) {
       const int r = 4 * wave + r4;
       const uint16_t* row = base + (int64_t)b * bst + (int64_t)min(kt + r, a.N - 1) * rst;
-      if (R == 512 || lane < 32) copy16_to_lds(row, voff, &buf[r * RS]);
+      if (R == 512 || lane < 32) copy16_to_lds_rfl(row, voff, &buf[r * RS]);
     }
   };
   auto copy_k = [&](int j) {  // K tile j, and the mask bytes of this wave's token for it (lanes 0-1)
@@ -509,22 +517,21 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
   };
   auto copy_v = [&](int j) { copy_rows(vt_lds[j & 1], a.v, a.v_sb, a.v_sn, j * 32); };
 
-  const int ntiles = (nkeys + 31) / 32;
-  if (ntiles > 0) {
-    copy_k(0);
-    copy_v(0);
-    if (ntiles > 1) {
-      copy_k(1);
-      copy_v(1);
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(KOPS + 4, 15));  // tile 0 landed; tile 1 may be in flight
+  if (tb < te) {
+    copy_k(tb);
+    copy_v(tb);
+    if (te - tb > 1) {
+      copy_k(tb + 1);
+      copy_v(tb + 1);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(KOPS + 4, 15));  // tile tb landed; tile tb+1 may be in flight
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     }
     plain_barrier();
   }
-  for (int i = 0; i < ntiles; ++i) {
+  for (int i = tb; i < te; ++i) {
     const int kt = i * 32, par = i & 1;
-    const bool more = i + 1 < ntiles, more2 = i + 2 < ntiles;
+    const bool more = i + 1 < te, more2 = i + 2 < te;
     floatx4 sb[2];  // this wave's block: S^T (role 0) or dP^T (role 1), keys kt + 16 kb + 4g + r, row l16
     {
       const uint16_t* ap = (role == 0 ? kt_lds[par] : vt_lds[par]) + l16 * RS + 8 * g;
@@ -593,7 +600,8 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
     }
   }
   if (u < ntok) {  // lane holds dQ^T[col 16cb + 4g + r][head l16] of token i0 + u
-    float* dqp = a.dq + (int64_t)b * a.dq_sb + (int64_t)(i0 + u) * a.dq_si + (int64_t)l16 * a.dq_sh + col0 + 4 * g;
+    float* dqp = a.dq + blockIdx.z * a.dq_ss + (int64_t)b * a.dq_sb + (int64_t)(i0 + u) * a.dq_si +
+                 (int64_t)l16 * a.dq_sh + col0 + 4 * g;
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) *reinterpret_cast<floatx4*>(dqp + 16 * cb) = acc[cb];
   }
@@ -887,9 +895,23 @@ __global__ __launch_bounds__(256) void khop_bound_kernel(const uint8_t* mask, in
     return;
   }
   const uint8_t* row = mask + (t / Lq) * m_sb + (t % Lq) * m_si;
+  // the bytes before the row's first 16-byte boundary, then whole 16-byte words (all in flight at once), then the
+  // tail; the highest nonzero byte of a little-endian word w is byte (31 - clz(w)) / 8
+  const int head = min(N, (int)((16u - (reinterpret_cast<uintptr_t>(row) & 15u)) & 15u));
+  const int nch = (N - head) >> 4, tail0 = head + 16 * nch;
   int last = -1;
-  for (int j = lane; j < N; j += 64)
-    if (row[j]) last = j;
+  if (lane < head && row[lane]) last = lane;
+  const u32x4* body = reinterpret_cast<const u32x4*>(row + head);
+#pragma unroll 4
+  for (int c = lane; c < nch; c += 64) {
+    const u32x4 w = __builtin_nontemporal_load(body + c);
+    const int base = head + 16 * c;
+    if (w[3]) last = base + 12 + (31 - __clz(w[3])) / 8;
+    else if (w[2]) last = base + 8 + (31 - __clz(w[2])) / 8;
+    else if (w[1]) last = base + 4 + (31 - __clz(w[1])) / 8;
+    else if (w[0]) last = base + (31 - __clz(w[0])) / 8;
+  }
+  if (tail0 + lane < N && row[tail0 + lane]) last = tail0 + lane;  // the tail is shorter than 16 bytes
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) last = max(last, __shfl_xor(last, off));
   if (lane == 0) bound[t] = last + 1;
@@ -925,6 +947,15 @@ __global__ __launch_bounds__(256) void khop_split_sum_kernel(const float* part, 
 }
 
 inline bool kh_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Key ranges of the multi-query dq kernel: 1 when the B * ceil(Lq / 4) token groups fill the GPU, else enough
+// ranges for about 512 workgroups, at least 4 key tiles (128 keys) each and at most 64.
+inline int kh_dq_splits(int B, int Lq, int N) {
+  const int64_t groups = (int64_t)B * ((Lq + 3) / 4);
+  if (groups >= 128) return 1;
+  const int by_tiles = max(1, (N + 31) / 32 / 4);
+  return (int)max((int64_t)1, min(min((int64_t)64, (512 + groups - 1) / groups), (int64_t)by_tiles));
+}
 
 int kh_check(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_sn,
              const void* v, int64_t v_sb, int64_t v_sn, int B, int Lq, int N, int R, int heads) {
@@ -999,6 +1030,16 @@ extern "C" int hla_s6_khop_forward(const void* q, int64_t q_sb, int64_t q_si, in
   return check_launch("khop_forward");
 }
 
+extern "C" int64_t hla_s6_khop_backward_workspace(int32_t B, int32_t Lq, int32_t N, int32_t width,
+                                                   int32_t key_splits) {
+  using namespace hla;
+  if (B < 1 || Lq < 0 || N < 1 || width < 1 || key_splits < 1) return 0;
+  const int64_t kv = key_splits > 1 ? 2 * (int64_t)key_splits * B * N * width : 0;
+  const int qs = (width == 512 || width == 256) && N % 16 == 0 && Lq > 0 ? kh_dq_splits(B, Lq, N) : 1;
+  const int64_t dqp = qs > 1 ? (int64_t)qs * B * Lq * 16 * width : 0;
+  return max(kv, dqp);
+}
+
 extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k,
                                     int64_t k_sb, int64_t k_sn, const void* v, int64_t v_sb, int64_t v_sn,
                                     const uint8_t* mask, int64_t m_sb, int64_t m_si, const int32_t* bound, int32_t B,
@@ -1056,11 +1097,27 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
                      dq_sb % 4 == 0 && dq_si % 4 == 0 && dq_sh % 4 == 0 &&
                      (!mask || (kh_aligned16(mask) && m_sb % 16 == 0 && m_si % 16 == 0));
     if (dq4) {
-      const dim3 grid4((unsigned)((Lq + 3) / 4), (unsigned)B);
+      // few token groups (a single query per row): key ranges with fp32 partials in the workspace, summed in a
+      // fixed order into a contiguous dq
+      const int64_t part_q = (int64_t)B * Lq * 16 * width;
+      int qs = kh_dq_splits(B, Lq, N);
+      if (qs > 1 && !(workspace && kh_aligned16(workspace) && workspace_floats >= qs * part_q &&
+                      dq_sb == (int64_t)Lq * 16 * width && dq_si == 16 * width && dq_sh == width))
+        qs = 1;
+      if (qs > 1) {
+        p.dq = workspace;
+        p.dq_ss = part_q;
+      }
+      const dim3 grid4((unsigned)((Lq + 3) / 4), (unsigned)B, (unsigned)qs);
       if (width == 512 && mask) hipLaunchKernelGGL((khop_dq4<512, true>), grid4, dim3(kKhThreads), 0, st, p);
       else if (width == 512) hipLaunchKernelGGL((khop_dq4<512, false>), grid4, dim3(kKhThreads), 0, st, p);
       else if (mask) hipLaunchKernelGGL((khop_dq4<256, true>), grid4, dim3(kKhThreads), 0, st, p);
       else hipLaunchKernelGGL((khop_dq4<256, false>), grid4, dim3(kKhThreads), 0, st, p);
+      if (qs > 1) {
+        if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
+        hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part_q + 255) / 256)), dim3(256), 0, st,
+                           workspace, part_q, qs, part_q, dq);
+      }
     } else {
       const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
       HLA_KH_DISPATCH(khop_dq, width, grid, p, st);

@@ -1,6 +1,8 @@
-"""Multi-query causal history attention with backward on MI355X: the interface of ``hla/latent/history_gemm.py``
-(``causal_history_gemm``) and of ``hla/latent/fused_history.py:126-153`` (``causal_history_attention``) over the HIP
-kernels of ``khop.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward``, ``hla_s6_khop_backward``).
+"""History attention over contiguous latent rows with backward on MI355X: the interface of
+``hla/latent/history_gemm.py`` (``causal_history_gemm``) and of ``hla/latent/fused_history.py`` (the single-query
+``history_attention`` of lines 49-54 and the multi-query ``causal_history_attention`` of lines 126-153) over the HIP
+kernels of ``khop.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward``, ``hla_s6_khop_backward``) and
+``history.hip`` (``hla_s6_masked_history``, the single-query forward).
 
 Every query row ``(b, i, h)`` attends over the latent rows ``k[b, j], v[b, j]`` that ``mask[b, i, j]`` shows (all
 heads share the rows). The kernels compute with bf16 GEMM operands and fp32 accumulation and softmax (the
@@ -101,33 +103,42 @@ class _CausalHistory(torch.autograd.Function):
         qb, kb, vb, m8, bound, lse, z = ctx.saved_tensors
         scale, q_dtype, k_dtype, v_dtype = ctx.settings
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
-        B, Lq, H, R = qb.shape
-        N = kb.shape[1]
-        dev = qb.device
-        dzb = _bf16_rows('dz', dz if dz is not None else torch.zeros_like(z))
-        dl = None if dlse is None else dlse.to(torch.float32).contiguous()
-        delta = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
-        dq = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev) if need_q else None
-        need_kv = need_k or need_v
-        dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
-        dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
-        # key tiles of the dk / dv kernel: 64 keys on the multi-query form (widths 512 / 256, N a multiple of 16),
-        # whose causal load is balanced best with about 8 workgroups per CU (12 ranges at B=4, L=2880: 3.78 ms
-        # forward + backward against 4.15 ms with 6 and 4.11 ms with 32); 4 per CU on the 32-key form
-        mq = R in (256, 512) and N % 16 == 0
-        splits = _key_splits(-(-N // (64 if mq else 32)) * B, dev, 8 if mq else 4) if need_kv else 1
-        ws = torch.empty(2 * splits * B * N * R, dtype=torch.float32, device=dev) if splits > 1 else None
-        _lib.call('hla_s6_khop_backward', _lib.ptr(qb), qb.stride(0), qb.stride(1), qb.stride(2), _lib.ptr(kb),
-                  kb.stride(0), kb.stride(1), _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(m8), m8.stride(0),
-                  m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, scale, _lib.ptr(z), z.stride(0), z.stride(1),
-                  z.stride(2), _lib.ptr(lse), _lib.ptr(dzb), dzb.stride(0), dzb.stride(1), dzb.stride(2), _lib.ptr(dl),
-                  _lib.ptr(delta), _lib.ptr(dq), 0 if dq is None else dq.stride(0), 0 if dq is None else dq.stride(1),
-                  0 if dq is None else dq.stride(2), _lib.ptr(dk), 0 if dk is None else dk.stride(0),
-                  0 if dk is None else dk.stride(1), _lib.ptr(dv), 0 if dv is None else dv.stride(0),
-                  0 if dv is None else dv.stride(1), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(),
-                  _lib.stream(dev))
+        dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v)
         return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
                 dv.to(v_dtype) if need_v else None, None, None)
+
+
+def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv):
+    """dq [B, Lq, 16, R], dk / dv [B, N, R] (fp32, None where not needed) of z, lse = forward(q [B, Lq, 16, R], k, v,
+    mask bytes m8 [B, Lq, N]) for the cotangents dz [B, Lq, 16, R] and dlse [B, 16, Lq] (None = 0)."""
+    B, Lq, H, R = qb.shape
+    N = kb.shape[1]
+    dev = qb.device
+    dzb = _bf16_rows('dz', dz if dz is not None else torch.zeros_like(z))
+    dl = None if dlse is None else dlse.to(torch.float32).contiguous()
+    delta = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    dq = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev) if need_q else None
+    dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+    dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+    # key tiles of the dk / dv kernel: 64 keys on the multi-query form (widths 512 / 256, N a multiple of 16),
+    # whose causal load is balanced best with about 8 workgroups per CU (12 ranges at B=4, L=2880: 3.78 ms
+    # forward + backward against 4.15 ms with 6 and 4.11 ms with 32); 4 per CU on the 32-key form
+    # (row ranges split a tile's query rows, which the kernels take two at a time: at most ceil(Lq / 2) of them)
+    mq = R in (256, 512) and N % 16 == 0
+    splits = min(_key_splits(-(-N // (64 if mq else 32)) * B, dev, 8 if mq else 4), -(-Lq // 2)) if need_kv else 1
+    splits = max(1, splits)
+    floats = _lib.load().hla_s6_khop_backward_workspace(B, Lq, N, R, splits)
+    ws = torch.empty(floats, dtype=torch.float32, device=dev) if floats > 0 else None
+    _lib.call('hla_s6_khop_backward', _lib.ptr(qb), qb.stride(0), qb.stride(1), qb.stride(2), _lib.ptr(kb),
+              kb.stride(0), kb.stride(1), _lib.ptr(vb), vb.stride(0), vb.stride(1), _lib.ptr(m8), m8.stride(0),
+              m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, scale, _lib.ptr(z), z.stride(0), z.stride(1),
+              z.stride(2), _lib.ptr(lse), _lib.ptr(dzb), dzb.stride(0), dzb.stride(1), dzb.stride(2), _lib.ptr(dl),
+              _lib.ptr(delta), _lib.ptr(dq), 0 if dq is None else dq.stride(0), 0 if dq is None else dq.stride(1),
+              0 if dq is None else dq.stride(2), _lib.ptr(dk), 0 if dk is None else dk.stride(0),
+              0 if dk is None else dk.stride(1), _lib.ptr(dv), 0 if dv is None else dv.stride(0),
+              0 if dv is None else dv.stride(1), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+              _lib.stream(dev))
+    return dq, dk, dv
 
 
 def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHUNK, precision='bf16',
@@ -159,6 +170,76 @@ def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHU
                          f'(got H={H}, Rk={Rk}, Rv={v.shape[-1]})')
     s6_ops._dev(q, k, v, mask)
     return _CausalHistory.apply(q, k, v, mask, float(scale))
+
+
+SINGLE_WIDTHS = (128, 256, 512, 1024)  # forward; the backward takes WIDTHS
+
+
+class _History(torch.autograd.Function):
+    """``hla/latent/fused_history.py:23-46``: forward on the split kernel over contiguous rows with a key mask
+    (``hla_s6_masked_history``), backward on the K-hop kernels with one query per batch row."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale):
+        B, H, R = q.shape
+        N = k.shape[1]
+        dev = q.device
+        qb = _bf16_rows('q', q)
+        kb = k.to(torch.bfloat16).contiguous()
+        vb = v.to(torch.bfloat16).contiguous()
+        m = mask if mask.dtype == torch.bool else mask.bool()
+        m8 = m.contiguous().view(torch.uint8)
+        bound = torch.empty(B, dtype=torch.int32, device=dev)
+        st = _lib.stream(dev)
+        _lib.call('hla_s6_khop_bounds', _lib.ptr(m8), m8.stride(0), N, B, 1, N, _lib.ptr(bound), st)
+        splits = s6_ops.mi355x_kv_splits(N, B, _lib.device_cus(dev.index or 0), width=R)
+        ws = torch.empty(B * splits * H * (R + 1), dtype=torch.float32, device=dev) if splits > 1 else None
+        z = torch.empty(B, H, R, dtype=torch.bfloat16, device=dev)
+        lse = torch.empty(B, H, dtype=torch.float32, device=dev)
+        _lib.call('hla_s6_masked_history', _lib.ptr(qb), qb.stride(0), qb.stride(1), _lib.ptr(kb), _lib.ptr(vb),
+                  kb.stride(0), kb.stride(1), _lib.ptr(m8), m8.stride(0), _lib.ptr(bound), B, N, H, R, float(scale),
+                  splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(z), z.stride(0), z.stride(1),
+                  _lib.ptr(lse), st)
+        ctx.save_for_backward(qb, kb, vb, m8, bound, lse, z)
+        ctx.settings = (float(scale), q.dtype, k.dtype, v.dtype)
+        return z.to(q.dtype), lse
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dz, dlse):
+        qb, kb, vb, m8, bound, lse, z = ctx.saved_tensors
+        scale, q_dtype, k_dtype, v_dtype = ctx.settings
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        R = qb.shape[-1]
+        if R not in WIDTHS:
+            raise ValueError(f'history_attention backward: the HIP kernels take widths {WIDTHS} (got {R})')
+        dq, dk, dv = _backward(qb[:, None], kb, vb, m8[:, None], bound, lse[:, :, None], z[:, None],
+                               None if dz is None else dz[:, None], None if dlse is None else dlse[:, :, None],
+                               scale, need_q, need_k or need_v)
+        return (dq[:, 0].to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
+                dv.to(v_dtype) if need_v else None, None, None)
+
+
+def history_attention(q, k, v, mask, scale, reference_forward=False):
+    """Single-query history attention (``hla/latent/fused_history.py:49-54``): q [B, 16, R] against the contiguous
+    rows k, v [B, N, R] that mask [B, N] (True = visible) shows. Returns z [B, 16, R] in q.dtype and lse [B, 16]
+    (fp32, natural log; z = 0 and lse = -inf for a row with no visible key), differentiable in q, k and v (the
+    cache gradients keep in-window writers trainable). bf16 operands, fp32 accumulation and softmax.
+    ``reference_forward`` (the reference's dense torch forward) is refused: the HIP forward is the only one here."""
+    if (q.ndim != 3 or k.ndim != 3 or k.shape != v.shape or mask.shape != k.shape[:2] or q.shape[0] != k.shape[0]
+            or q.shape[-1] != k.shape[-1]):
+        raise ValueError('Expected Q[B,H,R], K/V[B,N,R], mask[B,N]')
+    s6_ops._dev(q, k, v, mask)
+    if k.shape[1] < 1:
+        raise ValueError('History must contain a storage row')
+    if reference_forward:
+        raise ValueError('reference_forward: the dense torch forward is not part of the MI355X path')
+    if q.shape[1] != HEADS or q.shape[-1] not in SINGLE_WIDTHS:
+        raise ValueError(f'the HIP kernels take {HEADS} heads and widths {SINGLE_WIDTHS} '
+                         f'(got H={q.shape[1]}, R={q.shape[-1]})')
+    if q.shape[0] == 0:
+        return q.new_zeros(q.shape), torch.empty(0, HEADS, dtype=torch.float32, device=q.device)
+    return _History.apply(q, k, v, mask, float(scale))
 
 
 HISTORY_BACKENDS = ('triton', 'gemm', 'hip')

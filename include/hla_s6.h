@@ -304,6 +304,11 @@ int hla_s6_khop_forward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh,
                         int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N, int32_t heads,
                         int32_t width, float scale, void *z, int64_t z_sb, int64_t z_si, int64_t z_sh, float *lse,
                         void *stream);
+/* hla_s6_khop_backward_workspace: the workspace floats hla_s6_khop_backward uses for these sizes and key_splits:
+ *   the dk / dv partials (2 * key_splits * B * N * width with key_splits > 1) or, when few token groups leave the
+ *   GPU idle (B * ceil(Lq / 4) < 128, widths 512 / 256, N a multiple of 16), dq partials over key ranges (then dq
+ *   must be contiguous), whichever is larger; with less workspace dq runs without key ranges. */
+int64_t hla_s6_khop_backward_workspace(int32_t B, int32_t Lq, int32_t N, int32_t width, int32_t key_splits);
 int hla_s6_khop_backward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void *k, int64_t k_sb,
                          int64_t k_sn, const void *v, int64_t v_sb, int64_t v_sn, const uint8_t *mask, int64_t m_sb,
                          int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N, int32_t heads,
@@ -312,6 +317,21 @@ int hla_s6_khop_backward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh
                          const float *dlse, float *delta, float *dq, int64_t dq_sb, int64_t dq_si, int64_t dq_sh,
                          float *dk, int64_t dk_sb, int64_t dk_sn, float *dv, int64_t dv_sb, int64_t dv_sn,
                          int32_t key_splits, float *workspace, int64_t workspace_floats, void *stream);
+
+/* ---- single-query history attention over contiguous rows with a key mask (HF rolling engine) ---------------
+ * Replaces the forward of fused_history.history_attention (hla/latent/fused_history.py:23-35,49-54; Triton
+ * _forward, hla/latent/history_kernels.py:11-33): q [B, 16, width] (strides q_sb, q_sh), k / v [B, N, width] with
+ * the same strides (kv_sb, kv_sn), mask [B, N] bytes (nonzero = visible; row stride m_sb, unit last stride; NULL =
+ * every key below the bound), bound [B] = 1 + the last visible key (hla_s6_khop_bounds with Lq = 1). Writes z
+ * [B, 16, width] bf16 (strides z_sb, z_sh) and lse [B, 16] fp32 (natural log; z = 0 and lse = -inf for a row with no
+ * visible key). width in {128, 256, 512, 1024}; num_splits > 1 splits each row's keys over that many workgroups
+ * (workspace of at least B * num_splits * 16 * (width + 1) floats) and adds the reduction launch. The backward is
+ * hla_s6_khop_backward with Lq = 1. */
+int hla_s6_masked_history(const void *q, int64_t q_sb, int64_t q_sh, const void *k, const void *v, int64_t kv_sb,
+                          int64_t kv_sn, const uint8_t *mask, int64_t m_sb, const int32_t *bound, int32_t B,
+                          int32_t N, int32_t num_heads, int32_t width, float scale, int32_t num_splits,
+                          float *workspace, int64_t workspace_floats, void *z, int64_t z_sb, int64_t z_sh,
+                          float *lse, void *stream);
 
 #ifdef __cplusplus
 }

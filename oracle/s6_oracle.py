@@ -428,6 +428,23 @@ def causal_history_backward(q, k, v, mask, scale, lse, dz, dlse=None, z=None, dt
     return dq, dk, dv
 
 
+def single_history(q, k, v, mask, scale, dtype=np.float64):
+    """Single-query form (``reference`` of ``hla/latent/fused_history.py:11-20``): q ``[B, H, R]`` against k, v
+    ``[B, N, R]`` with ``mask [B, N]``; returns ``z [B, H, R]`` and ``lse [B, H]`` (``z = 0``, ``lse = -inf`` on a
+    row with no visible key). The multi-query form with one query per batch row."""
+    z, lse = causal_history(np.asarray(q)[:, None], k, v, np.asarray(mask, bool)[:, None], scale, dtype)
+    return z[:, 0], lse[:, :, 0]
+
+
+def single_history_backward(q, k, v, mask, scale, lse, dz, dlse=None, dtype=np.float64):
+    """``(dq [B, H, R], dk, dv [B, N, R])`` of ``single_history`` (the Triton ``_backward_q`` / ``_backward_kv`` of
+    ``hla/latent/history_kernels.py:36-81``: ``dS = P (v.dz - delta + dlse)``, ``dq = scale dS k``)."""
+    dq, dk, dv = causal_history_backward(np.asarray(q)[:, None], k, v, np.asarray(mask, bool)[:, None], scale,
+                                         np.asarray(lse)[:, :, None], np.asarray(dz)[:, None],
+                                         None if dlse is None else np.asarray(dlse)[:, :, None], dtype=dtype)
+    return dq[:, 0], dk, dv
+
+
 def rel_l2(a, b):
     """Relative L2 error ``||a - b|| / ||b||`` in float64."""
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)

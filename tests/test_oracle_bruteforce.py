@@ -474,3 +474,45 @@ def test_causal_history_planted_mistakes_fail():
     assert np.abs(dq - dq0).max() > 1e-3
     _, dkv, _ = O.causal_history_backward(q, v, k, mask, 0.5, lse, dz, dlse)
     assert np.abs(dk - dkv).max() > 1e-3
+
+
+def test_single_history_matches_per_row_softmax_and_its_gradient():
+    """The single-query form (fused_history.reference): per (b, h) softmax over the visible keys, an empty row gives
+    z = 0 and lse = -inf, and its backward is the finite-difference gradient of sum(z dz) + sum(lse dlse)."""
+    rng = np.random.default_rng(31)
+    B, H, N, R = 3, 2, 7, 3
+    q, k, v = rng.standard_normal((B, H, R)), rng.standard_normal((B, N, R)), rng.standard_normal((B, N, R))
+    mask = rng.random((B, N)) < 0.5
+    mask[0] = False
+    mask[1, 2] = True
+    scale = 0.45
+    z, lse = O.single_history(q, k, v, mask, scale)
+    assert z.shape == (B, H, R) and lse.shape == (B, H)
+    for b in range(B):
+        keys = np.flatnonzero(mask[b])
+        for h in range(H):
+            if keys.size == 0:
+                assert (z[b, h] == 0).all() and lse[b, h] == -np.inf
+                continue
+            out, l = _softmax64(k[b, keys] @ q[b, h] * scale, v[b, keys])
+            np.testing.assert_allclose(z[b, h], out, rtol=1e-12, atol=1e-12)
+            np.testing.assert_allclose(lse[b, h], l, rtol=1e-12)
+    dz, dlse = rng.standard_normal(z.shape), rng.standard_normal(lse.shape)
+
+    def objective(q_, k_, v_):
+        z_, l_ = O.single_history(q_, k_, v_, mask, scale)
+        return float((z_ * dz).sum() + np.where(np.isfinite(l_), l_ * dlse, 0.0).sum())
+
+    grads = O.single_history_backward(q, k, v, mask, scale, lse, dz, dlse)
+    eps = 1e-6
+    for pos, (x, g) in enumerate(zip((q, k, v), grads)):
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            a, m = [q, k, v], [q, k, v]
+            a[pos], m[pos] = xp, xm
+            num[idx] = (objective(*a) - objective(*m)) / (2 * eps)
+        np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7, err_msg='qkv'[pos])
+    assert (grads[0][0] == 0).all()
