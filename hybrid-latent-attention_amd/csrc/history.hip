@@ -1812,14 +1812,20 @@ __global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_
   }
 }
 
-// Split reduction: one workgroup per (token, head), thread i < R/4 owns output columns [4i, 4i+4).
+// Split reduction: one workgroup per (token, head) of 4 slot groups x R/4 threads; thread (group q, i) owns output
+// columns [4i, 4i+4) of the slots s = q (mod 4), and the 4 groups' sums are added in LDS in a fixed order.
+constexpr int kCombineGroups = 4;
 template <int R>
-constexpr int combine_threads() { return R / 4 < 64 ? 64 : R / 4; }
+constexpr int combine_threads() { return kCombineGroups * (R / 4); }
 
 template <int R>
 __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryParams a) {
+  constexpr int CT = R / 4, NG = kCombineGroups;
   __shared__ int64_t red[2 * combine_threads<R>() / 64];
-  const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x;
+  __shared__ float mx_s[NG];
+  __shared__ floatx4 acc_s[NG - 1][CT];
+  __shared__ float den_s[NG - 1];
+  const int t = blockIdx.x, h = blockIdx.y, i = threadIdx.x % CT, q = threadIdx.x / CT;
   const int S_all = a.num_splits;
   // slots past the row's work hold lse = -inf; with the lengths at hand they are not read at all
   int S = S_all;
@@ -1827,29 +1833,34 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
     const int64_t cap = (int64_t)a.bt_cols * a.block_size;
     S = min(S_all, used_slots(a.ctx[t], cap, split_chunk(a.ctx, a.T, cap, S_all, red)));
   }
-  if (i >= R / 4) return;
   const float* ls = a.ws_lse + (int64_t)t * S_all * kHeads + h;
-  float mx = -INFINITY;
-  for (int s = 0; s < S; ++s) mx = fmaxf(mx, ls[(int64_t)s * kHeads]);
+  float mq = -INFINITY;
+  for (int s = q; s < S; s += NG) mq = fmaxf(mq, ls[(int64_t)s * kHeads]);
+  if (i == 0) mx_s[q] = mq;
+  __syncthreads();
+  float mx = mx_s[0];
+#pragma unroll
+  for (int g = 1; g < NG; ++g) mx = fmaxf(mx, mx_s[g]);
   uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * i;
-  if (mx == -INFINITY) {
-    *reinterpret_cast<uint2*>(op) = uint2{0u, 0u};
-    if (i == 0) a.lse[lse_index(a, t, h)] = -INFINITY;
+  if (mx == -INFINITY) {  // uniform over the workgroup
+    if (q == 0) *reinterpret_cast<uint2*>(op) = uint2{0u, 0u};
+    if (q == 0 && i == 0) a.lse[lse_index(a, t, h)] = -INFINITY;
     return;
   }
   const float* base = a.ws_o + ((int64_t)t * S_all * kHeads + h) * R + 4 * i;
-  // Eight partial rows in flight. One code path for every slot count (a slot past S or without work adds an exact
-  // zero through fma(0, 0, acc)), so the result does not depend on how many empty slots are read.
+  // Eight of the group's partial rows in flight. One code path for every slot count (a slot past S or without work
+  // adds an exact zero through fma(0, 0, acc)), so the result does not depend on how many empty slots are read.
   float den = 0.f;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = 0; s0 < S; s0 += 8) {
+  for (int s0 = q; s0 < S; s0 += 8 * NG) {
     floatx4 o[8];
     float w[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const bool in = s0 + u < S;
-      o[u] = in ? *reinterpret_cast<const floatx4*>(base + (int64_t)(s0 + u) * kHeads * R) : floatx4{0.f, 0.f, 0.f, 0.f};
-      const float l_s = in ? ls[(int64_t)(s0 + u) * kHeads] : -INFINITY;
+      const int sl = s0 + u * NG;
+      const bool in = sl < S;
+      o[u] = in ? *reinterpret_cast<const floatx4*>(base + (int64_t)sl * kHeads * R) : floatx4{0.f, 0.f, 0.f, 0.f};
+      const float l_s = in ? ls[(int64_t)sl * kHeads] : -INFINITY;
       w[u] = l_s == -INFINITY ? 0.f : __expf(l_s - mx);
     }
 #pragma unroll
@@ -1859,6 +1870,17 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[e] = __builtin_fmaf(ou[e], w[u], acc[e]);
     }
+  }
+  if (q > 0) {
+    acc_s[q - 1][i] = acc;
+    if (i == 0) den_s[q - 1] = den;
+  }
+  __syncthreads();
+  if (q != 0) return;
+#pragma unroll
+  for (int g = 0; g < NG - 1; ++g) {
+    acc += acc_s[g][i];
+    den += den_s[g];
   }
   acc = acc * (1.0f / den);
   *reinterpret_cast<uint2*>(op) = uint2{pack2(acc[0], acc[1]), pack2(acc[2], acc[3])};
