@@ -5,8 +5,9 @@
 ``include/hla_s6.h``. The directory name is not a Python identifier: import it with
 ``importlib.import_module('hybrid-latent-attention_amd')`` with the repository root on ``sys.path``.
 ``rollout_cache`` writes and reads the ``s6-rollout-cache-v1`` snapshot of a finished request; ``history_gemm`` is
-the differentiable multi-query history attention of K-hop replay.
+the differentiable history attention over contiguous rows (multi-query for K-hop replay, single-query for the HF
+engine); ``batched_engine`` is the HF rolling engine's joint attention over history rows and the current chunk.
 """
-from . import _lib, history_gemm, rollout_cache, s6_layer, s6_ops
+from . import _lib, batched_engine, history_gemm, rollout_cache, s6_layer, s6_ops
 
-__all__ = ['_lib', 'history_gemm', 'rollout_cache', 's6_layer', 's6_ops']
+__all__ = ['_lib', 'batched_engine', 'history_gemm', 'rollout_cache', 's6_layer', 's6_ops']

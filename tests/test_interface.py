@@ -41,7 +41,7 @@ def _params(obj):
     return list(inspect.signature(obj).parameters)
 
 
-@pytest.mark.parametrize('module', ['s6_ops', 's6_layer', 'history_gemm'])
+@pytest.mark.parametrize('module', ['s6_ops', 's6_layer', 'history_gemm', 'batched_engine'])
 def test_reference_parameter_lists(pkg, module):
     mod = getattr(pkg, module)
     for qual, want in IFACE[module].items():
