@@ -618,11 +618,13 @@ __device__ __forceinline__ void group_stage_a(const TileRegs<R>& r, const u32x4 
 }
 
 // Stage B: exchange the S partials, online softmax per token, O^T += V^T P^T (the V^T operand is read once and
-// reused by every token). Keys >= n[u] are masked for token u.
-template <int R, int NQ>
+// reused by every token). Keys >= n[u] are masked for token u, and with kMask the keys whose byte r of mk[u] is 0
+// (keys 4g + r of the tile).
+template <int R, int NQ, bool kMask = false>
 __device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4* sx, const uint16_t* vs, int key0,
                                         const int (&n)[NQ], int count, float scale_log2, int wave, int lane,
-                                        floatx4 (&oacc)[NQ][Geo<R>::NT], float (&m)[NQ], float (&l)[NQ]) {
+                                        floatx4 (&oacc)[NQ][Geo<R>::NT], float (&m)[NQ], float (&l)[NQ],
+                                        const uint32_t (&mk)[NQ]) {
   using G = Geo<R>;
 #pragma unroll
   for (int u = 0; u < NQ; ++u) sx[(u * G::WAVES + wave) * 64 + lane] = sacc[u];
@@ -641,7 +643,8 @@ __device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4
       for (int w = 1; w < G::WAVES; ++w) s += sx[(u * G::WAVES + w) * 64 + lane];
       float sc[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = (kb + r < n[u]) ? s[r] * scale_log2 : -INFINITY;
+      for (int r = 0; r < 4; ++r)
+        sc[r] = (kb + r < n[u] && (!kMask || ((mk[u] >> (8 * r)) & 255u) != 0)) ? s[r] * scale_log2 : -INFINITY;
       float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
       mx = wave_max16x4(mx);
       const bool raise = mx > m[u] + kLazy;  // per head (lane column); false while the token has no key yet
@@ -690,7 +693,7 @@ __device__ __forceinline__ void store_split(const HistoryParams& a, int t, int s
       const floatx4 o = oacc[nt] * inv;
       *reinterpret_cast<uint2*>(op + 16 * nt) = uint2{pack2(o[0], o[1]), pack2(o[2], o[3])};
     }
-    if (wave == 0 && g == 0) a.lse[(int64_t)hq * a.T + t] = lse;
+    if (wave == 0 && g == 0) a.lse[lse_index(a, t, hq)] = lse;
     return;
   }
   const int64_t part_row = ((int64_t)t * a.num_splits + s) * kHeads + hq;
@@ -700,10 +703,33 @@ __device__ __forceinline__ void store_split(const HistoryParams& a, int t, int s
   if (wave == 0 && g == 0) a.ws_lse[part_row] = lse;
 }
 
+// Mask bytes of keys kb .. kb+3 (kb = key0 + 4g) of the pass's tokens tp + u (u < count): bytes at or past a
+// token's bound n[u] are not read (the bound hides those keys); 0xffffffff without a mask.
+template <int NQ>
+__device__ __forceinline__ void load_token_masks(const HistoryParams& a, int tp, int count, const int (&n)[NQ],
+                                                 int key0, int lane, uint32_t (&mk)[NQ]) {
+  const int kb = key0 + 4 * (lane >> 4);
+#pragma unroll
+  for (int u = 0; u < NQ; ++u) {
+    mk[u] = 0xffffffffu;
+    if (!a.mask || u >= count) continue;
+    const uint8_t* mr = a.mask + (int64_t)(tp + u) * a.mask_st;
+    if (kb + 4 <= n[u] && (reinterpret_cast<uintptr_t>(mr) & 3u) == 0) {
+      mk[u] = *reinterpret_cast<const uint32_t*>(mr + kb);
+    } else {
+      mk[u] = 0u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (kb + e < n[u]) mk[u] |= (uint32_t)mr[kb + e] << (8 * e);
+    }
+  }
+}
+
 // One workgroup per (group of NQ consecutive tokens, KV split). The tokens of a group that share a block-table row
 // (one request of a chunked-prefill step) are processed together, every K/V tile read once for all of them; a
-// group that spans several rows takes one pass per row.
-template <int R, int NQ>
+// group that spans several rows takes one pass per row. kRows: contiguous rows (bt == null; token t reads rows
+// [t / tok_per_row] at page_stride) with an optional byte mask per (token, key).
+template <int R, int NQ, bool kRows = false>
 __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a) {
   using G = Geo<R>;
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][G::VBUF];
@@ -751,7 +777,8 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
     }
     if (j_begin < j_end) {  // uniform over the workgroup
       RowSource src{};
-      src.btr = a.bt + row * a.bt_stride;
+      if constexpr (kRows) src.base = row * a.page_stride;  // (the per-token masks are loaded separately)
+      else src.btr = a.bt + row * a.bt_stride;
       u32x4 qreg[NQ][G::KI];
 #pragma unroll
       for (int u = 0; u < NQ; ++u) {
@@ -764,12 +791,22 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
       // a slower wave may still be reading (the barrier in between orders them); the wave-private K/V copies may
       // be rewritten by the next tile because a wave's own LDS accesses stay in order.
       TileRegs<R> regs;
-      load_tile<R, false>(a, src, n_max, j_begin, col0, lane, regs);
+      uint32_t mk[NQ], mk_next[NQ];
+#pragma unroll
+      for (int u = 0; u < NQ; ++u) mk_next[u] = 0xffffffffu;
+      load_tile<R, false, kRows>(a, src, n_max, j_begin, col0, lane, regs);
+      if (kRows) load_token_masks<NQ>(a, tp, count, n, j_begin * kTile, lane, mk_next);
       for (int jt = j_begin; jt < j_end; ++jt) {
         floatx4 sa[NQ];
         group_stage_a<R, NQ>(regs, qreg, v_lds[wave], k_lds[wave], lane, count, sa);
-        if (jt + 1 < j_end) load_tile<R, false>(a, src, n_max, jt + 1, col0, lane, regs);
-        group_stage_b<R, NQ>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane, oacc, m, l);
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) mk[u] = mk_next[u];
+        if (jt + 1 < j_end) {
+          load_tile<R, false, kRows>(a, src, n_max, jt + 1, col0, lane, regs);
+          if (kRows) load_token_masks<NQ>(a, tp, count, n, (jt + 1) * kTile, lane, mk_next);
+        }
+        group_stage_b<R, NQ, kRows>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane,
+                                    oacc, m, l, mk);
         par ^= 1;
       }
     }
@@ -2278,7 +2315,7 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   // start on 16-byte boundaries (its bytes are copied in 16-byte pieces), history_mq2 (width 512) anything else
   const bool mq4 = HLA_MQ4 && (width == 512 || width == 256) && scale > 0.f &&
                    (!mask || (((uintptr_t)mask & 15u) == 0 && mask_st % 16 == 0));
-  if (!HLA_MQ_V2 || N % kTile != 0 || !(mq4 || width == 512)) return HLA_S6_EUNSUPPORTED;
+  if (N % kTile != 0 || (width != 1024 && (!HLA_MQ_V2 || !(mq4 || width == 512)))) return HLA_S6_EUNSUPPORTED;
   HistoryParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
@@ -2305,7 +2342,12 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.direct = true;
   p.mask = mask;
   p.mask_st = mask_st;
-  if (mq4) {
+  if (width == 1024) {  // four tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
+    p.lse_rows = true;
+    p.page_stride = (int64_t)N * k_sn;
+    hipLaunchKernelGGL((history_group<1024, 4, true>), dim3((unsigned)((p.T + 3) / 4), 1), dim3(Geo<1024>::THREADS), 0,
+                       stream, p);
+  } else if (mq4) {
     const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
     if (width == 512 && HLA_MQ5_512 && mask) hipLaunchKernelGGL((history_mq5<512, 2>), grid4, dim3(512), 0, stream, p);
     else if (width == 512 && HLA_MQ5_512) hipLaunchKernelGGL((history_mq5<512, 1>), grid4, dim3(512), 0, stream, p);

@@ -958,12 +958,12 @@ inline int kh_dq_splits(int B, int Lq, int N) {
 }
 
 int kh_check(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void* k, int64_t k_sb, int64_t k_sn,
-             const void* v, int64_t v_sb, int64_t v_sn, int B, int Lq, int N, int R, int heads) {
+             const void* v, int64_t v_sb, int64_t v_sn, int B, int Lq, int N, int R, int heads, bool forward = false) {
   HLA_REQUIRE(B >= 1 && B <= 65535 && Lq >= 0 && N >= 1, HLA_S6_EINVAL, "khop: bad sizes B=%d Lq=%d N=%d", B, Lq,
               N);
   HLA_REQUIRE(heads == 16, HLA_S6_EUNSUPPORTED, "khop: %d query heads (16 supported)", heads);
-  HLA_REQUIRE(R == 128 || R == 256 || R == 512, HLA_S6_EUNSUPPORTED, "khop: latent width %d not in {128, 256, 512}",
-              R);
+  HLA_REQUIRE(R == 128 || R == 256 || R == 512 || (forward && R == 1024), HLA_S6_EUNSUPPORTED,
+              "khop: latent width %d not in {128, 256, 512}%s", R, forward ? " (or 1024 forward)" : "");
   HLA_REQUIRE(q && k && v, HLA_S6_EINVAL, "khop: null input");
   HLA_REQUIRE(kh_aligned16(q) && kh_aligned16(k) && kh_aligned16(v) && q_sb % 8 == 0 && q_si % 8 == 0 &&
                   q_sh % 8 == 0 && k_sb % 8 == 0 && k_sn % 8 == 0 && v_sb % 8 == 0 && v_sn % 8 == 0,
@@ -1000,17 +1000,21 @@ extern "C" int hla_s6_khop_forward(const void* q, int64_t q_sb, int64_t q_si, in
                                    int32_t Lq, int32_t N, int32_t heads, int32_t width, float scale, void* z,
                                    int64_t z_sb, int64_t z_si, int64_t z_sh, float* lse, void* stream) {
   using namespace hla;
-  int rc = kh_check(q, q_sb, q_si, q_sh, k, k_sb, k_sn, v, v_sb, v_sn, B, Lq, N, width, heads);
+  int rc = kh_check(q, q_sb, q_si, q_sh, k, k_sb, k_sn, v, v_sb, v_sn, B, Lq, N, width, heads, true);
   if (rc != HLA_S6_OK) return rc;
   if (Lq == 0) return HLA_S6_OK;
   HLA_REQUIRE(bound && z && lse, HLA_S6_EINVAL, "khop_forward: null bound / output");
+  const bool linear = q_sb == (int64_t)Lq * q_si && z_sb == (int64_t)Lq * z_si && k_sn == v_sn &&
+                      k_sb == (int64_t)N * k_sn && v_sb == (int64_t)N * v_sn && (!mask || m_sb == (int64_t)Lq * m_si);
+  HLA_REQUIRE(width != 1024 || (linear && N % 16 == 0), HLA_S6_EUNSUPPORTED,
+              "khop_forward: width 1024 needs token-linear q / z / mask rows, contiguous k / v and N a multiple of 16");
   // rows linear in the token index (t = b * Lq + i): the multi-query history kernel of the serving path runs it
-  if (q_sb == (int64_t)Lq * q_si && z_sb == (int64_t)Lq * z_si && k_sn == v_sn && k_sb == (int64_t)N * k_sn &&
-      v_sb == (int64_t)N * v_sn && (!mask || m_sb == (int64_t)Lq * m_si)) {
+  if (linear) {
     rc = khop_forward_mq(q, q_si, q_sh, k, v, k_sn, B, Lq, N, width, mask, m_si, bound, scale, z, z_si, z_sh, lse,
                          as_stream(stream));
     if (rc != HLA_S6_EUNSUPPORTED) return rc;
   }
+  HLA_REQUIRE(width != 1024, HLA_S6_EUNSUPPORTED, "khop_forward: width 1024 runs on the multi-query form only");
   KhopParams p = {};
   p.q = static_cast<const uint16_t*>(q);
   p.q_sb = q_sb; p.q_si = q_si; p.q_sh = q_sh;

@@ -21,7 +21,8 @@ DEFAULT_CHUNK = 128
 DEFAULT_MAX_ELEMENTS = 1 << 26
 KEY_ALIGN = 16
 HEADS = 16
-WIDTHS = (128, 256, 512)
+WIDTHS = (128, 256, 512)          # forward and backward
+FORWARD_WIDTHS = WIDTHS + (1024,)  # 1024: forward only (token-linear rows, N a multiple of 16)
 
 
 def bf16_fp32_output_supported(device) -> bool:
@@ -80,8 +81,14 @@ class _CausalHistory(torch.autograd.Function):
         N = k.shape[1]
         dev = q.device
         qb, kb, vb = _bf16_rows('q', q), _bf16_rows('k', k), _bf16_rows('v', v)
+        if qb.stride(0) != Lq * qb.stride(1):      # token-linear query rows: the multi-query kernels need them
+            qb = qb.contiguous()
+        if R == 1024:
+            kb, vb = kb.contiguous(), vb.contiguous()
+            if N % KEY_ALIGN:
+                raise ValueError(f'width 1024 needs a key count that is a multiple of {KEY_ALIGN} (got {N})')
         m = mask if mask.dtype == torch.bool else mask.bool()
-        if m.stride(-1) != 1:
+        if m.stride(-1) != 1 or (R == 1024 and m.stride(0) != Lq * m.stride(1)):
             m = m.contiguous()
         m8 = m.view(torch.uint8)
         bound = torch.empty(B * Lq, dtype=torch.int32, device=dev)
@@ -103,6 +110,9 @@ class _CausalHistory(torch.autograd.Function):
         qb, kb, vb, m8, bound, lse, z = ctx.saved_tensors
         scale, q_dtype, k_dtype, v_dtype = ctx.settings
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        if qb.shape[-1] not in WIDTHS:
+            raise ValueError(f'causal_history_gemm backward: the HIP kernels take widths {WIDTHS} '
+                             f'(got {qb.shape[-1]}; 1024 is forward only)')
         dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v)
         return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
                 dv.to(v_dtype) if need_v else None, None, None)
@@ -165,8 +175,8 @@ def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHU
                          f'fp32 accumulation (precision="bf16")')
     if chunk < 1 or max_elements < 1:
         raise ValueError('chunk and max_elements must be positive')
-    if H != HEADS or v.shape[-1] != Rk or Rk not in WIDTHS:
-        raise ValueError(f'the HIP kernels take {HEADS} heads and equal K/V widths in {WIDTHS} '
+    if H != HEADS or v.shape[-1] != Rk or Rk not in FORWARD_WIDTHS:
+        raise ValueError(f'the HIP kernels take {HEADS} heads and equal K/V widths in {FORWARD_WIDTHS} '
                          f'(got H={H}, Rk={Rk}, Rv={v.shape[-1]})')
     s6_ops._dev(q, k, v, mask)
     return _CausalHistory.apply(q, k, v, mask, float(scale))

@@ -216,8 +216,46 @@ def test_rejects_unsupported_shapes_and_precision():
     k = torch.zeros(1, 4, 1024, device='cuda', dtype=torch.bfloat16)
     m = torch.ones(1, 4, 4, dtype=torch.bool, device='cuda')
     with pytest.raises(ValueError, match='widths'):
+        hg.causal_history_gemm(q[..., :768], k[..., :768], k[..., :768], m, 1.0)
+    with pytest.raises(ValueError, match='multiple of 16'):   # width 1024 takes whole 16-key groups
         hg.causal_history_gemm(q, k, k, m, 1.0)
     with pytest.raises(ValueError, match='precision'):
         hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0, precision='fp32')
     with pytest.raises(ValueError, match='Inconsistent'):
         hg.causal_history_gemm(q[..., :256], k[..., :256], k[:, :3, :256], m, 1.0)
+
+
+@pytest.mark.parametrize('kind,B,Lq,N', [('benchmark', 2, 48, 48), ('khop', 2, 19, 64), ('any', 3, 29, 96)])
+def test_width_1024_forward_matches_the_oracle(kind, B, Lq, N):
+    """Width 1024 (the reference benchmark's widest latent): forward on the four-token group kernel over contiguous
+    rows with per-token masks; its backward is refused with ValueError."""
+    R = 1024
+    q, k, v, mask = case(3 * N + Lq, B, Lq, N, R, kind)
+    scale = 1 / math.sqrt(128)
+    got = run(q, k, v, mask, scale, need_grad=False)
+    z, lse = O.causal_history(q, k, v, mask, scale)
+    assert_attention_close(got['z'], z, 'z')
+    assert_lse_close(got['lse'], lse)
+    empty = ~mask.any(-1)
+    assert (got['z'][empty] == 0).all() and np.isneginf(got['lse'].transpose(0, 2, 1)[empty]).all()
+    qt = torch.tensor(q, device='cuda').to(torch.bfloat16).requires_grad_(True)
+    kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (k, v))
+    zt, lt = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), scale)
+    with pytest.raises(ValueError, match='forward only'):
+        torch.autograd.grad(zt.float().sum(), [qt])
+
+
+def test_transposed_query_view_of_the_reference_benchmark():
+    """The reference benchmark's production query layout ([B, H, L, R] storage viewed as [B, L, H, R]) gives the
+    same results as contiguous queries (it is made token-linear for the multi-query kernels)."""
+    B, L, R = 2, 64, 512
+    q, k, v, mask = case(91, B, L, L, R, 'benchmark')
+    scale = 1 / math.sqrt(128)
+    qt = torch.tensor(q, device='cuda').to(torch.bfloat16)
+    qv = qt.transpose(1, 2).contiguous().transpose(1, 2)
+    assert qv.stride(0) != L * qv.stride(1)
+    kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (k, v))
+    mt = torch.tensor(mask, device='cuda')
+    z1, l1 = hg.causal_history_gemm(qt, kt, vt, mt, scale)
+    z2, l2 = hg.causal_history_gemm(qv, kt, vt, mt, scale)
+    assert torch.equal(z1, z2) and torch.equal(l1, l2)
