@@ -1313,6 +1313,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 #ifndef HLA_MQ5
 #define HLA_MQ5 1  // 256-wide multi-query steps: history_mq5 (4 waves, no score exchange) instead of history_mq4
 #endif
+#ifndef HLA_KH1024_NQ
+#define HLA_KH1024_NQ 2  // tokens per workgroup of the 1024-wide K-hop forward (history_group)
+#endif
 #ifndef HLA_MQ5_512
 #define HLA_MQ5_512 1  // 512-wide multi-query steps: history_mq5 (8 waves of one token) instead of history_mq4
 #endif
@@ -2205,6 +2208,9 @@ int launch(const HistoryParams& p, hipStream_t stream) {
       hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
     else if (p.group == 4 && R <= 512)
       hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
+    else if (p.group == 4 && R == 1024)  // four 1024-wide tokens spill registers: two per workgroup run twice as fast
+      hipLaunchKernelGGL((history_group<R, 2>), dim3((unsigned)((p.T + 1) / 2), p.num_splits), dim3(Geo<R>::THREADS),
+                         0, stream, p);
     else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
@@ -2345,7 +2351,8 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   if (width == 1024) {  // four tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
     p.lse_rows = true;
     p.page_stride = (int64_t)N * k_sn;
-    hipLaunchKernelGGL((history_group<1024, 4, true>), dim3((unsigned)((p.T + 3) / 4), 1), dim3(Geo<1024>::THREADS), 0,
+    hipLaunchKernelGGL((history_group<1024, HLA_KH1024_NQ, true>),
+                       dim3((unsigned)((p.T + HLA_KH1024_NQ - 1) / HLA_KH1024_NQ), 1), dim3(Geo<1024>::THREADS), 0,
                        stream, p);
   } else if (mq4) {
     const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);

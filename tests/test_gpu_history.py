@@ -155,7 +155,7 @@ def test_two_stage_history_is_bitwise_the_op(ops, width, splits):
         ops.history_partials(q, k, v, bt, c, SCALE, splits, None)
 
 
-@pytest.mark.parametrize('width', [512, 256])
+@pytest.mark.parametrize('width', [1024, 512, 256])
 @pytest.mark.parametrize('splits', [1, 5])
 @pytest.mark.parametrize('group', [1, 2, 4])
 def test_grouped_history_matches_oracle(ops, width, splits, group):
