@@ -946,7 +946,37 @@ __global__ __launch_bounds__(256) void khop_split_sum_kernel(const float* part, 
   out[n] = s;
 }
 
+// The same over 4 consecutive floats per thread (count and split_stride multiples of 4, 16-byte aligned buffers),
+// every split's load in flight before the adds, which keep the split order: bitwise the scalar kernel's result.
+__global__ __launch_bounds__(256) void khop_split_sum4_kernel(const float* part, int64_t split_stride, int splits,
+                                                               int64_t count, float* out) {
+  const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= count) return;
+  floatx4 s = *reinterpret_cast<const floatx4*>(part + n);
+  int p = 1;
+  for (; p + 8 <= splits; p += 8) {
+    floatx4 x[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const floatx4*>(part + (int64_t)(p + u) * split_stride + n);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += x[u];
+  }
+  for (; p < splits; ++p) s += *reinterpret_cast<const floatx4*>(part + (int64_t)p * split_stride + n);
+  *reinterpret_cast<floatx4*>(out + n) = s;
+}
+
 inline bool kh_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// out = the fixed-order sum of `splits` partials of `count` floats at `split_stride` (one launch)
+inline void kh_split_sum(const float* part, int64_t split_stride, int splits, int64_t count, float* out,
+                         hipStream_t st) {
+  if (count % 4 == 0 && split_stride % 4 == 0 && kh_aligned16(part) && kh_aligned16(out))
+    hipLaunchKernelGGL(khop_split_sum4_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st, part,
+                       split_stride, splits, count, out);
+  else
+    hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, part,
+                       split_stride, splits, count, out);
+}
 
 // Key ranges of the multi-query dq kernel: 1 when the B * ceil(Lq / 4) token groups fill the GPU, else enough
 // ranges for about 512 workgroups, at least 4 key tiles (128 keys) each and at most 64.
@@ -1119,8 +1149,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
       else hipLaunchKernelGGL((khop_dq4<256, false>), grid4, dim3(kKhThreads), 0, st, p);
       if (qs > 1) {
         if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
-        hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part_q + 255) / 256)), dim3(256), 0, st,
-                           workspace, part_q, qs, part_q, dq);
+        kh_split_sum(workspace, part_q, qs, part_q, dq, st);
       }
     } else {
       const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
@@ -1157,10 +1186,8 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
     }
     if ((rc = check_launch("khop_dkdv")) != HLA_S6_OK) return rc;
     if (split) {
-      hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part + 255) / 256)), dim3(256), 0, st, workspace,
-                         part, key_splits, part, dk);
-      hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((part + 255) / 256)), dim3(256), 0, st,
-                         workspace + key_splits * part, part, key_splits, part, dv);
+      kh_split_sum(workspace, part, key_splits, part, dk, st);
+      kh_split_sum(workspace + key_splits * part, part, key_splits, part, dv, st);
       if ((rc = check_launch("khop_split_sum")) != HLA_S6_OK) return rc;
     }
   }
