@@ -194,9 +194,9 @@ class _History(torch.autograd.Function):
         B, H, R = q.shape
         N = k.shape[1]
         dev = q.device
-        qb = _bf16_rows('q', q)
-        kb = k.to(torch.bfloat16).contiguous()
-        vb = v.to(torch.bfloat16).contiguous()
+        qb, kb, vb = _bf16_rows('q', q), _bf16_rows('k', k), _bf16_rows('v', v)
+        if kb.stride() != vb.stride():                # one row geometry for both (e.g. fields of packed rows)
+            kb, vb = kb.contiguous(), vb.contiguous()
         m = mask if mask.dtype == torch.bool else mask.bool()
         m8 = m.contiguous().view(torch.uint8)
         bound = torch.empty(B, dtype=torch.int32, device=dev)

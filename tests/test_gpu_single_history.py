@@ -185,3 +185,25 @@ def test_key_bounds_of_mask_rows(N, offset):
     lib.call('hla_s6_khop_bounds', lib.ptr(m8), Lq * stride, stride, B, Lq, N, lib.ptr(bound), lib.stream(buf.device))
     want = [int(np.flatnonzero(r)[-1]) + 1 if r.any() else 0 for r in rows]
     assert bound.cpu().tolist() == want
+
+
+def test_fields_of_packed_rows_without_copies():
+    """K and V as the fields of the HF engine's packed rows [B, N, 1536] (row stride 1536): the same results as
+    contiguous copies, forward and gradients."""
+    rng = np.random.default_rng(77)
+    B, N, R = 3, 160, 512
+    packed = bf16.round_bf16(rng.standard_normal((B, N, 1536)).astype(np.float32))
+    q = bf16.round_bf16(rng.standard_normal((B, 16, R)).astype(np.float32))
+    mask = rng.random((B, N)) < 0.5
+    pt = torch.tensor(packed, device='cuda').to(torch.bfloat16).requires_grad_(True)
+    qt = torch.tensor(q, device='cuda').to(torch.bfloat16)
+    mt = torch.tensor(mask, device='cuda')
+    z, lse = hg.history_attention(qt, pt[..., :R], pt[..., R:2 * R], mt, 0.05)
+    (gp,) = torch.autograd.grad([z], [pt], [torch.ones_like(z)])
+    kc = pt.detach()[..., :R].contiguous().requires_grad_(True)
+    vc = pt.detach()[..., R:2 * R].contiguous().requires_grad_(True)
+    z2, lse2 = hg.history_attention(qt, kc, vc, mt, 0.05)
+    gk, gv = torch.autograd.grad([z2], [kc, vc], [torch.ones_like(z2)])
+    assert torch.equal(z, z2) and torch.equal(lse, lse2)
+    assert torch.equal(gp[..., :R], gk) and torch.equal(gp[..., R:2 * R], gv)
+    assert (gp[..., 2 * R:] == 0).all()
