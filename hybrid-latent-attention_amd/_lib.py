@@ -59,7 +59,7 @@ SIGNATURES = {
     'hla_s6_khop_backward_workspace': [I32, I32, I32, I32, I32],
     'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
                              P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,
-                             I32, P, I64, P],
+                             I32, P, I64, I32, P],
 }
 
 RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64,

@@ -60,7 +60,19 @@ struct KhopParams {
   int key_splits;  // dkdv: row ranges per key tile (partials of split s go to dk + s * dk_ss)
   int64_t dk_ss, dv_ss;
   int64_t dq_ss;   // dq4 with key ranges (gridDim.z > 1): the partial of range z goes to dq + z * dq_ss
+  bool dq_bf16, kv_bf16;  // the kernel writes dq (dk, dv) as bf16 (strides in bf16 elements) instead of fp32
 };
+
+// Gradient stores: fp32, or bf16 rounded to nearest even (the rounding of a torch cast) into a bf16 array whose
+// element offset is i.
+__device__ __forceinline__ void kh_store1(float* p, int64_t i, float v, bool bf) {
+  if (bf) reinterpret_cast<uint16_t*>(p)[i] = f2bf(v);
+  else p[i] = v;
+}
+__device__ __forceinline__ void kh_store4(float* p, int64_t i, floatx4 v, bool bf) {
+  if (bf) *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p) + i) = uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+  else *reinterpret_cast<floatx4*>(p + i) = v;
+}
 
 template <int R>
 struct KhGeo {
@@ -430,9 +442,10 @@ __global__ __launch_bounds__(kKhThreads) void khop_dq(KhopParams a) {
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * mb + 4 * g + r, tok = row >> 4, h = row & 15;
         if (tok >= ntok) continue;
-        float* dqp = a.dq + (int64_t)b * a.dq_sb + (int64_t)(i0 + tok) * a.dq_si + (int64_t)h * a.dq_sh;
+        const int64_t o = (int64_t)b * a.dq_sb + (int64_t)(i0 + tok) * a.dq_si + (int64_t)h * a.dq_sh;
 #pragma unroll
-        for (int cb = 0; cb < G::CB; ++cb) dqp[wave * G::QW + 16 * cb + l16] = acc[mb][cb][r];
+        for (int cb = 0; cb < G::CB; ++cb)
+          kh_store1(a.dq, o + wave * G::QW + 16 * cb + l16, acc[mb][cb][r], a.dq_bf16);
       }
   }
 }
@@ -600,10 +613,10 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
     }
   }
   if (u < ntok) {  // lane holds dQ^T[col 16cb + 4g + r][head l16] of token i0 + u
-    float* dqp = a.dq + blockIdx.z * a.dq_ss + (int64_t)b * a.dq_sb + (int64_t)(i0 + u) * a.dq_si +
-                 (int64_t)l16 * a.dq_sh + col0 + 4 * g;
+    const int64_t o = blockIdx.z * a.dq_ss + (int64_t)b * a.dq_sb + (int64_t)(i0 + u) * a.dq_si +
+                      (int64_t)l16 * a.dq_sh + col0 + 4 * g;
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) *reinterpret_cast<floatx4*>(dqp + 16 * cb) = acc[cb];
+    for (int cb = 0; cb < CB; ++cb) kh_store4(a.dq, o + 16 * cb, acc[cb], a.dq_bf16);
   }
 }
 
@@ -691,8 +704,7 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
   }
   {
     const int l16 = lane & 15, g = lane >> 4;
-    float* dkb = a.dk + split * a.dk_ss + (int64_t)b * a.dk_sb;
-    float* dvb = a.dv + split * a.dv_ss + (int64_t)b * a.dv_sb;
+    const int64_t ok = split * a.dk_ss + (int64_t)b * a.dk_sb, ov = split * a.dv_ss + (int64_t)b * a.dv_sb;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
@@ -702,8 +714,8 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
 #pragma unroll
         for (int cb = 0; cb < G::CB; ++cb) {
           const int col = wave * G::QW + 16 * cb + l16;
-          dkb[(int64_t)key * a.dk_sn + col] = dk_acc[mb][cb][r];
-          dvb[(int64_t)key * a.dv_sn + col] = dv_acc[mb][cb][r];
+          kh_store1(a.dk, ok + (int64_t)key * a.dk_sn + col, dk_acc[mb][cb][r], a.kv_bf16);
+          kh_store1(a.dv, ov + (int64_t)key * a.dv_sn + col, dv_acc[mb][cb][r], a.kv_bf16);
         }
       }
   }
@@ -876,10 +888,11 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dkdv4(KhopParams a) {
     }
   }
   if (key < a.N) {  // lane holds dK^T (role 0) or dV^T (role 1) [col 16 cb + 4g + r][key]
-    float* out = role == 0 ? a.dk + split * a.dk_ss + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_sn
-                           : a.dv + split * a.dv_ss + (int64_t)b * a.dv_sb + (int64_t)key * a.dv_sn;
+    float* out = role == 0 ? a.dk : a.dv;
+    const int64_t o = role == 0 ? split * a.dk_ss + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_sn
+                                : split * a.dv_ss + (int64_t)b * a.dv_sb + (int64_t)key * a.dv_sn;
 #pragma unroll
-    for (int cb = 0; cb < CBO; ++cb) *reinterpret_cast<floatx4*>(out + 16 * cb + 4 * g) = acc[cb];
+    for (int cb = 0; cb < CBO; ++cb) kh_store4(out, o + 16 * cb + 4 * g, acc[cb], a.kv_bf16);
   }
 }
 
@@ -936,20 +949,21 @@ __global__ __launch_bounds__(256) void khop_delta_kernel(const uint16_t* dz, int
   if (lane == 0) delta[((int64_t)b * 16 + h) * Lq + i] = s;
 }
 
-// Sum of the per-split dk / dv partials (fixed order): out[n] = sum_s part[s][n], n < count.
+// Sum of the per-split dk / dv / dq partials (fixed order): out[n] = sum_s part[s][n], n < count; out is fp32, or
+// bf16 (round to nearest even) with out_bf16.
 __global__ __launch_bounds__(256) void khop_split_sum_kernel(const float* part, int64_t split_stride, int splits,
-                                                              int64_t count, float* out) {
+                                                              int64_t count, float* out, bool out_bf16) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= count) return;
   float s = part[n];
   for (int p = 1; p < splits; ++p) s += part[p * split_stride + n];
-  out[n] = s;
+  kh_store1(out, n, s, out_bf16);
 }
 
 // The same over 4 consecutive floats per thread (count and split_stride multiples of 4, 16-byte aligned buffers),
 // every split's load in flight before the adds, which keep the split order: bitwise the scalar kernel's result.
 __global__ __launch_bounds__(256) void khop_split_sum4_kernel(const float* part, int64_t split_stride, int splits,
-                                                               int64_t count, float* out) {
+                                                               int64_t count, float* out, bool out_bf16) {
   const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= count) return;
   floatx4 s = *reinterpret_cast<const floatx4*>(part + n);
@@ -962,20 +976,20 @@ __global__ __launch_bounds__(256) void khop_split_sum4_kernel(const float* part,
     for (int u = 0; u < 8; ++u) s += x[u];
   }
   for (; p < splits; ++p) s += *reinterpret_cast<const floatx4*>(part + (int64_t)p * split_stride + n);
-  *reinterpret_cast<floatx4*>(out + n) = s;
+  kh_store4(out, n, s, out_bf16);
 }
 
 inline bool kh_aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // out = the fixed-order sum of `splits` partials of `count` floats at `split_stride` (one launch)
 inline void kh_split_sum(const float* part, int64_t split_stride, int splits, int64_t count, float* out,
-                         hipStream_t st) {
+                         bool out_bf16, hipStream_t st) {
   if (count % 4 == 0 && split_stride % 4 == 0 && kh_aligned16(part) && kh_aligned16(out))
     hipLaunchKernelGGL(khop_split_sum4_kernel, dim3((unsigned)((count / 4 + 255) / 256)), dim3(256), 0, st, part,
-                       split_stride, splits, count, out);
+                       split_stride, splits, count, out, out_bf16);
   else
     hipLaunchKernelGGL(khop_split_sum_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, st, part,
-                       split_stride, splits, count, out);
+                       split_stride, splits, count, out, out_bf16);
 }
 
 // Key ranges of the multi-query dq kernel: 1 when the B * ceil(Lq / 4) token groups fill the GPU, else enough
@@ -1082,7 +1096,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
                                     int64_t dz_sb, int64_t dz_si, int64_t dz_sh, const float* dlse, float* delta,
                                     float* dq, int64_t dq_sb, int64_t dq_si, int64_t dq_sh, float* dk, int64_t dk_sb,
                                     int64_t dk_sn, float* dv, int64_t dv_sb, int64_t dv_sn, int32_t key_splits,
-                                    float* workspace, int64_t workspace_floats, void* stream) {
+                                    float* workspace, int64_t workspace_floats, int32_t grads_bf16, void* stream) {
   using namespace hla;
   int rc = kh_check(q, q_sb, q_si, q_sh, k, k_sb, k_sn, v, v_sb, v_sn, B, Lq, N, width, heads);
   if (rc != HLA_S6_OK) return rc;
@@ -1142,6 +1156,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
         p.dq = workspace;
         p.dq_ss = part_q;
       }
+      p.dq_bf16 = grads_bf16 != 0 && qs == 1;
       const dim3 grid4((unsigned)((Lq + 3) / 4), (unsigned)B, (unsigned)qs);
       if (width == 512 && mask) hipLaunchKernelGGL((khop_dq4<512, true>), grid4, dim3(kKhThreads), 0, st, p);
       else if (width == 512) hipLaunchKernelGGL((khop_dq4<512, false>), grid4, dim3(kKhThreads), 0, st, p);
@@ -1149,10 +1164,11 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
       else hipLaunchKernelGGL((khop_dq4<256, false>), grid4, dim3(kKhThreads), 0, st, p);
       if (qs > 1) {
         if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
-        kh_split_sum(workspace, part_q, qs, part_q, dq, st);
+        kh_split_sum(workspace, part_q, qs, part_q, dq, grads_bf16 != 0, st);
       }
     } else {
       const dim3 grid((unsigned)((Lq + 1) / 2), (unsigned)B);
+      p.dq_bf16 = grads_bf16 != 0;
       HLA_KH_DISPATCH(khop_dq, width, grid, p, st);
     }
     if ((rc = check_launch("khop_dq")) != HLA_S6_OK) return rc;
@@ -1163,6 +1179,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
                            dv_sn == width),
                 HLA_S6_EINVAL, "khop_backward: with key splits dk / dv must be contiguous [B, N, width]");
     p.key_splits = key_splits;
+    p.kv_bf16 = grads_bf16 != 0 && !split;
     p.dk = split ? workspace : dk;
     p.dv = split ? workspace + key_splits * part : dv;
     p.dk_sb = split ? (int64_t)N * width : dk_sb;
@@ -1186,8 +1203,8 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
     }
     if ((rc = check_launch("khop_dkdv")) != HLA_S6_OK) return rc;
     if (split) {
-      kh_split_sum(workspace, part, key_splits, part, dk, st);
-      kh_split_sum(workspace + key_splits * part, part, key_splits, part, dv, st);
+      kh_split_sum(workspace, part, key_splits, part, dk, grads_bf16 != 0, st);
+      kh_split_sum(workspace + key_splits * part, part, key_splits, part, dv, grads_bf16 != 0, st);
       if ((rc = check_launch("khop_split_sum")) != HLA_S6_OK) return rc;
     }
   }

@@ -113,23 +113,26 @@ class _CausalHistory(torch.autograd.Function):
         if qb.shape[-1] not in WIDTHS:
             raise ValueError(f'causal_history_gemm backward: the HIP kernels take widths {WIDTHS} '
                              f'(got {qb.shape[-1]}; 1024 is forward only)')
-        dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v)
+        bf = q_dtype == k_dtype == v_dtype == torch.bfloat16
+        dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v, bf)
         return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
                 dv.to(v_dtype) if need_v else None, None, None)
 
 
-def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv):
-    """dq [B, Lq, 16, R], dk / dv [B, N, R] (fp32, None where not needed) of z, lse = forward(q [B, Lq, 16, R], k, v,
-    mask bytes m8 [B, Lq, N]) for the cotangents dz [B, Lq, 16, R] and dlse [B, 16, Lq] (None = 0)."""
+def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv, bf16_grads=False):
+    """dq [B, Lq, 16, R], dk / dv [B, N, R] (fp32, or bf16 written by the kernels with ``bf16_grads``; None where not
+    needed) of z, lse = forward(q [B, Lq, 16, R], k, v, mask bytes m8 [B, Lq, N]) for the cotangents dz
+    [B, Lq, 16, R] and dlse [B, 16, Lq] (None = 0)."""
     B, Lq, H, R = qb.shape
     N = kb.shape[1]
     dev = qb.device
     dzb = _bf16_rows('dz', dz if dz is not None else torch.zeros_like(z))
     dl = None if dlse is None else dlse.to(torch.float32).contiguous()
     delta = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
-    dq = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev) if need_q else None
-    dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
-    dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+    gd = torch.bfloat16 if bf16_grads else torch.float32
+    dq = torch.empty(B, Lq, H, R, dtype=gd, device=dev) if need_q else None
+    dk = torch.empty(B, N, R, dtype=gd, device=dev) if need_kv else None
+    dv = torch.empty(B, N, R, dtype=gd, device=dev) if need_kv else None
     # key tiles of the dk / dv kernel: 64 keys on the multi-query form (widths 512 / 256, N a multiple of 16),
     # whose causal load is balanced best with about 8 workgroups per CU (12 ranges at B=4, L=2880: 3.78 ms
     # forward + backward against 4.15 ms with 6 and 4.11 ms with 32); 4 per CU on the 32-key form
@@ -147,7 +150,7 @@ def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv):
               0 if dq is None else dq.stride(2), _lib.ptr(dk), 0 if dk is None else dk.stride(0),
               0 if dk is None else dk.stride(1), _lib.ptr(dv), 0 if dv is None else dv.stride(0),
               0 if dv is None else dv.stride(1), splits, _lib.ptr(ws), 0 if ws is None else ws.numel(),
-              _lib.stream(dev))
+              int(bf16_grads), _lib.stream(dev))
     return dq, dk, dv
 
 
@@ -225,7 +228,7 @@ class _History(torch.autograd.Function):
             raise ValueError(f'history_attention backward: the HIP kernels take widths {WIDTHS} (got {R})')
         dq, dk, dv = _backward(qb[:, None], kb, vb, m8[:, None], bound, lse[:, :, None], z[:, None],
                                None if dz is None else dz[:, None], None if dlse is None else dlse[:, :, None],
-                               scale, need_q, need_k or need_v)
+                               scale, need_q, need_k or need_v, q_dtype == k_dtype == v_dtype == torch.bfloat16)
         return (dq[:, 0].to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
                 dv.to(v_dtype) if need_v else None, None, None)
 

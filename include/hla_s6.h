@@ -296,7 +296,9 @@ int hla_s6_gather_packed_rows(const int64_t *cache_addrs, int32_t num_layers, in
  *   `delta` [B, 16, Lq], then dq [B, Lq, 16, width] (NULL: skipped) and dk / dv [B, N, width] fp32 (both NULL:
  *   skipped). key_splits > 1 splits each key tile's query rows over that many workgroups, with fp32 partials in
  *   `workspace` (at least 2 * key_splits * B * N * width floats; dk / dv then contiguous) summed in a fixed order,
- *   so results are deterministic for a given key_splits. Up to 5 launches. */
+ *   so results are deterministic for a given key_splits. With grads_bf16 != 0, dq / dk / dv are bf16 arrays (the
+ *   float pointers are reinterpreted, strides in bf16 elements), each value the fp32 result rounded to nearest
+ *   even. Up to 5 launches. */
 int hla_s6_khop_bounds(const uint8_t *mask, int64_t m_sb, int64_t m_si, int32_t B, int32_t Lq, int32_t N,
                        int32_t *bound, void *stream);
 int hla_s6_khop_forward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void *k, int64_t k_sb,
@@ -316,7 +318,8 @@ int hla_s6_khop_backward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh
                          const float *lse, const void *dz, int64_t dz_sb, int64_t dz_si, int64_t dz_sh,
                          const float *dlse, float *delta, float *dq, int64_t dq_sb, int64_t dq_si, int64_t dq_sh,
                          float *dk, int64_t dk_sb, int64_t dk_sn, float *dv, int64_t dv_sb, int64_t dv_sn,
-                         int32_t key_splits, float *workspace, int64_t workspace_floats, void *stream);
+                         int32_t key_splits, float *workspace, int64_t workspace_floats, int32_t grads_bf16,
+                         void *stream);
 
 /* ---- single-query history attention over contiguous rows with a key mask (HF rolling engine) ---------------
  * Replaces the forward of fused_history.history_attention (hla/latent/fused_history.py:23-35,49-54; Triton

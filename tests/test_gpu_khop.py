@@ -155,7 +155,7 @@ def test_mask_rows_off_16_byte_boundaries_and_no_mask(R):
              kt.stride(1), lib.ptr(vt), vt.stride(0), vt.stride(1), None, 0, 0, lib.ptr(bound), B, Lq, N, 16, R, scale,
              lib.ptr(z2), z2.stride(0), z2.stride(1), z2.stride(2), lib.ptr(lse2), lib.ptr(dzt), dzt.stride(0),
              dzt.stride(1), dzt.stride(2), None, lib.ptr(delta), lib.ptr(dq), dq.stride(0), dq.stride(1), dq.stride(2),
-             None, 0, 0, None, 0, 0, 1, None, 0, st)
+             None, 0, 0, None, 0, 0, 1, None, 0, 0, st)
     dqo, _, _ = O.causal_history_backward(q, k, v, np.ones((B, Lq, N), bool), scale, lo2, dz, None,
                                           z=bf16.round_bf16(zo2.astype(np.float32)))
     assert_grad_close(dq.cpu().numpy(), dqo, 'dq (no mask)')
@@ -259,3 +259,23 @@ def test_transposed_query_view_of_the_reference_benchmark():
     z1, l1 = hg.causal_history_gemm(qt, kt, vt, mt, scale)
     z2, l2 = hg.causal_history_gemm(qv, kt, vt, mt, scale)
     assert torch.equal(z1, z2) and torch.equal(l1, l2)
+
+
+@pytest.mark.parametrize('R,B,Lq,N,kind', [(128, 2, 21, 70, 'khop'), (256, 2, 48, 48, 'benchmark'),
+                                           (512, 3, 29, 96, 'any'), (512, 4, 2, 256, 'any')])
+def test_bf16_gradients_are_the_rounded_fp32_gradients(R, B, Lq, N, kind):
+    """bf16 leaves get gradients written as bf16 by the kernels (no fp32 copy): bitwise the fp32 gradients of the
+    same bf16 inputs rounded to nearest even, on the direct, row-range and key-range (one query) paths."""
+    q, k, v, mask = case(R + Lq + N, B, Lq, N, R, kind)
+    rng = np.random.default_rng(R * Lq)
+    dz = torch.tensor(bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32)), device='cuda')
+    dl = torch.tensor(rng.standard_normal((B, 16, Lq)).astype(np.float32), device='cuda')
+    mt = torch.tensor(mask, device='cuda')
+    grads = {}
+    for dt in (torch.float32, torch.bfloat16):
+        leaves = [torch.tensor(x, device='cuda').to(torch.bfloat16).to(dt).requires_grad_(True) for x in (q, k, v)]
+        z, lse = hg.causal_history_gemm(*leaves, mt, 0.08)
+        grads[dt] = torch.autograd.grad([z, lse], leaves, [dz.to(dt), dl])
+    for name, g32, g16 in zip('qkv', grads[torch.float32], grads[torch.bfloat16]):
+        assert g16.dtype == torch.bfloat16
+        assert torch.equal(g32.to(torch.bfloat16).view(torch.int16), g16.view(torch.int16)), name
