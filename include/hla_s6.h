@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 2
+#define HLA_S6_ABI_VERSION 3
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
