@@ -109,6 +109,8 @@ struct HistoryParams {
   const uint8_t* mask;
   int64_t mask_st;
   bool lse_rows;  // lse of history_split / history_combine in [rows][16][tok_per_row] instead of [16][T]
+  bool reverse_groups;  // history_mq5: workgroup b takes token group gridDim.x - 1 - b (the K-hop causal rows put
+                        // the longest groups last in token order; dispatching them first shortens the tail)
 };
 
 template <int R>
@@ -1313,6 +1315,9 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
 #ifndef HLA_MQ5
 #define HLA_MQ5 1  // 256-wide multi-query steps: history_mq5 (4 waves, no score exchange) instead of history_mq4
 #endif
+#ifndef HLA_KH_REVERSE
+#define HLA_KH_REVERSE 1  // K-hop forward on history_mq5: token groups dispatched last to first
+#endif
 #ifndef HLA_KH1024_NQ
 #define HLA_KH1024_NQ 2  // tokens per workgroup of the 1024-wide K-hop forward (history_group)
 #endif
@@ -1624,7 +1629,8 @@ __global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_
   const int S = a.num_splits, s = blockIdx.y;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;
   const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
-  const int t_begin = blockIdx.x * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
+  const int grp = a.reverse_groups ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int t_begin = grp * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
 
   for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
     const int64_t row = table_row(a, tp);
@@ -2348,6 +2354,7 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.direct = true;
   p.mask = mask;
   p.mask_st = mask_st;
+  p.reverse_groups = HLA_KH_REVERSE;
   if (width == 1024) {  // four tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
     p.lse_rows = true;
     p.page_stride = (int64_t)N * k_sn;

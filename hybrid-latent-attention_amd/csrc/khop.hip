@@ -476,7 +476,9 @@ __global__ __launch_bounds__(kKhThreads, 1) void khop_dq4(KhopParams a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, g = lane >> 4;
   const int u = wave >> 1, role = wave & 1, col0 = role * C;
-  const int b = blockIdx.y, i0 = blockIdx.x * 4;
+  // token groups dispatched last to first: under a causal mask the last tokens see the most keys, so the longest
+  // workgroups start first and the tail of the launch is short
+  const int b = blockIdx.y, i0 = (gridDim.x - 1 - blockIdx.x) * 4;
   const int ntok = min(4, a.Lq - i0);
   const int iu = i0 + min(u, ntok - 1);  // this wave's token (clamped: waves past the last token store nothing)
   if (tid < 4) bound_s[tid] = tid < ntok ? min(a.bound[(int64_t)b * a.Lq + i0 + tid], a.N) : 0;
