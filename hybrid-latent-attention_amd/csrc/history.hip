@@ -109,8 +109,9 @@ struct HistoryParams {
   const uint8_t* mask;
   int64_t mask_st;
   bool lse_rows;  // lse of history_split / history_combine in [rows][16][tok_per_row] instead of [16][T]
-  bool reverse_groups;  // history_mq5: workgroup b takes token group gridDim.x - 1 - b (the K-hop causal rows put
-                        // the longest groups last in token order; dispatching them first shortens the tail)
+  bool reverse_groups;  // history_mq5 / history_group: workgroup b takes token group gridDim.x - 1 - b (the K-hop
+                        // causal rows put the longest groups last in token order; dispatching them first shortens
+                        // the tail)
 };
 
 template <int R>
@@ -749,7 +750,8 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
   // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
   // ragged batch get split counts proportional to their length and every split has equal work.
   const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
-  const int t_begin = blockIdx.x * NQ, t_end = min(t_begin + NQ, a.T);
+  const int grp = a.reverse_groups ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+  const int t_begin = grp * NQ, t_end = min(t_begin + NQ, a.T);
 
   int par = 0;  // score-exchange buffer of the next tile; alternates over every tile of every pass
   for (int tp = t_begin; tp < t_end;) {
