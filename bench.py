@@ -479,10 +479,10 @@ def khop_workload(args, pkg, device):
 
     def fwd():
         with torch.no_grad():
-            hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
+            hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision='bf16')
 
     def train():  # gradients returned, not accumulated into .grad (as the reference's operator benchmark does)
-        z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True)
+        z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision='bf16')
         torch.autograd.grad([z, lse], [q, k, v], [dz, dlse])
 
     ms_f = time_graph(fwd, args.steps, args.warmup)

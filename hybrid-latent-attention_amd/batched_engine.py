@@ -37,7 +37,7 @@ def _history_block(qc, ck, cv, mask, scale):
     B, H, n, r = qc.shape
     q = qc.transpose(1, 2).contiguous()                       # [B, n, H, r]: token-linear rows for the MFMA kernel
     m = mask[:, None, :].expand(B, n, mask.shape[1]).contiguous()
-    z, lse = history_gemm.causal_history_gemm(q, ck, cv, m, scale)
+    z, lse = history_gemm.causal_history_gemm(q, ck, cv, m, scale, precision='bf16')
     return z.transpose(1, 2), lse
 
 

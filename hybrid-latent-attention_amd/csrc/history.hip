@@ -29,29 +29,10 @@ namespace hla {
 
 namespace {
 
-// Tuning of the split kernel: tiles in flight per workgroup, V copies in LDS, non-temporal K/V loads,
-// waves-per-EU hint, K staged through LDS, latent columns per wave.
-#ifndef HLA_HIST_DEPTH
-#define HLA_HIST_DEPTH 1
-#endif
-#ifndef HLA_HIST_VBUF
-#define HLA_HIST_VBUF 1
-#endif
-#ifndef HLA_HIST_WPE
-#define HLA_HIST_WPE 3  // keeps the accumulators out of AGPRs: 3 waves per SIMD instead of 2
-#endif
-#ifndef HLA_HIST_KLDS
-#define HLA_HIST_KLDS 1
-#endif
-#ifndef HLA_HIST_WCOLS
-#define HLA_HIST_WCOLS 128
-#endif
-#ifndef HLA_MQ_V2
-#define HLA_MQ_V2 1  // multi-query steps: history_mq2 (token-per-wave-pair) instead of history_mq
-#endif
-#ifndef HLA_HIST_VTR
-#define HLA_HIST_VTR 1  // V^T operands by ds_read_b64_tr_b16 (else four 16-bit LDS reads)
-#endif
+// Split-kernel constants: latent columns per wave; the compiler is held to 3 waves per SIMD, which keeps the
+// accumulators out of AGPRs.
+constexpr int kWaveCols = 128;
+constexpr int kSplitWavesPerEu = 3;
 
 constexpr int kHeads = 16;
 constexpr int kTile = 16;
@@ -116,7 +97,7 @@ struct HistoryParams {
 
 template <int R>
 struct Geo {
-  static constexpr int WAVES = R >= HLA_HIST_WCOLS ? R / HLA_HIST_WCOLS : 1;  // one wave per 128 latent columns
+  static constexpr int WAVES = R >= kWaveCols ? R / kWaveCols : 1;  // one wave per 128 latent columns
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int QW = R / WAVES;      // latent columns per wave
   static constexpr int KI = QW / 32;        // 16-byte K pieces per lane per tile (= MFMA k-steps)
@@ -124,7 +105,7 @@ struct Geo {
   static constexpr int NT = QW / 16;        // 16-column O^T tiles per wave
   static constexpr int CPR = QW / 8;        // 16-byte chunks per V row (wave's columns)
   static constexpr int VS = QW + 8;         // LDS row stride of the K copy, in bf16 (conflict-free row reads)
-  static constexpr int VSV = QW + (HLA_HIST_VTR ? 16 : 8);  // of the V copy (conflict-free transposed reads)
+  static constexpr int VSV = QW + 16;      // of the V copy (conflict-free transposed reads)
   static constexpr int VBUF = kTile * VSV;  // one wave buffer, in bf16
 };
 
@@ -329,10 +310,6 @@ __device__ __forceinline__ void load_tile(const HistoryParams& a, const RowSourc
     const int64_t page = min(max((int64_t)src.btr[key0 / a.block_size], (int64_t)0), a.num_blocks - 1);
     base = page * a.page_stride + (int64_t)(key0 % a.block_size) * a.row_stride + col0;
   }
-  const int hq = lane & 15, g = lane >> 4;
-#if HLA_HIST_KLDS
-  (void)hq;
-  (void)g;
 #pragma unroll
   for (int it = 0; it < G::KI; ++it) {  // same coalesced chunk layout as V: 4 rows x 256 bytes per instruction
     const int c = it * 64 + lane;
@@ -340,12 +317,6 @@ __device__ __forceinline__ void load_tile(const HistoryParams& a, const RowSourc
     r.k[it] = (key0 + key < n) ? ld_stream<NT>(a.k + base + (int64_t)key * a.row_stride + (c % G::CPR) * 8)
                                : u32x4{0u, 0u, 0u, 0u};
   }
-#else
-  const bool kval = key0 + hq < n;
-  const uint16_t* kp = a.k + base + (int64_t)hq * a.row_stride + 8 * g;
-#pragma unroll
-  for (int i = 0; i < G::KI; ++i) r.k[i] = kval ? ld_stream<NT>(kp + 32 * i) : u32x4{0u, 0u, 0u, 0u};
-#endif
 #pragma unroll
   for (int it = 0; it < G::VC; ++it) {
     const int c = it * 64 + lane;
@@ -366,7 +337,6 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
     st16(vs + (c / G::CPR) * G::VSV + (c % G::CPR) * 8, r.v[it]);
   }
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#if HLA_HIST_KLDS
 #pragma unroll
   for (int it = 0; it < G::KI; ++it) {
     const int c = it * 64 + lane;
@@ -376,11 +346,6 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
 #pragma unroll
   for (int i = 0; i < G::KI; ++i)
     acc = mfma16x16x32(*reinterpret_cast<const u32x4*>(ks + hq * G::VS + 32 * i + 8 * g), qreg[i], acc);
-#else
-  (void)ks;
-#pragma unroll
-  for (int i = 0; i < G::KI; ++i) acc = mfma16x16x32(r.k[i], qreg[i], acc);
-#endif
   return acc;
 }
 
@@ -390,15 +355,8 @@ __device__ __forceinline__ floatx4 stage_a(const TileRegs<R>& r, const u32x4 (&q
 template <int R>
 __device__ __forceinline__ short4v vt_operand(const uint16_t* vs, int nt, int g, int hq) {
   using G = Geo<R>;
-#if HLA_HIST_VTR
   const uint16_t* p = vs + (4 * g + (hq >> 2)) * G::VSV + 16 * nt + 4 * (hq & 3);
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)p);
-#else
-  short4v va;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) va[e] = (short)vs[(4 * g + e) * G::VSV + 16 * nt + hq];
-  return va;
-#endif
 }
 
 // Stage B: exchange S partials, online softmax, O^T += V^T P^T. With kMask, byte r of mk hides key 4g + r of the
@@ -478,14 +436,12 @@ __device__ __forceinline__ int64_t lse_index(const HistoryParams& a, int t, int 
 // partials may then see no key at all (a zero output and lse = -inf)
 template <int R, bool NT, bool kRows = false>
 __global__ __launch_bounds__(Geo<R>::THREADS)
-#if HLA_HIST_WPE
-__attribute__((amdgpu_waves_per_eu(HLA_HIST_WPE, HLA_HIST_WPE)))
-#endif
+__attribute__((amdgpu_waves_per_eu(kSplitWavesPerEu, kSplitWavesPerEu)))
 void history_split(HistoryParams a) {
   using G = Geo<R>;
-  constexpr int DEPTH = HLA_HIST_DEPTH, NVB = HLA_HIST_VBUF;
+  constexpr int DEPTH = 1, NVB = 1;  // tiles in flight per wave, V copies in LDS
   __shared__ __attribute__((aligned(16))) uint16_t v_lds[G::WAVES][NVB][G::VBUF];
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][HLA_HIST_KLDS ? G::VBUF : 8];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[G::WAVES][G::VBUF];
   __shared__ floatx4 s_lds[2][G::WAVES * 64];
   __shared__ int64_t red_lds[2 * G::WAVES];
   __shared__ int item_lds[G::WAVES + 2];
@@ -822,252 +778,8 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
 }
 
 // ---- multi-query history (chunked prefill) ------------------------------------------------------------------
-// history_mq: one workgroup per (group of 4 consecutive tokens, KV slot): the 64 query rows (4 tokens x 16 heads)
-// of tokens that share a block-table row read every K/V tile once. NW waves (8 from R = 256: two per SIMD) split
-// the latent columns (R/NW each). Per 32-key tile:
-//   * S^T[32 keys x 32 rows] partials per wave and row block (two blocks of 32 rows) on v_mfma_f32_32x32x16_bf16:
-//     the K fragment (A operand, lane: key l%32, 8 latent columns) comes straight from global memory through the
-//     caches (the rows are shared by the group's tokens and by the request's other groups); Q^T (B operand) stays
-//     in registers for the whole row;
-//   * the NW partials meet in LDS; wave w owns 64/NW rows: it sums their partials, runs the online softmax (the
-//     running maximum is only raised when a tile exceeds it by more than 2^8, so most tiles need no rescale) and
-//     writes P^T in the B-operand layout and the rows' rescale factors to LDS;
-//   * O^T[R/NW columns x 64 rows] += V^T P^T on v_mfma_f32_32x32x16_bf16: V goes through wave-private LDS and comes
-//     back transposed by ds_read_b64_tr_b16.
-constexpr int kMqTokens = 4;              // tokens per workgroup
-constexpr int kMqRows = 16 * kMqTokens;   // query rows per workgroup
+constexpr int kMqTokens = 4;              // tokens per workgroup of history_mq2
 constexpr int kMqKeys = 32;               // keys per tile
-
-template <int R>
-struct MqGeo {
-  static constexpr int NW = R >= 256 ? 8 : 4;         // waves (two per SIMD from R = 256)
-  static constexpr int QW = R / NW;                   // latent columns per wave
-  static constexpr int KS = QW / 16;                  // 16-column k-steps of S^T per tile
-  static constexpr int CB = QW / 32;                  // 32-column blocks of O^T
-  static constexpr int CPR = QW / 8;                  // 16-byte chunks per V row (the wave's columns)
-  static constexpr int VLD = kMqKeys * CPR / 64;      // 16-byte V loads per lane per tile
-  static constexpr int VS = QW + 32;                  // LDS row stride of the V copy (bf16)
-  static constexpr int KST = QW + 8;                  // LDS row stride of the K copy (conflict-free row reads)
-  static constexpr int RO = kMqRows / NW;             // softmax rows owned per wave
-  static constexpr int KG = 64 / RO;                  // key groups of an owned row (lanes sharing the row)
-  static constexpr int KPL = kMqKeys / KG;            // keys per owner lane (a multiple of 4)
-};
-
-template <int R>
-__global__ __launch_bounds__(64 * MqGeo<R>::NW) void history_mq(HistoryParams a) {
-  using G = MqGeo<R>;
-  constexpr int NW = G::NW;
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[NW][kMqKeys * G::VS];
-  __shared__ __attribute__((aligned(16))) float sx[NW][2][64][20];     // S^T partials (16 floats + pad per lane)
-  static_assert(kMqKeys * G::KST * 2 <= 2 * 64 * 20 * 4, "the K copy must fit the wave's exchange buffer");
-  __shared__ __attribute__((aligned(16))) u32x4 p_lds[2][2][64];        // P^T B operands [row block][k-step][lane]
-  __shared__ float alpha_s[kMqRows], l_s[kMqRows], m_s[kMqRows];
-  __shared__ int64_t red_lds[2 * NW];
-
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, hh = lane >> 5;          // MFMA lane coordinates
-  const int own_c = lane % G::RO, own_j = lane / G::RO;  // softmax owner: row RO*wave + own_c, keys KPL*own_j ..
-  const int own_row = G::RO * wave + own_c;           // row of the workgroup (token own_row/16, head own_row%16)
-  const int qb_o = own_row >> 5, rb = own_row & 31;   // its row block and row within the block
-  const int S = a.num_splits, s = blockIdx.y;
-  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
-  const int col0 = wave * G::QW;
-  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
-  const int t_begin = blockIdx.x * kMqTokens, t_end = min(t_begin + kMqTokens, a.T);
-  uint16_t* vs = v_lds[wave];
-
-  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
-    const int64_t row = table_row(a, tp);
-    int te = tp + 1;
-    while (te < t_end && table_row(a, te) == row) ++te;
-    const int count = te - tp;
-    int n[kMqTokens];
-    int n_max = 0;
-#pragma unroll
-    for (int u = 0; u < kMqTokens; ++u) {
-      n[u] = u < count ? (int)min((int64_t)a.ctx[tp + u], cap) : 0;
-      n_max = max(n_max, n[u]);
-    }
-    const int tiles16 = (n_max + kTile - 1) / kTile;
-    const int j0 = S > 1 ? s * chunk : 0;
-    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
-    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);  // keys of this slot
-    const int own_u = own_row >> 4;
-    const int own_n = min(k1, own_u == 0 ? n[0] : own_u == 1 ? n[1] : own_u == 2 ? n[2] : n[3]);
-
-    float m_own = -INFINITY, l_own = 0.f;
-    floatx16 o[G::CB][2];
-#pragma unroll
-    for (int cb = 0; cb < G::CB; ++cb) o[cb][0] = o[cb][1] = floatx16{};
-    if (k0 < k1) {  // uniform over the workgroup
-      const int32_t* btr = a.bt + row * a.bt_stride;
-      u32x4 qf[2][G::KS];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const int tq = tp + min(2 * qb + (l32 >> 4), count - 1);
-        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)(l32 & 15) * a.q_sh + col0 + 8 * hh;
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) qf[qb][ks] = ld16(qp + 16 * ks);
-      }
-      // This lane's share of the K and V slices of a tile, coalesced (chunk c = it*64 + lane: row c / CPR, 16-byte
-      // piece c % CPR); keys past the slot read row k1 - 1 (K: masked scores; V: zeroed). The next tile's slices
-      // are loaded as soon as the current ones are in LDS, so they are in flight during the whole tile. K goes
-      // through the wave's own partial-exchange buffer (free until the partials are written) and comes back in the
-      // A-operand layout (lane: key l32, 8 latent columns).
-      u32x4 kr[G::VLD], vr[G::VLD];
-      auto load_kv = [&](int kt) {
-#pragma unroll
-        for (int it = 0; it < G::VLD; ++it) {
-          const int c = it * 64 + lane, vrow = c / G::CPR;
-          const int key = min(kt + vrow, k1 - 1);
-          const int64_t page = min(max((int64_t)btr[key / a.block_size], (int64_t)0), a.num_blocks - 1);
-          const int64_t off = page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride + col0 + (c % G::CPR) * 8;
-          kr[it] = ld16(a.k + off);
-          const u32x4 x = ld16(a.v + off);
-          vr[it] = kt + vrow < k1 ? x : u32x4{0u, 0u, 0u, 0u};
-        }
-      };
-      load_kv(k0);
-      for (int kt = k0; kt < k1; kt += kMqKeys) {
-        uint16_t* ks_lds = reinterpret_cast<uint16_t*>(&sx[wave][0][0][0]);
-#pragma unroll
-        for (int it = 0; it < G::VLD; ++it) {
-          const int c = it * 64 + lane;
-          st16(ks_lds + (c / G::CPR) * G::KST + (c % G::CPR) * 8, kr[it]);
-          st16(vs + (c / G::CPR) * G::VS + (c % G::CPR) * 8, vr[it]);
-        }
-        if (kt + kMqKeys < k1) load_kv(kt + kMqKeys);
-        u32x4 kf[G::KS];
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) kf[ks] = *reinterpret_cast<const u32x4*>(ks_lds + l32 * G::KST + 16 * ks + 8 * hh);
-        floatx16 sacc[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-        for (int ks = 0; ks < G::KS; ++ks) {
-          sacc[0] = mfma32x32x16(kf[ks], qf[0][ks], sacc[0]);
-          sacc[1] = mfma32x32x16(kf[ks], qf[1][ks], sacc[1]);
-        }
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int q4 = 0; q4 < 4; ++q4)
-            *reinterpret_cast<floatx4*>(&sx[wave][qb][lane][4 * q4]) =
-                floatx4{sacc[qb][4 * q4], sacc[qb][4 * q4 + 1], sacc[qb][4 * q4 + 2], sacc[qb][4 * q4 + 3]};
-        __syncthreads();
-        {  // owner softmax: row rb of block qb_o, keys kt + KPL*own_j + e
-          float sc[G::KPL];
-#pragma unroll
-          for (int q = 0; q < G::KPL / 4; ++q) {
-            const int key = G::KPL * own_j + 4 * q;  // D layout: keys 8jj + 4h + i at lane rb + 32h, entries 4jj..
-            const float* src = &sx[0][qb_o][rb + 32 * ((key >> 2) & 1)][4 * (key >> 3)];
-            floatx4 x = *reinterpret_cast<const floatx4*>(src);
-#pragma unroll
-            for (int p = 1; p < NW; ++p) x += *reinterpret_cast<const floatx4*>(src + p * (2 * 64 * 20));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sc[4 * q + e] = kt + key + e < own_n ? x[e] * a.scale_log2 : -INFINITY;
-          }
-          float mx = sc[0];
-#pragma unroll
-          for (int e = 1; e < G::KPL; ++e) mx = fmaxf(mx, sc[e]);
-#pragma unroll
-          for (int off = G::RO; off < 64; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-          float alpha = 1.f;
-          const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
-          if (__any(raise)) {
-            const float m_new = raise ? mx : m_own;
-            alpha = fast_exp2(m_own - m_new);  // 0 on the first raise (m_own = -inf)
-            l_own *= alpha;
-            m_own = m_new;
-          }
-          const float m_use = m_own == -INFINITY ? 0.f : m_own;
-          float p[G::KPL], ps = 0.f;
-#pragma unroll
-          for (int e = 0; e < G::KPL; ++e) {
-            p[e] = fast_exp2(sc[e] - m_use);
-            ps += p[e];
-          }
-#pragma unroll
-          for (int off = G::RO; off < 64; off <<= 1) ps += __shfl_xor(ps, off);
-          l_own += ps;
-#pragma unroll
-          for (int q = 0; q < G::KPL / 4; ++q) {  // P^T B operand: lane rb + 32*(key/8 % 2), keys key%16 ..
-            const int key = G::KPL * own_j + 4 * q;
-            uint2* dst = reinterpret_cast<uint2*>(&p_lds[qb_o][key >> 4][rb + 32 * ((key >> 3) & 1)]) + ((key >> 2) & 1);
-            *dst = uint2{pack2(p[4 * q], p[4 * q + 1]), pack2(p[4 * q + 2], p[4 * q + 3])};
-          }
-          if (own_j == 0) alpha_s[own_row] = alpha;
-        }
-        __syncthreads();
-        {  // rescale O where a row's maximum was raised, then O^T += V^T P^T
-          const float al0 = alpha_s[l32], al1 = alpha_s[32 + l32];
-          if (__any(al0 != 1.f || al1 != 1.f)) {
-#pragma unroll
-            for (int cb = 0; cb < G::CB; ++cb) {
-              o[cb][0] = o[cb][0] * al0;
-              o[cb][1] = o[cb][1] * al1;
-            }
-          }
-          u32x4 pf[2][2];
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) pf[qb][ks] = p_lds[qb][ks][lane];
-          const int g = lane >> 4, i16 = lane & 15;
-#pragma unroll
-          for (int cb = 0; cb < G::CB; ++cb) {
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              // lane i16 of group g: column 32cb + 16(g%2) + i16, keys 16ks + 8(g/2) + e
-              const uint16_t* vp = vs + (16 * ks + 8 * (g >> 1) + (i16 >> 2)) * G::VS + 32 * cb + 16 * (g & 1) +
-                                   4 * (i16 & 3);
-              const short4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
-              const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                  (__attribute__((address_space(3))) short4v*)(vp + 4 * G::VS));
-              const u32x4 vt = join_tr(lo, hi);
-              o[cb][0] = mfma32x32x16(vt, pf[0][ks], o[cb][0]);
-              o[cb][1] = mfma32x32x16(vt, pf[1][ks], o[cb][1]);
-            }
-          }
-        }
-      }
-    }
-    if (own_j == 0) {  // owners publish their rows' softmax state
-      l_s[own_row] = l_own;
-      m_s[own_row] = m_own;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      const int r = 32 * qb + l32, u = r >> 4, h = r & 15;
-      if (u >= count) continue;
-      const int t = tp + u;
-      const float l = l_s[r];
-      const bool any = l > 0.f;
-      const float inv = any ? 1.0f / l : 0.f;
-      const float lse = any ? (m_s[r] + log2f(l)) * kLn2 : -INFINITY;
-#pragma unroll
-      for (int cb = 0; cb < G::CB; ++cb) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = col0 + 32 * cb + 8 * j + 4 * hh;
-          const floatx4 v = {o[cb][qb][4 * j] * inv, o[cb][qb][4 * j + 1] * inv, o[cb][qb][4 * j + 2] * inv,
-                             o[cb][qb][4 * j + 3] * inv};
-          if (a.direct) {
-            *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
-                uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-          } else {
-            *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
-          }
-        }
-      }
-      if (wave == 0 && hh == 0) {
-        if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
-        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
-      }
-    }
-    __syncthreads();  // the next pass reuses the LDS exchange
-    tp = te;
-  }
-}
 
 // history_mq2: one workgroup per (group of 4 consecutive tokens, KV slot) with 8 waves; wave w owns token w / 2 (its
 // 16 heads are the 16 query rows) and latent column half w % 2. Per 32-key tile:
@@ -1300,306 +1012,24 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
   }
 }
 
-// history_mq4 (the 512- and 256-wide latents): one workgroup per (group of 8 consecutive tokens, KV slot) with 8
-// waves; wave w owns tokens 2(w/2) and 2(w/2) + 1 of the pass (32 query rows, so every K and V operand read from LDS
-// feeds two MFMAs) and latent column half w % 2. The per-tile phases are those of history_mq2 (S^T partials over the
-// wave's columns, swap of partials with the partner half, online softmax, O^T += V^T P^T with P^T in registers); the
-// K and V tiles go global -> LDS by direct loads (global_load_lds_dwordx4: 16 bytes per lane, one row per
-// instruction: all 64 lanes for a 1 KB row, lanes 0-31 for a 512 B one; wave w copies rows 4w .. 4w+3) into three
-// rotating tile buffers. At tile i the buffers hold K(i), V(i) and K(i+1); after the exchange barrier V(i+1) replaces
-// K(i), after the P V barrier K(i+2) replaces V(i), so every copy is requested about one tile ahead. The copies are
-// waited for explicitly (s_waitcnt vmcnt counting the copies issued after the awaited one) and the tile loop
-// synchronizes with plain s_barrier behind those waits: a copy still in flight for a later tile is never waited for
-// at a barrier.
-#ifndef HLA_MQ4
-#define HLA_MQ4 1  // 512-wide multi-query steps: history_mq4 (8 tokens per workgroup) instead of history_mq2
-#endif
-#ifndef HLA_MQ5
-#define HLA_MQ5 1  // 256-wide multi-query steps: history_mq5 (4 waves, no score exchange) instead of history_mq4
-#endif
-#ifndef HLA_KH_REVERSE
-#define HLA_KH_REVERSE 1  // K-hop forward on history_mq5: token groups dispatched last to first
-#endif
-#ifndef HLA_KH1024_NQ
-#define HLA_KH1024_NQ 2  // tokens per workgroup of the 1024-wide K-hop forward (history_group)
-#endif
-#ifndef HLA_MQ5_512
-#define HLA_MQ5_512 1  // 512-wide multi-query steps: history_mq5 (8 waves of one token) instead of history_mq4
-#endif
-constexpr int kMq4Tokens = 8;           // tokens per workgroup
+constexpr int kMq4Tokens = 8;           // tokens per workgroup of history_mq5
 constexpr int kMq4Keys = 32;            // keys per tile
-
-// kMode 0: paged rows; 1: contiguous rows (identity pages: row t / tok_per_row, lse [rows, 16, tok_per_row]);
-// 2: contiguous rows with a visibility mask (key j of token t visible where mask[t * mask_st + j] != 0; the mask
-// bytes of a tile travel with its K copy into LDS, 32 per token, so the loop issues no other global load).
-template <int R, int kMode>
-__global__ __launch_bounds__(512, 1) void history_mq4(HistoryParams a) {
-  static_assert(R == 512 || R == 256, "rows of 1 KB (one copy instruction) or 512 B (half of one)");
-  constexpr bool kContig = kMode != 0, kMask = kMode == 2;
-  constexpr int KOPS = kMask ? 5 : 4;  // copy instructions per wave for a K tile (4 rows, and its mask bytes)
-  // C latent columns per wave; LDS row stride R + 16 keeps rows 8 banks apart, as in history_mq2
-  constexpr int C = R / 2, KS = C / 32, CB = C / 16, RS = R + 16;
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[3][kMq4Keys * RS];
-  __shared__ __attribute__((aligned(16))) floatx4 xs[8][2][2][64];  // S^T partials [wave][token][key block][lane]
-  // mask bytes [tile parity][column half][pair][token of the pair * 32 + key] (one copy per column half, each
-  // written by its own wave)
-  __shared__ __attribute__((aligned(16))) uint8_t mk_lds[kMask ? 2 : 1][2][4][64];
-  __shared__ int32_t pg_lds[kMq2Pages];
-  __shared__ int64_t red_lds[16];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int l16 = lane & 15, g = lane >> 4;
-  const int pair = wave >> 1, half = wave & 1, col0 = half * C;
-  const int S = a.num_splits, s = blockIdx.y;
-  const int64_t cap = (int64_t)a.bt_cols * a.block_size;
-  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
-  const int t_begin = blockIdx.x * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
-
-  for (int tp = t_begin; tp < t_end;) {  // passes: runs of tokens that share a table row
-    const int64_t row = table_row(a, tp);
-    int te = tp + 1;
-    while (te < t_end && table_row(a, te) == row) ++te;
-    const int count = te - tp;
-    int n_max = 0, n_tok[2] = {0, 0};
-#pragma unroll
-    for (int v = 0; v < kMq4Tokens; ++v) {
-      const int n = v < count ? (int)min((int64_t)a.ctx[tp + v], cap) : 0;
-      n_max = max(n_max, n);
-      if (v == 2 * pair) n_tok[0] = n;
-      if (v == 2 * pair + 1) n_tok[1] = n;
-    }
-    const int tiles16 = (n_max + kTile - 1) / kTile;
-    const int j0 = S > 1 ? s * chunk : 0;
-    const int j1 = S > 1 ? min(tiles16, j0 + chunk) : tiles16;
-    const int k0 = j0 * kTile, k1 = min(n_max, j1 * kTile);
-    const int own_n[2] = {min(k1, n_tok[0]), min(k1, n_tok[1])};
-    float m_own[2] = {-INFINITY, -INFINITY}, l_own[2] = {0.f, 0.f};
-    floatx4 o[2][CB];
-#pragma unroll
-    for (int x = 0; x < 2; ++x)
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) o[x][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
-    if (k0 < k1) {  // uniform over the workgroup
-      const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
-      u32x4 qf[2][KS];
-#pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        const int tq = tp + min(2 * pair + x, count - 1);
-        const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + col0 + 8 * g;
-#pragma unroll
-        for (int k = 0; k < KS; ++k) qf[x][k] = ld16(qp + 32 * k);
-      }
-      const int p0 = k0 / a.block_size, np = (k1 - 1) / a.block_size - p0 + 1;
-      const bool pg_local = np <= kMq2Pages;
-      __syncthreads();  // the previous pass's readers of the tiles and pages are done
-      auto table_page = [&](int p) -> int64_t {  // clamped entry p of the row (identity pages: contiguous rows)
-        return kContig ? row * a.bt_cols + p : min(max((int64_t)btr[p], (int64_t)0), a.num_blocks - 1);
-      };
-      if (pg_local)
-        for (int i = tid; i < np; i += 512) pg_lds[i] = (int32_t)table_page(p0 + i);
-      __syncthreads();
-      // the query loads are complete before the first copy: the compiler does not see the copies, so no wait it
-      // places for an earlier load may end up counting them
-      __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
-      const bool page16 = a.block_size == kTile;
-      // rows 4 * wave .. + 3 of the tile at key kt into buffer b (keys past the slot's range read its last row). With
-      // 16-row pages and a whole tile the four rows sit in one page (entry kt / 16 + wave / 4, rows 4 * wave % 16 ..).
-      const uint32_t voff = 16u * lane;
-      // mask bytes of this wave's two tokens for the tile at key kt: lanes 0-3, token l / 2, bytes 16 (l % 2) ..
-      // (a chunk past the row's end is read from its last 16 bytes instead: those keys are past every bound)
-      auto copy_mask = [&](int kt) {
-        if (lane < 4) {
-          const int tq = tp + min(2 * pair + (lane >> 1), count - 1);
-          const int c0 = min(kt + 16 * (lane & 1), (int)cap - 16);
-          copy16_to_lds_v(a.mask + (int64_t)tq * a.mask_st + c0, &mk_lds[((kt - k0) / kMq4Keys) & 1][half][pair][0]);
-        }
-      };
-      auto copy = [&](int b, const uint16_t* base, int kt) {
-        if (kMask && base == a.k) copy_mask(kt);
-        if (page16 && pg_local && kt + kMq4Keys <= k1) {
-          const int64_t page = __builtin_amdgcn_readfirstlane(pg_lds[(kt >> 4) - p0 + (wave >> 2)]);
-          const uint16_t* src = base + page * a.page_stride + (int64_t)((4 * wave) & 15) * a.row_stride;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (R == 512 || lane < 32) copy16_to_lds(src + i * a.row_stride, voff, &tiles[b][(4 * wave + i) * RS]);
-        } else {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = min(kt + 4 * wave + i, k1 - 1), p = key / a.block_size;
-            const int64_t page = uniform64(pg_local ? (int64_t)pg_lds[p - p0] : table_page(p));
-            if (R == 512 || lane < 32)
-              copy16_to_lds(base + page * a.page_stride + (int64_t)(key % a.block_size) * a.row_stride, voff,
-                            &tiles[b][(4 * wave + i) * RS]);
-          }
-        }
-      };
-      const int ntiles = (k1 - k0 + kMq4Keys - 1) / kMq4Keys;
-      int kb = 0, vb = 1, nk = 2;
-      copy(kb, a.k, k0);
-      copy(vb, a.v, k0);
-      if (ntiles > 1) {
-        copy(nk, a.k, k0 + kMq4Keys);
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(4 + KOPS, 15));  // K(0) landed; V(0) and K(1) may be in flight
-      } else {
-        __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 15));
-      }
-      plain_barrier();
-      for (int i = 0; i < ntiles; ++i) {
-        const int kt = k0 + i * kMq4Keys;
-        const bool more = i + 1 < ntiles, more2 = i + 2 < ntiles;
-        {  // S^T partials of both tokens over this wave's columns
-          const uint16_t* kp = &tiles[kb][l16 * RS + col0 + 8 * g];
-          floatx4 sp[2][2];
-#pragma unroll
-          for (int x = 0; x < 2; ++x) sp[x][0] = sp[x][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-          u32x4 ka = *reinterpret_cast<const u32x4*>(kp), kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS);
-#pragma unroll
-          for (int k = 0; k < KS; ++k) {  // the next k-step's fragments are requested before this one's MFMAs
-            const u32x4 ca = ka, cc = kc;
-            if (k + 1 < KS) {
-              ka = *reinterpret_cast<const u32x4*>(kp + 32 * (k + 1));
-              kc = *reinterpret_cast<const u32x4*>(kp + 16 * RS + 32 * (k + 1));
-            }
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-              sp[x][0] = mfma16x16x32(ca, qf[x][k], sp[x][0]);
-              sp[x][1] = mfma16x16x32(cc, qf[x][k], sp[x][1]);
-            }
-          }
-#pragma unroll
-          for (int x = 0; x < 2; ++x) {
-            xs[wave][x][0][lane] = sp[x][0];
-            xs[wave][x][1][lane] = sp[x][1];
-          }
-        }
-        // V(i) landed (only K(i+1) may still be in flight) and the partials are in LDS
-        if (more) __builtin_amdgcn_s_waitcnt(waitcnt_imm(KOPS, 0));
-        else __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 0));
-        plain_barrier();
-        if (more) copy(kb, a.v, kt + kMq4Keys);  // V(i+1) into K(i)'s buffer: every wave is past its S^T
-        // online softmax of row l16 of token x over the full scores; returns P^T packed as the B operand
-        auto softmax_tok = [&](int x) -> u32x4 {
-          const floatx4 mine0 = xs[wave][x][0][lane], mine1 = xs[wave][x][1][lane];
-          const floatx4 other0 = xs[wave ^ 1][x][0][lane], other1 = xs[wave ^ 1][x][1][lane];
-          const int n = own_n[x];
-          // unscaled scores; IEEE addition commutes, so both column halves hold the same values
-          float sc[2][4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            sc[0][r] = mine0[r] + other0[r];
-            sc[1][r] = mine1[r] + other1[r];
-          }
-          if (kMask) {  // mask bytes of keys 4g + r and 16 + 4g + r of token x
-            const uint8_t* mb = &mk_lds[i & 1][half][pair][32 * x + 4 * g];
-            const uint32_t m0 = *reinterpret_cast<const uint32_t*>(mb), m1 = *reinterpret_cast<const uint32_t*>(mb + 16);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (kt + 4 * g + r >= n || ((m0 >> (8 * r)) & 255u) == 0) sc[0][r] = -INFINITY;
-              if (kt + 16 + 4 * g + r >= n || ((m1 >> (8 * r)) & 255u) == 0) sc[1][r] = -INFINITY;
-            }
-          } else if (kt + kMq4Keys > n) {  // wave-uniform: the tile runs past the row's history
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              if (kt + 4 * g + r >= n) sc[0][r] = -INFINITY;
-              if (kt + 16 + 4 * g + r >= n) sc[1][r] = -INFINITY;
-            }
-          }
-          // (scores are finite or -inf: rows past the history are masked before any NaN they hold is used)
-          float mx = max3_nn(max3_nn(sc[0][0], sc[0][1], sc[0][2]), max3_nn(sc[0][3], sc[1][0], sc[1][1]),
-                             max_nn(sc[1][2], sc[1][3]));
-          // the scale is positive, so the maximum of the scaled scores is the scaled maximum (log2 units)
-          mx = wave_max16x4_nn(mx) * a.scale_log2;
-          const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
-          if (__any(raise)) {
-            const float m_new = raise ? mx : m_own[x];
-            const float alpha = fast_exp2(m_own[x] - m_new);  // 0 on the first raise (m_own = -inf)
-            l_own[x] *= alpha;  // this lane's share of the row sum
-            m_own[x] = m_new;
-#pragma unroll
-            for (int cb = 0; cb < CB; ++cb) o[x][cb] *= alpha;
-          }
-          const float m_use = m_own[x] == -INFINITY ? 0.f : m_own[x];
-          float p[2][4], ps = 0.f;
-#pragma unroll
-          for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              p[kb2][r] = fast_exp2(__builtin_fmaf(sc[kb2][r], a.scale_log2, -m_use));
-              ps += p[kb2][r];
-            }
-          l_own[x] += ps;  // the four lanes of a row are summed once, after the last tile
-          return u32x4{pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
-                       pack2_hw(p[1][2], p[1][3])};
-        };
-        // O^T += V^T P^T (k slot 8g + e <-> key 4g + e, e < 4; key 16 + 4g + e - 4, e >= 4)
-        const uint16_t* vp = &tiles[vb][(4 * g + (l16 >> 2)) * RS + col0 + 4 * (l16 & 3)];
-        auto vfrag = [&](int cb) {
-          const short4v lo =
-              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(vp + 16 * cb));
-          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) short4v*)(vp + 16 * RS + 16 * cb));
-          return join_tr(lo, hi);
-        };
-        {
-          const u32x4 pb0 = softmax_tok(0), pb1 = softmax_tok(1);
-          u32x4 vt = vfrag(0);
-#pragma unroll
-          for (int cb = 0; cb < CB; ++cb) {  // the next fragment is requested before this one's MFMAs; it feeds both
-            const u32x4 cur = vt;           // tokens' MFMAs
-            if (cb + 1 < CB) vt = vfrag(cb + 1);
-            o[0][cb] = mfma16x16x32(cur, pb0, o[0][cb]);
-            o[1][cb] = mfma16x16x32(cur, pb1, o[1][cb]);
-          }
-        }
-        if (more) {
-          // K(i+1) landed (only V(i+1) may still be in flight); every wave is done with V(i) and the partials
-          __builtin_amdgcn_s_waitcnt(waitcnt_imm(4, 0));
-          plain_barrier();
-          if (more2) copy(vb, a.k, kt + 2 * kMq4Keys);  // K(i+2) into V(i)'s buffer
-          const int freed = kb;
-          kb = nk;
-          nk = vb;
-          vb = freed;
-        }
-      }
-    }
-#pragma unroll
-    for (int x = 0; x < 2; ++x) l_own[x] = wave_sum16x4(l_own[x]);
-#pragma unroll
-    for (int x = 0; x < 2; ++x) {
-      if (2 * pair + x >= count) continue;
-      const int t = tp + 2 * pair + x, h = l16;  // lane holds O^T[col 16cb + 4g + r][head l16] of token t
-      const bool any = l_own[x] > 0.f;
-      const float inv = any ? 1.0f / l_own[x] : 0.f;
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int col = col0 + 16 * cb + 4 * g;
-        const floatx4 v = o[x][cb] * inv;
-        if (a.direct)
-          *reinterpret_cast<uint2*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + col) =
-              uint2{pack2(v[0], v[1]), pack2(v[2], v[3])};
-        else
-          *reinterpret_cast<floatx4*>(a.ws_o + (((int64_t)t * S + s) * kHeads + h) * R + col) = v;
-      }
-      if (half == 0 && g == 0) {
-        const float lse = any ? (m_own[x] + log2f(l_own[x])) * kLn2 : -INFINITY;
-        if (kContig)
-          a.lse[((int64_t)(t / a.tok_per_row) * kHeads + h) * a.tok_per_row + t % a.tok_per_row] = lse;
-        else if (a.direct) a.lse[(int64_t)h * a.T + t] = lse;
-        else a.ws_lse[((int64_t)t * S + s) * kHeads + h] = lse;
-      }
-    }
-    tp = te;
-  }
-}
+constexpr bool kKhopReverse = true;     // K-hop forward: token groups dispatched last to first
+constexpr int kKhop1024Tokens = 2;      // tokens per workgroup of the 1024-wide K-hop forward (history_group)
 
 // history_mq5: one workgroup per (group of 8 consecutive tokens, KV slot); each wave owns TPW tokens of the pass
 // and all R latent columns, so its scores need no exchange with another wave: per 32-key tile it computes S^T for
-// its tokens (every K fragment read from LDS feeds their MFMAs), runs the online softmax of history_mq4 and adds
-// V^T P^T. K and V tiles go global -> LDS by direct copies (one row per instruction: half a wave for a 512-byte row,
-// the whole wave for a 1 KB one; wave w copying rows 32 / NW * w ..) into four buffers (K and V of tiles i and i+1);
-// one barrier per tile, after which tile i+2 replaces tile i, so every copy has a tile of time.
+// its tokens (every K fragment read from LDS feeds their MFMAs), runs an online softmax per query row (a row's 32
+// keys sit in 4 lanes; NaN-free max3 chains and permlane swaps for the cross-lane steps; the running maximum is
+// raised lazily, only when a tile exceeds it by more than 2^8; each lane keeps its share of the row sum) and adds
+// V^T P^T with P^T in registers (the score layout is the B-operand layout under a fixed permutation of the 32 keys
+// over the MFMA k index, which the two transposing reads of V^T follow). K and V tiles go global -> LDS by direct
+// copies (global_load_lds_dwordx4, 16 bytes per lane, one row per instruction: half a wave for a 512-byte row, the
+// whole wave for a 1 KB one; wave w copying rows 32 / NW * w ..) into four buffers (K and V of tiles i and i+1);
+// one barrier per tile, after which tile i+2 replaces tile i, so every copy has a tile of time. The copies are
+// waited for explicitly (s_waitcnt vmcnt counting the copies issued after the awaited ones) and the loop
+// synchronizes with plain s_barrier behind those waits, so a copy still in flight for a later tile is never waited
+// for at a barrier.
 //   R = 256: 4 waves of 2 tokens, 74 KB of LDS: two workgroups per CU, whose tiles run out of step;
 //   R = 512: 8 waves of 1 token (the registers hold 16 query rows x 512 columns), 139 KB of LDS.
 constexpr int kMq5Pages = 1024;  // block-table entries of a pass kept in LDS (longer passes read them from memory)
@@ -2203,24 +1633,15 @@ template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
-    if (p.group == 4 && R == 256 && HLA_MQ5 && p.scale_log2 > 0.f)  // mq5 and mq4 fold a positive scale
-      hipLaunchKernelGGL((history_mq5<256, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
-                         dim3(256), 0, stream, p);
-    else if (p.group == 4 && R == 512 && HLA_MQ5_512 && p.scale_log2 > 0.f)
-      hipLaunchKernelGGL((history_mq5<512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
-                         dim3(512), 0, stream, p);
-    else if (p.group == 4 && (R == 512 || R == 256) && HLA_MQ4 && p.scale_log2 > 0.f)
-      hipLaunchKernelGGL((history_mq4<R == 256 ? 256 : 512, 0>), dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits),
-                         dim3(512), 0, stream, p);
-    else if (p.group == 4 && R <= 512 && HLA_MQ_V2)
-      hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
+    if (p.group == 4 && (R == 256 || R == 512) && p.scale_log2 > 0.f)  // history_mq5 folds a positive scale
+      hipLaunchKernelGGL((history_mq5<R == 256 ? 256 : 512, 0>),
+                         dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits), dim3(64 * Mq5Geo<R == 256 ? 256 : 512>::NW),
+                         0, stream, p);
     else if (p.group == 4 && R <= 512)
-      hipLaunchKernelGGL(history_mq<R <= 512 ? R : 512>, grid, dim3(64 * MqGeo<R <= 512 ? R : 512>::NW), 0, stream, p);
-    else if (p.group == 4 && R == 1024)  // four 1024-wide tokens spill registers: two per workgroup run twice as fast
+      hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
+    else  // two tokens per workgroup (four 1024-wide tokens would spill registers and run twice as slow)
       hipLaunchKernelGGL((history_group<R, 2>), dim3((unsigned)((p.T + 1) / 2), p.num_splits), dim3(Geo<R>::THREADS),
                          0, stream, p);
-    else if (p.group == 4) hipLaunchKernelGGL((history_group<R, 4>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
-    else hipLaunchKernelGGL((history_group<R, 2>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   } else {
     const dim3 grid(split_workgroups(p.T, p.num_splits));
     if (p.shared_rows) hipLaunchKernelGGL((history_split<R, false>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
@@ -2325,11 +1746,11 @@ namespace hla {
 int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
                     int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
                     void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream) {
-  // widths 512 and 256 run faster here than in khop_fwd; history_mq4 takes a positive scale and a mask whose rows
+  // widths 512 and 256 run faster here than in khop_fwd; history_mq5 takes a positive scale and a mask whose rows
   // start on 16-byte boundaries (its bytes are copied in 16-byte pieces), history_mq2 (width 512) anything else
-  const bool mq4 = HLA_MQ4 && (width == 512 || width == 256) && scale > 0.f &&
+  const bool mq5 = (width == 512 || width == 256) && scale > 0.f &&
                    (!mask || (((uintptr_t)mask & 15u) == 0 && mask_st % 16 == 0));
-  if (N % kTile != 0 || (width != 1024 && (!HLA_MQ_V2 || !(mq4 || width == 512)))) return HLA_S6_EUNSUPPORTED;
+  if (N % kTile != 0 || (width != 1024 && !(mq5 || width == 512))) return HLA_S6_EUNSUPPORTED;
   HistoryParams p{};
   p.q = static_cast<const uint16_t*>(q);
   p.q_st = q_st;
@@ -2356,23 +1777,19 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.direct = true;
   p.mask = mask;
   p.mask_st = mask_st;
-  p.reverse_groups = HLA_KH_REVERSE;
-  if (width == 1024) {  // four tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
+  p.reverse_groups = kKhopReverse;
+  if (width == 1024) {  // kKhop1024Tokens tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
     p.lse_rows = true;
     p.page_stride = (int64_t)N * k_sn;
-    hipLaunchKernelGGL((history_group<1024, HLA_KH1024_NQ, true>),
-                       dim3((unsigned)((p.T + HLA_KH1024_NQ - 1) / HLA_KH1024_NQ), 1), dim3(Geo<1024>::THREADS), 0,
+    hipLaunchKernelGGL((history_group<1024, kKhop1024Tokens, true>),
+                       dim3((unsigned)((p.T + kKhop1024Tokens - 1) / kKhop1024Tokens), 1), dim3(Geo<1024>::THREADS), 0,
                        stream, p);
-  } else if (mq4) {
-    const dim3 grid4((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
-    if (width == 512 && HLA_MQ5_512 && mask) hipLaunchKernelGGL((history_mq5<512, 2>), grid4, dim3(512), 0, stream, p);
-    else if (width == 512 && HLA_MQ5_512) hipLaunchKernelGGL((history_mq5<512, 1>), grid4, dim3(512), 0, stream, p);
-    else if (width == 512 && mask) hipLaunchKernelGGL((history_mq4<512, 2>), grid4, dim3(512), 0, stream, p);
-    else if (width == 512) hipLaunchKernelGGL((history_mq4<512, 1>), grid4, dim3(512), 0, stream, p);
-    else if (HLA_MQ5 && mask) hipLaunchKernelGGL((history_mq5<256, 2>), grid4, dim3(256), 0, stream, p);
-    else if (HLA_MQ5) hipLaunchKernelGGL((history_mq5<256, 1>), grid4, dim3(256), 0, stream, p);
-    else if (mask) hipLaunchKernelGGL((history_mq4<256, 2>), grid4, dim3(512), 0, stream, p);
-    else hipLaunchKernelGGL((history_mq4<256, 1>), grid4, dim3(512), 0, stream, p);
+  } else if (mq5) {
+    const dim3 grid5((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
+    if (width == 512 && mask) hipLaunchKernelGGL((history_mq5<512, 2>), grid5, dim3(512), 0, stream, p);
+    else if (width == 512) hipLaunchKernelGGL((history_mq5<512, 1>), grid5, dim3(512), 0, stream, p);
+    else if (mask) hipLaunchKernelGGL((history_mq5<256, 2>), grid5, dim3(256), 0, stream, p);
+    else hipLaunchKernelGGL((history_mq5<256, 1>), grid5, dim3(256), 0, stream, p);
   } else {
     const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
     hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p);

@@ -20,12 +20,6 @@
 namespace hla {
 namespace {
 
-#ifndef HLA_KH_DQ4
-#define HLA_KH_DQ4 1  // dq on khop_dq4 (4 tokens per workgroup, direct tile copies) where the shapes allow
-#endif
-#ifndef HLA_KH_DKDV4
-#define HLA_KH_DKDV4 1  // dk / dv on khop_dkdv4 (64-key tiles, tokens streamed by direct copies) where shapes allow
-#endif
 
 constexpr int kKhRows = 32;   // query rows per step (2 tokens x 16 heads)
 constexpr int kKhKeys = 32;   // keys per step
@@ -1154,7 +1148,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
     p.dq = dq;
     p.dq_sb = dq_sb; p.dq_si = dq_si; p.dq_sh = dq_sh;
     // the multi-query form: widths 512 / 256, whole 16-key groups, 16-byte aligned fp32 dq rows and mask rows
-    const bool dq4 = HLA_KH_DQ4 && (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(dq) &&
+    const bool dq4 = (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(dq) &&
                      dq_sb % 4 == 0 && dq_si % 4 == 0 && dq_sh % 4 == 0 &&
                      (!mask || (kh_aligned16(mask) && m_sb % 16 == 0 && m_si % 16 == 0));
     if (dq4) {
@@ -1201,7 +1195,7 @@ extern "C" int hla_s6_khop_backward(const void* q, int64_t q_sb, int64_t q_si, i
     p.dv_sn = split ? width : dv_sn;
     p.dk_ss = p.dv_ss = part;
     // the multi-query form: widths 512 / 256, whole 16-key groups, 16-byte aligned fp32 dk / dv rows and mask rows
-    const bool kv4 = HLA_KH_DKDV4 && (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(p.dk) &&
+    const bool kv4 = (width == 512 || width == 256) && N % 16 == 0 && kh_aligned16(p.dk) &&
                      kh_aligned16(p.dv) && p.dk_sb % 4 == 0 && p.dk_sn % 4 == 0 && p.dv_sb % 4 == 0 &&
                      p.dv_sn % 4 == 0 && (!mask || (kh_aligned16(mask) && m_sb % 16 == 0 && m_si % 16 == 0));
     if (kv4) {

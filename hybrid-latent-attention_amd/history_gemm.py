@@ -5,9 +5,12 @@ kernels of ``khop.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward``, ``hla_
 ``history.hip`` (``hla_s6_masked_history``, the single-query forward).
 
 Every query row ``(b, i, h)`` attends over the latent rows ``k[b, j], v[b, j]`` that ``mask[b, i, j]`` shows (all
-heads share the rows). The kernels compute with bf16 GEMM operands and fp32 accumulation and softmax (the
-reference's ``precision='bf16'`` mode); they derive each query's key bound from the mask, so ``causal`` needs no
-promise and only documents intent. No ``[B, H, Lq, N]`` tensor is ever formed.
+heads share the rows). The kernels compute with bf16 GEMM operands and fp32 accumulation and softmax: the
+reference's ``precision='bf16'`` mode, which callers select explicitly. The reference's default modes (``'fp32'``,
+IEEE fp32 GEMMs, and ``'tf32'``; ``hla/latent/history_gemm.py:19-24,270-271``) and its fp32 CUDA-core ``'triton'``
+backend (``hla/latent/fused_history.py:129-130``) have no kernels here and raise ``ValueError``, so that no call
+narrows its arithmetic without asking. The kernels derive each query's key bound from the mask, so ``causal`` needs
+no promise and only documents intent. No ``[B, H, Lq, N]`` tensor is ever formed.
 """
 from __future__ import annotations
 
@@ -16,7 +19,8 @@ from torch.autograd.function import once_differentiable
 
 from . import _lib, s6_ops
 
-PRECISIONS = ('bf16',)
+PRECISIONS = ('fp32', 'tf32', 'bf16')   # the reference's modes
+KERNEL_PRECISIONS = ('bf16',)          # the modes the HIP kernels compute
 DEFAULT_CHUNK = 128
 DEFAULT_MAX_ELEMENTS = 1 << 26
 KEY_ALIGN = 16
@@ -30,35 +34,14 @@ def bf16_fp32_output_supported(device) -> bool:
     return True
 
 
-def _round_up(value: int, multiple: int) -> int:
-    return -(-value // multiple) * multiple
-
-
-def chunk_plan(Lq: int, N: int, batch: int, heads: int, *, causal: bool, chunk: int,
-               max_elements: int = DEFAULT_MAX_ELEMENTS, padded_keys: int | None = None, align: int = 1):
-    """``(start, end, key_end)`` query chunks of the reference's chunked GEMM (``history_gemm.py:109-130``): with
-    ``causal`` a chunk ending at ``end`` needs keys ``< end - 1 + N - Lq`` rounded up to ``align``. The HIP kernels
-    do not chunk (each query's bound comes from the mask); the plan is kept for callers that size work with it."""
-    total = N if padded_keys is None else padded_keys
-    shift = N - Lq
-    rows = max(1, min(chunk, max_elements // max(1, batch * heads * total)))
-    for start in range(0, Lq, rows):
-        end = min(Lq, start + rows)
-        if causal:
-            needed = end - 1 + shift
-            key_end = min(total, _round_up(needed, align)) if needed > 0 else 0
-        else:
-            key_end = total
-        yield start, end, key_end
-
-
-def causal_mask_is_consistent(mask: torch.Tensor) -> bool:
-    """True when ``mask [B, Lq, N]`` shows no key at or after the query position ``i + N - Lq``."""
-    B, Lq, N = mask.shape
-    shift = N - Lq
-    forbidden = (torch.arange(N, device=mask.device)[None, :]
-                 >= torch.arange(Lq, device=mask.device)[:, None] + shift)
-    return not bool((mask.bool() & forbidden[None]).any())
+def _check_precision(precision):
+    """``ValueError`` unless ``precision`` is a mode the kernels compute (the reference's message for unknown modes,
+    ``hla/latent/history_gemm.py:287-288``; a clear refusal for its fp32 / tf32 modes)."""
+    if precision not in PRECISIONS:
+        raise ValueError(f'Unknown precision {precision!r}; expected one of {PRECISIONS}')
+    if precision not in KERNEL_PRECISIONS:
+        raise ValueError(f'precision={precision!r} has no MI355X kernel: the HIP kernels compute with bf16 operands '
+                         f'and fp32 accumulation; pass precision="bf16"')
 
 
 def _bf16_rows(name, t):
@@ -154,14 +137,15 @@ def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv, b
     return dq, dk, dv
 
 
-def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHUNK, precision='bf16',
+def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHUNK, precision='fp32',
                         max_elements=DEFAULT_MAX_ELEMENTS):
     """Causal history attention (``hla/latent/history_gemm.py:270-294``).
 
     q: [B, Lq, 16, R], k: [B, N, R], v: [B, N, R], mask: [B, Lq, N] (True = visible). Returns z [B, Lq, 16, R] in
     q.dtype and lse [B, 16, Lq] (fp32, -inf on rows with no visible history, where z is 0); differentiable in q, k
-    and v. ``causal`` asks for the reference's promise check only; ``chunk`` and ``max_elements`` are accepted for
-    signature parity (the kernels do not chunk).
+    and v. ``precision`` must be ``'bf16'`` (bf16 operands, fp32 accumulation); the reference's default ``'fp32'``
+    and ``'tf32'`` raise ``ValueError``. ``causal`` asks for the reference's promise check only; ``chunk`` and
+    ``max_elements`` are accepted for signature parity (the kernels do not chunk).
     """
     if q.ndim != 4 or k.ndim != 3 or v.ndim != 3 or mask.ndim != 3:
         raise ValueError(f'Expected Q[B,Lq,H,R], K[B,N,R], V[B,N,Rv], mask[B,Lq,N], got '
@@ -173,9 +157,7 @@ def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHU
         raise ValueError('Inconsistent history attention shapes')
     if causal and N < Lq:
         raise ValueError('Causal history requires at least as many keys as queries')
-    if precision not in PRECISIONS:
-        raise ValueError(f'Unsupported precision {precision!r}: the MI355X kernels compute with bf16 operands and '
-                         f'fp32 accumulation (precision="bf16")')
+    _check_precision(precision)
     if chunk < 1 or max_elements < 1:
         raise ValueError('chunk and max_elements must be positive')
     if H != HEADS or v.shape[-1] != Rk or Rk not in FORWARD_WIDTHS:
@@ -255,15 +237,23 @@ def history_attention(q, k, v, mask, scale, reference_forward=False):
     return _History.apply(q, k, v, mask, float(scale))
 
 
-HISTORY_BACKENDS = ('triton', 'gemm', 'hip')
+HISTORY_BACKENDS = ('triton', 'reference', 'gemm')
 
 
-def causal_history_attention(q, k, v, mask, scale, reference_forward=False, *, backend='gemm', precision='bf16',
+def causal_history_attention(q, k, v, mask, scale, reference_forward=False, *, backend='triton', precision='fp32',
                              chunk=None, causal=False):
-    """``hla/latent/fused_history.py:126-153`` with every backend name served by the one HIP path (``'reference'``,
-    the dense torch autograd form, belongs to the tests)."""
+    """``hla/latent/fused_history.py:129-153``: ``backend='gemm'`` runs ``causal_history_gemm`` with ``precision``
+    (``'bf16'``: the HIP kernels). The reference's default ``'triton'`` backend (fp32 CUDA-core kernels) and its
+    ``'reference'`` backend (dense fp32 torch autograd) compute in fp32, which no kernel here does: both raise
+    ``ValueError`` rather than run at bf16."""
+    if q.ndim != 4 or k.ndim != 3 or v.ndim != 3 or mask.ndim != 3:
+        raise ValueError(f'Expected Q[B,Lq,H,R], K/V[B,N,R], mask[B,Lq,N], got {tuple(q.shape)}, {tuple(k.shape)}, '
+                         f'{tuple(v.shape)}, {tuple(mask.shape)}')
     if backend not in HISTORY_BACKENDS:
         raise ValueError(f'Unknown causal history backend {backend!r}; expected one of {HISTORY_BACKENDS}')
+    if backend != 'gemm':
+        raise ValueError(f'backend={backend!r} computes in fp32, which has no MI355X kernel: use backend="gemm", '
+                         f'precision="bf16" (bf16 MFMA operands, fp32 accumulation)')
     return causal_history_gemm(q, k, v, mask, scale, causal=causal, chunk=chunk or DEFAULT_CHUNK,
                                precision=precision)
 

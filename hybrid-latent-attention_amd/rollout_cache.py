@@ -1,12 +1,12 @@
 """The ``s6-rollout-cache-v1`` snapshot of one finished request: every layer's committed latent rows, gathered
-from the paged caches through the request's block lists before vLLM reuses the blocks, written as one file, and
-read back with the reference's guards for training replay.
+from the paged caches through the request's block lists before vLLM reuses the blocks, written as one file for
+training replay.
 
-Writer: ``hla/vllm_latent/cache_export.py:159-188`` (``RolloutCacheExporter.export``); reader:
-``hla/latent/history_snapshot.py:55-105`` (``validate_snapshot``, ``load_rollout_snapshot``). The file is a
-``torch.save`` dict ``{schema, version, request_id, cfg, prompt_ids, length, first_response_logits, rows}`` with
-``rows`` a tuple of per-layer ``[1, length, 2r + 2r1]`` tensors in the packed row layout of
-``hla/latent/register.py:73-79``, readable with ``torch.load(weights_only=True)``.
+Writer: ``hla/vllm_latent/cache_export.py:159-188`` (``RolloutCacheExporter.export``). The file is a ``torch.save``
+dict ``{schema, version, request_id, cfg, prompt_ids, length, first_response_logits, rows}`` with ``rows`` a tuple of
+per-layer ``[1, length, 2r + 2r1]`` tensors in the packed row layout of ``hla/latent/register.py:73-79``, readable
+with ``torch.load(weights_only=True)``; the training side reads it with its own loader
+(``hla/latent/history_snapshot.py:78-105``), which is not part of this package.
 
 On MI355X the gather of all layers is ONE HIP launch (``hla_s6_gather_packed_rows``) into a device buffer, followed
 by one device-to-host copy into pinned memory; the per-layer rows of the file are views of that one host buffer.
@@ -17,14 +17,12 @@ from __future__ import annotations
 
 import os
 import time
-from dataclasses import dataclass
 
 import torch
 
 from . import _lib, s6_ops
 
 SCHEMA = 's6-rollout-cache-v1'
-SNAPSHOT_SCHEMA = 's6-khop-snapshot-v1'
 
 
 class PackedRowGather:
@@ -121,73 +119,3 @@ def export_request(path, layer_caches, main_blocks, l1_blocks, length, *, versio
                             length=length, first_response_logits=first_response_logits)
     record['seconds'] = time.perf_counter() - tick
     return record
-
-
-@dataclass
-class HistorySnapshot:
-    """The fields of ``hla/latent/history_snapshot.py:16-26``."""
-    rows: tuple
-    positions: torch.Tensor
-    prompt_length: int
-    response_length: int
-    first_response_logits: torch.Tensor
-    dtype: torch.dtype
-    source: str = 'reference_collect'
-    schema: str = SNAPSHOT_SCHEMA
-
-
-def validate_snapshot(snapshot, student):
-    """The layout guards of ``hla/latent/history_snapshot.py:55-75``."""
-    cfg = student.cfg
-    if snapshot.schema != SNAPSHOT_SCHEMA or snapshot.source not in ('reference_collect', 'vllm_rollout'):
-        raise ValueError('Unsupported history snapshot schema or source')
-    if snapshot.prompt_length < 1 or snapshot.response_length < 1:
-        raise ValueError('Snapshot prompt/response must be nonempty')
-    length = snapshot.prompt_length + snapshot.response_length - 1
-    width = cfg['rank'] + cfg['rank_v'] + 2 * cfg['rank1']
-    if len(snapshot.rows) != cfg['num_layers']:
-        raise ValueError('Snapshot layer count differs from the student')
-    for row in snapshot.rows:
-        if tuple(row.shape) != (1, length, width):
-            raise ValueError('Snapshot row layout differs from packed S6 ranks')
-        if row.dtype != snapshot.dtype:
-            raise ValueError('Snapshot dtype is not uniform across layers')
-    if tuple(snapshot.positions.shape) != (length,) or \
-            not bool((snapshot.positions == torch.arange(length, device=snapshot.positions.device)).all()):
-        raise ValueError('Snapshot positions are not contiguous absolute indices')
-    if snapshot.first_response_logits.ndim != 3 or tuple(snapshot.first_response_logits.shape[:2]) != (1, 1):
-        raise ValueError('Snapshot must keep exactly the first response logits')
-    return snapshot
-
-
-def load_rollout_snapshot(trajectory, student):
-    """Load one request's rows with the staleness / alignment guards of ``hla/latent/history_snapshot.py:78-105``
-    (same checks, same messages); ``trajectory`` carries ``ids [1, L]``, ``prompt``, ``version``,
-    ``history_ref``, ``request_id`` and ``truncated``."""
-    ref = trajectory.history_ref
-    if not ref or ref.get('version') != trajectory.version or ref.get('request_id') != trajectory.request_id:
-        raise ValueError('Missing, stale or mismatched rollout cache reference')
-    data = torch.load(ref['path'], map_location='cpu', weights_only=True)
-    length = trajectory.ids.shape[1] - 1
-    if data.get('schema') != SCHEMA or data.get('version') != trajectory.version or \
-            data.get('request_id') != trajectory.request_id or data.get('cfg') != student.cfg:
-        raise ValueError('Rollout snapshot schema/version/request/config mismatch')
-    response_length = trajectory.ids.shape[1] - trajectory.prompt
-    if data.get('length') != length or ref.get('length') != length:
-        raise ValueError(f'Rollout cache length mismatch: exported {data.get("length")}, '
-                         f'reference {ref.get("length")}, trajectory needs {length} '
-                         f'(request {trajectory.request_id}, prompt {trajectory.prompt}, '
-                         f'response {response_length}, truncated {getattr(trajectory, "truncated", False)})')
-    if data.get('prompt_ids') != trajectory.ids[0, :trajectory.prompt].tolist():
-        raise ValueError(f'Rollout cache prompt tokens differ from the trajectory '
-                         f'(request {trajectory.request_id})')
-    if ref.get('token_ids') != trajectory.ids[0].tolist():
-        raise ValueError(f'Rollout cache token ids differ from the trajectory '
-                         f'(request {trajectory.request_id})')
-    device = trajectory.ids.device
-    rows = tuple(row.to(device) for row in data['rows'])
-    snapshot = HistorySnapshot(rows=rows, positions=torch.arange(length, device=device),
-                               prompt_length=trajectory.prompt, response_length=response_length,
-                               first_response_logits=data['first_response_logits'].to(device),
-                               dtype=rows[0].dtype, source='vllm_rollout')
-    return validate_snapshot(snapshot, student)

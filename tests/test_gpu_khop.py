@@ -54,7 +54,7 @@ def run(q, k, v, mask, scale, need_grad=True, dz=None, dlse=None):
     dev = lambda x, grad: torch.tensor(x, device='cuda').to(torch.bfloat16).requires_grad_(grad)
     qt, kt, vt = dev(q, need_grad), dev(k, need_grad), dev(v, need_grad)
     mt = torch.tensor(mask, device='cuda')
-    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale, causal=True)
+    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale, causal=True, precision='bf16')
     out = {'z': z.detach().float().cpu().numpy(), 'lse': lse.detach().cpu().numpy()}
     if need_grad:
         dzt = torch.tensor(dz, device='cuda').to(torch.bfloat16)
@@ -129,7 +129,7 @@ def test_mask_rows_off_16_byte_boundaries_and_no_mask(R):
     qt, kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (q, k, v))
     mt = torch.tensor(wide, device='cuda')[..., :N]
     assert mt.stride(1) % 16 != 0
-    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale)
+    z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale, precision='bf16')
     zo, lo = O.causal_history(q, k, v, mask, scale)
     assert_attention_close(z.float().cpu().numpy(), zo, 'z (strided mask)')
     assert_lse_close(lse.cpu().numpy(), lo)
@@ -173,7 +173,7 @@ def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
     qt = torch.tensor(q, device='cuda').to(torch.bfloat16).requires_grad_(True)
     kt = torch.tensor(k, device='cuda').to(torch.bfloat16)
     vt = torch.tensor(v, device='cuda').to(torch.bfloat16)
-    z, lse = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), 0.1)
+    z, lse = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), 0.1, precision='bf16')
     (gq,) = torch.autograd.grad((z.float() * torch.tensor(dz, device='cuda')).sum()
                                 + torch.where(torch.isfinite(lse), lse * torch.tensor(dlse, device='cuda'), 0.).sum(),
                                 [qt])
@@ -202,7 +202,7 @@ def test_fp32_inputs_and_transposed_query_view():
     q = torch.randn(B, 16, L, R, device='cuda').transpose(1, 2)
     k, v = torch.randn(B, L, R, device='cuda'), torch.randn(B, L, R, device='cuda')
     mask = torch.tensor(benchmark_mask([L, 20], L), device='cuda')
-    z, lse = hg.causal_history_gemm(q, k, v, mask, 0.125, causal=True)
+    z, lse = hg.causal_history_gemm(q, k, v, mask, 0.125, causal=True, precision='bf16')
     assert z.dtype == torch.float32 and lse.shape == (B, 16, L)
     qn, kn, vn = (bf16.round_bf16(t.contiguous().cpu().numpy()) for t in (q, k, v))
     zo, lo = O.causal_history(qn, kn, vn, mask.cpu().numpy(), 0.125)
@@ -216,13 +216,24 @@ def test_rejects_unsupported_shapes_and_precision():
     k = torch.zeros(1, 4, 1024, device='cuda', dtype=torch.bfloat16)
     m = torch.ones(1, 4, 4, dtype=torch.bool, device='cuda')
     with pytest.raises(ValueError, match='widths'):
-        hg.causal_history_gemm(q[..., :768], k[..., :768], k[..., :768], m, 1.0)
+        hg.causal_history_gemm(q[..., :768], k[..., :768], k[..., :768], m, 1.0, precision='bf16')
     with pytest.raises(ValueError, match='multiple of 16'):   # width 1024 takes whole 16-key groups
-        hg.causal_history_gemm(q, k, k, m, 1.0)
-    with pytest.raises(ValueError, match='precision'):
-        hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0, precision='fp32')
+        hg.causal_history_gemm(q, k, k, m, 1.0, precision='bf16')
+    for precision in ('fp32', 'tf32'):    # the reference's fp32 modes (fp32 is its default) have no kernel here
+        with pytest.raises(ValueError, match='no MI355X kernel'):
+            hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0, precision=precision)
+    with pytest.raises(ValueError, match='no MI355X kernel'):
+        hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0)
+    with pytest.raises(ValueError, match='Unknown precision'):
+        hg.causal_history_gemm(q[..., :256], k[..., :256], k[..., :256], m, 1.0, precision='fp16')
+    for backend in ('triton', 'reference'):
+        with pytest.raises(ValueError, match='fp32'):
+            hg.causal_history_attention(q[..., :256], k[..., :256], k[..., :256], m, 1.0, backend=backend)
+    z, _ = hg.causal_history_attention(q[..., :256], k[..., :256], k[..., :256], m, 1.0, backend='gemm',
+                                       precision='bf16')
+    assert z.shape == (1, 4, 16, 256)
     with pytest.raises(ValueError, match='Inconsistent'):
-        hg.causal_history_gemm(q[..., :256], k[..., :256], k[:, :3, :256], m, 1.0)
+        hg.causal_history_gemm(q[..., :256], k[..., :256], k[:, :3, :256], m, 1.0, precision='bf16')
 
 
 @pytest.mark.parametrize('kind,B,Lq,N', [('benchmark', 2, 48, 48), ('khop', 2, 19, 64), ('any', 3, 29, 96)])
@@ -240,7 +251,7 @@ def test_width_1024_forward_matches_the_oracle(kind, B, Lq, N):
     assert (got['z'][empty] == 0).all() and np.isneginf(got['lse'].transpose(0, 2, 1)[empty]).all()
     qt = torch.tensor(q, device='cuda').to(torch.bfloat16).requires_grad_(True)
     kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (k, v))
-    zt, lt = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), scale)
+    zt, lt = hg.causal_history_gemm(qt, kt, vt, torch.tensor(mask, device='cuda'), scale, precision='bf16')
     with pytest.raises(ValueError, match='forward only'):
         torch.autograd.grad(zt.float().sum(), [qt])
 
@@ -256,8 +267,8 @@ def test_transposed_query_view_of_the_reference_benchmark():
     assert qv.stride(0) != L * qv.stride(1)
     kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (k, v))
     mt = torch.tensor(mask, device='cuda')
-    z1, l1 = hg.causal_history_gemm(qt, kt, vt, mt, scale)
-    z2, l2 = hg.causal_history_gemm(qv, kt, vt, mt, scale)
+    z1, l1 = hg.causal_history_gemm(qt, kt, vt, mt, scale, precision='bf16')
+    z2, l2 = hg.causal_history_gemm(qv, kt, vt, mt, scale, precision='bf16')
     assert torch.equal(z1, z2) and torch.equal(l1, l2)
 
 
@@ -274,7 +285,7 @@ def test_bf16_gradients_are_the_rounded_fp32_gradients(R, B, Lq, N, kind):
     grads = {}
     for dt in (torch.float32, torch.bfloat16):
         leaves = [torch.tensor(x, device='cuda').to(torch.bfloat16).to(dt).requires_grad_(True) for x in (q, k, v)]
-        z, lse = hg.causal_history_gemm(*leaves, mt, 0.08)
+        z, lse = hg.causal_history_gemm(*leaves, mt, 0.08, precision='bf16')
         grads[dt] = torch.autograd.grad([z, lse], leaves, [dz.to(dt), dl])
     for name, g32, g16 in zip('qkv', grads[torch.float32], grads[torch.bfloat16]):
         assert g16.dtype == torch.bfloat16
