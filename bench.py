@@ -5,7 +5,9 @@ One step = the attention path of one full S6 decode step: 24 layers x 4 loops, e
 (A_t GEMM + latent RoPE), the exact window over the last 32 tokens plus the current one, the paged latent history
 (loop 0 reads the 256-wide loop-1 latent, loops 1-3 the 512-wide main latent), the B_t projection and the LSE merge.
 Inputs are synthetic and random-init, resident in HBM before timing; the whole step is captured once in a HIP graph
-and replayed. Prints one JSON line (the value is microseconds per layer = step time / 24; lower is better).
+and replayed. Prints one JSON line (the value is microseconds per layer = step time / 24; lower is better); its
+"configs" key holds the same measurement of the other configurations (B=32 ragged contexts, B=8 at context 32768,
+and chunked prefill of 4 requests x 3 and x 512 tokens on 8192 latent rows), each with its roofline fraction.
 """
 from __future__ import annotations
 
@@ -58,6 +60,9 @@ def parse():
                    help='only run a plain 1 GiB device copy three times (scales the FETCH_SIZE / WRITE_SIZE counters '
                         'of a PMC profile to bytes)')
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--no-secondary', action='store_true',
+                   help='decode: skip the other configurations (ragged, long context, multi-query Q=3 and Q=512) '
+                        'that the default run appends to the headline line under "configs"')
     p.add_argument('--seed', type=int, default=0)
     p.add_argument('--table', choices=('random', 'identity'), default='random',
                    help='latent block tables: a random permutation of the page pool, or pages in order')
@@ -299,21 +304,71 @@ def cpu_baseline(wl, sample=8):
                       f'history rows read and x(1 + 3) loops; extrapolated'}
 
 
-def secondary(args, wl, B, context, layers, queries, splits):
-    """One JSON line for the ragged / long-context / multi-query workloads (not the headline metric)."""
-    ms = time_graph(wl.step, args.steps, args.warmup)
+def secondary_metrics(kind, wl, B, context, layers, queries, splits, steps, warmup):
+    """Step time and roofline fractions of a ragged / long-context / multi-query workload (HIP-graph replay)."""
+    ms = time_graph(wl.step, steps, warmup)
     us_layer = ms * 1000 / layers
     hist_bytes, flops = wl.history_bytes_per_layer(), wl.history_flops_per_layer()
     gbps, tflops = hist_bytes / (us_layer * 1e3), flops / (us_layer * 1e6)
-    out = {'workload': args.workload, 'value': round(us_layer, 2), 'unit': 'us/layer', 'B': B, 'queries': queries,
-           'context': context, 'contexts': wl.hist if args.workload == 'ragged' else None, 'layers': layers,
-           'loops': LOOPS, 'kv_splits': splits, 'steps': args.steps, 'ms_per_step': round(ms, 4),
-           'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
-           'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
-           'history_tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
-           'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True,
-           'cpu_baseline': None if args.no_cpu_baseline else cpu_baseline(wl)}
+    return {'workload': kind, 'value': round(us_layer, 2), 'unit': 'us/layer', 'B': B, 'queries': queries,
+            'context': context, 'contexts': wl.hist if kind == 'ragged' else None, 'layers': layers,
+            'loops': LOOPS, 'kv_splits': splits, 'steps': steps, 'ms_per_step': round(ms, 4),
+            'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
+            'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
+            'history_tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
+            'bound': 'mfma' if kind == 'prefill' and queries >= 64 else 'hbm',
+            'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True}
+
+
+def secondary(args, wl, B, context, layers, queries, splits):
+    """One JSON line for the ragged / long-context / multi-query workloads (not the headline metric)."""
+    out = secondary_metrics(args.workload, wl, B, context, layers, queries, splits, args.steps, args.warmup)
+    out['cpu_baseline'] = None if args.no_cpu_baseline else cpu_baseline(wl)
     print(json.dumps(out), flush=True)
+
+
+# The other benchmark configurations measured by the default run (name: workload, B, context, layers, queries)
+SECONDARY = (('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, LAYERS, 1),
+             ('long_b8_ctx32768', 'long', 8, 32768, 1, 1),
+             ('prefill_b4_q3_ctx8192', 'prefill', 4, 8192, 1, 3),
+             ('prefill_b4_q512_ctx8192', 'prefill', 4, 8192, 1, 512))
+
+
+def workload_shape(kind, B, context, queries, seed):
+    """History lengths of the requests of a workload and whether its steps take the multi-query kernels."""
+    if kind == 'ragged':
+        hist = np.random.default_rng(seed).integers(1024, context + 1, B).tolist()
+    elif kind == 'prefill':
+        hist = [context + WINDOW] * B                          # `context` latent rows + the exact window
+    else:
+        hist = [context] * B
+    return hist, (4 if queries >= 16 else 1)                   # the step's history_group (StepContext)
+
+
+def build_workload(ops, layer, kind, B, context, layers, queries, seed, device, cus, splits_override=0,
+                   table='random'):
+    hist, group = workload_shape(kind, B, context, queries, seed)
+    splits = {w: splits_override or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w,
+                                                         tokens_per_group=group)
+              for w in (RANK, RANK1)}
+    print(f'bench: building workload {kind} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
+          f'splits={splits} cus={cus}', file=sys.stderr, flush=True)
+    wl = Workload(ops, layer, hist, queries, splits, seed, device, table, layers)
+    torch.cuda.synchronize()
+    return wl, splits
+
+
+def measure_secondaries(ops, layer, args, device, cus):
+    """The ragged, long-context and both multi-query configurations, one after another (each workload freed before
+    the next is built): a dict of their metrics for the headline line."""
+    out = {}
+    for name, kind, B, context, layers, queries in SECONDARY:
+        wl, splits = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus)
+        out[name] = secondary_metrics(kind, wl, B, context, layers, queries, splits, args.steps, args.warmup)
+        del wl
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
 
 
 HIDDEN = 2048
@@ -637,20 +692,8 @@ def main():
                 'prefill': (4, 8192, 1)}[args.workload]
     B, context, layers = args.batch or defaults[0], args.context or defaults[1], args.layers or defaults[2]
     queries = args.queries if args.workload == 'prefill' else 1
-    if args.workload == 'ragged':
-        hist = np.random.default_rng(args.seed).integers(1024, context + 1, B).tolist()
-    elif args.workload == 'prefill':
-        hist = [context + WINDOW] * B                          # `context` latent rows + the exact window
-    else:
-        hist = [context] * B
-    group = 4 if queries >= 16 else 1                        # the step's history_group (StepContext)
-    splits = {w: args.splits or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w,
-                                                     tokens_per_group=group)
-              for w in (RANK, RANK1)}
-    print(f'bench: building workload {args.workload} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
-          f'splits={splits} cus={cus}', file=sys.stderr, flush=True)
-    wl = Workload(ops, layer, hist, queries, splits, args.seed, device, args.table, layers)
-    torch.cuda.synchronize()
+    wl, splits = build_workload(ops, layer, args.workload, B, context, layers, queries, args.seed, device, cus,
+                                args.splits, args.table)
     if args.workload != 'decode' and not args.kernel_only:
         return secondary(args, wl, B, context, layers, queries, splits)
 
@@ -672,6 +715,13 @@ def main():
     if not args.no_cpu_baseline:
         print('bench: cpu baseline', file=sys.stderr, flush=True)
         base = cpu_baseline(wl)
+    others = None
+    if not args.no_secondary:
+        del wl
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        print('bench: the other configurations', file=sys.stderr, flush=True)
+        others = measure_secondaries(ops, layer, args, device, cus)
     result = {
         'metric': METRIC, 'value': round(us_layer, 3), 'unit': 'us/layer', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': False, 'scaling': 'weak',
@@ -689,6 +739,7 @@ def main():
                      'us_per_launch': round(op_us, 2), 'algorithmic_bytes_per_launch': op_bytes,
                      'reduce_us_per_launch': round(reduce_us, 2)},
         'cpu_baseline': base,
+        'configs': others,
     }
     print(json.dumps(result), flush=True)
 

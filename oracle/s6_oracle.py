@@ -450,3 +450,118 @@ def rel_l2(a, b):
     a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
     den = math.sqrt(float((b * b).sum()))
     return math.sqrt(float(((a - b) ** 2).sum())) / (den if den > 0 else 1.0)
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# HF rolling engine: one softmax over latent history blocks and the exact current chunk, with its gradient
+# ----------------------------------------------------------------------------------------------------------------
+
+def hf_rope(x, cos, sin):
+    """``x cos + rotate_half(x) sin`` with cos / sin ``[B, n, w]`` broadcast over the heads of ``x [B, H, n, w]``;
+    follows ``apply_rope`` (``hla/latent/register.py:19-20``)."""
+    return x * cos[:, None] + rotate_half(x) * sin[:, None]
+
+
+def hf_rope_backward(dy, cos, sin):
+    """Cotangent of ``x`` for ``y = hf_rope(x, cos, sin)``: ``dy cos + R^T (dy sin)`` where ``R = rotate_half``
+    (``R [a, b] = [-b, a]``, so ``R^T [u, w] = [w, -u]``)."""
+    u = dy * sin[:, None]
+    a, b = np.split(u, 2, axis=-1)
+    return dy * cos[:, None] + np.concatenate((b, -a), -1)
+
+
+def rope_latent_tables(cos, sin, width):
+    """The teacher's cos / sin ``[..., d]`` re-indexed for a latent of ``width`` columns: pair ``i`` takes frequency
+    ``i % (d / 2)``, both halves alike; follows ``rope_latent`` (``hla/latent/register.py:23-25``)."""
+    idx = np.arange(width // 2) % (cos.shape[-1] // 2)
+    return (np.concatenate((cos[..., idx], cos[..., idx]), -1), np.concatenate((sin[..., idx], sin[..., idx]), -1))
+
+
+def _mixed_parts(q, k, v, cos, sin, valid, hist_k, hist_v, masks, A, scale, dtype):
+    f = lambda x: np.asarray(x, dtype)
+    q, k, v, cos, sin = f(q), f(k), f(v), f(cos), f(sin)
+    n = q.shape[2]
+    qr, kr = hf_rope(q, cos, sin), hf_rope(k, cos, sin)
+    valid = np.asarray(valid, bool)
+    visible = (valid[:, None, None, :] & np.tril(np.ones((n, n), bool))) | ~valid[:, None, :, None]
+    scores = []
+    qc = None
+    if hist_k:
+        r = hist_k[0].shape[-1]
+        c_r, s_r = rope_latent_tables(cos, sin, r)
+        qc = hf_rope(np.einsum('bhid,hdr->bhir', q, f(A)), c_r, s_r)
+        for ck, m in zip(hist_k, masks):
+            s = np.einsum('bhir,bjr->bhij', qc, f(ck)) * dtype(scale)
+            scores.append(np.where(np.asarray(m, bool)[:, None, None, :], s, -np.inf))
+    scores.append(np.where(visible, np.einsum('bhid,bhjd->bhij', qr, kr) * dtype(scale), -np.inf))
+    s = np.concatenate(scores, -1)
+    peak = s.max(-1, keepdims=True)
+    p = np.exp(s - peak)
+    p = p / p.sum(-1, keepdims=True)
+    return qr, kr, qc, p
+
+
+def mixed_attention(q, k, v, cos, sin, valid, hist_k, hist_v, masks, A, B, scale, dtype=np.float64):
+    """One softmax over ``[latent scores of every history block || causal exact scores of the chunk]``; follows
+    ``mixed_attention`` (``hla/latent/batched_engine.py:154-182``) without its bf16 rounding points.
+
+    q, k, v ``[B, H, n, d]`` (pre-RoPE q and k), cos / sin ``[B, n, d]``, valid ``[B, n]``; ``hist_k`` / ``hist_v``
+    the history blocks' latent K / V fields ``[B, N_k, r]`` (``LatentLayer.fields``) with ``masks`` ``[B, N_k]``;
+    ``A [H, d, r]`` / ``B [H, r, d]`` the loop's readers. Valid queries see the chunk's valid keys up to their own
+    position and the visible rows of every block; an invalid query sees every key of the chunk. Returns
+    ``[B, H, n, d]``: ``P_chunk v + (sum_k P_k cv_k) B``."""
+    _, _, _, p = _mixed_parts(q, k, v, cos, sin, valid, hist_k, hist_v, masks, A, scale, dtype)
+    n = q.shape[2]
+    out = p[..., -n:] @ np.asarray(v, dtype)
+    if hist_k:
+        z, off = 0, 0
+        for cv in hist_v:
+            w = cv.shape[1]
+            z = z + np.einsum('bhij,bjr->bhir', p[..., off:off + w], np.asarray(cv, dtype))
+            off += w
+        out = out + np.einsum('bhir,hrd->bhid', z, np.asarray(B, dtype))
+    return out
+
+
+def mixed_attention_backward(q, k, v, cos, sin, valid, hist_k, hist_v, masks, A, B, scale, dout, dtype=np.float64):
+    """Gradients of ``sum(mixed_attention(...) * dout)`` with respect to ``q, k, v``, every block's ``hist_k`` /
+    ``hist_v`` and the readers ``A``, ``B``: a dict ``{q, k, v, hist_k: [...], hist_v: [...], A, B}`` (``A`` / ``B``
+    None without history). Softmax backward over the concatenated scores (``dS = P (dP - sum(P dP))``), then the
+    chain through the products, the latent query absorption and both RoPEs."""
+    f = lambda x: np.asarray(x, dtype)
+    qr, kr, qc, p = _mixed_parts(q, k, v, cos, sin, valid, hist_k, hist_v, masks, A, scale, dtype)
+    g = f(dout)
+    n = q.shape[2]
+    widths = [ck.shape[1] for ck in hist_k]
+    offs = np.cumsum([0] + widths)
+    p_cur = p[..., -n:]
+    dp_cur = np.einsum('bhid,bhjd->bhij', g, f(v))
+    res = {'v': np.einsum('bhij,bhid->bhjd', p_cur, g), 'hist_k': [], 'hist_v': [], 'A': None, 'B': None}
+    dps = []
+    if hist_k:
+        z = sum(np.einsum('bhij,bjr->bhir', p[..., offs[i]:offs[i + 1]], f(cv)) for i, cv in enumerate(hist_v))
+        dz = np.einsum('bhid,hrd->bhir', g, f(B))
+        res['B'] = np.einsum('bhir,bhid->hrd', z, g)
+        for i, cv in enumerate(hist_v):
+            pk = p[..., offs[i]:offs[i + 1]]
+            dps.append(np.einsum('bhir,bjr->bhij', dz, f(cv)))
+            res['hist_v'].append(np.einsum('bhij,bhir->bjr', pk, dz))
+    dp = np.concatenate(dps + [dp_cur], -1)
+    ds = p * (dp - (p * dp).sum(-1, keepdims=True)) * dtype(scale)
+    ds_cur = ds[..., -n:]
+    dqr = np.einsum('bhij,bhjd->bhid', ds_cur, kr)
+    res['k'] = hf_rope_backward(np.einsum('bhij,bhid->bhjd', ds_cur, qr), f(cos), f(sin))
+    dq = hf_rope_backward(dqr, f(cos), f(sin))
+    if hist_k:
+        r = hist_k[0].shape[-1]
+        c_r, s_r = rope_latent_tables(f(cos), f(sin), r)
+        dqc = 0
+        for i, ck in enumerate(hist_k):
+            dsk = ds[..., offs[i]:offs[i + 1]]
+            dqc = dqc + np.einsum('bhij,bjr->bhir', dsk, f(ck))
+            res['hist_k'].append(np.einsum('bhij,bhir->bjr', dsk, qc))
+        dpre = hf_rope_backward(dqc, c_r, s_r)
+        dq = dq + np.einsum('bhir,hdr->bhid', dpre, f(A))
+        res['A'] = np.einsum('bhid,bhir->hdr', f(q), dpre)
+    res['q'] = dq
+    return res

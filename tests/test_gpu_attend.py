@@ -92,7 +92,8 @@ def test_config1_single_decode(ops, layer):
 @pytest.mark.parametrize('rows,splits', [(8, 1), (8, 8), (8, 64), (8, 300), (40, 24)])
 def test_ragged_batch_all_loops(ops, layer, rows, splits):
     """Ragged decode rows (one without history, one with history inside the window only, two padding tokens);
-    slot counts from one to more than the rows' chunks, with one and four tokens per epilogue workgroup."""
+    slot counts from one to more than the rows' chunks. These steps have fewer than 64 rows, so the epilogue runs
+    one token per workgroup; steps of 64 rows or more (four tokens per workgroup) are in test_gpu_configs.py."""
     rng = np.random.default_rng(1 + splits + rows)
     history = rng.integers(1024, 4096, rows)
     history[2], history[5] = 0, 20                       # no history at all; history inside the window only

@@ -1,12 +1,12 @@
 """The HF rolling engine's joint attention (``batched_engine.mixed_attention``, hla/latent/batched_engine.py:154-182)
-with the latent history on the K-hop kernels, against a float32 torch restatement of the reference's dense joint
-softmax (one softmax over the concatenated [history block scores || causal current scores], probabilities times the
-latent values, then the B reader), outputs and gradients.
+with the latent history on the K-hop kernels, against the oracle's float64 joint softmax (``O.mixed_attention``, one
+softmax over the concatenated [history block scores || causal current scores]) and its gradient
+(``O.mixed_attention_backward``), both pinned on the CPU by per-query brute force and finite differences.
 
-Bars: outputs of valid queries within the attention tolerance (max-abs 2e-2, rel-L2 5e-3) of the float32 form;
-gradients of q, k, v and the packed history rows within relative L2 2e-2 (bf16 operands of every kernel product).
-The latent module is a stand-in with the shapes and field layout of ``register.LatentLayer`` (q absorption, latent
-RoPE by ``rope_latent``, packed rows ``[K 512 | V 512 | K1 256 | V1 256]``).
+Bars: outputs of valid queries within the attention tolerance (max-abs 2e-2, rel-L2 5e-3) of the oracle;
+gradients of q, k, v, the packed history rows and the A / B readers within relative L2 2e-2 (bf16 operands of every
+kernel product). The latent module is a stand-in with the shapes and field layout of ``register.LatentLayer`` (q
+absorption, latent RoPE by ``rope_latent``, packed rows ``[K 512 | V 512 | K1 256 | V1 256]``).
 """
 import importlib
 import math
@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import s6_oracle as O
 from s6util import assert_attention_close, rel_l2
 
 pytestmark = pytest.mark.gpu
@@ -38,13 +39,6 @@ class Latent:
         self.A = [w(HEADS, HD, RANK1)] + [w(HEADS, HD, RANK) for _ in range(3)]
         self.B = [w(HEADS, RANK1, HD)] + [w(HEADS, RANK, HD) for _ in range(3)]
 
-    def cast(self, dtype):
-        other = Latent.__new__(Latent)
-        other.head_dim = HD
-        other.A = [a.to(dtype) for a in self.A]
-        other.B = [b.to(dtype) for b in self.B]
-        return other
-
     def readers(self, loop):
         return self.A[loop], self.B[loop], RANK1 if loop == 0 else RANK
 
@@ -59,34 +53,6 @@ class Latent:
             row = packed[..., 2 * RANK:]
             return row[..., :RANK1], row[..., RANK1:]
         return packed[..., :RANK], packed[..., RANK:2 * RANK]
-
-
-def reference(sl, loop, q, k, v, cos, sin, valid, blocks, masks):
-    """The reference's dense form in float32: one softmax over [block scores..., current scores]."""
-    scale = 1 / math.sqrt(HD)
-    qr, kr = be.apply_rope(q, cos, sin), be.apply_rope(k, cos, sin)
-    n = valid.shape[1]
-    visible = valid[:, None, None, :] & torch.ones(n, n, device='cuda', dtype=torch.bool).tril()
-    visible = visible | ~valid[:, None, :, None]
-    current = (qr @ kr.transpose(-1, -2).contiguous()) * scale
-    scores, values = [], []
-    qc = sl.query(loop, q, cos, sin)
-    for block, mask in zip(blocks, masks):
-        ck, cv = sl.fields(loop, block)
-        s = torch.matmul(qc, ck.transpose(-1, -2).contiguous()[:, None]) * scale
-        scores.append(s.masked_fill(~mask[:, None, None, :], float('-inf')))
-        values.append(cv)
-    scores.append(current.masked_fill(~visible, float('-inf')))
-    probs = torch.softmax(torch.cat(scores, -1), -1)
-    out = probs[..., -n:] @ v
-    if blocks:
-        z, off = 0, 0
-        for cv in values:
-            w = cv.shape[1]
-            z = z + torch.matmul(probs[..., off:off + w], cv[:, None])
-            off += w
-        out = out + torch.matmul(z, sl.readers(loop)[1][None])
-    return out
 
 
 def rope_tables(B, n, start, gen):
@@ -118,27 +84,44 @@ def make_case(seed, B, n, sizes, loop, valid_kind):
     return Latent(gen, torch.bfloat16), q, k, v, cos, sin, valid, blocks, masks
 
 
+def f64(t):
+    return t.detach().double().cpu().numpy()
+
+
 @pytest.mark.parametrize('loop', [0, 2])
 @pytest.mark.parametrize('B,n,sizes,valid_kind', [(2, 16, (160,), 'all'), (3, 9, (64, 48), 'left'),
                                                   (2, 33, (96, 37), 'holes'), (2, 7, (), 'left')])
-def test_mixed_attention_matches_the_dense_joint_softmax(loop, B, n, sizes, valid_kind):
+def test_mixed_attention_matches_the_oracle(loop, B, n, sizes, valid_kind):
     sl, q, k, v, cos, sin, valid, blocks, masks = make_case(11 * n + loop, B, n, sizes, loop, valid_kind)
-    leaves = [q, k, v, *blocks]
-    ours = [x.clone().requires_grad_(True) for x in leaves]
-    ref = [x.float().clone().requires_grad_(True) for x in leaves]
+    print(f'case loop={loop} B={B} n={n} blocks={sizes} valid={valid_kind}', flush=True)
+    ours = [x.clone().requires_grad_(True) for x in (q, k, v, *blocks)]
+    sl.A[loop].requires_grad_(True)
+    sl.B[loop].requires_grad_(True)
     out = be.mixed_attention(sl, loop, *ours[:3], cos, sin, valid, tuple(ours[3:]), tuple(masks))
-    want = reference(sl.cast(torch.float32), loop, *ref[:3], cos, sin, valid, tuple(ref[3:]), tuple(masks))
     assert out.dtype == torch.bfloat16 and out.shape == (B, HEADS, n, HD)
+    fields = [sl.fields(loop, f64(blk)) for blk in blocks]
+    args = (f64(q), f64(k), f64(v), f64(cos), f64(sin), valid.cpu().numpy(), [a for a, _ in fields],
+            [b for _, b in fields], [m.cpu().numpy() for m in masks], f64(sl.A[loop]), f64(sl.B[loop]), 1 / math.sqrt(HD))
+    want = O.mixed_attention(*args)
     vq = valid.cpu().numpy()
     got_v = out.detach().float().cpu().numpy().transpose(0, 2, 1, 3)[vq]
-    want_v = want.detach().cpu().numpy().transpose(0, 2, 1, 3)[vq]
-    assert_attention_close(got_v, want_v, 'mixed attention')
+    assert_attention_close(got_v, want.transpose(0, 2, 1, 3)[vq], 'mixed attention')
     g = torch.randn(out.shape, generator=torch.Generator(device='cuda').manual_seed(5), device='cuda')
     g = g * valid[:, None, :, None]                             # the loss reads valid queries only
-    grads = torch.autograd.grad(out.float(), ours, g)
-    wants = torch.autograd.grad(want, ref, g)
-    for name, a, b in zip(['q', 'k', 'v'] + [f'block{i}' for i in range(len(blocks))], grads, wants):
-        a, b = a.float().cpu().numpy(), b.cpu().numpy()
+    leaves = ours + ([sl.A[loop], sl.B[loop]] if blocks else [])
+    grads = torch.autograd.grad(out.float(), leaves, g)
+    wants = O.mixed_attention_backward(*args, f64(g))
+    packed = []                                                 # block gradients: the loop's K / V fields of the rows
+    for i, blk in enumerate(blocks):
+        dblk = np.zeros(blk.shape)
+        dk_, dv_ = sl.fields(loop, dblk)
+        dk_[...] = wants['hist_k'][i]
+        dv_[...] = wants['hist_v'][i]
+        packed.append(dblk)
+    want_list = [wants['q'], wants['k'], wants['v'], *packed] + ([wants['A'], wants['B']] if blocks else [])
+    names = ['q', 'k', 'v'] + [f'block{i}' for i in range(len(blocks))] + (['A', 'B'] if blocks else [])
+    for name, a, b in zip(names, grads, want_list):
+        a = a.double().cpu().numpy()
         assert np.isfinite(a).all(), name
         r = rel_l2(a, b)
         assert r <= 2e-2, f'{name}: rel-L2 {r:.3e}'

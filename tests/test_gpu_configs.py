@@ -1,0 +1,160 @@
+"""GPU parity of the decode step at the benchmark configurations' full shapes, against the oracle composite
+(``O.attend_decode``: exact window + current token, paged latent history, B_t, LSE merge), all four loops of a layer:
+
+* the headline step: 64 decode rows at context 8192 (+ 2 padding rows), 16 slots per row at width 512 and 32 at
+  256 (the MI355X split policy at 64 rows, the bench's split plan), which runs the four-token epilogue;
+* long context: 8 rows at context 32768, the history split over 8, 16 and 32 slots and the MI355X policy
+  (128 / 256);
+* ragged decode: 32 rows with contexts drawn from U[1024, 8192] on 65,536-page pools (2 GiB main latent, 1 GiB
+  loop-1 latent: page ids up to 65,535, byte offsets past 2^31).
+
+Caches live on the device; page 0 and every page no request references are +inf-poisoned, so a read outside a row's
+pages cannot go unseen. The oracle reads host copies of the referenced pages only (through a remapped table).
+Bars: max-abs 2e-2 and rel-L2 5e-3 against the fp32 oracle; padding rows exactly zero."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import s6_oracle as O
+from s6util import FakeLatentLayer, assert_attention_close, host_f32
+
+pytestmark = pytest.mark.gpu
+H, D, W, BLOCK = 16, 128, 32, 16
+SCALE = 1 / math.sqrt(D)
+WIDTHS = (512, 256)
+POS_INF = float('inf')
+
+
+class DeviceDecode:
+    """A decode step of ``len(hist)`` requests (one token each, ``pad`` padding tokens) with caches on the device:
+    per width one latent cache of ``pool`` pages whose tables are slices of one random permutation, one small exact
+    cache per loop holding the window pages, random readers of all four loops."""
+
+    def __init__(self, hist, pad=0, pool=None, seed=0):
+        g = torch.Generator(device='cuda').manual_seed(seed)
+        self.hist = np.asarray(hist, np.int64)
+        self.R, self.T = len(hist), len(hist) + pad
+        self.seq = self.hist + 1                                   # the current token is already in the exact cache
+        pages = -(-self.seq // BLOCK)
+        self.cols = int(pages.max())
+        self.pool = int(pool or pages.sum() + 1)
+        assert self.pool > pages.sum()
+        randn = lambda *s, std=1.0: (torch.randn(*s, generator=g, device='cuda') * std).to(torch.bfloat16)
+        self.tables, self.lat = {}, {}
+        for w in WIDTHS:
+            perm = (torch.randperm(self.pool - 1, generator=g, device='cuda') + 1).to(torch.int32).cpu().numpy()
+            table = np.zeros((self.R, self.cols), np.int32)
+            used = 0
+            for r in range(self.R):
+                table[r, :pages[r]] = perm[used:used + pages[r]]
+                used += pages[r]
+            cache = torch.empty(self.pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device='cuda').normal_(generator=g)
+            referenced = torch.zeros(self.pool, dtype=torch.bool, device='cuda')
+            referenced[torch.as_tensor(perm[:used], device='cuda').long()] = True
+            cache[~referenced] = POS_INF                           # page 0 and every unreferenced page
+            self.tables[w], self.lat[w] = table, cache
+        first, last = np.maximum(self.seq - 1 - W, 0) // BLOCK, (self.seq - 1) // BLOCK
+        ex_pool = int((last - first + 1).sum()) + 1
+        self.ex_table = np.zeros((self.R, self.cols), np.int32)
+        perm = np.random.default_rng(seed).permutation(np.arange(1, ex_pool)).astype(np.int32)
+        used = 0
+        for r in range(self.R):
+            n = int(last[r] - first[r] + 1)
+            self.ex_table[r, first[r]:last[r] + 1] = perm[used:used + n]
+            used += n
+        self.exact = []
+        for _ in range(4):
+            ex = randn(ex_pool, H, BLOCK, 2 * D)
+            ex[0] = POS_INF
+            self.exact.append(ex)
+        std = 1 / math.sqrt(2048)
+        self.sl = FakeLatentLayer(randn(H, D, 256, std=std), randn(H, 256, D, std=std), randn(3, H, D, 512, std=std),
+                                  randn(3, H, 512, D, std=std))
+        self.q_lat = [randn(self.T, H, 256 if loop == 0 else 512, std=(256 if loop == 0 else 512) ** -0.5)
+                      for loop in range(4)]
+        self.q_rope = [randn(self.T, H, D) for _ in range(4)]
+        self.dev_tables = {w: torch.as_tensor(t, device='cuda') for w, t in self.tables.items()}
+        self.dev_ex_table = torch.as_tensor(self.ex_table, device='cuda')
+
+    def context(self, layer, ops, splits_by_width):
+        positions = np.concatenate((self.hist, np.ones(self.T - self.R, np.int64)))
+        ws = ops.S6Workspace.for_splits(H, self.T, splits_by_width)
+        return layer.StepContext(torch.as_tensor(positions, device='cuda'),
+                                 torch.arange(self.R + 1, dtype=torch.int32, device='cuda'),
+                                 torch.as_tensor(self.seq.astype(np.int32), device='cuda'), 1, self.T, {}, SCALE,
+                                 ops.HIP_BACKENDS, ws, splits_by_width[512], window=W,
+                                 max_seqlen_k=int(self.seq.max()), kv_splits_by_width=splits_by_width)
+
+    def run(self, layer, ctx, loop):
+        w = 256 if loop == 0 else 512
+        return layer.attend(self.sl, loop, self.q_lat[loop], self.q_rope[loop], None, None, self.lat[w],
+                            self.dev_tables[w], None, None, ctx, (self.exact[loop], self.dev_ex_table))
+
+    def oracle(self, loop):
+        """O.attend_decode on host copies of the pages the rows reference (the table remapped to them)."""
+        w = 256 if loop == 0 else 512
+        table = self.tables[w]
+        ctx_lat = np.maximum(self.hist - W, 0)
+        need = -(-ctx_lat // BLOCK)
+        used = np.unique(np.concatenate([table[r, :need[r]] for r in range(self.R)] + [np.zeros(1, np.int32)]))
+        remap = np.zeros(self.pool, np.int64)
+        remap[used] = np.arange(used.size)
+        lat = self.lat[w][torch.as_tensor(used, device='cuda').long()].float().cpu().numpy()
+        tok_table = np.zeros((self.T, self.cols), np.int64)
+        tok_table[:self.R] = remap[table]
+        ctx_lat_t = np.zeros(self.T, np.int64)
+        ctx_lat_t[:self.R] = ctx_lat
+        ex = host_f32(self.exact[loop])
+        B = host_f32(self.sl.readers(loop)[1])
+        invalid = np.arange(self.T) >= self.R
+        return O.attend_decode(host_f32(self.q_lat[loop]), host_f32(self.q_rope[loop]), B, lat[..., :w], lat[..., w:],
+                               tok_table, ctx_lat_t, ex[..., :D], ex[..., D:], self.ex_table,
+                               np.arange(self.R + 1), self.seq, W, SCALE, invalid, rounding=False)
+
+
+def _check(case, layer, ops, splits_by_width, loops=range(4), wants=None):
+    ctx = case.context(layer, ops, splits_by_width)
+    wants = {} if wants is None else wants
+    for loop in loops:
+        print(f'case R={case.R} T={case.T} loop={loop} splits={splits_by_width}', flush=True)
+        out = host_f32(case.run(layer, ctx, loop))
+        if loop not in wants:
+            wants[loop] = case.oracle(loop)
+        assert_attention_close(out[:case.R], wants[loop][:case.R], f'loop {loop}')
+        assert (out[case.R:] == 0).all()
+    return wants
+
+
+@pytest.mark.parametrize('pad', [0, 2])
+def test_headline_decode_step(ops, layer, pad):
+    """64 rows at context 8192 (8160 latent rows + the 32-row window + the current token), all four loops, with the
+    split counts the bench runs; 64 rows or more take the four-token epilogue."""
+    cus = 256
+    splits = {w: ops.mi355x_kv_splits(8193, 64, cus, width=w) for w in WIDTHS}
+    assert splits == {512: 16, 256: 32}
+    case = DeviceDecode([8192] * 64, pad=pad, seed=30 + pad)
+    assert case.T >= 64
+    _check(case, layer, ops, splits)
+
+
+def test_long_context_split_counts(ops, layer):
+    """8 rows at context 32768; the same step over 8, 16 and 32 slots per row and the MI355X policy (128 / 256)."""
+    case = DeviceDecode([32768] * 8, pad=1, seed=40)
+    policy = {w: ops.mi355x_kv_splits(32769, 8, 256, width=w) for w in WIDTHS}
+    assert policy == {512: 128, 256: 256}
+    wants = None
+    for splits in ({512: 8, 256: 8}, {512: 16, 256: 16}, {512: 32, 256: 32}, policy):
+        wants = _check(case, layer, ops, splits, wants=wants)
+
+
+def test_ragged_decode_on_full_pools(ops, layer):
+    """32 rows with contexts from U[1024, 8192] whose tables are slices of one permutation of a 65,536-page pool
+    (the benchmark's pools: 2 GiB main latent, 1 GiB loop-1 latent), all four loops, the MI355X policy."""
+    hist = np.random.default_rng(50).integers(1024, 8193, 32)
+    case = DeviceDecode(hist, pad=2, pool=65536, seed=50)
+    assert case.lat[512].numel() * 2 == 2 << 30 and case.lat[256].numel() * 2 == 1 << 30
+    assert max(int(case.tables[w].max()) for w in WIDTHS) > 65000
+    splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
+    _check(case, layer, ops, splits)

@@ -100,6 +100,43 @@ def _table(layer, width, rows=4096, theta=1e6):
     return layer.latent_rope_table(rows, inv, width, torch.bfloat16)
 
 
+def _bf16_ulp(x):
+    """Spacing of bf16 values at |x| (8 significant bits), in float64."""
+    a = np.maximum(np.abs(np.asarray(x, np.float64)), 2.0 ** -126)
+    return 2.0 ** (np.floor(np.log2(a)) - 7)
+
+
+@pytest.mark.parametrize('width', [512, 256])
+def test_latent_rope_table_on_the_device(layer, width):
+    """The persistent [65536, w] bf16 table built on the device (hla/vllm_latent/s6_layer.py:16-29) against the
+    oracle's. The frequencies come from torch's fp32 pow, as the reference's do; they must lie within 2 fp32 ulp of
+    the correctly rounded theta^(-2i/128). Given the frequencies, the fp32 angles are IEEE products; cos / sin of the
+    same fp32 angle differ between math libraries by about an fp32 ulp, which moves a bf16 rounding in a few entries
+    in 10^5, so every entry must lie within one bf16 ulp of the float64 cos / sin of the fp32 angle and at least
+    99.99 % of the entries must equal the oracle's table (built from the same frequencies) bit for bit. Row 0 is
+    exactly [1 ... 1 | 0 ... 0] (hla/tests/test_s6_ops.py:36)."""
+    inv = layer.latent_inv_freq(128, 1e6)
+    inv_h = inv.numpy()
+    exact_inv = (1.0 / (1e6 ** (np.arange(0, 128, 2) / 128.0))).astype(np.float32)
+    assert inv_h.dtype == np.float32 and np.abs(inv_h.view(np.int32) - exact_inv.view(np.int32)).max() <= 2
+    table = layer.latent_rope_table(65536, inv.to(CUDA), width, torch.bfloat16)
+    inv_o = inv_h
+    assert table.shape == (65536, width) and table.dtype == torch.bfloat16
+    got = host_f32(table)
+    want = bf16.round_bf16(O.latent_rope_table(65536, inv_o, width))
+    idx = np.arange(width // 2) % 64
+    angle = np.arange(65536, dtype=np.float32)[:, None] * inv_o[idx][None, :]
+    exact = np.concatenate((np.cos(angle.astype(np.float64)), np.sin(angle.astype(np.float64))), -1)
+    assert (got[0, :width // 2] == 1).all() and (got[0, width // 2:] == 0).all()
+    err = np.abs(got.astype(np.float64) - exact)
+    bad = err > _bf16_ulp(exact) + 2.0 ** -20
+    assert not bad.any(), f'{int(bad.sum())} entries more than one bf16 ulp off, first at {np.argwhere(bad)[:3].tolist()}'
+    same = float((got == want).mean())
+    assert same >= 0.9999, f'only {same:.6f} of the entries equal the oracle table'
+    # the pairing: column c and c + w/2 hold cos and sin of the same angle (frequency c % 64)
+    np.testing.assert_allclose(got[:, :width // 2] ** 2 + got[:, width // 2:] ** 2, 1.0, atol=2e-2)
+
+
 @pytest.mark.parametrize('width', [512, 256])
 def test_latent_rope_layouts_bit_exact(ops, layer, width):
     rng = np.random.default_rng(4)

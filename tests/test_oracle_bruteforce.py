@@ -516,3 +516,250 @@ def test_single_history_matches_per_row_softmax_and_its_gradient():
             num[idx] = (objective(*a) - objective(*m)) / (2 * eps)
         np.testing.assert_allclose(g, num, rtol=1e-6, atol=1e-7, err_msg='qkv'[pos])
     assert (grads[0][0] == 0).all()
+
+
+# ---------------------------------------------------------------------------------------------- prefill / mixed composite
+
+def _chunk_case(seed=13):
+    """Three requests of a prefill / mixed step (a chunk after history, a decode row, a fresh prompt) plus two
+    padding tokens, on tiny shapes with distinct latent and exact page tables."""
+    rng = np.random.default_rng(seed)
+    H, d, r, block, W = 2, 8, 12, 4, 3
+    lens, hist = np.array([4, 1, 3]), np.array([11, 5, 0])
+    qsl = np.concatenate(([0], np.cumsum(lens))).astype(np.int32)
+    T = int(qsl[-1]) + 2
+    seq = (hist + lens).astype(np.int32)
+    req, valid, ctx, ctx_lat = O.step_context(qsl, seq, T, W)
+    lat = rng.standard_normal((40, 1, block, 2 * r)).astype(np.float32)
+    ex = rng.standard_normal((40, H, block, 2 * d)).astype(np.float32)
+    lat[0] = INF
+    ex[0] = INF                                     # the null page: any read past a row's pages is loud
+    lt = np.stack([rng.permutation(np.arange(1, 40))[:5] for _ in range(3)]).astype(np.int32)
+    et = np.stack([rng.permutation(np.arange(1, 40))[:5] for _ in range(3)]).astype(np.int32)
+    f = lambda *s: rng.standard_normal(s).astype(np.float32)
+    case = dict(q_lat=f(T, H, r), q_rope=f(T, H, d), k_rope=f(T, H, d), v=f(T, H, d), B=f(H, r, d), lat=lat, ex=ex,
+                lt=lt, et=et, req=req, valid=valid, ctx=ctx, ctx_lat=ctx_lat, qsl=qsl, W=W, scale=0.35, r=r, d=d,
+                block=block, H=H, T=T)
+    return case
+
+
+def _attend_chunk(c):
+    r, d = c['r'], c['d']
+    return O.attend_chunk(c['q_lat'], c['q_rope'], c['k_rope'], c['v'], c['B'], c['lat'][..., :r], c['lat'][..., r:],
+                          {'latent': c['lt'][c['req']], 'exact': c['et'][c['req']]}, c['ctx'], c['ctx_lat'], c['qsl'],
+                          c['W'], c['scale'], ~c['valid'], c['ex'][..., :d], c['ex'][..., d:], rounding=False,
+                          dtype=np.float64)
+
+
+def _check_attend_chunk(out, c):
+    """One float64 softmax per (token, head) over the union of its keys: the causal chunk of its request, the exact
+    window rows [ctx - W, ctx) of the exact cache, and the latent rows [0, ctx - W) read through B[h]."""
+    r, d, block, s = c['r'], c['d'], c['block'], c['scale']
+    for t in range(c['T']):
+        if not c['valid'][t]:
+            assert (out[t] == 0).all()
+            continue
+        rq, n = int(c['req'][t]), int(c['ctx'][t])
+        for h in range(c['H']):
+            scores, vals = [], []
+            for u in range(int(c['qsl'][rq]), t + 1):
+                scores.append(float(c['k_rope'][u, h].astype(np.float64) @ c['q_rope'][t, h]) * s)
+                vals.append(c['v'][u, h].astype(np.float64))
+            for p in range(max(0, n - c['W']), n):
+                row = c['ex'][c['et'][rq, p // block], h, p % block].astype(np.float64)
+                scores.append(float(row[:d] @ c['q_rope'][t, h]) * s)
+                vals.append(row[d:])
+            for j in range(max(0, n - c['W'])):
+                row = c['lat'][c['lt'][rq, j // block], 0, j % block].astype(np.float64)
+                scores.append(float(row[:r] @ c['q_lat'][t, h]) * s)
+                vals.append(row[r:] @ c['B'][h].astype(np.float64))
+            want, _ = _softmax64(np.array(scores), np.array(vals))
+            np.testing.assert_allclose(out[t, h], want, rtol=1e-6, atol=1e-6)
+
+
+def test_attend_chunk_is_one_joint_softmax():
+    """The prefill / mixed branch of attend (hla/vllm_latent/s6_layer.py:101-115): causal chunk + exact window over
+    history rows [ctx - W, ctx) + latent history [0, ctx - W) through B_t equal one softmax over all of them."""
+    c = _chunk_case()
+    assert c['ctx'].tolist()[:8] == [11, 11, 11, 11, 5, 0, 0, 0] and c['ctx_lat'].tolist()[:5] == [8] * 4 + [2]
+    _check_attend_chunk(_attend_chunk(c), c)
+
+
+def test_attend_chunk_planted_mistakes_fail(monkeypatch):
+    """Plausible wiring mistakes inside the composite, planted in the oracle one at a time, fail the pin."""
+    c = _chunk_case()
+    real = {name: getattr(O, name) for name in ('window_history', 'history_attention', 'chunk_attention', 'absorb')}
+
+    def window_on_latent_ctx(q, k, v, table, ctx, *a, **kw):          # ctx_latent handed to the window
+        return real['window_history'](q, k, v, table, np.maximum(ctx - c['W'], 0), *a, **kw)
+
+    def history_over_ctx(q, k, v, table, ctx, *a, **kw):              # latent rows overlap the exact window
+        return real['history_attention'](q, k, v, table, np.where(ctx > 0, ctx + c['W'], 0), *a, **kw)
+
+    def window_shifted(q, k, v, table, ctx, *a, **kw):                # window one row early
+        return real['window_history'](q, k, v, table, np.maximum(ctx - 1, 0), *a, **kw)
+
+    def chunk_not_causal(q, k, v, qsl, invalid, scale, rounding=False, dtype=np.float32):
+        qsl_all = np.array([0, q.shape[0]])                             # every token sees the whole step
+        return real['chunk_attention'](q, k, v, qsl_all, invalid, scale, rounding, dtype)
+
+    def readout_heads_swapped(x, w, *a, **kw):
+        return real['absorb'](x, w[::-1], *a, **kw)
+
+    for name, fn in (('window_history', window_on_latent_ctx), ('history_attention', history_over_ctx),
+                     ('window_history', window_shifted), ('chunk_attention', chunk_not_causal),
+                     ('absorb', readout_heads_swapped)):
+        monkeypatch.setattr(O, name, fn)
+        with pytest.raises(AssertionError):
+            _check_attend_chunk(_attend_chunk(c), c)
+        monkeypatch.setattr(O, name, real[name])
+    _check_attend_chunk(_attend_chunk(c), c)
+
+
+# ---------------------------------------------------------------------------------------------- HF engine joint softmax
+
+def _rotate_pairs(x, cos_pair, sin_pair):
+    """Rotation of the pairs (c, c + w/2) of x by the angles whose cos / sin are given per pair (explicit loop)."""
+    w = x.shape[-1]
+    y = np.empty(w)
+    for c in range(w // 2):
+        a, b = x[c], x[c + w // 2]
+        y[c] = a * cos_pair[c] - b * sin_pair[c]
+        y[c + w // 2] = b * cos_pair[c] + a * sin_pair[c]
+    return y
+
+
+def _mixed_case(seed, B=2, H=2, n=5, d=4, r=6, sizes=(6, 3)):
+    rng = np.random.default_rng(seed)
+    f = lambda *s: rng.standard_normal(s)
+    q, k, v = f(B, H, n, d), f(B, H, n, d), f(B, H, n, d)
+    pos = rng.integers(0, 50, B)[:, None] + np.arange(n)[None]
+    inv = 1.0 / (100.0 ** (np.arange(0, d, 2) / d))
+    ang = pos[..., None] * inv                                       # [B, n, d/2]
+    cos, sin = np.concatenate((np.cos(ang),) * 2, -1), np.concatenate((np.sin(ang),) * 2, -1)
+    valid = np.ones((B, n), bool)
+    valid[0, :2] = False                                             # left padding
+    hist_k = [f(B, N, r) for N in sizes]
+    hist_v = [f(B, N, r) for N in sizes]
+    masks = [rng.random((B, N)) < 0.7 for N in sizes]
+    if masks:
+        masks[0][1] = False                                          # a row that sees nothing of a block
+    A, Bw = f(H, d, r) * 0.5, f(H, r, d) * 0.5
+    return dict(q=q, k=k, v=v, cos=cos, sin=sin, valid=valid, hist_k=hist_k, hist_v=hist_v, masks=masks, A=A, B=Bw,
+                scale=0.6, ang=ang)
+
+
+def _mixed(c, **over):
+    c = dict(c, **over)
+    return O.mixed_attention(c['q'], c['k'], c['v'], c['cos'], c['sin'], c['valid'], c['hist_k'], c['hist_v'],
+                             c['masks'], c['A'], c['B'], c['scale'])
+
+
+def _check_mixed(out, c):
+    """Per (b, h, i): one float64 softmax over the block rows the query's mask shows (latent query q A rotated pair
+    by pair with teacher frequency c % (d/2), values through B[h]) and the chunk keys it sees (RoPE'd q / k)."""
+    q, k, v, ang, valid, s = c['q'], c['k'], c['v'], c['ang'], c['valid'], c['scale']
+    Bn, H, n, d = q.shape
+    half = d // 2
+    for b in range(Bn):
+        for h in range(H):
+            for i in range(n):
+                qr = _rotate_pairs(q[b, h, i], np.cos(ang[b, i]), np.sin(ang[b, i]))
+                scores, vals = [], []
+                for ck, cv, m in zip(c['hist_k'], c['hist_v'], c['masks']):
+                    r = ck.shape[-1]
+                    idx = np.arange(r // 2) % half
+                    qc = _rotate_pairs(q[b, h, i] @ c['A'][h], np.cos(ang[b, i, idx]), np.sin(ang[b, i, idx]))
+                    for j in range(ck.shape[1]):
+                        if m[b, j]:
+                            scores.append(float(qc @ ck[b, j]) * s)
+                            vals.append(cv[b, j] @ c['B'][h])
+                for j in range(n):
+                    if (valid[b, i] and valid[b, j] and j <= i) or not valid[b, i]:
+                        kr = _rotate_pairs(k[b, h, j], np.cos(ang[b, j]), np.sin(ang[b, j]))
+                        scores.append(float(qr @ kr) * s)
+                        vals.append(v[b, h, j])
+                want, _ = _softmax64(np.array(scores), np.array(vals))
+                np.testing.assert_allclose(out[b, h, i], want, rtol=1e-9, atol=1e-9)
+
+
+@pytest.mark.parametrize('sizes', [(6, 3), (), (4,)])
+def test_mixed_attention_is_one_softmax_per_query(sizes):
+    """The HF rolling engine's joint attention (hla/latent/batched_engine.py:154-182) against explicit per-query
+    softmaxes (padding queries see the whole chunk; rows a block hides are skipped)."""
+    c = _mixed_case(21 + len(sizes), sizes=sizes)
+    _check_mixed(_mixed(c), c)
+
+
+def test_mixed_attention_planted_mistakes_fail(monkeypatch):
+    c = _mixed_case(22)
+    real_tables, real_rope = O.rope_latent_tables, O.hf_rope
+
+    def tables_clamped(cos, sin, width):                             # pairs past d/2 reuse the last frequency
+        idx = np.minimum(np.arange(width // 2), cos.shape[-1] // 2 - 1)
+        return np.concatenate((cos[..., idx],) * 2, -1), np.concatenate((sin[..., idx],) * 2, -1)
+
+    def rope_wrong_sign(x, cos, sin):
+        return x * cos[:, None] - O.rotate_half(x) * sin[:, None]
+
+    for name, fn in (('rope_latent_tables', tables_clamped), ('hf_rope', rope_wrong_sign)):
+        monkeypatch.setattr(O, name, fn)
+        with pytest.raises(AssertionError):
+            _check_mixed(_mixed(c), c)
+    monkeypatch.setattr(O, 'rope_latent_tables', real_tables)
+    monkeypatch.setattr(O, 'hf_rope', real_rope)
+    with pytest.raises(AssertionError):                               # a block's mask ignored
+        _check_mixed(_mixed(c, masks=[np.ones_like(m) for m in c['masks']]), c)
+    with pytest.raises(AssertionError):                               # padding queries limited to valid keys
+        _check_mixed(_mixed(c, valid=np.ones_like(c['valid'])), c)
+
+
+def _fd_check(c, grads, eps=1e-6, tol=1e-6):
+    """Central finite differences of sum(out * g) for every element of every differentiable input."""
+    g = c['g']
+    loss = lambda cc: float((_mixed(cc) * g).sum())
+    leaves = {'q': c['q'], 'k': c['k'], 'v': c['v'], 'A': c['A'], 'B': c['B']}
+    for i in range(len(c['hist_k'])):
+        leaves[f'hist_k{i}'] = c['hist_k'][i]
+        leaves[f'hist_v{i}'] = c['hist_v'][i]
+    for name, x in leaves.items():
+        want = grads[name[:6]][int(name[6:])] if name.startswith('hist') else grads[name]
+        got = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            old = x[idx]
+            x[idx] = old + eps
+            up = loss(c)
+            x[idx] = old - eps
+            down = loss(c)
+            x[idx] = old
+            got[idx] = (up - down) / (2 * eps)
+        np.testing.assert_allclose(want, got, rtol=tol, atol=tol, err_msg=name)
+
+
+def test_mixed_attention_backward_is_the_gradient():
+    c = _mixed_case(23, n=4, sizes=(5, 3))
+    c['g'] = np.random.default_rng(3).standard_normal(c['q'].shape)
+    grads = O.mixed_attention_backward(c['q'], c['k'], c['v'], c['cos'], c['sin'], c['valid'], c['hist_k'],
+                                       c['hist_v'], c['masks'], c['A'], c['B'], c['scale'], c['g'])
+    _fd_check(c, grads)
+    c0 = _mixed_case(24, n=3, sizes=())                               # no history: A and B have no gradient
+    c0['g'] = np.random.default_rng(4).standard_normal(c0['q'].shape)
+    g0 = O.mixed_attention_backward(c0['q'], c0['k'], c0['v'], c0['cos'], c0['sin'], c0['valid'], [], [], [], c0['A'],
+                                    c0['B'], c0['scale'], c0['g'])
+    assert g0['A'] is None and g0['B'] is None
+    g0['A'], g0['B'] = np.zeros_like(c0['A']), np.zeros_like(c0['B'])
+    _fd_check(c0, g0)
+
+
+def test_mixed_attention_backward_planted_mistake_fails(monkeypatch):
+    c = _mixed_case(25, n=3, sizes=(4,))
+    c['g'] = np.random.default_rng(5).standard_normal(c['q'].shape)
+
+    def rope_backward_untransposed(dy, cos, sin):                      # R instead of R^T
+        return dy * cos[:, None] + O.rotate_half(dy * sin[:, None])
+
+    monkeypatch.setattr(O, 'hf_rope_backward', rope_backward_untransposed)
+    grads = O.mixed_attention_backward(c['q'], c['k'], c['v'], c['cos'], c['sin'], c['valid'], c['hist_k'],
+                                       c['hist_v'], c['masks'], c['A'], c['B'], c['scale'], c['g'])
+    with pytest.raises(AssertionError):
+        _fd_check(c, grads)
