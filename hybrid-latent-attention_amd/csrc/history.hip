@@ -23,6 +23,8 @@
 // For the fused decode step the split workgroups of a token also compute its exact decode window (exact.h), the
 // heads spread over the splits, so history and window attention run in one launch; decode_epilogue then reduces
 // the split partials, applies B_t and merges with the window in a second one.
+#include <mutex>
+
 #include "exact.h"
 
 namespace hla {
@@ -1975,7 +1977,10 @@ extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t
   return check_launch("split_plan");
 }
 
-extern "C" int hla_s6_attend_decode(
+namespace hla {
+namespace {
+// The fused decode attention of one layer x loop behind hla_s6_attend_decode and hla_s6_attend_decode_static.
+int attend_decode(
     const void* q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void* lat_k, const void* lat_v,
     int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size, int64_t lat_num_blocks,
     const int32_t* lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols, const int64_t* token_requests,
@@ -1985,8 +1990,8 @@ extern "C" int hla_s6_attend_decode(
     const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
     int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
     int32_t num_splits, float* workspace, int64_t workspace_floats, const int32_t* plan, int64_t plan_len,
-    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
-  using namespace hla;
+    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh,
+    hipStream_t st) {
   HistoryParams p;
   int rc = fill_history(p, q_lat, num_tokens, num_heads, width, ql_st, ql_sh, lat_k, lat_v, lat_page_stride,
                         lat_row_stride, block_size, lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols,
@@ -2028,7 +2033,6 @@ extern "C" int hla_s6_attend_decode(
   HLA_REQUIRE((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && b_sh % 2 == 0 && b_sr % 2 == 0 &&
                   (reinterpret_cast<uintptr_t>(out) & 3u) == 0 && o_st % 2 == 0 && o_sh % 2 == 0,
               HLA_S6_EINVAL, "attend_decode: B and out need 4-byte aligned pairs");
-  hipStream_t st = as_stream(stream);
   if (plan && num_splits > 1) {
     HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL,
                 "attend_decode: split plan of %lld ints, need %lld", (long long)plan_len,
@@ -2060,4 +2064,127 @@ extern "C" int hla_s6_attend_decode(
     case 512: return launch_epilogue<512>(e, st);
     default: return launch_epilogue<1024>(e, st);
   }
+}
+}  // namespace
+}  // namespace hla
+
+extern "C" int hla_s6_attend_decode(
+    const void* q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void* lat_k, const void* lat_v,
+    int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size, int64_t lat_num_blocks,
+    const int32_t* lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols, const int64_t* token_requests,
+    const int32_t* ctx_latent, const void* q_rope, int64_t qr_st, int64_t qr_sh, const void* ex_k, const void* ex_v,
+    int64_t ex_page_stride, int64_t ex_row_stride, int64_t ex_head_stride, int32_t ex_block_size,
+    int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
+    const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
+    int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
+    int32_t num_splits, float* workspace, int64_t workspace_floats, const int32_t* plan, int64_t plan_len,
+    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+  return hla::attend_decode(q_lat, ql_st, ql_sh, width, lat_k, lat_v, lat_page_stride, lat_row_stride, block_size,
+                            lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols, token_requests, ctx_latent, q_rope,
+                            qr_st, qr_sh, ex_k, ex_v, ex_page_stride, ex_row_stride, ex_head_stride, ex_block_size,
+                            ex_num_blocks, ex_table, ex_bt_stride, ex_bt_cols, query_start_loc, seq_lens, num_reqs,
+                            window, B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, workspace,
+                            workspace_floats, plan, plan_len, o_hist, lse_hist, o_win, lse_win, out, o_st, o_sh,
+                            hla::as_stream(stream));
+}
+
+// ---- hla_s6_attend_decode_static: the fused decode step with its buffers in a static device array -------------
+// For callers that cannot allocate. `scratch` holds, per call, the split partials (T * S * 16 * (width + 1)
+// floats), the step's split plan, the history output and lse (written by a one-slot call), and the exact window's
+// output and lse, each region 256-byte aligned. Every GPU holds its own copy of the array for the life of the process; its
+// address on a device comes from hipGetSymbolAddress with that device current, once per device, and host code uses
+// only that address (the array's name is a host-side stand-in). Nothing in it needs clearing: every word a kernel of
+// the call reads was written earlier in the same call. Calls that overlap on one GPU share the array and race.
+namespace hla {
+namespace {
+constexpr int64_t kStaticScratchBytes = 48ll << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+}  // namespace hla
+
+static __device__ __align__(256) float scratch[hla::kStaticScratchBytes / sizeof(float)];
+
+namespace hla {
+namespace {
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// This device's copy of `scratch`, looked up on the first call on the device.
+int static_scratch(void** addr) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(HLA_S6_EDEVICE, "attend_decode_static: %s", hipGetErrorString(err));
+  HLA_REQUIRE(dev >= 0 && dev < kMaxDevices, HLA_S6_EDEVICE, "attend_decode_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p)
+      return fail(HLA_S6_EDEVICE, "attend_decode_static: no device address for the scratch array: %s",
+                  hipGetErrorString(err));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return HLA_S6_OK;
+}
+
+inline int64_t align256(int64_t bytes) { return (bytes + 255) / 256 * 256; }
+}  // namespace
+}  // namespace hla
+
+extern "C" int hla_s6_attend_decode_static(
+    const void* q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void* lat_k, const void* lat_v,
+    int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size, int64_t lat_num_blocks,
+    const int32_t* lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols, const int64_t* token_requests,
+    const int32_t* ctx_latent, const void* q_rope, int64_t qr_st, int64_t qr_sh, const void* ex_k, const void* ex_v,
+    int64_t ex_page_stride, int64_t ex_row_stride, int64_t ex_head_stride, int32_t ex_block_size,
+    int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
+    const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
+    int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
+    int32_t num_splits, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0 && num_splits >= 1 && num_splits <= kMaxSplits && num_heads == kHeads &&
+                  (width == 128 || width == 256 || width == 512 || width == 1024),
+              HLA_S6_EINVAL, "attend_decode_static: bad token count, split count, head count or width");
+  if (num_tokens == 0) return HLA_S6_OK;
+  const int64_t T = num_tokens, S = num_splits;
+  const int64_t ws_bytes = S > 1 ? align256(T * S * kHeads * (width + 1) * 4) : 0;
+  const int64_t plan_bytes = S > 1 ? align256(plan_ints(num_tokens, num_splits) * 4) : 0;
+  const int64_t hist_bytes = align256(T * kHeads * width * 2) + align256(kHeads * T * 4);
+  const int64_t win_bytes = align256(T * kHeads * kExactDim * 2) + align256(kHeads * T * 4);
+  const int64_t need = ws_bytes + plan_bytes + hist_bytes + win_bytes;
+  HLA_REQUIRE(need <= kStaticScratchBytes, HLA_S6_EWORKSPACE,
+              "attend_decode_static: %d tokens x %d splits at width %d need %lld scratch bytes, the static array "
+              "holds %lld",
+              num_tokens, num_splits, width, (long long)need, (long long)kStaticScratchBytes);
+  void* base = nullptr;
+  int rc = static_scratch(&base);
+  if (rc != HLA_S6_OK) return rc;
+  char* at = static_cast<char*>(base);
+  float* ws = S > 1 ? reinterpret_cast<float*>(at) : nullptr;
+  at += ws_bytes;
+  int32_t* plan = S > 1 ? reinterpret_cast<int32_t*>(at) : nullptr;
+  at += plan_bytes;
+  void* o_hist = at;  // written by a one-slot call only, as in hla_s6_attend_decode
+  at += align256(T * kHeads * width * 2);
+  float* lse_hist = reinterpret_cast<float*>(at);
+  at += align256(kHeads * T * 4);
+  void* o_win = at;
+  at += align256(T * kHeads * kExactDim * 2);
+  float* lse_win = reinterpret_cast<float*>(at);
+  hipStream_t st = as_stream(stream);
+  if (S > 1) {  // the step's split plan into the scratch (one small launch)
+    HLA_REQUIRE(ctx_latent != nullptr, HLA_S6_EINVAL, "attend_decode_static: null ctx_latent");
+    hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, st, ctx_latent, num_tokens,
+                       (int64_t)lat_bt_cols * block_size, num_splits, plan);
+    rc = check_launch("attend_decode_static: split plan");
+    if (rc != HLA_S6_OK) return rc;
+  }
+  return attend_decode(q_lat, ql_st, ql_sh, width, lat_k, lat_v, lat_page_stride, lat_row_stride, block_size,
+                       lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols, token_requests, ctx_latent, q_rope,
+                       qr_st, qr_sh, ex_k, ex_v, ex_page_stride, ex_row_stride, ex_head_stride, ex_block_size,
+                       ex_num_blocks, ex_table, ex_bt_stride, ex_bt_cols, query_start_loc, seq_lens, num_reqs, window,
+                       B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, ws,
+                       S > 1 ? ws_bytes / 4 : 0, plan, S > 1 ? plan_ints(num_tokens, num_splits) : 0, o_hist,
+                       lse_hist, o_win, lse_win, out, o_st, o_sh, st);
 }

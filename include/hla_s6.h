@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 3
+#define HLA_S6_ABI_VERSION 4
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -233,6 +233,28 @@ int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_
                          int64_t workspace_floats, const int32_t *plan, int64_t plan_len, void *o_hist,
                          float *lse_hist, void *o_win, float *lse_win, void *out, int64_t o_st, int64_t o_sh,
                          void *stream);
+
+/* hla_s6_attend_decode_static: no counterpart in the reference. hla_s6_attend_decode for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation): the
+ * same arguments without workspace, plan, o_hist, lse_hist, o_win and lse_win, which live in a static device array
+ * of the library instead (48 MiB on every GPU the library runs on, held until the process ends). The caller passes
+ * the inputs and `out`; the call computes the step's split plan itself (one extra small launch), then runs the
+ * kernels of hla_s6_attend_decode, so `out` equals what hla_s6_attend_decode writes for the same inputs. It calls no
+ * allocator. Sizes whose buffers exceed the array (T * S * 16 * (width + 1) floats of split partials plus the plan
+ * and the window outputs, each rounded up to 256 bytes) return HLA_S6_EWORKSPACE before any launch. Calls on one
+ * GPU share the array: calls that overlap in time on one GPU (other streams, other threads) race. */
+int hla_s6_attend_decode_static(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void *lat_k,
+                                const void *lat_v, int64_t lat_page_stride, int64_t lat_row_stride,
+                                int32_t block_size, int64_t lat_num_blocks, const int32_t *lat_table,
+                                int64_t lat_bt_stride, int32_t lat_bt_cols, const int64_t *token_requests,
+                                const int32_t *ctx_latent, const void *q_rope, int64_t qr_st, int64_t qr_sh,
+                                const void *ex_k, const void *ex_v, int64_t ex_page_stride, int64_t ex_row_stride,
+                                int64_t ex_head_stride, int32_t ex_block_size, int64_t ex_num_blocks,
+                                const int32_t *ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
+                                const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs,
+                                int32_t window, const void *B, int64_t b_sh, int64_t b_sr, const uint8_t *invalid,
+                                int32_t num_tokens, int32_t num_heads, float scale, int32_t num_splits, void *out,
+                                int64_t o_st, int64_t o_sh, void *stream);
 
 /* ---- a10 (slot-mapped row commit) -----------------------------------------------------------------
  * Slot of each token: block_table[token_requests[t], positions[t] / block_size] * block_size

@@ -186,3 +186,16 @@ def test_library_status_codes_map_to_reference_exceptions(pkg):
     with pytest.raises(RuntimeError, match='workspace overflow'):   # EWORKSPACE before any launch
         lib.call('hla_s6_history_attention', 16, 1, 16, 512, 512, 512, 16, 16, 1024, 1024, 16, 1, 16, 0, 1, None, 16,
                  1.0, 4, 16, 10, 16, 512, 512, 16, None)
+
+
+def test_static_decode_refuses_sizes_past_its_array(pkg):
+    """hla_s6_attend_decode_static checks its buffers against the static array before any device access: 4096 rows x
+    64 slots at width 512 (8.6 GB of split partials) raise RuntimeError; a bad width raises ValueError."""
+    lib = pkg._lib
+    args = [None if t is lib.P else 0 for t in lib.SIGNATURES['hla_s6_attend_decode_static']]
+    args[3], args[36], args[37], args[38], args[39] = 512, 4096, 16, 0.1, 64
+    with pytest.raises(RuntimeError, match='static array holds'):
+        lib.call('hla_s6_attend_decode_static', *args)
+    args[3] = 384
+    with pytest.raises(ValueError, match='width'):
+        lib.call('hla_s6_attend_decode_static', *args)

@@ -1,0 +1,104 @@
+"""hla_s6_attend_decode_static (the fused decode step with its buffers in the library's static device array) against
+hla_s6_attend_decode (caller-allocated workspace, plan and intermediates), through the C ABI: two calls in a row, the
+second smaller (fewer rows, fewer slots, the narrower latent), each bitwise equal to the allocating entry point
+(same kernels, same split plan); and sizes past the array refused before any launch."""
+import importlib
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from s6util import FakeLatentLayer
+
+pytestmark = pytest.mark.gpu
+H, D, W, BLOCK = 16, 128, 32, 16
+SCALE = 1 / math.sqrt(D)
+
+lib = importlib.import_module('hybrid-latent-attention_amd._lib')
+layer = importlib.import_module('hybrid-latent-attention_amd.s6_layer')
+ops = importlib.import_module('hybrid-latent-attention_amd.s6_ops')
+
+
+class Step:
+    """One decode step of ``len(hist)`` requests (+ ``pad`` padding rows) at one latent width, caches on the device."""
+
+    def __init__(self, hist, pad, width, splits, seed):
+        g = torch.Generator(device='cuda').manual_seed(seed)
+        self.R, self.T, self.w, self.splits = len(hist), len(hist) + pad, width, splits
+        hist = np.asarray(hist)
+        seq = hist + 1
+        cols = int(-(-seq.max() // BLOCK))
+        pool = self.R * cols + 1
+        rnd = lambda *s, std=1.0: (torch.randn(*s, generator=g, device='cuda') * std).to(torch.bfloat16)
+        perm = (torch.randperm(pool - 1, generator=g, device='cuda') + 1).to(torch.int32)
+        self.table = perm[:self.R * cols].view(self.R, cols).contiguous()
+        self.ex_table = (torch.randperm(pool - 1, generator=g, device='cuda') + 1).to(torch.int32)[:self.R * cols]
+        self.ex_table = self.ex_table.view(self.R, cols).contiguous()
+        self.cache = rnd(pool, 1, BLOCK, 2 * width)
+        self.exact = rnd(pool, H, BLOCK, 2 * D)
+        self.q_lat = rnd(self.T, H, width, std=width ** -0.5)
+        self.q_rope = rnd(self.T, H, D)
+        self.B = rnd(H, width, D, std=1 / math.sqrt(2048))
+        positions = np.concatenate((hist, np.ones(pad, np.int64)))
+        ws = ops.S6Workspace(H, width, self.T * splits)
+        self.ctx = layer.StepContext(torch.as_tensor(positions, device='cuda'),
+                                     torch.arange(self.R + 1, dtype=torch.int32, device='cuda'),
+                                     torch.as_tensor(seq.astype(np.int32), device='cuda'), 1, self.T, {}, SCALE,
+                                     ops.HIP_BACKENDS, ws, splits, window=W, max_seqlen_k=int(seq.max()))
+        A = rnd(H, D, width)
+        if width == 512:
+            self.loop, self.sl = 1, FakeLatentLayer(rnd(H, D, 256), rnd(H, 256, D), A[None].repeat(3, 1, 1, 1),
+                                                    self.B[None].repeat(3, 1, 1, 1))
+        else:
+            self.loop, self.sl = 0, FakeLatentLayer(A, self.B, rnd(3, H, D, 512), rnd(3, H, 512, D))
+
+    def allocating(self):
+        """The existing path: s6_layer.attend's decode branch (hla_s6_attend_decode with the step's plan)."""
+        return layer.attend(self.sl, self.loop, self.q_lat, self.q_rope, None, None, self.cache, self.table, None,
+                            None, self.ctx, (self.exact, self.ex_table))
+
+    def static(self):
+        ctx, w, d = self.ctx, self.w, D
+        out = torch.empty(self.T, H, D, dtype=torch.bfloat16, device='cuda')
+        c, ex = self.cache, self.exact
+        lib.call('hla_s6_attend_decode_static', lib.ptr(self.q_lat), self.q_lat.stride(0), self.q_lat.stride(1), w,
+                 lib.ptr(c), lib.ptr(c[..., w:]), c.stride(0), c.stride(2), c.shape[2], c.shape[0],
+                 lib.ptr(self.table), self.table.stride(0), self.table.shape[1], lib.ptr(ctx.token_requests),
+                 lib.ptr(ctx.ctx_latent), lib.ptr(self.q_rope), self.q_rope.stride(0), self.q_rope.stride(1),
+                 lib.ptr(ex), lib.ptr(ex[..., d:]), ex.stride(0), ex.stride(2), ex.stride(1), ex.shape[2],
+                 ex.shape[0], lib.ptr(self.ex_table), self.ex_table.stride(0), self.ex_table.shape[1],
+                 lib.ptr(ctx.query_start_loc), lib.ptr(ctx.seq_lens), self.R, W, lib.ptr(self.B), self.B.stride(0),
+                 self.B.stride(1), lib.ptr(ctx.invalid), self.T, H, SCALE, self.splits, lib.ptr(out), out.stride(0),
+                 out.stride(1), lib.stream(out.device))
+        return out
+
+
+def test_static_entry_equals_the_allocating_one_on_two_calls():
+    big = Step(np.random.default_rng(1).integers(1, 6000, 64), pad=2, width=512, splits=16, seed=1)
+    small = Step([700, 0, 45, 2900, 20], pad=1, width=256, splits=4, seed=2)
+    for name, step in (('first call (66 rows, width 512, 16 slots)', big),
+                       ('second call (6 rows, width 256, 4 slots)', small)):
+        print(f'case {name}', flush=True)
+        want = step.allocating()
+        got = step.static()
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all(), name
+        assert torch.equal(got, want), f'{name}: max diff {(got.float() - want.float()).abs().max().item()}'
+        assert (got[step.R:] == 0).all()
+    # one slot: the one-slot history output and lse also live in the array
+    one = Step([1500, 300, 0], pad=0, width=512, splits=1, seed=3)
+    assert torch.equal(one.static(), one.allocating())
+
+
+def refusal_args(num_tokens, num_splits, width=512):
+    """Arguments of hla_s6_attend_decode_static with null pointers and zero strides around the sizes."""
+    args = [None if t is lib.P else 0 for t in lib.SIGNATURES['hla_s6_attend_decode_static']]
+    args[3], args[36], args[37], args[38], args[39] = width, num_tokens, H, SCALE, num_splits
+    return args
+
+
+def test_static_entry_refuses_sizes_past_the_array():
+    """4096 rows x 64 slots at width 512 need 8.6 GB of partials: refused before any launch or device access."""
+    with pytest.raises(RuntimeError, match='static array holds'):
+        lib.call('hla_s6_attend_decode_static', *refusal_args(4096, 64))
