@@ -413,8 +413,15 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   }
 }
 
-// The decode exact windows of the step, one (token, head) row per wave: wave v of the grid (of nv) computes rows
-// v, v + nv, ... of the 16*T, so they spread over the first workgroups of every XCD and add no workgroup.
+// The decode exact windows of the step, one (token, head) row per wave job: wave v of nv computes rows v, v + nv, ...
+// of the 16*T. The split kernel appends window_workgroups() workgroups for them after its history workgroups, so
+// the window runs beside the history instead of ahead of it on the first workgroups.
+constexpr int kWindowJobsPerWave = 4;
+
+__host__ __device__ inline unsigned window_workgroups(int T, int waves) {
+  return (unsigned)((kHeads * T + kWindowJobsPerWave * waves - 1) / (kWindowJobsPerWave * waves));
+}
+
 __device__ void window_jobs(const WindowPart& w, int T, float scale_log2, int v, int nv, int lane) {
   for (int j = v; j < kHeads * T; j += nv) {
     const int t = j / kHeads, h = j % kHeads;
@@ -453,6 +460,11 @@ void history_split(HistoryParams a) {
   const int hq = lane & 15, g = lane >> 4;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;  // keys the block table can address
   const int b = blockIdx.x;                                 // dispatch order
+  const int nh = (int)split_workgroups(a.T, S);  // history workgroups; the ones after them take window jobs
+  if (b >= nh) {  // a window workgroup of the fused decode step (uniform over the workgroup)
+    window_jobs(a.win, a.T, a.scale_log2, (b - nh) * G::WAVES + wave, (gridDim.x - nh) * G::WAVES, lane);
+    return;
+  }
 
   // Split plan: every row is cut in chunks of `chunk` tiles (the same for every row of the step); workgroup b takes
   // the b-th (row, chunk) pair of the step, so the work is balanced over the workgroups and the XCDs.
@@ -466,8 +478,6 @@ void history_split(HistoryParams a) {
     chunk = split_chunk(a.ctx, a.T, cap, S, red_lds);
     find_item(a.ctx, a.T, cap, chunk, b, item_lds, item_lds + G::WAVES, t, s);
   }
-  // the exact decode windows (the fused decode step), spread over the first waves of the grid
-  if (a.has_window) window_jobs(a.win, a.T, a.scale_log2, b * G::WAVES + wave, gridDim.x * G::WAVES, lane);
   if (S > 1 && b < a.T && wave == 0 && g == 0) {  // slots of row b past its work: an empty partial for stage 2
     const int used = a.plan ? a.plan[1 + b] : used_slots(a.ctx[b], cap, chunk);
     for (int e = used; e < S; ++e) a.ws_lse[((int64_t)b * S + e) * kHeads + hq] = -INFINITY;
@@ -1645,7 +1655,7 @@ int launch(const HistoryParams& p, hipStream_t stream) {
       hipLaunchKernelGGL((history_group<R, 2>), dim3((unsigned)((p.T + 1) / 2), p.num_splits), dim3(Geo<R>::THREADS),
                          0, stream, p);
   } else {
-    const dim3 grid(split_workgroups(p.T, p.num_splits));
+    const dim3 grid(split_workgroups(p.T, p.num_splits) + (p.has_window ? window_workgroups(p.T, Geo<R>::WAVES) : 0u));
     if (p.shared_rows) hipLaunchKernelGGL((history_split<R, false>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
     else hipLaunchKernelGGL((history_split<R, true>), grid, dim3(Geo<R>::THREADS), 0, stream, p);
   }
