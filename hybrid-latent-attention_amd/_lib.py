@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -42,13 +42,13 @@ SIGNATURES = {
                                       I64, I32, I64, P, I64, I32, I32, F32, P, I64, I64, P, P],
     'hla_s6_merge_states': [P, I64, I64, P, P, I64, I64, P, P, I32, I32, I32, I32, P, I64, I64, P, P],
     'hla_s6_attend_decode': [P, I64, I64, I32, P, P, I64, I64, I32, I64, P, I64, I32, P, P, P, I64, I64, P, P, I64, I64,
-                             I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32, F32, I32, P, I64, P,
-                             I64, P, P, P, P, P, I64, I64, P],
+                             I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32, F32, I32, I32, P,
+                             I64, P, I64, P, P, P, P, P, I64, I64, P],
     'hla_s6_attend_decode_static': [P, I64, I64, I32, P, P, I64, I64, I32, I64, P, I64, I32, P, P, P, I64, I64, P, P,
                                     I64, I64, I64, I32, I64, P, I64, I32, P, P, I32, I32, P, I64, I64, P, I32, I32,
-                                    F32, I32, P, I64, I64, P],
+                                    F32, I32, I32, P, I64, I64, P],
     'hla_s6_split_plan_ints': [I32, I32],
-    'hla_s6_split_plan': [P, I32, I64, I32, P, I64, P],
+    'hla_s6_split_plan': [P, I32, I64, I32, P, I32, P, I64, P],
     'hla_s6_slot_mapping': [P, I64, I32, P, P, P, I32, I32, P, P],
     'hla_s6_store_rows': [P, I64, P, I64, I32, I32, P, P, I64, I64, I32, I64, P],
     'hla_s6_write_rows': [P, I32, I32, I64, P, I32, I64, P, I64, P, I64, P, P, P, I32, I64, P, I64, I64, I32, I64, P],

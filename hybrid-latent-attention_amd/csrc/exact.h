@@ -133,25 +133,36 @@ __device__ __forceinline__ int request_of(const int32_t* qsl, int R, int t) {
   return min(lo - 1, R - 1);
 }
 
-// Decode-window key range of token t (window_attention_fa semantics): query i of a request with Lq queries sits at
-// p = seq_len - Lq + i and reads keys [max(0, p - window), p]. Returns false for padding tokens.
+// Decode-window key range of token t: query i of a request with Lq queries sits at p = seq_len - Lq + i and reads
+// keys [max(0, p - window), p] (window_attention_fa semantics), or with chunk_start [max(0, seq_len - Lq - window), p]:
+// the window's history rows before the chunk and the chunk's keys up to the query (the chunk attention and the
+// window history of a prefill step in one range). Both are [seq_len - 1 - window, seq_len - 1] for Lq = 1. Returns
+// false for padding tokens.
 __device__ __forceinline__ bool decode_window_range(const int32_t* qsl, const int32_t* seq_lens, int R, int t,
-                                                    int window, int& req, int& lo, int& hi) {
+                                                    int window, int& req, int& lo, int& hi, bool chunk_start = false,
+                                                    const int64_t* token_requests = nullptr) {
   lo = hi = 0;
   req = 0;
-  // one query per request up to token t (a decode batch): token t is request t, found with two independent loads
-  // instead of a dependent binary search
-  const bool direct = t < R && qsl[t] == t && qsl[t + 1] == t + 1;
-  if (!direct) {
+  bool direct;
+  if (token_requests) {  // the step's token -> request map: no search
     if (t >= qsl[R]) return false;
-    req = request_of(qsl, R, t);
+    req = (int)token_requests[t];
+    direct = false;
   } else {
-    req = t;
+    // one query per request up to token t (a decode batch): token t is request t, found with two independent loads
+    // instead of a dependent binary search
+    direct = t < R && qsl[t] == t && qsl[t + 1] == t + 1;
+    if (!direct) {
+      if (t >= qsl[R]) return false;
+      req = request_of(qsl, R, t);
+    } else {
+      req = t;
+    }
   }
   const int lq = direct ? 1 : qsl[req + 1] - qsl[req];
   const int p = seq_lens[req] - lq + (direct ? 0 : t - qsl[req]);
   if (p >= 0) {
-    lo = max(0, p - window);
+    lo = max(0, (chunk_start ? seq_lens[req] - lq : p) - window);
     hi = p + 1;
   }
   return true;

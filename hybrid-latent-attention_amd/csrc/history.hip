@@ -52,6 +52,8 @@ struct WindowPart {  // decode exact window, computed by the extra row of workgr
   const int32_t* seq_lens;
   int num_reqs;
   int window;
+  bool chunk_start;  // keys [seq_len - Lq - window, p] (prefill chunks) instead of [p - window, p]
+  const int64_t* token_requests;  // request of each token (nullable: searched in qsl)
   uint16_t* out;  // [T, 16, 128]
   int64_t o_st, o_sh;
   float* lse;  // [16, T]
@@ -204,12 +206,20 @@ __device__ void find_item(const int32_t* ctx, int T, int64_t cap, int chunk, int
 // NI = split_workgroups(T, S); rows past the end of the list are -1.
 inline int64_t plan_ints(int T, int S) { return 1 + (int64_t)T + 2 * (int64_t)split_workgroups(T, S); }
 
+// Tokens of one request whose chunks the plan lists chunk-major (at most this many, all with the same slot count)
+constexpr int kPlanGroup = 16;
+
 // The split plan of a step, computed once by one workgroup and read by every split kernel of the step (every layer
 // and loop with the same lengths and slot count) instead of being derived in each workgroup. The N items, rows in
 // order, are cut in 8 contiguous shares of q = ceil(N/8); item i goes to workgroup (i % q) * 8 + i / q, i.e. share
 // i / q lands on one XCD (workgroups are dealt to the XCDs round-robin), so every XCD gets the same number of
-// items and a row's chunks mostly share an XCD (its query is read from HBM once).
-__global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, int S, int32_t* plan) {
+// items and a row's chunks mostly share an XCD (its query is read from HBM once). With qsl (the step's request
+// boundaries), the rows of a request of 2 .. kPlanGroup tokens that all use the same number of slots (a short
+// prefill chunk: they read the same latent rows) list their items chunk-major within the request's range: the
+// tokens' copies of one chunk are consecutive items, land on one XCD at about the same time and read the chunk's
+// rows from HBM once, the other tokens' reads hitting the L2.
+__global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, int S,
+                                                         const int32_t* qsl, int R, int32_t* plan) {
   __shared__ int64_t red[8];
   __shared__ int wsum[4];
   __shared__ int carry_s;
@@ -250,8 +260,20 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
     for (int w = 0; w < wave; ++w) base += wsum[w];
     const int first = base + x - u;
     if (r < T) {
+      // position k of the row in its request's chunk-major group of m rows (k = 0, m = 1: row-major)
+      int k = 0, m = 1;
+      if (qsl && r < qsl[R]) {
+        const int req = request_of(qsl, R, r), g0 = qsl[req], gm = qsl[req + 1] - g0;
+        bool same = gm > 1 && gm <= kPlanGroup;
+        for (int e = 0; same && e < gm; ++e) same = used[g0 + e] == u;
+        if (same) {
+          k = r - g0;
+          m = gm;
+        }
+      }
+      const int group0 = first - k * u;  // the group's first item (its rows' ranges are contiguous)
       for (int c = 0; c < u; ++c) {
-        const int i = first + c, b = (i % q) * 8 + i / q;
+        const int i = group0 + c * m + k, b = (i % q) * 8 + i / q;
         rows[b] = r;
         slots[b] = c;
       }
@@ -415,18 +437,21 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
 
 // The decode exact windows of the step, one (token, head) row per wave job: wave v of nv computes rows v, v + nv, ...
 // of the 16*T. The split kernel appends window_workgroups() workgroups for them after its history workgroups, so
-// the window runs beside the history instead of ahead of it on the first workgroups.
-constexpr int kWindowJobsPerWave = 4;
+// the window runs beside the history instead of ahead of it on the first workgroups. A job is a chain of dependent
+// loads (request bounds, page table, rows) of several microseconds: a wave takes four with 64 tokens or more
+// (hidden behind a long history), one in smaller steps, whose history is short.
+__host__ __device__ inline int window_jobs_per_wave(int T) { return T >= 64 ? 4 : 1; }
 
 __host__ __device__ inline unsigned window_workgroups(int T, int waves) {
-  return (unsigned)((kHeads * T + kWindowJobsPerWave * waves - 1) / (kWindowJobsPerWave * waves));
+  const int per = window_jobs_per_wave(T) * waves;
+  return (unsigned)((kHeads * T + per - 1) / per);
 }
 
 __device__ void window_jobs(const WindowPart& w, int T, float scale_log2, int v, int nv, int lane) {
   for (int j = v; j < kHeads * T; j += nv) {
     const int t = j / kHeads, h = j % kHeads;
     int req, lo, hi;
-    decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi);
+    decode_window_range(w.qsl, w.seq_lens, w.num_reqs, t, w.window, req, lo, hi, w.chunk_start, w.token_requests);
     ExactSource src = w.src;
     hi = (int)min((int64_t)hi, (int64_t)w.bt_cols * src.block_size);
     src.table_row = w.bt + (int64_t)req * w.bt_stride;
@@ -1973,8 +1998,9 @@ extern "C" int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits
   return num_tokens < 0 || num_splits < 1 ? -1 : hla::plan_ints(num_tokens, num_splits);
 }
 
-extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t cap, int32_t num_splits, int32_t* plan,
-                                 int64_t plan_len, void* stream) {
+extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t cap, int32_t num_splits,
+                                 const int32_t* query_start_loc, int32_t num_reqs, int32_t* plan, int64_t plan_len,
+                                 void* stream) {
   using namespace hla;
   HLA_REQUIRE(num_tokens >= 0 && num_splits >= 1 && num_splits <= kMaxSplits && cap >= 0, HLA_S6_EINVAL,
               "split_plan: bad token count, slot count or key capacity");
@@ -1982,8 +2008,9 @@ extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t
   HLA_REQUIRE(ctx && plan, HLA_S6_EINVAL, "split_plan: null pointer argument");
   HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL, "split_plan: %lld ints, need %lld",
               (long long)plan_len, (long long)plan_ints(num_tokens, num_splits));
+  HLA_REQUIRE(!query_start_loc || num_reqs >= 1, HLA_S6_EINVAL, "split_plan: query_start_loc needs num_reqs >= 1");
   hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, as_stream(stream), ctx, num_tokens, cap, num_splits,
-                     plan);
+                     query_start_loc, num_reqs, plan);
   return check_launch("split_plan");
 }
 
@@ -1999,9 +2026,9 @@ int attend_decode(
     int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
     const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
     int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
-    int32_t num_splits, float* workspace, int64_t workspace_floats, const int32_t* plan, int64_t plan_len,
-    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh,
-    hipStream_t st) {
+    int32_t num_splits, int32_t max_query_len, float* workspace, int64_t workspace_floats, const int32_t* plan,
+    int64_t plan_len, void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st,
+    int64_t o_sh, hipStream_t st) {
   HistoryParams p;
   int rc = fill_history(p, q_lat, num_tokens, num_heads, width, ql_st, ql_sh, lat_k, lat_v, lat_page_stride,
                         lat_row_stride, block_size, lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols,
@@ -2036,6 +2063,8 @@ int attend_decode(
   w.seq_lens = seq_lens;
   w.num_reqs = num_reqs;
   w.window = window;
+  w.chunk_start = true;  // = the decode window for one-token requests; the chunk + window history otherwise
+  w.token_requests = token_requests;
   w.out = static_cast<uint16_t*>(o_win);
   w.o_st = (int64_t)num_heads * kExactDim;
   w.o_sh = kExactDim;
@@ -2050,6 +2079,7 @@ int attend_decode(
     p.plan = plan;
   }
   p.combine = false;  // the epilogue reduces the splits
+  p.shared_rows = max_query_len > 1;  // tokens of a chunk read the same rows: cached loads (decode: streaming)
   rc = dispatch(p, width, st);
   if (rc != HLA_S6_OK) return rc;
   EpilogueParams e = {};
@@ -2087,15 +2117,16 @@ extern "C" int hla_s6_attend_decode(
     int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
     const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
     int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
-    int32_t num_splits, float* workspace, int64_t workspace_floats, const int32_t* plan, int64_t plan_len,
-    void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+    int32_t num_splits, int32_t max_query_len, float* workspace, int64_t workspace_floats, const int32_t* plan,
+    int64_t plan_len, void* o_hist, float* lse_hist, void* o_win, float* lse_win, void* out, int64_t o_st,
+    int64_t o_sh, void* stream) {
   return hla::attend_decode(q_lat, ql_st, ql_sh, width, lat_k, lat_v, lat_page_stride, lat_row_stride, block_size,
                             lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols, token_requests, ctx_latent, q_rope,
                             qr_st, qr_sh, ex_k, ex_v, ex_page_stride, ex_row_stride, ex_head_stride, ex_block_size,
                             ex_num_blocks, ex_table, ex_bt_stride, ex_bt_cols, query_start_loc, seq_lens, num_reqs,
-                            window, B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, workspace,
-                            workspace_floats, plan, plan_len, o_hist, lse_hist, o_win, lse_win, out, o_st, o_sh,
-                            hla::as_stream(stream));
+                            window, B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, max_query_len,
+                            workspace, workspace_floats, plan, plan_len, o_hist, lse_hist, o_win, lse_win, out, o_st,
+                            o_sh, hla::as_stream(stream));
 }
 
 // ---- hla_s6_attend_decode_static: the fused decode step with its buffers in a static device array -------------
@@ -2151,7 +2182,7 @@ extern "C" int hla_s6_attend_decode_static(
     int64_t ex_num_blocks, const int32_t* ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
     const int32_t* query_start_loc, const int32_t* seq_lens, int32_t num_reqs, int32_t window, const void* B,
     int64_t b_sh, int64_t b_sr, const uint8_t* invalid, int32_t num_tokens, int32_t num_heads, float scale,
-    int32_t num_splits, void* out, int64_t o_st, int64_t o_sh, void* stream) {
+    int32_t num_splits, int32_t max_query_len, void* out, int64_t o_st, int64_t o_sh, void* stream) {
   using namespace hla;
   HLA_REQUIRE(num_tokens >= 0 && num_splits >= 1 && num_splits <= kMaxSplits && num_heads == kHeads &&
                   (width == 128 || width == 256 || width == 512 || width == 1024),
@@ -2184,9 +2215,11 @@ extern "C" int hla_s6_attend_decode_static(
   float* lse_win = reinterpret_cast<float*>(at);
   hipStream_t st = as_stream(stream);
   if (S > 1) {  // the step's split plan into the scratch (one small launch)
-    HLA_REQUIRE(ctx_latent != nullptr, HLA_S6_EINVAL, "attend_decode_static: null ctx_latent");
+    HLA_REQUIRE(ctx_latent && query_start_loc && num_reqs >= 1, HLA_S6_EINVAL,
+                "attend_decode_static: null ctx_latent or query_start_loc");
     hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, st, ctx_latent, num_tokens,
-                       (int64_t)lat_bt_cols * block_size, num_splits, plan);
+                       (int64_t)lat_bt_cols * block_size, num_splits, max_query_len > 1 ? query_start_loc : nullptr,
+                       num_reqs, plan);
     rc = check_launch("attend_decode_static: split plan");
     if (rc != HLA_S6_OK) return rc;
   }
@@ -2194,7 +2227,7 @@ extern "C" int hla_s6_attend_decode_static(
                        lat_num_blocks, lat_table, lat_bt_stride, lat_bt_cols, token_requests, ctx_latent, q_rope,
                        qr_st, qr_sh, ex_k, ex_v, ex_page_stride, ex_row_stride, ex_head_stride, ex_block_size,
                        ex_num_blocks, ex_table, ex_bt_stride, ex_bt_cols, query_start_loc, seq_lens, num_reqs, window,
-                       B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, ws,
+                       B, b_sh, b_sr, invalid, num_tokens, num_heads, scale, num_splits, max_query_len, ws,
                        S > 1 ? ws_bytes / 4 : 0, plan, S > 1 ? plan_ints(num_tokens, num_splits) : 0, o_hist,
                        lse_hist, o_win, lse_win, out, o_st, o_sh, st);
 }

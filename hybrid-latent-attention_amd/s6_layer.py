@@ -89,6 +89,9 @@ class StepContext:
         # gives the GPU more workgroups
         self.history_group = 4 if (max_query_len or 1) >= 16 else 1
         self.history_needed = True
+        # chunks shorter than FUSED_CHUNK_TOKENS attend through the fused decode path, reading their own keys from
+        # the exact cache (which the adapter writes before attending); False: the reference's op sequence
+        self.fused_chunks = True
         self.md_present = query_start_loc is not None
         if not self.md_present:
             query_start_loc = torch.tensor([0, num_tokens], dtype=torch.int32, device=device)
@@ -121,7 +124,8 @@ class StepContext:
         ``cap`` addressable rows: one small launch per distinct (splits, cap) per step, read by every layer."""
         key = (int(splits), int(cap))
         if key not in self._plans:
-            self._plans[key] = s6_ops.split_plan(self.ctx_latent, key[1], key[0])
+            qsl = self.query_start_loc if self.max_query_len > 1 else None   # short chunks share rows
+            self._plans[key] = s6_ops.split_plan(self.ctx_latent, key[1], key[0], qsl)
         return self._plans[key]
 
     def slots(self, table, block_size):
@@ -149,6 +153,11 @@ class StepContext:
         return latent_query(q_pre_rope, A, self.positions, self.tables[width], self.backends.rope, self.rope_flat)
 
 
+# Steps whose longest chunk is shorter than this take the fused decode path (one token per history workgroup);
+# longer chunks take the multi-query kernels (eight tokens of a request per workgroup).
+FUSED_CHUNK_TOKENS = 16
+
+
 def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_scale, ctx, window=None):
     """One softmax over the paged latent history (fully visible) and the causal current chunk
     (``hla/vllm_latent/s6_layer.py:87-115``).
@@ -157,10 +166,15 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     layer's ``[num_blocks,1,block,2w]`` tensor or None (no history); ``block_table`` is the per-request table;
     ``window`` is ``(exact_cache, per-request block_table)`` or None. Returns ``[T,H,d]`` with ``~valid`` rows zeroed.
     Decode steps with history run as one fused call (history + exact window in one launch, the split reduction,
-    then the ``B_t`` projection fused with the LSE merge); other steps compose the single ops in the reference's
-    order.
+    then the ``B_t`` projection fused with the LSE merge). So do steps whose chunks are shorter than
+    ``FUSED_CHUNK_TOKENS`` tokens (``ctx.fused_chunks``): their exact part is one softmax per query over the exact
+    cache's rows ``[ctx - W, p]``, the window history and the chunk up to the query, which the adapter has written
+    to the exact cache before attending (``hla/vllm_latent/ouro_latent.py:120-122``), so it equals the reference's
+    causal chunk of ``k_rope`` / ``v`` merged with its window history. Other steps compose the single ops in the
+    reference's order.
     """
-    fused = window is not None and ctx.md_present and ctx.max_query_len == 1
+    fused = window is not None and ctx.md_present and (ctx.max_query_len == 1 or
+                                                       (ctx.fused_chunks and ctx.max_query_len < FUSED_CHUNK_TOKENS))
     has_history = cache is not None and ctx.md_present and ctx.history_needed
     if fused and has_history:
         return _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window)
@@ -188,8 +202,9 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
 
 
 def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
-    """Decode branch with history: one ``hla_s6_attend_decode`` call (two launches: the split history kernel, which
-    also computes the exact window, then the epilogue that reduces the splits, applies B_t and merges)."""
+    """Decode branch with history (and short chunks): one ``hla_s6_attend_decode`` call (two launches: the split
+    history kernel, whose last workgroups compute the exact windows, then the epilogue that reduces the splits,
+    applies B_t and merges)."""
     for kind in ('history', 'merge', 'chunk'):
         s6_ops._backend(kind, getattr(ctx.backends, kind))
     _, B, _ = sl.readers(loop)
@@ -233,7 +248,8 @@ def _attend_decode(sl, loop, q_lat, q_rope, cache, block_table, ctx, window):
               _lib.ptr(exact[..., d:]), exact.stride(0), exact.stride(2), exact.stride(1), exact.shape[2],
               exact.shape[0], _lib.ptr(ex_table), ex_table.stride(0), ex_table.shape[1], _lib.ptr(qsl), _lib.ptr(seq),
               R, int(ctx.window), _lib.ptr(B), B.stride(0), B.stride(1), _lib.ptr(ctx.invalid), T, H, float(ctx.scale),
-              splits, _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(plan), 0 if plan is None else plan.numel(),
+              splits, int(ctx.max_query_len), _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.ptr(plan),
+              0 if plan is None else plan.numel(),
               _lib.ptr(o_hist),
               _lib.ptr(lse_hist), _lib.ptr(o_win), _lib.ptr(lse_win), _lib.ptr(out), out.stride(0), out.stride(1),
               _lib.stream(dev))

@@ -277,17 +277,20 @@ def history_partials(q, k, v, block_table, ctx, scale, num_kv_splits, workspace,
     return ws
 
 
-def split_plan(ctx, cap, num_kv_splits):
+def split_plan(ctx, cap, num_kv_splits, query_start_loc=None):
     """The split plan of the history kernels for history lengths ``ctx[T]`` (int32), ``cap`` addressable rows per
     token and ``num_kv_splits`` slots per row (``hla_s6_split_plan``): computed once on the GPU, reusable by every
-    history call of the step with the same lengths."""
-    _dev(ctx)
+    history call of the step with the same lengths. With ``query_start_loc``, the tokens of a short chunk (2..16
+    tokens of a request with equal lengths) have their chunks listed together, so their shared rows are read from
+    HBM once."""
+    _dev(ctx, query_start_loc)
     ctx = _int('ctx', ctx, I32)
+    qsl = None if query_start_loc is None else _int('query_start_loc', query_start_loc, I32)
     T, splits = ctx.shape[0], int(num_kv_splits)
     n = _lib.load().hla_s6_split_plan_ints(T, splits)
     plan = torch.empty(max(int(n), 1), dtype=I32, device=ctx.device)
-    _lib.call('hla_s6_split_plan', _lib.ptr(ctx), T, int(cap), splits, _lib.ptr(plan), plan.numel(),
-              _lib.stream(ctx.device))
+    _lib.call('hla_s6_split_plan', _lib.ptr(ctx), T, int(cap), splits, _lib.ptr(qsl),
+              0 if qsl is None else qsl.shape[0] - 1, _lib.ptr(plan), plan.numel(), _lib.stream(ctx.device))
     return plan
 
 

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 4
+#define HLA_S6_ABI_VERSION 5
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -199,27 +199,35 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
  * slots per row), chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S))) with tiles = ceil(min(ctx[t],
  * cap) / 16), and give the chunks to workgroups as one balanced list. hla_s6_split_plan computes that list once
  * per step (one small launch) into `plan` (int32, hla_s6_split_plan_ints(T, S) entries; caller-owned) so that every
- * fused decode call of the step reads it instead of deriving it per workgroup. It depends only on ctx, cap and S.
- * cap = the latent table's columns * block_size. */
+ * fused decode call of the step reads it instead of deriving it per workgroup. It depends only on ctx, cap, S and
+ * query_start_loc. cap = the latent table's columns * block_size. With query_start_loc (nullable; num_reqs + 1
+ * entries), the tokens of a request of 2..16 tokens that all use the same number of slots (a short prefill chunk:
+ * they read the same latent rows) have their chunks listed chunk-major, so one XCD reads each chunk for all of them
+ * at about the same time. */
 int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits);
-int hla_s6_split_plan(const int32_t *ctx, int32_t num_tokens, int64_t cap, int32_t num_splits, int32_t *plan,
-                      int64_t plan_len, void *stream);
+int hla_s6_split_plan(const int32_t *ctx, int32_t num_tokens, int64_t cap, int32_t num_splits,
+                      const int32_t *query_start_loc, int32_t num_reqs, int32_t *plan, int64_t plan_len,
+                      void *stream);
 
 /* ---- a9: fused decode attention of one layer x loop --------------------------------------------------
  * Replaces the decode branch of s6_layer.attend (hla/vllm_latent/s6_layer.py:97-100,110-115):
  * window_attention_fa + history_attention + the B_t einsum + merge_states, in two launches:
  *   1. the split kernel of hla_s6_history_partials over q_lat and the latent cache (per-request table
- *      `lat_table`, row of token t = token_requests[t], ctx_latent[t] rows); the workgroups of token t also
- *      compute its exact decode window (mode 0 of hla_s6_window_attention over q_rope and the loop's exact
- *      cache), its 16 heads spread over the token's splits;
+ *      `lat_table`, row of token t = token_requests[t], ctx_latent[t] rows); workgroups appended after the history
+ *      ones compute the exact windows of the step over q_rope and the loop's exact cache: query i of a request with
+ *      Lq queries (p = seq_len - Lq + i) reads the exact keys [max(0, seq_len - Lq - window), p] (for Lq = 1 the
+ *      window_attention_fa keys [p - window, p] of mode 0 of hla_s6_window_attention; for a short prefill chunk the
+ *      window history and the chunk's causal keys, which the caller has written to the exact cache);
  *   2. an epilogue that reduces the split partials by LSE (o_hist rounded to bf16 as the history op returns
  *      it), then writes out = merge(bf16(o_hist @ B[h]), o_win) with the merge_states conventions (invalid
  *      rows zeroed).
  * The intermediates o_hist [T, 16, width] bf16, lse_hist [16, T], o_win [T, 16, 128] bf16 and lse_win [16, T]
- * are caller-owned contiguous buffers (they hold the two partial attentions on return). B is [16, width, 128]
- * with strides (b_sh, b_sr, 1). Workspace as for hla_s6_history_attention. `plan` (nullable, plan_len ints) is the
- * step's hla_s6_split_plan for (ctx_latent, lat_bt_cols * block_size, num_splits); without it each workgroup derives
- * its share itself. */
+ * are caller-owned contiguous buffers: o_win / lse_win hold the exact-window partial on return, o_hist / lse_hist
+ * the history partial when num_splits == 1 (with more slots it lives in the workspace). B is [16, width, 128]
+ * with strides (b_sh, b_sr, 1). max_query_len > 1 (tokens of a request read the same latent rows) loads the rows
+ * through the caches instead of streaming them. Workspace as for hla_s6_history_attention. `plan` (nullable,
+ * plan_len ints) is the step's hla_s6_split_plan for (ctx_latent, lat_bt_cols * block_size, num_splits); without it
+ * each workgroup derives its share itself. */
 int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_t width, const void *lat_k,
                          const void *lat_v, int64_t lat_page_stride, int64_t lat_row_stride, int32_t block_size,
                          int64_t lat_num_blocks, const int32_t *lat_table, int64_t lat_bt_stride, int32_t lat_bt_cols,
@@ -229,10 +237,10 @@ int hla_s6_attend_decode(const void *q_lat, int64_t ql_st, int64_t ql_sh, int32_
                          const int32_t *ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
                          const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs, int32_t window,
                          const void *B, int64_t b_sh, int64_t b_sr, const uint8_t *invalid, int32_t num_tokens,
-                         int32_t num_heads, float scale, int32_t num_splits, float *workspace,
-                         int64_t workspace_floats, const int32_t *plan, int64_t plan_len, void *o_hist,
-                         float *lse_hist, void *o_win, float *lse_win, void *out, int64_t o_st, int64_t o_sh,
-                         void *stream);
+                         int32_t num_heads, float scale, int32_t num_splits, int32_t max_query_len,
+                         float *workspace, int64_t workspace_floats, const int32_t *plan, int64_t plan_len,
+                         void *o_hist, float *lse_hist, void *o_win, float *lse_win, void *out, int64_t o_st,
+                         int64_t o_sh, void *stream);
 
 /* hla_s6_attend_decode_static: no counterpart in the reference. hla_s6_attend_decode for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid allocation): the
@@ -253,8 +261,8 @@ int hla_s6_attend_decode_static(const void *q_lat, int64_t ql_st, int64_t ql_sh,
                                 const int32_t *ex_table, int64_t ex_bt_stride, int32_t ex_bt_cols,
                                 const int32_t *query_start_loc, const int32_t *seq_lens, int32_t num_reqs,
                                 int32_t window, const void *B, int64_t b_sh, int64_t b_sr, const uint8_t *invalid,
-                                int32_t num_tokens, int32_t num_heads, float scale, int32_t num_splits, void *out,
-                                int64_t o_st, int64_t o_sh, void *stream);
+                                int32_t num_tokens, int32_t num_heads, float scale, int32_t num_splits,
+                                int32_t max_query_len, void *out, int64_t o_st, int64_t o_sh, void *stream);
 
 /* ---- a10 (slot-mapped row commit) -----------------------------------------------------------------
  * Slot of each token: block_table[token_requests[t], positions[t] / block_size] * block_size

@@ -137,11 +137,14 @@ def test_latent_query_then_attend_matches_fp32_reference(ops, layer):
         assert_attention_close(host_f32(out), want, f'loop {loop}')
 
 
-@pytest.mark.parametrize('lens,splits', [((6, 1, 3), 1), ((40, 1, 17), 1), ((40, 1, 17), 4)])
-def test_prefill_and_mixed_branch(ops, layer, lens, splits):
-    """max_query_len > 1: causal chunk + exact window over history rows [ctx - W, ctx) + latent history; chunks of
-    16 tokens or more take the multi-query history kernel (four tokens of a request per workgroup)."""
-    rng = np.random.default_rng(4 + sum(lens) + splits)
+@pytest.mark.parametrize('lens,splits,fused', [((6, 1, 3), 1, True), ((6, 1, 3), 8, True), ((6, 1, 3), 4, False),
+                                               ((15, 1, 2), 8, True), ((40, 1, 17), 1, True), ((40, 1, 17), 4, True)])
+def test_prefill_and_mixed_branch(ops, layer, lens, splits, fused):
+    """max_query_len > 1: causal chunk + exact window over history rows [ctx - W, ctx) + latent history. Chunks
+    shorter than 16 tokens take the fused decode path (exact rows [ctx - W, p] of the exact cache, which holds the
+    chunk as the adapter writes it first); longer ones the multi-query history kernel (eight tokens of a request
+    per workgroup) with the chunk from k_rope / v. Both against the oracle's reference composite."""
+    rng = np.random.default_rng(4 + sum(lens) + splits + fused)
     w = 512
     # request 0: prefill after 900 history rows; request 1: decode after 40; request 2: fresh prompt
     lens, hist = np.array(lens), np.array([900, 40, 0])
@@ -160,9 +163,15 @@ def test_prefill_and_mixed_branch(ops, layer, lens, splits):
                          dev_bf16(random_bits(rng, (3, H, D, w))), dev_bf16(np.stack([B] * 3)))
     q_lat = random_bits(rng, (T, H, w), 1 / math.sqrt(w))
     q_rope, k_rope, v = (random_bits(rng, (T, H, D)) for _ in range(3))
+    for r in range(3):   # the adapter writes the chunk's k / v to the exact cache before attending
+        for i in range(int(lens[r])):
+            pos, tok = int(hist[r]) + i, int(qsl[r]) + i
+            ex[et[r, pos // BLOCK], :, pos % BLOCK, :D] = k_rope[tok]
+            ex[et[r, pos // BLOCK], :, pos % BLOCK, D:] = v[tok]
     ws = ops.S6Workspace(H, w, T * splits)
     ctx = layer.StepContext(dev_i64(positions), dev_i32(qsl), dev_i32(seq), int(lens.max()), T, {}, SCALE,
                             ops.HIP_BACKENDS, ws, splits, window=W, max_seqlen_k=int(seq.max()))
+    ctx.fused_chunks = fused
     assert ctx.history_group == (4 if lens.max() >= 16 else 1)
     out = layer.attend(sl, 1, dev_bf16(q_lat), dev_bf16(q_rope), dev_bf16(k_rope), dev_bf16(v), dev_bf16(lat),
                        dev_i32(lt), None, None, ctx, (dev_bf16(ex), dev_i32(et)))

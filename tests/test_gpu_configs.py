@@ -6,7 +6,9 @@
 * long context: 8 rows at context 32768, the history split over 8, 16 and 32 slots and the MI355X policy
   (128 / 256);
 * ragged decode: 32 rows with contexts drawn from U[1024, 8192] on 65,536-page pools (2 GiB main latent, 1 GiB
-  loop-1 latent: page ids up to 65,535, byte offsets past 2^31).
+  loop-1 latent: page ids up to 65,535, byte offsets past 2^31);
+* short-chunk prefill: 4 requests x 3 tokens on 8192 latent rows (against ``O.attend_chunk``), on the fused path and
+  the reference's op sequence, and a mixed step of decode rows and chunks of 2..15 tokens.
 
 Caches live on the device; page 0 and every page no request references are +inf-poisoned, so a read outside a row's
 pages cannot go unseen. The oracle reads host copies of the referenced pages only (through a remapped table).
@@ -28,15 +30,18 @@ POS_INF = float('inf')
 
 
 class DeviceDecode:
-    """A decode step of ``len(hist)`` requests (one token each, ``pad`` padding tokens) with caches on the device:
-    per width one latent cache of ``pool`` pages whose tables are slices of one random permutation, one small exact
-    cache per loop holding the window pages, random readers of all four loops."""
+    """A step of ``len(hist)`` requests (``lens`` new tokens each, default one: a decode step; ``pad`` padding
+    tokens) with caches on the device: per width one latent cache of ``pool`` pages whose tables are slices of one
+    random permutation, one small exact cache per loop holding the window pages and the step's tokens (the adapter
+    writes them before attending), random readers of all four loops."""
 
-    def __init__(self, hist, pad=0, pool=None, seed=0):
+    def __init__(self, hist, pad=0, pool=None, seed=0, lens=None):
         g = torch.Generator(device='cuda').manual_seed(seed)
         self.hist = np.asarray(hist, np.int64)
-        self.R, self.T = len(hist), len(hist) + pad
-        self.seq = self.hist + 1                                   # the current token is already in the exact cache
+        self.lens = np.ones(len(hist), np.int64) if lens is None else np.asarray(lens, np.int64)
+        self.qsl = np.concatenate(([0], np.cumsum(self.lens))).astype(np.int32)
+        self.R, self.T = len(hist), int(self.lens.sum()) + pad
+        self.seq = self.hist + self.lens                           # the step's tokens are already in the exact cache
         pages = -(-self.seq // BLOCK)
         self.cols = int(pages.max())
         self.pool = int(pool or pages.sum() + 1)
@@ -55,7 +60,7 @@ class DeviceDecode:
             referenced[torch.as_tensor(perm[:used], device='cuda').long()] = True
             cache[~referenced] = POS_INF                           # page 0 and every unreferenced page
             self.tables[w], self.lat[w] = table, cache
-        first, last = np.maximum(self.seq - 1 - W, 0) // BLOCK, (self.seq - 1) // BLOCK
+        first, last = np.maximum(self.hist - W, 0) // BLOCK, (self.seq - 1) // BLOCK
         ex_pool = int((last - first + 1).sum()) + 1
         self.ex_table = np.zeros((self.R, self.cols), np.int32)
         perm = np.random.default_rng(seed).permutation(np.arange(1, ex_pool)).astype(np.int32)
@@ -79,21 +84,30 @@ class DeviceDecode:
         self.dev_ex_table = torch.as_tensor(self.ex_table, device='cuda')
 
     def context(self, layer, ops, splits_by_width):
-        positions = np.concatenate((self.hist, np.ones(self.T - self.R, np.int64)))
+        positions = np.concatenate([np.arange(h, h + n) for h, n in zip(self.hist, self.lens)] +
+                                   [np.ones(self.T - int(self.lens.sum()), np.int64)])
         ws = ops.S6Workspace.for_splits(H, self.T, splits_by_width)
-        return layer.StepContext(torch.as_tensor(positions, device='cuda'),
-                                 torch.arange(self.R + 1, dtype=torch.int32, device='cuda'),
-                                 torch.as_tensor(self.seq.astype(np.int32), device='cuda'), 1, self.T, {}, SCALE,
-                                 ops.HIP_BACKENDS, ws, splits_by_width[512], window=W,
+        return layer.StepContext(torch.as_tensor(positions, device='cuda'), torch.as_tensor(self.qsl, device='cuda'),
+                                 torch.as_tensor(self.seq.astype(np.int32), device='cuda'), int(self.lens.max()),
+                                 self.T, {}, SCALE, ops.HIP_BACKENDS, ws, splits_by_width[512], window=W,
                                  max_seqlen_k=int(self.seq.max()), kv_splits_by_width=splits_by_width)
 
     def run(self, layer, ctx, loop):
         w = 256 if loop == 0 else 512
-        return layer.attend(self.sl, loop, self.q_lat[loop], self.q_rope[loop], None, None, self.lat[w],
+        k_rope = v = None
+        if not (self.lens == 1).all():   # the reference's branch reads the chunk from k_rope / v
+            req, valid, _, _ = O.step_context(self.qsl, self.seq, self.T, W)
+            pos = np.where(valid, self.hist[req] + np.arange(self.T) - self.qsl[req], 0)
+            pages = torch.as_tensor(self.ex_table[req, pos // BLOCK], device='cuda').long()
+            rows = self.exact[loop][pages, :, torch.as_tensor(pos % BLOCK, device='cuda')]   # [T, H, 2D]
+            k_rope, v = rows[..., :D].contiguous(), rows[..., D:].contiguous()
+        return layer.attend(self.sl, loop, self.q_lat[loop], self.q_rope[loop], k_rope, v, self.lat[w],
                             self.dev_tables[w], None, None, ctx, (self.exact[loop], self.dev_ex_table))
 
     def oracle(self, loop):
-        """O.attend_decode on host copies of the pages the rows reference (the table remapped to them)."""
+        """The oracle composite on host copies of the pages the rows reference (the table remapped to them):
+        O.attend_decode for a decode step, O.attend_chunk (the reference's causal chunk of k_rope / v + window
+        history + latent history) otherwise, with the chunk's k / v read back from the exact cache."""
         w = 256 if loop == 0 else 512
         table = self.tables[w]
         ctx_lat = np.maximum(self.hist - W, 0)
@@ -102,28 +116,37 @@ class DeviceDecode:
         remap = np.zeros(self.pool, np.int64)
         remap[used] = np.arange(used.size)
         lat = self.lat[w][torch.as_tensor(used, device='cuda').long()].float().cpu().numpy()
-        tok_table = np.zeros((self.T, self.cols), np.int64)
-        tok_table[:self.R] = remap[table]
-        ctx_lat_t = np.zeros(self.T, np.int64)
-        ctx_lat_t[:self.R] = ctx_lat
+        req, valid, ctx, ctx_lat_t = O.step_context(self.qsl, self.seq, self.T, W)
+        tok_table = np.where(valid[:, None], remap[table][req], 0)
         ex = host_f32(self.exact[loop])
         B = host_f32(self.sl.readers(loop)[1])
-        invalid = np.arange(self.T) >= self.R
-        return O.attend_decode(host_f32(self.q_lat[loop]), host_f32(self.q_rope[loop]), B, lat[..., :w], lat[..., w:],
-                               tok_table, ctx_lat_t, ex[..., :D], ex[..., D:], self.ex_table,
-                               np.arange(self.R + 1), self.seq, W, SCALE, invalid, rounding=False)
+        q_lat, q_rope = host_f32(self.q_lat[loop]), host_f32(self.q_rope[loop])
+        if (self.lens == 1).all():
+            return O.attend_decode(q_lat, q_rope, B, lat[..., :w], lat[..., w:], tok_table, ctx_lat_t, ex[..., :D],
+                                   ex[..., D:], self.ex_table, self.qsl, self.seq, W, SCALE, ~valid, rounding=False)
+        k_rope, v = np.zeros((self.T, H, D), np.float32), np.zeros((self.T, H, D), np.float32)
+        for t in np.nonzero(valid)[0]:
+            p = int(self.hist[req[t]] + t - self.qsl[req[t]])
+            row = ex[self.ex_table[req[t], p // BLOCK], :, p % BLOCK]
+            k_rope[t], v[t] = row[:, :D], row[:, D:]
+        return O.attend_chunk(q_lat, q_rope, k_rope, v, B, lat[..., :w], lat[..., w:],
+                              {'latent': tok_table, 'exact': self.ex_table[req]}, ctx, ctx_lat_t, self.qsl, W, SCALE,
+                              ~valid, ex[..., :D], ex[..., D:], rounding=False)
 
 
-def _check(case, layer, ops, splits_by_width, loops=range(4), wants=None):
+def _check(case, layer, ops, splits_by_width, loops=range(4), wants=None, fused=True):
     ctx = case.context(layer, ops, splits_by_width)
+    ctx.fused_chunks = fused
     wants = {} if wants is None else wants
+    n = int(case.lens.sum())
     for loop in loops:
-        print(f'case R={case.R} T={case.T} loop={loop} splits={splits_by_width}', flush=True)
+        print(f'case R={case.R} T={case.T} lens<={case.lens.max()} loop={loop} splits={splits_by_width} '
+              f'fused={fused}', flush=True)
         out = host_f32(case.run(layer, ctx, loop))
         if loop not in wants:
             wants[loop] = case.oracle(loop)
-        assert_attention_close(out[:case.R], wants[loop][:case.R], f'loop {loop}')
-        assert (out[case.R:] == 0).all()
+        assert_attention_close(out[:n], wants[loop][:n], f'loop {loop}')
+        assert (out[n:] == 0).all()
     return wants
 
 
@@ -158,3 +181,16 @@ def test_ragged_decode_on_full_pools(ops, layer):
     assert max(int(case.tables[w].max()) for w in WIDTHS) > 65000
     splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
     _check(case, layer, ops, splits)
+
+
+def test_short_chunk_prefill(ops, layer):
+    """Chunked prefill of 4 requests x 3 tokens on 8192 latent rows (+ the 32-row window): the K-hop-sized step,
+    on the fused path (the chunk's keys from the exact cache) and on the reference's op sequence, all four loops;
+    then a mixed step (decode rows, chunks of 2..15 tokens, a fresh prompt of 5, padding)."""
+    case = DeviceDecode([8192 + W] * 4, pad=2, seed=60, lens=[3] * 4)
+    splits = {w: ops.mi355x_kv_splits(8192 + W + 3, 12, 256, width=w) for w in WIDTHS}
+    wants = _check(case, layer, ops, splits)
+    _check(case, layer, ops, splits, wants=wants, fused=False)
+    mixed = DeviceDecode([3000, 17, 900, 0, 5000, 40, 1200], pad=3, seed=61, lens=[1, 15, 4, 5, 2, 1, 9])
+    splits = {w: ops.mi355x_kv_splits(int(mixed.seq.max()), mixed.T, 256, width=w) for w in WIDTHS}
+    _check(mixed, layer, ops, splits, loops=(0, 1))

@@ -329,37 +329,61 @@ def test_merge_lse(ops):
     assert_lse_close(host_f32(lse), want_lse)
 
 
-def _plan_restated(ctx, cap, S):
-    """The split plan's documented formula in plain Python (an independent restatement for the integer check)."""
+def _plan_restated(ctx, cap, S, qsl=None):
+    """The split plan's documented formula in plain Python (an independent restatement for the integer check): the
+    (row, chunk) items in row order, except that the rows of a request of 2..16 tokens with equal slot counts list
+    theirs chunk-major (chunk 0 of every row, then chunk 1, ...)."""
     tiles = [-(-min(int(c), cap) // 16) for c in ctx]
     T = len(ctx)
     chunk = max(1, -(-max(tiles) // S), -(-2 * sum(tiles) // (T * S)))
     used = [-(-t // chunk) for t in tiles]
     ni = T if S == 1 else -(-T * ((S + 1) // 2 + 1) // 8) * 8
+    groups, r = [], 0                                        # runs of rows listed together
+    bounds = [] if qsl is None else [(int(qsl[k]), int(qsl[k + 1])) for k in range(len(qsl) - 1)]
+    for lo, hi in bounds:
+        while r < lo:
+            groups.append([r])
+            r += 1
+        if 2 <= hi - lo <= 16 and len({used[x] for x in range(lo, hi)}) == 1:
+            groups.append(list(range(lo, hi)))
+            r = hi
+    groups += [[x] for x in range(r, T)]
+    items = []
+    for g in groups:
+        for c in range(used[g[0]]):
+            items += [(x, c) for x in g]
     rows, slots = [-1] * ni, [None] * ni
-    q = -(-sum(used) // 8)                                   # eight contiguous shares, one per XCD
-    i = 0
-    for r, u in enumerate(used):
-        for c in range(u):
-            b = (i % q) * 8 + i // q
-            rows[b], slots[b] = r, c
-            i += 1
+    q = -(-len(items) // 8)                                  # eight contiguous shares, one per XCD
+    for i, (x, c) in enumerate(items):
+        b = (i % q) * 8 + i // q
+        rows[b], slots[b] = x, c
     return chunk, used, rows, slots
 
 
-@pytest.mark.parametrize('T,S', [(1, 2), (5, 7), (64, 16), (300, 32), (8, 1024), (700, 3)])
-def test_split_plan_is_the_documented_balanced_list(ops, T, S):
+@pytest.mark.parametrize('T,S,grouped', [(1, 2, False), (5, 7, False), (64, 16, False), (300, 32, False),
+                                         (8, 1024, False), (700, 3, False), (60, 66, True), (300, 32, True)])
+def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped):
     rng = np.random.default_rng(T * 1000 + S)
     ctx = rng.integers(0, 20000, T).astype(np.int32)
     ctx[::7] = 0                                            # rows without history
+    qsl = None
+    if grouped:   # requests of 1..20 tokens, most with one length per request (short chunks), two padding rows
+        lens = rng.integers(1, 21, T)
+        qsl = np.concatenate(([0], np.cumsum(lens)))
+        qsl = qsl[qsl <= T - 2].astype(np.int32)
+        for k in range(len(qsl) - 1):
+            if k % 5:                                       # every fifth request keeps ragged lengths
+                ctx[qsl[k]:qsl[k + 1]] = ctx[qsl[k]]
     cap = 16 * 1000                                         # rows past the table's reach are not read
     lib = ops._lib.load()
     n = lib.hla_s6_split_plan_ints(T, S)
     plan = torch.full((n,), -7, dtype=torch.int32, device='cuda')
     ctx_d = dev_i32(ctx)
-    ops._lib.call('hla_s6_split_plan', ctx_d.data_ptr(), T, cap, S, plan.data_ptr(), n, ops._lib.stream())
+    qsl_d = None if qsl is None else dev_i32(qsl)
+    ops._lib.call('hla_s6_split_plan', ctx_d.data_ptr(), T, cap, S, None if qsl is None else qsl_d.data_ptr(),
+                  0 if qsl is None else len(qsl) - 1, plan.data_ptr(), n, ops._lib.stream())
     got = plan.cpu().tolist()
-    chunk, used, rows, slots = _plan_restated(ctx, cap, S)
+    chunk, used, rows, slots = _plan_restated(ctx, cap, S, qsl)
     ni = len(rows)
     assert n == 1 + T + 2 * ni
     assert got[0] == chunk and got[1:1 + T] == used
@@ -374,4 +398,5 @@ def test_split_plan_rejects_a_short_buffer(ops):
     plan = torch.empty(3, dtype=torch.int32, device='cuda')
     ctx = torch.ones(4, dtype=torch.int32, device='cuda')
     with pytest.raises(ValueError, match='need'):
-        ops._lib.call('hla_s6_split_plan', ctx.data_ptr(), 4, 1024, 8, plan.data_ptr(), plan.numel(), ops._lib.stream())
+        ops._lib.call('hla_s6_split_plan', ctx.data_ptr(), 4, 1024, 8, None, 0, plan.data_ptr(), plan.numel(),
+                      ops._lib.stream())

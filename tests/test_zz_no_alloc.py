@@ -69,7 +69,7 @@ class Step:
                  lib.ptr(ex), lib.ptr(ex[..., d:]), ex.stride(0), ex.stride(2), ex.stride(1), ex.shape[2],
                  ex.shape[0], lib.ptr(self.ex_table), self.ex_table.stride(0), self.ex_table.shape[1],
                  lib.ptr(ctx.query_start_loc), lib.ptr(ctx.seq_lens), self.R, W, lib.ptr(self.B), self.B.stride(0),
-                 self.B.stride(1), lib.ptr(ctx.invalid), self.T, H, SCALE, self.splits, lib.ptr(out), out.stride(0),
+                 self.B.stride(1), lib.ptr(ctx.invalid), self.T, H, SCALE, self.splits, 1, lib.ptr(out), out.stride(0),
                  out.stride(1), lib.stream(out.device))
         return out
 
