@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -59,6 +59,10 @@ SIGNATURES = {
                             I64, I64, I64, P, P],
     'hla_s6_masked_history': [P, I64, I64, P, P, I64, I64, P, I64, P, I32, I32, I32, I32, F32, I32, P, I64, P, I64,
                               I64, P, P],
+    'hla_s6_hf_chunk_forward': [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P, I64, I32, I32, I32, I32, F32,
+                                P, I64, I64, I64, P, I64, I64, P],
+    'hla_s6_hf_chunk_backward': [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, I64, P, I64, I32, I32, I32, I32,
+                                 F32, P, I64, I64, I64, P, I64, I64, P, I64, I64, I64, P, P, P, P, P, I64, I64, I64, P],
     'hla_s6_khop_backward_workspace': [I32, I32, I32, I32, I32],
     'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
                              P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,

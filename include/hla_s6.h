@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 5
+#define HLA_S6_ABI_VERSION 6
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -365,6 +365,27 @@ int hla_s6_masked_history(const void *q, int64_t q_sb, int64_t q_sh, const void 
                           int32_t N, int32_t num_heads, int32_t width, float scale, int32_t num_splits,
                           float *workspace, int64_t workspace_floats, void *z, int64_t z_sb, int64_t z_sh,
                           float *lse, void *stream);
+
+/* ---- a11: the HF rolling engine's current-chunk attention with backward ----------------------------------
+ * Replaces the exact part of batched_engine.mixed_attention (hla/latent/batched_engine.py:156-162): per batch row
+ * and head, one softmax of the chunk's queries over its keys, q / k / v [B, 16, n, 128] bf16 (strides (sb, sh, si),
+ * unit last) already RoPE'd, scores scaled by `scale`; valid [B, n] bytes (row stride valid_sb): a valid query i
+ * sees the valid keys j <= i, an invalid query every key of the chunk (batched_engine.py:157-160). Forward: o
+ * [B, 16, n, 128] fp32, lse [B, 16, n] fp32 (natural log, strides (l_sb, l_sh, 1)); one launch. Backward: from dout
+ * (fp32, o's layout) and dlse (nullable, lse's layout): delta = dout . o into `delta` (lse's layout), then dq, dk,
+ * dv fp32 [B, 16, n, 128] (strides (g_sb, g_sh, g_si)); two launches. */
+int hla_s6_hf_chunk_forward(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_si, const void *k, int64_t k_sb,
+                            int64_t k_sh, int64_t k_si, const void *v, int64_t v_sb, int64_t v_sh, int64_t v_si,
+                            const uint8_t *valid, int64_t valid_sb, int32_t B, int32_t heads, int32_t n,
+                            int32_t head_dim, float scale, float *o, int64_t o_sb, int64_t o_sh, int64_t o_si,
+                            float *lse, int64_t l_sb, int64_t l_sh, void *stream);
+int hla_s6_hf_chunk_backward(const void *q, int64_t q_sb, int64_t q_sh, int64_t q_si, const void *k, int64_t k_sb,
+                             int64_t k_sh, int64_t k_si, const void *v, int64_t v_sb, int64_t v_sh, int64_t v_si,
+                             const uint8_t *valid, int64_t valid_sb, int32_t B, int32_t heads, int32_t n,
+                             int32_t head_dim, float scale, const float *o, int64_t o_sb, int64_t o_sh, int64_t o_si,
+                             const float *lse, int64_t l_sb, int64_t l_sh, const float *dout, int64_t d_sb,
+                             int64_t d_sh, int64_t d_si, const float *dlse, float *delta, float *dq, float *dk,
+                             float *dv, int64_t g_sb, int64_t g_sh, int64_t g_si, void *stream);
 
 #ifdef __cplusplus
 }

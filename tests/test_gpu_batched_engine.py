@@ -1,5 +1,5 @@
 """The HF rolling engine's joint attention (``batched_engine.mixed_attention``, hla/latent/batched_engine.py:154-182)
-with the latent history on the K-hop kernels, against the oracle's float64 joint softmax (``O.mixed_attention``, one
+with the current chunk on the HIP chunk kernels and the latent history on the K-hop kernels, against the oracle's float64 joint softmax (``O.mixed_attention``, one
 softmax over the concatenated [history block scores || causal current scores]) and its gradient
 (``O.mixed_attention_backward``), both pinned on the CPU by per-query brute force and finite differences.
 
@@ -90,7 +90,8 @@ def f64(t):
 
 @pytest.mark.parametrize('loop', [0, 2])
 @pytest.mark.parametrize('B,n,sizes,valid_kind', [(2, 16, (160,), 'all'), (3, 9, (64, 48), 'left'),
-                                                  (2, 33, (96, 37), 'holes'), (2, 7, (), 'left')])
+                                                  (2, 33, (96, 37), 'holes'), (2, 7, (), 'left'),
+                                                  (2, 130, (), 'holes'), (1, 300, (80,), 'left')])
 def test_mixed_attention_matches_the_oracle(loop, B, n, sizes, valid_kind):
     sl, q, k, v, cos, sin, valid, blocks, masks = make_case(11 * n + loop, B, n, sizes, loop, valid_kind)
     print(f'case loop={loop} B={B} n={n} blocks={sizes} valid={valid_kind}', flush=True)
