@@ -1406,11 +1406,14 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
 // out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for TB tokens of one head per workgroup (4, or
 // 1 for small steps so that the split reduction spreads over enough workgroups):
 //   1. o_hist: LSE reduction of the split partials (or the direct bf16 output with one split), rounded to bf16 as the
-//      history op's output is, kept in LDS;
-//   2. the B_t product as a GEMV: wave q sums rows [q*R/4, (q+1)*R/4) of B[h]; lane (g, c) = (lane/16, lane%16)
-//      reads row 4*step + g, output columns [8c, 8c+8) (one 16-byte load: a wave instruction covers 4 whole B rows)
-//      and accumulates TB x 8 outputs; the 16 partials of each output (4 waves x 4 lane groups) are summed in LDS;
-//   3. the merge_states LSE merge with the window partial (invalid rows zeroed), rounded once to bf16.
+//      history op's output is, kept in LDS as bf16 pairs;
+//   2. the B_t product as a GEMV on bf16 pairs: wave q sums rows [q*R/4, (q+1)*R/4) of B[h]; lane (g, c) =
+//      (lane/16, lane%16) reads rows k = 8*step + 2g and k + 1, output columns [8c, 8c+8) (16-byte loads: a wave
+//      instruction covers 4 whole B rows), pairs the two rows' values of each column (v_perm_b32) and accumulates
+//      TB x 8 outputs with v_dot2_f32_bf16 against (o[k], o[k+1]) (exact bf16 products, fp32 sums); the 16 partials
+//      of each output (4 waves x 4 lane groups) are summed in LDS;
+//   3. the merge_states LSE merge with the window partial (invalid rows zeroed), rounded once to bf16. The window
+//      partial of a thread's merge item is loaded at the start, with the split partials.
 
 struct EpilogueParams {
   int T, S;
@@ -1437,10 +1440,11 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
   constexpr int ITEMS = TB * C4;                               // combine items (token, 4 columns)
   constexpr int IPT = ITEMS > kThreads ? ITEMS / kThreads : 1;  // items per thread
   constexpr int SG = ITEMS < kThreads ? kThreads / ITEMS : 1;   // slot groups: threads sharing one item's slots
-  constexpr int NB = R / 16;                                   // B rows per lane in the GEMV
-  constexpr int PB = NB <= 32 ? NB : 0;                        // rows prefetched into registers
+  constexpr int NB = R / 32;                                   // GEMV steps: two B rows per lane each
+  constexpr int PB = NB <= 16 ? NB : 0;                        // steps whose rows are prefetched into registers
   static_assert(ITEMS % kThreads == 0 || kThreads % ITEMS == 0, "items must tile the workgroup");
-  __shared__ float o_s[TB][R];
+  static_assert(TB * D / 2 <= kThreads, "one merge item per thread");
+  __shared__ uint32_t o_s[TB][R / 2];  // bf16 pairs
   __shared__ float lse_s[TB];
   __shared__ floatx4 part[16][TB][D / 4];
   __shared__ float slot_lse[TB][kEpiSlots<TB>];  // lse of every slot of the TB tokens for head h
@@ -1450,8 +1454,19 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
   const int h = blockIdx.y, t0 = blockIdx.x * TB, tid = threadIdx.x;
   const int S = a.S;
   const int q = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
-  u32x4 bv[PB > 0 ? PB : 1];
-  const uint16_t* brow = a.B + (int64_t)h * a.b_sh + (int64_t)(q * (R / 4) + g) * a.b_sr + 8 * c;
+  u32x4 bv[PB > 0 ? PB : 1][2];
+  const uint16_t* brow = a.B + (int64_t)h * a.b_sh + (int64_t)(q * (R / 4) + 2 * g) * a.b_sr + 8 * c;
+  // the window partial of this thread's merge item (token t0 + tid / 64, columns 2 * (tid % 64) and + 1)
+  const int m_tb = tid / (D / 2), m_dp = tid % (D / 2), m_t = t0 + m_tb;
+  const bool m_live = tid < TB * D / 2 && m_t < a.T;
+  float w_lse = -INFINITY;
+  uint32_t w_o = 0u;
+  bool w_inv = false;
+  if (m_live) {
+    w_lse = a.lse_win[(int64_t)h * a.T + m_t];
+    w_o = *reinterpret_cast<const uint32_t*>(a.o_win + ((int64_t)m_t * kHeads + h) * D + 2 * m_dp);
+    w_inv = a.invalid && a.invalid[m_t];
+  }
 
   // 1. history output of the TB tokens. Every load of the phase is issued before the first wait: the split
   //    partials and their lse (an empty split left no partial; a select drops it, so its bytes never matter),
@@ -1518,7 +1533,10 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       load(0, all);
     }
 #pragma unroll
-    for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
+    for (int step = 0; step < PB; ++step) {
+      bv[step][0] = ld16(brow + (int64_t)(8 * step) * a.b_sr);
+      bv[step][1] = ld16(brow + (int64_t)(8 * step + 1) * a.b_sr);
+    }
     __syncthreads();
     if (tid < TB) {
       int u = 0;
@@ -1570,26 +1588,28 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       if (item >= ITEMS) continue;  // slot groups past the first have merged into it
       const int tb = item / C4, c4 = item % C4;
       const floatx4 o = m[it] == -INFINITY ? floatx4{0.f, 0.f, 0.f, 0.f} : acc[it] * (1.0f / den[it]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o_s[tb][4 * c4 + e] = rbf(o[e]);
+      o_s[tb][2 * c4] = pack2(o[0], o[1]);
+      o_s[tb][2 * c4 + 1] = pack2(o[2], o[3]);
       if (c4 == 0) lse_s[tb] = m[it] == -INFINITY ? -INFINITY : m[it] + logf(den[it]);
     }
   } else {
 #pragma unroll
-    for (int step = 0; step < PB; ++step) bv[step] = ld16(brow + (int64_t)(4 * step) * a.b_sr);
+    for (int step = 0; step < PB; ++step) {
+      bv[step][0] = ld16(brow + (int64_t)(8 * step) * a.b_sr);
+      bv[step][1] = ld16(brow + (int64_t)(8 * step + 1) * a.b_sr);
+    }
     if (tid < TB) lse_s[tid] = t0 + tid < a.T ? a.lse_hist[(int64_t)h * a.T + t0 + tid] : -INFINITY;
     for (int item = tid; item < TB * R / 2; item += kThreads) {
       const int tb = item / (R / 2), c2 = item % (R / 2), t = t0 + tb;
-      const uint32_t w2 = t < a.T ? *reinterpret_cast<const uint32_t*>(a.o_hist + ((int64_t)t * kHeads + h) * R + 2 * c2)
-                                  : 0u;
-      o_s[tb][2 * c2] = lo_bf(w2);
-      o_s[tb][2 * c2 + 1] = hi_bf(w2);
+      o_s[tb][c2] = t < a.T ? *reinterpret_cast<const uint32_t*>(a.o_hist + ((int64_t)t * kHeads + h) * R + 2 * c2)
+                            : 0u;
     }
   }
   __syncthreads();
 
   // 2. GEMV with B[h]
   {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     float acc[TB][8];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
@@ -1597,19 +1617,21 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       for (int e = 0; e < 8; ++e) acc[tb][e] = 0.f;
 #pragma unroll
     for (int step = 0; step < NB; ++step) {
-      const u32x4 bs = PB > 0 ? bv[step < PB ? step : 0] : ld16(brow + (int64_t)(4 * step) * a.b_sr);
-      float b[8];
+      const u32x4 b0 = PB > 0 ? bv[step < PB ? step : 0][0] : ld16(brow + (int64_t)(8 * step) * a.b_sr);
+      const u32x4 b1 = PB > 0 ? bv[step < PB ? step : 0][1] : ld16(brow + (int64_t)(8 * step + 1) * a.b_sr);
+      uint32_t bp[8];  // (B[k][col], B[k + 1][col]) for the lane's 8 columns
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        b[2 * e] = lo_bf(bs[e]);
-        b[2 * e + 1] = hi_bf(bs[e]);
+        bp[2 * e] = __builtin_amdgcn_perm(b1[e], b0[e], 0x05040100u);
+        bp[2 * e + 1] = __builtin_amdgcn_perm(b1[e], b0[e], 0x07060302u);
       }
-      const int r = q * (R / 4) + 4 * step + g;
+      const int k2 = (q * (R / 4) + 8 * step + 2 * g) / 2;
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
-        const float o = o_s[tb][r];
+        const bf16x2_t o = __builtin_bit_cast(bf16x2_t, o_s[tb][k2]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[tb][e] += o * b[e];
+        for (int e = 0; e < 8; ++e)
+          acc[tb][e] = __builtin_amdgcn_fdot2_f32_bf16(o, __builtin_bit_cast(bf16x2_t, bp[e]), acc[tb][e], false);
       }
     }
 #pragma unroll
@@ -1620,10 +1642,9 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
   }
   __syncthreads();
 
-  // 3. merge with the window partial
-  for (int item = tid; item < TB * D / 2; item += kThreads) {
-    const int tb = item / (D / 2), dp = item % (D / 2), t = t0 + tb;
-    if (t >= a.T) continue;
+  // 3. merge with the window partial: one item (token, column pair) per thread
+  if (m_live) {
+    const int tb = m_tb, dp = m_dp, t = m_t;
     float y0 = 0.f, y1 = 0.f;
     const float* pf = reinterpret_cast<const float*>(&part[0][tb][0]) + 2 * dp;
 #pragma unroll
@@ -1631,7 +1652,7 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       y0 += pf[p * TB * D];
       y1 += pf[p * TB * D + 1];
     }
-    float lx = lse_s[tb], lb = a.lse_win[(int64_t)h * a.T + t];
+    float lx = lse_s[tb], lb = w_lse;
     if (lx == INFINITY) lx = -INFINITY;  // +inf lse counts as empty
     if (lb == INFINITY) lb = -INFINITY;
     float peak = fmaxf(lx, lb);
@@ -1644,9 +1665,9 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
     } else {
       wx = wb = 0.f;
     }
-    const uint32_t ow = *reinterpret_cast<const uint32_t*>(a.o_win + ((int64_t)t * kHeads + h) * D + 2 * dp);
+    const uint32_t ow = w_o;
     uint32_t res = pack2(rbf(y0) * wx + lo_bf(ow) * wb, rbf(y1) * wx + hi_bf(ow) * wb);
-    if (a.invalid && a.invalid[t]) res = 0u;
+    if (w_inv) res = 0u;
     *reinterpret_cast<uint32_t*>(a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 2 * dp) = res;
   }
 }
