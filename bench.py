@@ -328,7 +328,7 @@ def secondary(args, wl, B, context, layers, queries, splits):
 
 
 # The other benchmark configurations measured by the default run (name: workload, B, context, layers, queries)
-SECONDARY = (('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, LAYERS, 1),
+SECONDARY = (('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, 1, 1),
              ('long_b8_ctx32768', 'long', 8, 32768, 1, 1),
              ('prefill_b4_q3_ctx8192', 'prefill', 4, 8192, 1, 3),
              ('prefill_b4_q512_ctx8192', 'prefill', 4, 8192, 1, 512))
@@ -688,7 +688,7 @@ def main():
     if args.workload == 'rows':
         return rows_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
-    defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, LAYERS), 'long': (8, 32768, 1),
+    defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, 1), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]
     B, context, layers = args.batch or defaults[0], args.context or defaults[1], args.layers or defaults[2]
     queries = args.queries if args.workload == 'prefill' else 1

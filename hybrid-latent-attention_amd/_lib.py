@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -24,7 +24,7 @@ SIGNATURES = {
     'hla_s6_abi_version': [],
     'hla_s6_last_error': [],
     'hla_s6_device_cus': [ctypes.c_int, ctypes.POINTER(ctypes.c_int)],
-    'hla_s6_step_metadata': [P, I32, P, I32, I32, P, P, P, P, P, P],
+    'hla_s6_step_metadata': [P, I32, P, I32, I32, P, P, P, P, P, P, P],
     'hla_s6_gather_block_table': [P, I64, I32, I32, P, I32, P, I64, P],
     'hla_s6_latent_rope': [P, I32, I32, I32, I64, I64, P, P, I32, I64, P],
     'hla_s6_absorb': [P, I32, I32, I32, I64, I64, P, I64, I64, I32, P, I64, I64, P, P, I32, I64, P],

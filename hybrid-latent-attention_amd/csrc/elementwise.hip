@@ -10,7 +10,8 @@ inline unsigned blocks_for(int64_t n, int threads) { return (unsigned)((n + thre
 
 // ---- a1: token -> request, valid, ctx, ctx_latent, history --------------------------------------
 __global__ void step_metadata_kernel(const int32_t* qsl, int R, const int32_t* seq_lens, int T, int window,
-                                     int64_t* treq, uint8_t* valid, int32_t* ctx, int32_t* ctx_lat, int32_t* hist) {
+                                     int64_t* treq, uint8_t* valid, uint8_t* invalid, int32_t* ctx, int32_t* ctx_lat,
+                                     int32_t* hist) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (hist && i < R) hist[i] = max(seq_lens[i] - (qsl[i + 1] - qsl[i]), 0);
   if (i >= T) return;
@@ -24,6 +25,7 @@ __global__ void step_metadata_kernel(const int32_t* qsl, int R, const int32_t* s
   const bool v = i < qsl[R];
   if (treq) treq[i] = req;
   if (valid) valid[i] = v ? 1 : 0;
+  if (invalid) invalid[i] = v ? 0 : 1;
   if (ctx || ctx_lat) {
     const int c = v ? max(seq_lens[req] - (qsl[req + 1] - qsl[req]), 0) : 0;
     if (ctx) ctx[i] = c;
@@ -154,7 +156,8 @@ using namespace hla;
 
 extern "C" int hla_s6_step_metadata(const int32_t* query_start_loc, int32_t num_reqs, const int32_t* seq_lens,
                                     int32_t num_tokens, int32_t window, int64_t* token_requests, uint8_t* valid,
-                                    int32_t* ctx, int32_t* ctx_latent, int32_t* history, void* stream) {
+                                    uint8_t* invalid, int32_t* ctx, int32_t* ctx_latent, int32_t* history,
+                                    void* stream) {
   HLA_REQUIRE(num_reqs >= 1 && num_tokens >= 0 && window >= 0, HLA_S6_EINVAL,
               "step_metadata: need num_reqs >= 1, num_tokens >= 0, window >= 0");
   HLA_REQUIRE(query_start_loc, HLA_S6_EINVAL, "step_metadata: null query_start_loc");
@@ -162,8 +165,8 @@ extern "C" int hla_s6_step_metadata(const int32_t* query_start_loc, int32_t num_
               "step_metadata: ctx, ctx_latent and history need seq_lens");
   const int n = max(num_tokens, num_reqs);
   hipLaunchKernelGGL(step_metadata_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, as_stream(stream),
-                     query_start_loc, num_reqs, seq_lens, num_tokens, window, token_requests, valid, ctx, ctx_latent,
-                     history);
+                     query_start_loc, num_reqs, seq_lens, num_tokens, window, token_requests, valid, invalid, ctx,
+                     ctx_latent, history);
   return check_launch("step_metadata");
 }
 

@@ -223,6 +223,8 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
   __shared__ int64_t red[8];
   __shared__ int wsum[4];
   __shared__ int carry_s;
+  __shared__ int xs[256];       // inclusive prefix of the used slots over the rows of a block of 256
+  __shared__ int grp[256][3];   // first item of the row's group, rows in the group, row's position in it
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int chunk = split_chunk(ctx, T, cap, S, red);
   const int ni = (int)split_workgroups(T, S);
@@ -256,30 +258,42 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
     }
     if (lane == 63) wsum[wave] = x;
     __syncthreads();
-    int base = carry_s;
-    for (int w = 0; w < wave; ++w) base += wsum[w];
-    const int first = base + x - u;
-    if (r < T) {
-      // position k of the row in its request's chunk-major group of m rows (k = 0, m = 1: row-major)
-      int k = 0, m = 1;
-      if (qsl && r < qsl[R]) {
-        const int req = request_of(qsl, R, r), g0 = qsl[req], gm = qsl[req + 1] - g0;
-        bool same = gm > 1 && gm <= kPlanGroup;
-        for (int e = 0; same && e < gm; ++e) same = used[g0 + e] == u;
-        if (same) {
-          k = r - g0;
-          m = gm;
-        }
-      }
-      const int group0 = first - k * u;  // the group's first item (its rows' ranges are contiguous)
-      for (int c = 0; c < u; ++c) {
-        const int i = group0 + c * m + k, b = (i % q) * 8 + i / q;
-        rows[b] = r;
-        slots[b] = c;
+    int local = x;  // inclusive prefix within the block
+    for (int w = 0; w < wave; ++w) local += wsum[w];
+    const int first = carry_s + local - u;
+    // position k of the row in its request's chunk-major group of m rows (k = 0, m = 1: row-major)
+    int k = 0, m = 1;
+    if (r < T && qsl && r < qsl[R]) {
+      const int req = request_of(qsl, R, r), g0 = qsl[req], gm = qsl[req + 1] - g0;
+      bool same = gm > 1 && gm <= kPlanGroup;
+      for (int e = 0; same && e < gm; ++e) same = used[g0 + e] == u;
+      if (same) {
+        k = r - g0;
+        m = gm;
       }
     }
+    xs[tid] = local;
+    grp[tid][0] = first - k * u;  // the group's first item (its rows' ranges are contiguous)
+    grp[tid][1] = m;
+    grp[tid][2] = k;
     __syncthreads();
-    if (tid == 255) carry_s = base + x;
+    // the block's (row, chunk) pairs, spread over the threads: pair p belongs to the first row whose inclusive
+    // prefix exceeds p
+    const int pairs = xs[255];
+    for (int p = tid; p < pairs; p += 256) {
+      int lo = 0, hi = 255;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (xs[mid] > p) hi = mid;
+        else lo = mid + 1;
+      }
+      const int c = p - (lo ? xs[lo - 1] : 0);
+      const int i = grp[lo][0] + c * grp[lo][1] + grp[lo][2], b = (i % q) * 8 + i / q;
+      rows[b] = r0 + lo;
+      slots[b] = c;
+    }
+    __syncthreads();
+    if (tid == 255) carry_s += local;
     __syncthreads();
   }
 }

@@ -102,18 +102,32 @@ class StepContext:
         R = qsl.shape[0] - 1
         self.token_requests = torch.empty(num_tokens, dtype=torch.int64, device=device)
         self.valid = torch.empty(num_tokens, dtype=torch.bool, device=device)
+        self.invalid = torch.empty(num_tokens, dtype=torch.bool, device=device)
         self.ctx = torch.empty(num_tokens, dtype=torch.int32, device=device)
         self.ctx_latent = torch.empty(num_tokens, dtype=torch.int32, device=device)
         _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, _lib.ptr(seq), num_tokens, int(window or 0),
-                  _lib.ptr(self.token_requests), _lib.ptr(self.valid), _lib.ptr(self.ctx), _lib.ptr(self.ctx_latent),
-                  None, _lib.stream(device))
-        self.invalid, self.empty = ~self.valid, self.ctx == 0
-        self.empty_latent = self.ctx_latent == 0
+                  _lib.ptr(self.token_requests), _lib.ptr(self.valid), _lib.ptr(self.invalid), _lib.ptr(self.ctx),
+                  _lib.ptr(self.ctx_latent), None, _lib.stream(device))
+        self._empty = self._empty_latent = None
         self._block_tables = {}
         self._plans = {}
         self._slots = {}
         if workspace is not None:
             workspace.ensure(device)
+
+    @property
+    def empty(self):
+        """Tokens without history (``ctx == 0``), computed on first use: the fused steps never read it."""
+        if self._empty is None:
+            self._empty = self.ctx == 0
+        return self._empty
+
+    @property
+    def empty_latent(self):
+        """Tokens without latent history (``ctx_latent == 0``), computed on first use."""
+        if self._empty_latent is None:
+            self._empty_latent = self.ctx_latent == 0
+        return self._empty_latent
 
     def kv_splits(self, width):
         """History split count for a latent of ``width`` columns."""

@@ -119,7 +119,7 @@ def token_requests(query_start_loc, num_tokens):
     req = torch.empty(num_tokens, dtype=I64, device=qsl.device)
     valid = torch.empty(num_tokens, dtype=torch.bool, device=qsl.device)
     _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, None, num_tokens, 0, _lib.ptr(req), _lib.ptr(valid),
-              None, None, None, _lib.stream(qsl.device))
+              None, None, None, None, _lib.stream(qsl.device))
     return req, valid
 
 
@@ -130,8 +130,8 @@ def history_lengths(seq_lens, query_start_loc):
     seq = _int('seq_lens', seq_lens, I32)
     R = qsl.shape[0] - 1
     hist = torch.empty(R, dtype=I32, device=qsl.device)
-    _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, _lib.ptr(seq), 0, 0, None, None, None, None, _lib.ptr(hist),
-              _lib.stream(qsl.device))
+    _lib.call('hla_s6_step_metadata', _lib.ptr(qsl), R, _lib.ptr(seq), 0, 0, None, None, None, None, None,
+              _lib.ptr(hist), _lib.stream(qsl.device))
     return hist
 
 

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 6
+#define HLA_S6_ABI_VERSION 7
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -47,12 +47,13 @@ int hla_s6_device_cus(int device, int *cus);
  *   query_start_loc [num_reqs + 1] int32, seq_lens [num_reqs] int32.
  *   seq_lens may be NULL when ctx, ctx_latent and history are NULL.
  *   Outputs (each nullable): token_requests [num_tokens] int64 (clamped to num_reqs - 1),
- *   valid [num_tokens] uint8 (t < query_start_loc[num_reqs]), ctx [num_tokens] int32
+ *   valid [num_tokens] uint8 (t < query_start_loc[num_reqs]), invalid [num_tokens] uint8 (1 - valid, the
+ *   StepContext.invalid mask), ctx [num_tokens] int32
  *   (history length of the token's request, 0 on padding), ctx_latent [num_tokens] int32
  *   (max(ctx - window, 0), ctx when window == 0), history [num_reqs] int32. */
 int hla_s6_step_metadata(const int32_t *query_start_loc, int32_t num_reqs, const int32_t *seq_lens,
                          int32_t num_tokens, int32_t window, int64_t *token_requests, uint8_t *valid,
-                         int32_t *ctx, int32_t *ctx_latent, int32_t *history, void *stream);
+                         uint8_t *invalid, int32_t *ctx, int32_t *ctx_latent, int32_t *history, void *stream);
 
 /* Replaces StepContext.block_table (hla/vllm_latent/s6_layer.py:75-80):
  * out[t, c] = table[token_requests[t], c] for c < cols. */
