@@ -118,7 +118,9 @@ __global__ __launch_bounds__(64) void chunk_fwd(HfChunkParams a) {
     const bool raise = mx > m + 8.f;  // lazy rescale (the exponentials stay below 2^8)
     if (__any(raise)) {
       const float m_new = raise ? mx : m;
-      const float alpha = fast_exp2(m - m_new);
+      // 0 on the first raise (m = -inf); 1 in a column that does not raise, which may still have no visible key
+      // (a valid query after left padding, beside padding queries that see every key)
+      const float alpha = raise ? fast_exp2(m - m_new) : 1.f;
       l *= alpha;
       m = m_new;
 #pragma unroll

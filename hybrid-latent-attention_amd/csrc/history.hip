@@ -429,7 +429,7 @@ __device__ __forceinline__ void stage_b(floatx4 sacc, floatx4* sx, const uint16_
   const bool raise = mx > m + 8.f;  // false while the row has no key yet (mx = -inf)
   if (__any(raise)) {
     const float m_new = raise ? mx : m;
-    const float alpha = fast_exp2(m - m_new);  // 0 on the first raise (m = -inf)
+    const float alpha = raise ? fast_exp2(m - m_new) : 1.f;  // 0 on the first raise (m = -inf)
     l *= alpha;
     m = m_new;
 #pragma unroll
@@ -660,7 +660,7 @@ __device__ __forceinline__ void group_stage_b(const floatx4 (&sacc)[NQ], floatx4
       const bool raise = mx > m[u] + kLazy;  // per head (lane column); false while the token has no key yet
       if (__any(raise)) {
         const float m_new = raise ? mx : m[u];
-        const float alpha = fast_exp2(m[u] - m_new);  // 0 on the first raise (m = -inf)
+        const float alpha = raise ? fast_exp2(m[u] - m_new) : 1.f;  // 0 on the first raise (m = -inf)
         l[u] *= alpha;
 #pragma unroll
         for (int nt = 0; nt < G::NT; ++nt) oacc[u][nt] = oacc[u][nt] * alpha;
@@ -996,7 +996,7 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
           const bool raise = mx > m_own + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own;
-            const float alpha = fast_exp2(m_own - m_new);  // 0 on the first raise (m_own = -inf)
+            const float alpha = raise ? fast_exp2(m_own - m_new) : 1.f;  // 0 on the first raise (m_own = -inf)
             l_own *= alpha;
             m_own = m_new;
 #pragma unroll
@@ -1262,7 +1262,7 @@ __global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_
           const bool raise = mx > m_own[x] + 8.f;  // false while the row has no key yet (mx = -inf)
           if (__any(raise)) {
             const float m_new = raise ? mx : m_own[x];
-            const float alpha = fast_exp2(m_own[x] - m_new);  // 0 on the first raise (m_own = -inf)
+            const float alpha = raise ? fast_exp2(m_own[x] - m_new) : 1.f;  // 0 on the first raise (m_own = -inf)
             l_own[x] *= alpha;  // this lane's share of the row sum
             m_own[x] = m_new;
 #pragma unroll

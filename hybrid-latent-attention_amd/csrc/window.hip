@@ -67,12 +67,15 @@ int launch_exact(const ExactParams& p, hipStream_t stream, const char* what) {
   return check_launch(what);
 }
 
-// Causal attention inside each request's chunk: one wave per (16 consecutive tokens, head). The tokens of a wave
-// that belong to one request read that request's keys once, in tiles of 16:
-//   S^T[16 keys x 16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows straight from memory as the A
-//   operand, Q^T in registers), causal mask key <= query, online softmax per query column, and
-//   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x16_bf16 with V^T from a wave-private LDS copy read by
-//   ds_read_b64_tr_b16.
+// Causal attention inside each request's chunk: one workgroup of kChunkWaves waves per (kChunkQ consecutive tokens,
+// head), 16 queries per wave. The tokens of a workgroup that belong to one request read that request's keys in tiles
+// of 16 rows, each tile loaded once for the workgroup (one coalesced 16-byte piece of K and of V per thread, a few
+// tiles ahead in registers) and staged in LDS, double-buffered, one barrier per tile. Each wave then computes
+//   S^T[16 keys x 16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows from LDS as the A operand, Q^T in
+//   registers), causal mask key <= query, online softmax per query column, and
+//   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x16_bf16 with V^T read from LDS by ds_read_b64_tr_b16,
+// skipping the tiles wholly past its last query. Sharing the tiles over 64 queries instead of 16 cuts the L2 requests
+// of the causal re-reads fourfold, which bound the one-wave-per-16-tokens form.
 struct ChunkParams {
   const uint16_t *q, *k, *v;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;
@@ -89,15 +92,34 @@ struct ChunkParams {
   int bt_cols;
   const int32_t* seq_lens;
   int window;
+  int nblk, heads;  // token blocks of kChunkQ and heads: the grid is nblk * heads workgroups
 };
 
-constexpr int kChunkVS = kExactDim + 16;  // LDS row stride of the V tile (conflict-free transposed reads)
+constexpr int kChunkVS = kExactDim + 16;    // LDS row stride of the V tile (conflict-free transposed reads)
+constexpr int kChunkKS = kExactDim + 8;     // LDS row stride of the K tile (conflict-free 16-byte row reads)
+constexpr int kChunkWaves = 4;              // waves per workgroup, 16 queries each
+constexpr int kChunkQ = 16 * kChunkWaves;   // queries per workgroup
+constexpr int kChunkDepth = 4;              // key tiles in flight (registers) per thread
 
 template <bool kWin>
-__global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vs[16 * kChunkVS];
-  const int lane = threadIdx.x, hq = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, t_begin = blockIdx.x * 16, t_end = min(t_begin + 16, a.T);
+__global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
+  __shared__ __attribute__((aligned(16))) uint16_t ks_l[2][16 * kChunkKS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_l[2][16 * kChunkVS];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hq = lane & 15, g = lane >> 4;
+  // Workgroup b runs on XCD b % 8 (workgroups are dealt to the XCDs round-robin). With a multiple of 8 heads, the
+  // token blocks of head h all run on XCD h % 8, so the re-reads of a request's K/V rows by its token blocks hit
+  // that XCD's L2; an XCD takes its heads' token blocks last to first (the longest causal rows first).
+  const int b = blockIdx.x;
+  int h, tb;
+  if (a.heads % 8 == 0) {
+    const int k = b >> 3;
+    h = (b & 7) + 8 * (k / a.nblk);
+    tb = a.nblk - 1 - k % a.nblk;
+  } else {
+    h = b / a.nblk;
+    tb = a.nblk - 1 - b % a.nblk;
+  }
+  const int t_begin = tb * kChunkQ, t_end = min(t_begin + kChunkQ, a.T);
   const int valid_end = min(t_end, a.qsl[a.num_reqs]);
   for (int tp = t_begin; tp < t_end;) {
     int count, kb;
@@ -121,7 +143,10 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
       w_hi = max(min(w_hi, a.bt_cols * src.block_size), w_lo);  // never negative: the chunk tiles follow
       src.table_row = a.bt + (int64_t)r * a.bt_stride;
     }
-    const int tq = tp + min(hq, count - 1);   // query of this lane's column
+    // this wave's queries [qw, qw + cw) of the pass; a wave without one still takes part in the tile barriers
+    const int qw = tp + 16 * wave, cw = max(0, min(count - 16 * wave, 16));
+    const int last_q = qw + cw - 1;
+    const int tq = cw > 0 ? qw + min(hq, cw - 1) : tp;  // query of this lane's column
     u32x4 qb[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) qb[i] = ld16(a.q + (int64_t)tq * a.q_st + (int64_t)h * a.q_sh + 32 * i + 8 * g);
@@ -129,59 +154,50 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
-    const int q_pos = tp + hq;  // this column's query token (keys <= q_pos are visible)
+    const int q_pos = qw + hq;  // this column's query token (keys <= q_pos are visible)
     const int nwt = (w_hi - w_lo + 15) / 16;  // window tiles, taken before the chunk's (one online softmax)
     const int nct = ke > kb ? (ke - kb + 15) / 16 : 0;
-    for (int ti = 0; ti < nwt + nct; ++ti) {
+    // this thread's pieces of tile ti: row tid / 16, bytes 16 * (tid % 16) of K and of V (rows past the tile's
+    // keys zeroed)
+    auto load = [&](int ti, u32x4& kx, u32x4& vx) {
       const bool wt = kWin && ti < nwt;
       const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
       const int kend = wt ? w_hi : ke;
-      u32x4 kA[4], vr[4];
+      const int row = tid >> 4, d0 = (tid & 15) * 8, key = min(k0 + row, kend - 1);
       if (wt) {
         const uint16_t *kp, *vp;
-        src.rows(min(k0 + hq, kend - 1), h, 8 * g, kp, vp);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kA[i] = ld16(kp + 32 * i);
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-          const int c = it * 64 + lane, row = c >> 4;
-          src.rows(min(k0 + row, kend - 1), h, (c & 15) * 8, kp, vp);
-          const u32x4 x = ld16(vp);
-          vr[it] = k0 + row < kend ? x : u32x4{0u, 0u, 0u, 0u};
-        }
+        src.rows(key, h, d0, kp, vp);
+        kx = ld16(kp);
+        vx = ld16(vp);
       } else {
-        const int key = min(k0 + hq, ke - 1);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) kA[i] = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + 32 * i + 8 * g);
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {  // V rows k0 .. k0+15: chunk c = it*64 + lane is row c/16, piece c%16
-          const int c = it * 64 + lane, row = c >> 4;
-          const int key2 = min(k0 + row, ke - 1);
-          const u32x4 x = ld16(a.v + (int64_t)key2 * a.v_st + (int64_t)h * a.v_sh + (c & 15) * 8);
-          vr[it] = k0 + row < ke ? x : u32x4{0u, 0u, 0u, 0u};
-        }
+        kx = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + d0);
+        vx = ld16(a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + d0);
       }
+      if (k0 + row >= kend) kx = vx = u32x4{0u, 0u, 0u, 0u};
+    };
+    // this wave's part of tile ti from LDS: S^T, causal mask, online softmax, O^T += V^T P^T
+    auto compute = [&](int ti, const uint16_t* ks, const uint16_t* vs) {
+      const bool wt = kWin && ti < nwt;
+      const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
+      const int kend = wt ? w_hi : ke;
+      if (cw == 0 || (!wt && k0 > last_q)) return;  // no query of the wave sees a key of the tile (wave-uniform)
       floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s = mfma16x16x32(kA[i], qb[i], s);
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int c = it * 64 + lane;
-        st16(vs + (c >> 4) * kChunkVS + (c & 15) * 8, vr[it]);
-      }
+      for (int i = 0; i < 4; ++i)
+        s = mfma16x16x32(*reinterpret_cast<const u32x4*>(ks + hq * kChunkKS + 32 * i + 8 * g), qb[i], s);
       float sc[4];
-      // wave-uniform: every key of the tile is visible to every query of the pass (a window tile inside the
-      // window, or a chunk tile wholly before the pass's first query)
-      const bool full = wt ? k0 + 16 <= kend : k0 + 16 <= ke && k0 + 15 <= tp;
+      // wave-uniform: every key of the tile is visible to every query of the wave (a window tile inside the
+      // window, or a chunk tile wholly before the wave's first query)
+      const bool full = wt ? k0 + 16 <= kend : k0 + 16 <= ke && k0 + 15 <= qw;
       if (full) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = hq < count ? s[r] * a.scale_log2 : -INFINITY;
+        for (int r = 0; r < 4; ++r) sc[r] = hq < cw ? s[r] * a.scale_log2 : -INFINITY;
       } else {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int key = k0 + 4 * g + r;
           const bool vis = wt ? key < kend : key < ke && key <= q_pos;
-          sc[r] = (vis && hq < count) ? s[r] * a.scale_log2 : -INFINITY;
+          sc[r] = (vis && hq < cw) ? s[r] * a.scale_log2 : -INFINITY;
         }
       }
       // (scores are finite or -inf: masked keys never reach a maximum); the running maximum is raised lazily, only
@@ -191,7 +207,9 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
       const bool raise = mx > m + 8.f;  // false while the column has no visible key (mx = -inf)
       if (__any(raise)) {
         const float m_new = raise ? mx : m;
-        const float alpha = fast_exp2(m - m_new);  // 0 on the first raise (m = -inf)
+        // 0 on the first raise (m = -inf); 1 in a column that does not raise, which may still have no visible key
+        // (m = -inf: a column past the pass's queries)
+        const float alpha = raise ? fast_exp2(m - m_new) : 1.f;
         l *= alpha;
         m = m_new;
 #pragma unroll
@@ -212,10 +230,33 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
         const short4v va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
         oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
       }
+    };
+    // kChunkDepth register sets in rotation: set d holds tiles d, d + kChunkDepth, ... and is reloaded as soon as
+    // its tile is in LDS (compile-time indices: no register copies). LDS buffer ti % 2 is rewritten two tiles later,
+    // after the barrier that every wave passes only once it has computed the tile before
+    const int ntl = nwt + nct;
+    u32x4 kx[kChunkDepth], vx[kChunkDepth];
+#pragma unroll
+    for (int d = 0; d < kChunkDepth; ++d)
+      if (d < ntl) load(d, kx[d], vx[d]);
+    for (int ti0 = 0; ti0 < ntl; ti0 += kChunkDepth) {
+#pragma unroll
+      for (int d = 0; d < kChunkDepth; ++d) {
+        const int ti = ti0 + d;
+        if (ti < ntl) {  // (uniform over the workgroup)
+          uint16_t* ks = ks_l[ti & 1];
+          uint16_t* vs = vs_l[ti & 1];
+          st16(ks + (tid >> 4) * kChunkKS + (tid & 15) * 8, kx[d]);
+          st16(vs + (tid >> 4) * kChunkVS + (tid & 15) * 8, vx[d]);
+          if (ti + kChunkDepth < ntl) load(ti + kChunkDepth, kx[d], vx[d]);
+          __syncthreads();
+          compute(ti, ks, vs);
+        }
+      }
     }
     l = wave_sum16x4(l);
-    if (hq < count) {
-      const int t = tp + hq;
+    if (hq < cw) {
+      const int t = qw + hq;
       const bool any = l > 0.f;
       const float inv = any ? 1.0f / l : 0.f;
       uint16_t* op = a.out + (int64_t)t * a.o_st + (int64_t)h * a.o_sh + 4 * g;
@@ -226,6 +267,7 @@ __global__ __launch_bounds__(64) void chunk_mfma(ChunkParams a) {
       }
       if (g == 0) a.lse[(int64_t)h * a.T + t] = any ? (m + log2f(l)) * kLn2 : -INFINITY;
     }
+    __syncthreads();  // the next pass rewrites the LDS tiles
     tp += count;
   }
 }
@@ -327,7 +369,9 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
-  hipLaunchKernelGGL(chunk_mfma<false>, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0,
+  p.nblk = (num_tokens + kChunkQ - 1) / kChunkQ;
+  p.heads = num_heads;
+  hipLaunchKernelGGL(chunk_mfma<false>, dim3((unsigned)p.nblk * (unsigned)num_heads), dim3(64 * kChunkWaves), 0,
                      as_stream(stream), p);
   return check_launch("chunk_attention");
 }
@@ -387,7 +431,9 @@ extern "C" int hla_s6_chunk_window_attention(const void* q, const void* k, const
   p.bt_cols = bt_cols;
   p.seq_lens = seq_lens;
   p.window = window;
-  hipLaunchKernelGGL(chunk_mfma<true>, dim3((unsigned)((num_tokens + 15) / 16), num_heads), dim3(64), 0,
+  p.nblk = (num_tokens + kChunkQ - 1) / kChunkQ;
+  p.heads = num_heads;
+  hipLaunchKernelGGL(chunk_mfma<true>, dim3((unsigned)p.nblk * (unsigned)num_heads), dim3(64 * kChunkWaves), 0,
                      as_stream(stream), p);
   return check_launch("chunk_window_attention");
 }

@@ -77,6 +77,9 @@ def make_case(seed, B, n, sizes, loop, valid_kind):
     valid = torch.ones(B, n, dtype=torch.bool, device='cuda')
     if valid_kind == 'left':
         valid[0, :3] = False                                    # left padding
+    elif valid_kind == 'left20':
+        valid[0, :20] = False                                   # a 16-row block of padding and valid queries whose
+                                                                # first visible key lies in the block's own tile
     elif valid_kind == 'holes':
         valid[:, ::5] = False
         valid[:, 0] = True
@@ -91,7 +94,8 @@ def f64(t):
 @pytest.mark.parametrize('loop', [0, 2])
 @pytest.mark.parametrize('B,n,sizes,valid_kind', [(2, 16, (160,), 'all'), (3, 9, (64, 48), 'left'),
                                                   (2, 33, (96, 37), 'holes'), (2, 7, (), 'left'),
-                                                  (2, 130, (), 'holes'), (1, 300, (80,), 'left')])
+                                                  (2, 130, (), 'holes'), (1, 300, (80,), 'left'),
+                                                  (2, 48, (64,), 'left20')])
 def test_mixed_attention_matches_the_oracle(loop, B, n, sizes, valid_kind):
     sl, q, k, v, cos, sin, valid, blocks, masks = make_case(11 * n + loop, B, n, sizes, loop, valid_kind)
     print(f'case loop={loop} B={B} n={n} blocks={sizes} valid={valid_kind}', flush=True)
