@@ -39,14 +39,17 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop', 'rows'),
+    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop', 'rows',
+                                          'mixed'),
                    default='decode',
                    help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
                         'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
                         'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
                         'history, one layer x 4 loops; writer: the row writer and commit; export: the rollout-cache '
                         'gather; khop: multi-query history with backward (B=4, L=2880); rows: single-query history '
-                        'over contiguous rows with a key mask (B=8, 8192 rows). Only decode prints the headline line.')
+                        'over contiguous rows with a key mask (B=8, 8192 rows); mixed: the HF rolling engine\'s joint '
+                        'attention of a chunk over its history blocks with backward (B=8, 256-token chunk, blocks of '
+                        '2048 and 256 rows). Only decode prints the headline line.')
     p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 32 / 8 / 4 by workload)')
     p.add_argument('--context', type=int, default=0, help='history tokens before the step (default by workload)')
     p.add_argument('--queries', type=int, default=512, help='new tokens per request of --workload prefill')
@@ -643,6 +646,102 @@ def rows_workload(args, pkg, device):
                       'cpu_baseline': base}), flush=True)
 
 
+class EngineLatent:
+    """Random-init latent module of one layer with the interface the HF rolling engine's attention reads
+    (``register.LatentLayer``: ``readers``, ``query``, ``fields``, ``head_dim``): readers A_t / B_t per loop (loop 0
+    at the loop-1 width), the latent query RoPE'd with the teacher's frequencies folded over the latent width, and
+    the packed rows ``[K 512 | V 512 | K1 256 | V1 256]``."""
+
+    def __init__(self, pkg, device, gen):
+        w = lambda *s: (torch.randn(*s, generator=gen, device=device) / math.sqrt(s[-2])).to(torch.bfloat16)
+        self.be, self.head_dim = pkg.batched_engine, HEAD_DIM
+        self.A = [w(HEADS, HEAD_DIM, RANK1)] + [w(HEADS, HEAD_DIM, RANK) for _ in range(3)]
+        self.B = [w(HEADS, RANK1, HEAD_DIM)] + [w(HEADS, RANK, HEAD_DIM) for _ in range(3)]
+
+    def readers(self, loop):
+        return self.A[loop], self.B[loop], RANK1 if loop == 0 else RANK
+
+    def query(self, loop, q, cos, sin):
+        A, _, rank = self.readers(loop)
+        idx = torch.arange(rank // 2, device=cos.device) % (cos.shape[-1] // 2)
+        c, s = torch.cat((cos[..., idx], cos[..., idx]), -1), torch.cat((sin[..., idx], sin[..., idx]), -1)
+        return self.be.apply_rope(torch.matmul(q.float(), A.float()[None]).to(q.dtype), c, s)
+
+    def fields(self, loop, packed):
+        if loop == 0:
+            row = packed[..., 2 * RANK:]
+            return row[..., :RANK1], row[..., RANK1:]
+        return packed[..., :RANK], packed[..., RANK:2 * RANK]
+
+
+def mixed_workload(args, pkg, device):
+    """The HF rolling engine's joint attention (``hla/latent/batched_engine.py:154-182``) of a loop-2 (main-latent)
+    chunk: B = 8 rows of a 256-token chunk, row 0 left-padded by 20 tokens, over two history blocks
+    of 2048 and 256 packed rows (``--context`` sets the first) with 80 % of their rows visible. The chunk runs on the
+    HIP chunk kernels, the blocks on the multi-query history kernels, both with backward. Times the forward and the
+    forward + backward (gradients of q, k, v and the packed rows through autograd) eagerly, and reports the
+    attention FLOPs (the chunk's causal pairs and the blocks' rows, two GEMMs each forward) per second. One JSON
+    line."""
+    be = pkg.batched_engine
+    B, n, N0 = args.batch or 8, 256, args.context or 2048
+    sizes = (N0, 256)
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    bf = lambda *s: torch.randn(*s, generator=g, device=device).to(torch.bfloat16)
+    sl = EngineLatent(pkg, device, g)
+    q, k, v = (bf(B, HEADS, n, HEAD_DIM).requires_grad_(True) for _ in range(3))
+    blocks = [(bf(B, N, 2 * RANK + 2 * RANK1) * 0.5).requires_grad_(True) for N in sizes]
+    masks = [torch.rand(B, N, generator=g, device=device) < 0.8 for N in sizes]
+    valid = torch.ones(B, n, dtype=torch.bool, device=device)
+    valid[0, :20] = False
+    pos = sum(sizes) + torch.arange(n, device=device)[None].expand(B, n)
+    inv = 1.0 / (1e6 ** (torch.arange(0, HEAD_DIM, 2, device=device).float() / HEAD_DIM))
+    ang = torch.cat((pos[..., None] * inv, pos[..., None] * inv), -1)
+    cos, sin = ang.cos(), ang.sin()
+    dout = bf(B, HEADS, n, HEAD_DIM)
+    loop = 2
+
+    def fwd():
+        with torch.no_grad():
+            be.mixed_attention(sl, loop, q, k, v, cos, sin, valid, blocks, masks)
+
+    def train():
+        out = be.mixed_attention(sl, loop, q, k, v, cos, sin, valid, blocks, masks)
+        torch.autograd.grad(out, [q, k, v] + blocks, dout)
+
+    ms_f = time_eager(fwd, args.steps, args.warmup)
+    ms_t = time_eager(train, args.steps, args.warmup)
+    pairs_chunk = B * HEADS * n * (n + 1) // 2
+    rows_hist = sum(int(m.sum().item()) for m in masks) * HEADS * n
+    flops = 4 * HEAD_DIM * pairs_chunk + 4 * RANK * rows_hist
+    base = None
+    if not args.no_cpu_baseline:
+        from oracle import s6_oracle as O
+        f32 = lambda t: t.detach().float().cpu().numpy()
+        A, Bm, _ = sl.readers(loop)
+        fields = [sl.fields(loop, b[:1]) for b in blocks]
+        hk, hv = [f32(ck) for ck, _ in fields], [f32(cv) for _, cv in fields]
+        args_o = (f32(q[:1]), f32(k[:1]), f32(v[:1]), f32(cos[:1]), f32(sin[:1]), valid[:1].cpu().numpy(), hk, hv,
+                  [m[:1].cpu().numpy() for m in masks], f32(A), f32(Bm), 1 / math.sqrt(HEAD_DIM))
+        run = lambda: O.mixed_attention(*args_o, dtype=np.float32)
+        run()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            times.append(time.perf_counter() - t0)
+        base = {'value': round(float(np.median(times)) * 1e3 * B, 1), 'unit': 'ms per forward',
+                'cores': len(os.sched_getaffinity(0)), 'kind': 'port',
+                'sample': f'numpy oracle forward (float32) of row 0 of the {B}, median of 3, scaled x{B}; '
+                          'extrapolated'}
+    tflops = flops / (ms_f * 1e9)
+    print(json.dumps({'workload': 'mixed', 'value': round(ms_f * 1000, 1), 'unit': 'us per forward', 'B': B,
+                      'chunk': n, 'blocks': list(sizes), 'loop': loop, 'flops': flops,
+                      'tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
+                      'train_ms': round(ms_t, 3), 'steps': args.steps,
+                      'data': 'synthetic (randn q, k, v, packed rows, readers; 80 % visible rows; left padding)',
+                      'cpu_baseline': base}), flush=True)
+
+
 def time_eager(fn, steps, warmup):
     """Events around ``steps`` eager calls after ``warmup`` (for work that allocates, e.g. autograd backward)."""
     for _ in range(warmup):
@@ -687,6 +786,8 @@ def main():
         return khop_workload(args, pkg, device)
     if args.workload == 'rows':
         return rows_workload(args, pkg, device)
+    if args.workload == 'mixed':
+        return mixed_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
     defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, 1), 'long': (8, 32768, 1),
                 'prefill': (4, 8192, 1)}[args.workload]
