@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -67,6 +67,12 @@ SIGNATURES = {
     'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
                              P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,
                              I32, P, I64, I32, P],
+    'hla_s6_mixed_merge_forward': [I32, I32, I32, I32, I32, P, I64, I64, I64, P, I32, P, P, P, P, I64, I64, P, I64,
+                                   I64, I64, P],
+    'hla_s6_mixed_merge_backward': [I32, I32, I32, I32, I32, P, I64, I64, I64, P, I32, P, P, P, P, I64, I64, P, I64,
+                                    I64, I64, P, I64, I64, I64, P, P, P, P, P],
+    'hla_s6_rope_rows_forward': [I32, P, P, P, P, I32, I32, I32, I32, P, P, I64, I64, I32, P],
+    'hla_s6_rope_rows_backward': [I32, P, P, P, P, I32, I32, I32, I32, P, P, I64, I64, I32, P],
 }
 
 RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64,

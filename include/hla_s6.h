@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 7
+#define HLA_S6_ABI_VERSION 8
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -387,6 +387,49 @@ int hla_s6_hf_chunk_backward(const void *q, int64_t q_sb, int64_t q_sh, int64_t 
                              const float *lse, int64_t l_sb, int64_t l_sh, const float *dout, int64_t d_sb,
                              int64_t d_sh, int64_t d_si, const float *dlse, float *delta, float *dq, float *dk,
                              float *dv, int64_t g_sb, int64_t g_sh, int64_t g_si, void *stream);
+
+/* ---- a11: the joint softmax's merge and B_t projection with backward ------------------------------------------
+ * Replaces the LSE merge and the B_t product of batched_engine.mixed_attention (hla/latent/batched_engine.py:
+ * 171-181): with the chunk part (o_c [B, H, n, 128] fp32, strides (oc_sb, oc_sh, oc_si), unit last; lse_c [B, H, n]
+ * fp32 contiguous) and `parts` (at most 8) history blocks (z[p] [B, H, n, width] bf16, strides z_strides[3p ..
+ * 3p+2] = (sb, sh, si), unit last; lse_z[p] [B, H, n] fp32 contiguous; -inf where the query sees no row of the
+ * block), w_j = exp(lse_j - logsumexp(lse_c, lse_z[0], ..)) and
+ *   out = bf16(w_c o_c + bf16(sum_p w_p z[p]) @ Bt[h])      (Bt [H, width, 128] bf16, strides (b_sh, b_sr, 1))
+ * into out [B, H, n, 128] bf16 (strides (o_sb, o_sh, o_si)); a query with no key anywhere gets 0. width in
+ * {256, 512}, head_dim 128. `z`, `z_strides`, `lse_z` (and `dz`, `dz_strides`, `d_lse_z`) are host arrays of
+ * `parts` entries holding device pointers. One launch each.
+ * Backward, from dout [B, H, n, 128] bf16 (strides (do_sb, do_sh, do_si)): d_oc = w_c dout (fp32, o_c's layout
+ * with its own strides), dz[p] = bf16(w_p dout @ Bt[h]^T) (z's layout with its own strides), d_lse_c and
+ * d_lse_z[p] = w_j (a_j - <dout, out>) with a_c = <dout, o_c>, a_p = <dout @ Bt[h]^T, z[p]> (fp32, lse layout).
+ * The gradient of Bt is not computed here. */
+int hla_s6_mixed_merge_forward(int32_t batch, int32_t num_heads, int32_t chunk, int32_t width, int32_t head_dim,
+                               const float *o_c, int64_t oc_sb, int64_t oc_sh, int64_t oc_si, const float *lse_c,
+                               int32_t parts, const void *const *z, const int64_t *z_strides,
+                               const float *const *lse_z, const void *Bt, int64_t b_sh, int64_t b_sr, void *out,
+                               int64_t o_sb, int64_t o_sh, int64_t o_si, void *stream);
+int hla_s6_mixed_merge_backward(int32_t batch, int32_t num_heads, int32_t chunk, int32_t width, int32_t head_dim,
+                                const float *o_c, int64_t oc_sb, int64_t oc_sh, int64_t oc_si, const float *lse_c,
+                                int32_t parts, const void *const *z, const int64_t *z_strides,
+                                const float *const *lse_z, const void *Bt, int64_t b_sh, int64_t b_sr,
+                                const void *dout, int64_t do_sb, int64_t do_sh, int64_t do_si, float *d_oc,
+                                int64_t doc_sb, int64_t doc_sh, int64_t doc_si, float *d_lse_c, void *const *dz,
+                                const int64_t *dz_strides, float *const *d_lse_z, void *stream);
+
+/* a11: RoPE of the chunk's queries and keys (batched_engine.py:156 with register.apply_rope, register.py:14-20):
+ * y = bf16(x cos + rotate_half(x) sin) for `count` (1 or 2) tensors x[t] [B, H, n, d] bf16 (strides x_strides[3t ..
+ * 3t+2] = (sb, sh, si), unit last) into y[t] (bf16, its own strides), cos / sin [B, n, d] broadcast over the heads
+ * (strides (c_sb, c_si, 1), both tables alike; fp32, or bf16 with trig_bf16 != 0), evaluated as torch does: each
+ * product and the sum rounded to the tables' precision, then once to bf16. Backward: dx[t] = bf16(bf16(dy cos) +
+ * rotate_half^T(bf16(dy sin))) from dy[t] fp32 (its own strides), the roundings of autograd for a bf16 x. `x`, `y`,
+ * `dy`, `dx` and their strides are host arrays of `count` entries. d even; one launch each. */
+int hla_s6_rope_rows_forward(int32_t count, const void *const *x, const int64_t *x_strides, void *const *y,
+                             const int64_t *y_strides, int32_t batch, int32_t num_heads, int32_t chunk,
+                             int32_t head_dim, const void *cos, const void *sin, int64_t c_sb, int64_t c_si,
+                             int32_t trig_bf16, void *stream);
+int hla_s6_rope_rows_backward(int32_t count, const float *const *dy, const int64_t *dy_strides, void *const *dx,
+                              const int64_t *dx_strides, int32_t batch, int32_t num_heads, int32_t chunk,
+                              int32_t head_dim, const void *cos, const void *sin, int64_t c_sb, int64_t c_si,
+                              int32_t trig_bf16, void *stream);
 
 #ifdef __cplusplus
 }

@@ -130,3 +130,28 @@ def test_mixed_attention_matches_the_oracle(loop, B, n, sizes, valid_kind):
         assert np.isfinite(a).all(), name
         r = rel_l2(a, b)
         assert r <= 2e-2, f'{name}: rel-L2 {r:.3e}'
+
+
+@pytest.mark.parametrize('trig', [torch.float32, torch.bfloat16])
+def test_chunk_rope_kernels_match_torch_bitwise(trig):
+    """The RoPE kernels of the chunk's q / k equal torch's ``apply_rope(x, cos, sin).to(bf16)`` bit for bit (fp32 or
+    bf16 tables, positions from 7 to 2000, a ragged chunk of 37 rows), and the backward kernel equals autograd's
+    gradient of ``apply_rope`` for a bf16 x bit for bit."""
+    gen = torch.Generator(device='cuda').manual_seed(3)
+    B, n = 3, 37
+    print(f'case rope trig={trig}', flush=True)
+    q, k = (torch.randn(B, HEADS, n, HD, generator=gen, device='cuda').to(torch.bfloat16) for _ in range(2))
+    cos, sin = rope_tables(B, n, torch.tensor([100, 2000, 7], device='cuda'), gen)
+    cos, sin = cos.to(trig), sin.to(trig)
+    c, s = be._trig(cos, sin, B, n, HD)
+    qr, kr = torch.empty_like(q), torch.empty_like(k)
+    be._rope_call('hla_s6_rope_rows_forward', [q, k], [qr, kr], c, s)
+    for x, y in ((q, qr), (k, kr)):
+        assert torch.equal(y, be.apply_rope(x, cos, sin).to(torch.bfloat16))
+    x = q.clone().requires_grad_(True)
+    out = be.apply_rope(x, cos, sin)
+    dy = torch.randn(out.shape, generator=gen, device='cuda').to(out.dtype)
+    want, = torch.autograd.grad(out, x, dy)
+    dx = torch.empty_like(q)
+    be._rope_call('hla_s6_rope_rows_backward', [dy.float().contiguous()], [dx], c, s)
+    assert want.dtype == torch.bfloat16 and torch.equal(dx, want)
