@@ -88,7 +88,7 @@ class _CurrentChunk(torch.autograd.Function):
 
 
 def _trig(cos, sin, B, n, D):
-    """cos / sin broadcast to ``[B, n, D]`` with one layout for both (unit last stride, even strides), fp32 or bf16."""
+    """cos / sin broadcast to ``[B, n, D]`` with one layout for both (16-byte rows), fp32 or bf16."""
     tabs = []
     for t in (cos, sin):
         t = t.expand(B, n, D)
@@ -98,7 +98,8 @@ def _trig(cos, sin, B, n, D):
     c, s = tabs
     if c.dtype != s.dtype:
         c, s = c.float(), s.float()
-    if c.stride() != s.stride() or c.stride(-1) != 1 or c.stride(0) % 2 or c.stride(1) % 2:
+    if (c.stride() != s.stride() or c.stride(-1) != 1 or c.stride(0) % 8 or c.stride(1) % 8 or c.data_ptr() % 16
+            or s.data_ptr() % 16):
         c, s = c.contiguous(), s.contiguous()
     return c, s
 
@@ -119,8 +120,8 @@ class _RopedChunk(torch.autograd.Function):
     def forward(ctx, q, k, v, valid, cos, sin, scale):
         B, H, n, D = q.shape
         qb, kb = (t.to(torch.bfloat16) for t in (q, k))
-        qb, kb = (t if t.stride(-1) == 1 and all(x % 2 == 0 for x in t.stride()[:3]) else t.contiguous()
-                  for t in (qb, kb))
+        qb, kb = (t if t.stride(-1) == 1 and all(x % 8 == 0 for x in t.stride()[:3]) and t.data_ptr() % 16 == 0
+                  else t.contiguous() for t in (qb, kb))
         c, s = _trig(cos, sin, B, n, D)
         qr, kr = (torch.empty(B, H, n, D, dtype=torch.bfloat16, device=q.device) for _ in range(2))
         _rope_call('hla_s6_rope_rows_forward', [qb, kb], [qr, kr], c, s)

@@ -5,8 +5,10 @@
 // space. With w_j = exp(lse_j - logsumexp(lse_c, lse_0, ..)) the joint output is
 //   out = w_c o_c + bf16(sum_p w_p z_p) @ B_t[h]                                   (bf16 result, fp32 sums)
 // (the reference rounds the joint latent output z to bf16 before its product with B_t, batched_engine.py:177-180).
+// The finite values these kernels round to bf16 (z, out, d z) take the hardware conversion (round to nearest even).
 //
-// merge_fwd: one workgroup per (64 queries, head, 64 output columns); 4 waves of 16 queries x 4 column tiles on
+// merge_fwd: one workgroup per (64 queries, head, 64 output columns), the two column blocks of a query block on one
+// XCD (8 workgroups apart in dispatch order); 4 waves of 16 queries x 4 column tiles on
 // v_mfma_f32_16x16x32_bf16. Every global load is issued before the first barrier: the B_t slab B[h, :, 64 columns]
 // (into LDS row-major, rows 72 elements apart; the B operand comes back by two ds_read_b64_tr_b16 per step), the
 // lse of the wave's queries and the parts' z rows (the A operand: the lane's query, 8 consecutive latent columns per
@@ -51,12 +53,17 @@ struct MixedParams {
   float* dlz[kMixParts];  // [B,H,n] fp32 contiguous
 };
 
-// lse of query q (= b * n + i) of head h: l[0] of the chunk, l[1 + p] of block p (-inf past the blocks)
-__device__ __forceinline__ void mixed_lse(const MixedParams& a, int64_t q, int h, float (&l)[1 + kMixParts]) {
-  const int64_t row = (q / a.n) * a.H * a.n + (int64_t)h * a.n + q % a.n;
+// lse of query q (= b * n + i) of head h: l[0] of the chunk, l[1 + p] of block p (-inf past the blocks). Every
+// load is unconditional (the host points the unused block slots at valid memory) so that they all issue before the
+// first wait.
+__device__ __forceinline__ void mixed_lse(const MixedParams& a, int q, int h, float (&l)[1 + kMixParts]) {
+  const int64_t row = (int64_t)(q / a.n) * a.H * a.n + (int64_t)h * a.n + q % a.n;
   l[0] = a.lc[row];
+  float v[kMixParts];
 #pragma unroll
-  for (int p = 0; p < kMixParts; ++p) l[1 + p] = p < a.parts ? a.lz[p][row] : -INFINITY;
+  for (int p = 0; p < kMixParts; ++p) v[p] = a.lz[p][row];
+#pragma unroll
+  for (int p = 0; p < kMixParts; ++p) l[1 + p] = p < a.parts ? v[p] : -INFINITY;
 }
 
 // Joint-softmax weights from those lse: w_j = exp(l_j - logsumexp(l)). A block whose query sees no row
@@ -96,7 +103,7 @@ __device__ __forceinline__ u32x4 mixed_piece(const MixedParams& a, u32x4 z0, u32
       f[2 * e + 1] = __builtin_fmaf(w[1 + p], hi_bf(zp[e]), f[2 * e + 1]);
     }
   }
-  return u32x4{pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7])};
+  return u32x4{pack2_hw(f[0], f[1]), pack2_hw(f[2], f[3]), pack2_hw(f[4], f[5]), pack2_hw(f[6], f[7])};
 }
 
 template <int R>
@@ -106,9 +113,14 @@ __global__ __launch_bounds__(256) void merge_fwd(MixedParams a) {
   extern __shared__ __attribute__((aligned(16))) uint16_t wt[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, g = lane >> 4;
-  const int h = blockIdx.y, c0 = blockIdx.x * 64;
-  const int64_t Q = (int64_t)a.B * a.n;
-  const int64_t q0 = (int64_t)blockIdx.z * 64 + wave * 16;
+  // workgroup L takes column block (L / 8) % 2 of the (head, query block) pair (L % 8) + 8 (L / 16): the two column
+  // blocks of a query block are 8 workgroups apart, so they run on one XCD and the second reads z from its L2
+  const int L = blockIdx.x;
+  const int pair = (L & 7) + 8 * (L >> 4);
+  const int h = pair % a.H, c0 = ((L >> 3) & 1) * 64;
+  const int Q = a.B * a.n;
+  const int q0 = (pair / a.H) * 64 + wave * 16;
+  if (q0 - wave * 16 >= Q) return;  // past the last query block (uniform over the workgroup)
 
   // every global load before the first use: the slab, the lse of the A row and of the 4 output rows, blocks 0 and
   // 1 of the A row (query qa, latent columns 32 kk + 8 g .. + 8), o_c of the output rows
@@ -119,7 +131,7 @@ __global__ __launch_bounds__(256) void merge_fwd(MixedParams a) {
     const int c = i * 256 + tid;
     slab[i] = ld16(bh + (int64_t)(c >> 3) * a.b_sr + (c & 7) * 8);
   }
-  const int64_t qa = q0 + l16;
+  const int qa = q0 + l16;
   const bool a_live = qa < Q;
   const int64_t ab = (a_live ? qa : 0) / a.n, ai = (a_live ? qa : 0) % a.n;
   float la[1 + kMixParts];
@@ -127,27 +139,27 @@ __global__ __launch_bounds__(256) void merge_fwd(MixedParams a) {
   float lr[4][1 + kMixParts];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t q = q0 + 4 * g + r;
+    const int q = q0 + 4 * g + r;
     mixed_lse(a, q < Q ? q : Q - 1, h, lr[r]);
   }
-  const bool two = a.parts > 1;
+  // (block 1's slot holds block 0 when there is one block: its weight is then 0; dead lanes read query 0)
   const uint16_t* zr0 = a.z[0] + ab * a.z_sb[0] + (int64_t)h * a.z_sh[0] + ai * a.z_si[0] + 8 * g;
-  const uint16_t* zr1 = two ? a.z[1] + ab * a.z_sb[1] + (int64_t)h * a.z_sh[1] + ai * a.z_si[1] + 8 * g : zr0;
+  const uint16_t* zr1 = a.z[1] + ab * a.z_sb[1] + (int64_t)h * a.z_sh[1] + ai * a.z_si[1] + 8 * g;
   u32x4 z0[CH], z1[CH];
 #pragma unroll
   for (int kk = 0; kk < CH; ++kk) {
-    z0[kk] = a_live ? ld16(zr0 + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
-    z1[kk] = a_live && two ? ld16(zr1 + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
+    z0[kk] = ld16(zr0 + 32 * kk);
+    z1[kk] = ld16(zr1 + 32 * kk);
   }
   float ocv[4][4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t q = q0 + 4 * g + r;
+    const int q = q0 + 4 * g + r;
     const bool live = q < Q;
     const int64_t b = (live ? q : 0) / a.n, i = (live ? q : 0) % a.n;
     const float* orow = a.oc + b * a.oc_sb + (int64_t)h * a.oc_sh + i * a.oc_si + c0 + l16;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) ocv[r][t] = live ? orow[16 * t] : 0.f;
+    for (int t = 0; t < 4; ++t) ocv[r][t] = orow[16 * t];
   }
   // the slab into LDS: wt[k][local column]
 #pragma unroll
@@ -157,6 +169,10 @@ __global__ __launch_bounds__(256) void merge_fwd(MixedParams a) {
   }
   float wa[1 + kMixParts];
   mixed_weights(la, wa);
+  if (!a_live) {
+#pragma unroll
+    for (int j = 0; j <= kMixParts; ++j) wa[j] = 0.f;
+  }
   u32x4 xa[CH];
 #pragma unroll
   for (int kk = 0; kk < CH; ++kk) xa[kk] = mixed_piece(a, z0[kk], z1[kk], wa, ab, h, ai, 32 * kk + 8 * g, a_live);
@@ -190,108 +206,117 @@ __global__ __launch_bounds__(256) void merge_fwd(MixedParams a) {
   // lane holds (z @ B)[q0 + 4 g + r][c0 + 16 t + l16]
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t q = q0 + 4 * g + r;
+    const int q = q0 + 4 * g + r;
     if (q >= Q) continue;
     const int64_t b = q / a.n, i = q % a.n;
     uint16_t* orow = a.out + b * a.o_sb + (int64_t)h * a.o_sh + i * a.o_si + c0 + l16;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) orow[16 * t] = f2bf(__builtin_fmaf(wc[r], ocv[r][t], acc[t][r]));
+    for (int t = 0; t < 4; ++t) orow[16 * t] = (uint16_t)pack2_hw(__builtin_fmaf(wc[r], ocv[r][t], acc[t][r]), 0.f);
   }
 }
 
-// <g_t, z_p> over the lane's 4 latent columns of tile t, and d z_p there = bf16(w_p g_t)
-__device__ __forceinline__ float mixed_dz(const uint16_t* zr, uint16_t* dzr, floatx4 gt, float wp, bool live) {
-  const uint2 zz = live ? *reinterpret_cast<const uint2*>(zr) : uint2{0u, 0u};
-  if (live) *reinterpret_cast<uint2*>(dzr) = uint2{pack2(gt[0] * wp, gt[1] * wp), pack2(gt[2] * wp, gt[3] * wp)};
-  float s = gt[0] * lo_bf(zz.x);
-  s = __builtin_fmaf(gt[1], hi_bf(zz.x), s);
-  s = __builtin_fmaf(gt[2], lo_bf(zz.y), s);
-  return __builtin_fmaf(gt[3], hi_bf(zz.y), s);
-}
-
+// Backward in phases, each issuing all of its loads before its first wait (stores to d z would otherwise keep
+// the compiler from moving later loads above them: one memory latency per tile):
+//   1. dout and o_c of the lane's query, the lse of its parts; a_c;
+//   2. g^T = B[h] . dout^T for every 16-row latent tile (loads of B only);
+//   3. per block: its z over the lane's columns, then a_p and the d z stores;
+//   4. d o_c and the d lse.
 template <int R>
 __global__ __launch_bounds__(256) void merge_bwd(MixedParams a) {
   constexpr int NT = R / 16;  // 16-row latent tiles of g
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int l16 = lane & 15, g = lane >> 4;
   const int h = blockIdx.y;
-  const int64_t Q = (int64_t)a.B * a.n;
-  const int64_t q = (int64_t)blockIdx.x * 64 + wave * 16 + l16;  // the lane's query
+  const int Q = a.B * a.n;
+  const int q = blockIdx.x * 64 + wave * 16 + l16;  // the lane's query
   const bool live = q < Q;
-  const int64_t b = (live ? q : 0) / a.n, i = (live ? q : 0) % a.n;
+  const int64_t b = (live ? q : 0) / a.n, i = (live ? q : 0) % a.n;  // dead lanes read query 0 and store nothing
 
-  // dout row piece of the lane's query: head-dim columns 32 kk + 8 g .. + 8 (the MFMA B operand), and o_c there
+  // 1. dout row piece of the lane's query: head-dim columns 32 kk + 8 g .. + 8 (the MFMA B operand), o_c there
   const uint16_t* dr = a.dout + b * a.do_sb + (int64_t)h * a.do_sh + i * a.do_si + 8 * g;
   const float* orow = a.oc + b * a.oc_sb + (int64_t)h * a.oc_sh + i * a.oc_si + 8 * g;
   u32x4 dv[4];
   floatx4 ov[4][2];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    dv[kk] = live ? ld16(dr + 32 * kk) : u32x4{0u, 0u, 0u, 0u};
-    ov[kk][0] = live ? *reinterpret_cast<const floatx4*>(orow + 32 * kk) : floatx4{0.f, 0.f, 0.f, 0.f};
-    ov[kk][1] = live ? *reinterpret_cast<const floatx4*>(orow + 32 * kk + 4) : floatx4{0.f, 0.f, 0.f, 0.f};
+    dv[kk] = ld16(dr + 32 * kk);
+    ov[kk][0] = *reinterpret_cast<const floatx4*>(orow + 32 * kk);
+    ov[kk][1] = *reinterpret_cast<const floatx4*>(orow + 32 * kk + 4);
   }
   float l[1 + kMixParts], w[1 + kMixParts];
   mixed_lse(a, live ? q : Q - 1, h, l);
   mixed_weights(l, w);
-
-  // a_c and d o_c = w_c dout
+  floatx4 dd[4][2];  // dout in fp32
   float ac = 0.f;
-  {
-    float* drow = a.doc + b * a.doc_sb + (int64_t)h * a.doc_sh + i * a.doc_si + 8 * g;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      floatx4 d0, d1;
+  for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        d0[2 * e] = lo_bf(dv[kk][e]);
-        d0[2 * e + 1] = hi_bf(dv[kk][e]);
-        d1[2 * e] = lo_bf(dv[kk][2 + e]);
-        d1[2 * e + 1] = hi_bf(dv[kk][2 + e]);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ac = __builtin_fmaf(d0[e], ov[kk][0][e], __builtin_fmaf(d1[e], ov[kk][1][e], ac));
-      if (live) {
-        *reinterpret_cast<floatx4*>(drow + 32 * kk) = d0 * w[0];
-        *reinterpret_cast<floatx4*>(drow + 32 * kk + 4) = d1 * w[0];
-      }
+    for (int e = 0; e < 2; ++e) {
+      dd[kk][0][2 * e] = lo_bf(dv[kk][e]);
+      dd[kk][0][2 * e + 1] = hi_bf(dv[kk][e]);
+      dd[kk][1][2 * e] = lo_bf(dv[kk][2 + e]);
+      dd[kk][1][2 * e + 1] = hi_bf(dv[kk][2 + e]);
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      ac = __builtin_fmaf(dd[kk][0][e], ov[kk][0][e], __builtin_fmaf(dd[kk][1][e], ov[kk][1][e], ac));
   }
   ac = wave_sum16x4(ac);
 
-  // g^T = B[h] . dout^T one 16-row latent tile at a time: lane (g, l16) holds g[q][16 t + 4 g + rr]; each tile's
-  // products with blocks 0 and 1 (and the others, loaded in turn) and their d z are done before the next tile
+  // 2. g^T tiles: lane (g, l16) holds g[q][16 t + 4 g + rr]
   const uint16_t* bh = a.Bw + (int64_t)h * a.b_sh + (int64_t)l16 * a.b_sr + 8 * g;
-  const bool two = a.parts > 1;
-  const int64_t zo0 = b * a.z_sb[0] + (int64_t)h * a.z_sh[0] + i * a.z_si[0] + 4 * g;
-  const int64_t dzo0 = b * a.dz_sb[0] + (int64_t)h * a.dz_sh[0] + i * a.dz_si[0] + 4 * g;
-  const int64_t zo1 = two ? b * a.z_sb[1] + (int64_t)h * a.z_sh[1] + i * a.z_si[1] + 4 * g : zo0;
-  const int64_t dzo1 = two ? b * a.dz_sb[1] + (int64_t)h * a.dz_sh[1] + i * a.dz_si[1] + 4 * g : dzo0;
-  const uint16_t* z1 = two ? a.z[1] : a.z[0];
-  uint16_t* dz1 = two ? a.dz[1] : a.dz[0];
-  float s0 = 0.f, s1 = 0.f, sx[kMixParts];
-#pragma unroll
-  for (int p = 0; p < kMixParts; ++p) sx[p] = 0.f;
+  floatx4 gacc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const uint16_t* br = bh + (int64_t)(16 * t) * a.b_sr;
-    floatx4 gt = {0.f, 0.f, 0.f, 0.f};
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) gt = mfma16x16x32(ld16(br + 32 * kk), dv[kk], gt);
-    s0 += mixed_dz(a.z[0] + zo0 + 16 * t, a.dz[0] + dzo0 + 16 * t, gt, w[1], live);
-    if (two) s1 += mixed_dz(z1 + zo1 + 16 * t, dz1 + dzo1 + 16 * t, gt, w[2], live);
-    for (int p = 2; p < a.parts; ++p) {
-      const int64_t zo = b * a.z_sb[p] + (int64_t)h * a.z_sh[p] + i * a.z_si[p] + 4 * g + 16 * t;
-      const int64_t dzo = b * a.dz_sb[p] + (int64_t)h * a.dz_sh[p] + i * a.dz_si[p] + 4 * g + 16 * t;
-      sx[p] += mixed_dz(a.z[p] + zo, a.dz[p] + dzo, gt, w[1 + p], live);
-    }
+    for (int kk = 0; kk < 4; ++kk) acc = mfma16x16x32(ld16(br + 32 * kk), dv[kk], acc);
+    gacc[t] = acc;
   }
-  sx[0] = s0;
-  sx[1] = s1;
+
+  // 3. per block: a_p = <g, z_p> and d z_p = bf16(w_p g)
   float ap[kMixParts];
 #pragma unroll
-  for (int p = 0; p < kMixParts; ++p) ap[p] = p < a.parts ? wave_sum16x4(sx[p]) : 0.f;
-  if (!live || g != 0) return;
+  for (int p = 0; p < kMixParts; ++p) ap[p] = 0.f;
+#pragma unroll
+  for (int p = 0; p < kMixParts; ++p) {
+    if (p >= a.parts) break;
+    const uint16_t* zr = a.z[p] + b * a.z_sb[p] + (int64_t)h * a.z_sh[p] + i * a.z_si[p] + 4 * g;
+    uint2 zz[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) zz[t] = *reinterpret_cast<const uint2*>(zr + 16 * t);
+    float sdot = 0.f;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const floatx4 gt = gacc[t];
+      sdot = __builtin_fmaf(gt[0], lo_bf(zz[t].x), sdot);
+      sdot = __builtin_fmaf(gt[1], hi_bf(zz[t].x), sdot);
+      sdot = __builtin_fmaf(gt[2], lo_bf(zz[t].y), sdot);
+      sdot = __builtin_fmaf(gt[3], hi_bf(zz[t].y), sdot);
+    }
+    ap[p] = wave_sum16x4(sdot);
+    if (live) {
+      const float wp = w[1 + p];
+      uint16_t* dzr = a.dz[p] + b * a.dz_sb[p] + (int64_t)h * a.dz_sh[p] + i * a.dz_si[p] + 4 * g;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const floatx4 gt = gacc[t];
+        *reinterpret_cast<uint2*>(dzr + 16 * t) =
+            uint2{pack2_hw(gt[0] * wp, gt[1] * wp), pack2_hw(gt[2] * wp, gt[3] * wp)};
+      }
+    }
+  }
+
+  // 4. d o_c = w_c dout, d lse_j = w_j (a_j - D)
+  if (!live) return;
+  float* drow = a.doc + b * a.doc_sb + (int64_t)h * a.doc_sh + i * a.doc_si + 8 * g;
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk) {
+    *reinterpret_cast<floatx4*>(drow + 32 * kk) = dd[kk][0] * w[0];
+    *reinterpret_cast<floatx4*>(drow + 32 * kk + 4) = dd[kk][1] * w[0];
+  }
+  if (g != 0) return;
   float D = w[0] * ac;
 #pragma unroll
   for (int p = 0; p < kMixParts; ++p)
@@ -315,18 +340,18 @@ int fill_mixed(MixedParams& m, int32_t batch, int32_t heads, int32_t chunk, int3
               width);
   HLA_REQUIRE(head_dim == kMixD, HLA_S6_EUNSUPPORTED, "mixed_merge: head_dim %d (the kernels are built for 128)",
               head_dim);
-  HLA_REQUIRE(parts >= 0 && parts <= kMixParts, HLA_S6_EUNSUPPORTED,
-              "mixed_merge: %d history blocks (at most %d per call)", parts, kMixParts);
+  HLA_REQUIRE(parts >= 1 && parts <= kMixParts, HLA_S6_EUNSUPPORTED,
+              "mixed_merge: %d history blocks (1 to %d per call)", parts, kMixParts);
   const int64_t Q = (int64_t)batch * chunk;
-  HLA_REQUIRE((Q + 63) / 64 <= 65535, HLA_S6_EUNSUPPORTED, "mixed_merge: %lld queries per head exceed the grid",
-              (long long)Q);
+  HLA_REQUIRE((Q + 63) / 64 <= 65535 && (int64_t)heads * ((Q + 63) / 64) <= (1ll << 30), HLA_S6_EUNSUPPORTED,
+              "mixed_merge: %lld queries x %d heads exceed the grid", (long long)Q, heads);
   m = MixedParams{};
   m.B = batch;
   m.H = heads;
   m.n = chunk;
   m.parts = parts;
   if (Q == 0) return HLA_S6_OK;
-  HLA_REQUIRE(oc && lse_c && Bt && (parts == 0 || (z && z_strides && lse_z)), HLA_S6_EINVAL,
+  HLA_REQUIRE(oc && lse_c && Bt && z && z_strides && lse_z, HLA_S6_EINVAL,
               "mixed_merge: null pointer argument");
   HLA_REQUIRE(al16(oc) && oc_sb % 4 == 0 && oc_sh % 4 == 0 && oc_si % 4 == 0, HLA_S6_EINVAL,
               "mixed_merge: o_c rows must be 16-byte aligned with a unit last stride");
@@ -347,6 +372,13 @@ int fill_mixed(MixedParams& m, int32_t batch, int32_t heads, int32_t chunk, int3
     m.z_sh[p] = sh;
     m.z_si[p] = si;
     m.lz[p] = lse_z[p];
+  }
+  for (int p = parts; p < kMixParts; ++p) {  // unused slots: valid memory for the kernels' unconditional loads
+    m.z[p] = parts > 0 ? m.z[0] : nullptr;
+    m.z_sb[p] = m.z_sb[0];
+    m.z_sh[p] = m.z_sh[0];
+    m.z_si[p] = m.z_si[0];
+    m.lz[p] = lse_c;
   }
   m.Bw = static_cast<const uint16_t*>(Bt);
   m.b_sh = b_sh;
@@ -373,7 +405,9 @@ extern "C" int hla_s6_mixed_merge_forward(int32_t batch, int32_t num_heads, int3
   m.o_sb = o_sb;
   m.o_sh = o_sh;
   m.o_si = o_si;
-  const dim3 grid(kMixD / 64, (unsigned)num_heads, (unsigned)(((int64_t)batch * chunk + 63) / 64));
+  // 2 column blocks x heads x query blocks, numbered as the kernel decodes them (rounded up to whole groups of 16)
+  const int64_t pairs = (int64_t)num_heads * (((int64_t)batch * chunk + 63) / 64);
+  const dim3 grid((unsigned)((pairs + 7) / 8 * 16));
   const hipStream_t st = as_stream(stream);
   if (width == 512) {
     constexpr int lds = 512 * 72 * 2;
@@ -398,7 +432,7 @@ extern "C" int hla_s6_mixed_merge_backward(
   int rc = fill_mixed(m, batch, num_heads, chunk, width, head_dim, o_c, oc_sb, oc_sh, oc_si, lse_c, parts, z,
                       z_strides, lse_z, Bt, b_sh, b_sr);
   if (rc != HLA_S6_OK || (int64_t)batch * chunk == 0) return rc;
-  HLA_REQUIRE(dout && d_oc && d_lse_c && (parts == 0 || (dz && dz_strides && d_lse_z)), HLA_S6_EINVAL,
+  HLA_REQUIRE(dout && d_oc && d_lse_c && dz && dz_strides && d_lse_z, HLA_S6_EINVAL,
               "mixed_merge_backward: null pointer argument");
   HLA_REQUIRE(al16(dout) && do_sb % 8 == 0 && do_sh % 8 == 0 && do_si % 8 == 0, HLA_S6_EINVAL,
               "mixed_merge_backward: dout rows must be 16-byte aligned with a unit last stride");
@@ -436,7 +470,7 @@ extern "C" int hla_s6_mixed_merge_backward(
 // as torch evaluates it: with fp32 tables each product and the sum rounded to fp32 (x - rotate_half(x) is exact),
 // then the result rounded to bf16; with bf16 tables every operation rounded to bf16. The backward gives
 // dx = bf16(bf16(dy cos) + rotate_half^T(bf16(dy sin))) for dy fp32, autograd's order of roundings for a bf16 x.
-// One thread per 2 columns of each half of a row (32 threads per 128-wide row); up to two tensors per launch.
+// One thread per 8 columns of each half of a row (8 threads per 128-wide row); up to two tensors per launch.
 namespace hla {
 namespace {
 
@@ -452,20 +486,33 @@ struct RopeParams {
   bool trig_bf16;
 };
 
-__device__ __forceinline__ float2 rope_trig(const RopeParams& a, const void* t, int64_t off) {
+// 8 consecutive table values from column `off` (fp32, or bf16 with trig_bf16)
+__device__ __forceinline__ void rope_trig8(const RopeParams& a, const void* t, int64_t off, float (&v)[8]) {
   if (a.trig_bf16) {
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(t) + off);
-    return float2{lo_bf(w), hi_bf(w)};
+    const u32x4 w = ld16(static_cast<const uint16_t*>(t) + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = lo_bf(w[e]);
+      v[2 * e + 1] = hi_bf(w[e]);
+    }
+  } else {
+    const floatx4 x0 = *reinterpret_cast<const floatx4*>(static_cast<const float*>(t) + off);
+    const floatx4 x1 = *reinterpret_cast<const floatx4*>(static_cast<const float*>(t) + off + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = x0[e];
+      v[4 + e] = x1[e];
+    }
   }
-  return *reinterpret_cast<const float2*>(static_cast<const float*>(t) + off);
 }
 
 __device__ __forceinline__ float rope_mul(float a, float b, bool bf) { return bf ? rbf(__fmul_rn(a, b)) : __fmul_rn(a, b); }
 __device__ __forceinline__ float rope_add(float a, float b, bool bf) { return bf ? rbf(__fadd_rn(a, b)) : __fadd_rn(a, b); }
 
+// One thread per 8 columns of each half of a row: columns j .. j+7 and j+h2 .. j+h2+7 (16-byte accesses).
 template <bool kBackward>
 __global__ __launch_bounds__(256) void rope_rows(RopeParams a) {
-  const int per_row = a.d / 4;
+  const int per_row = a.d / 16;
   const int64_t rows = (int64_t)a.B * a.H * a.n;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t r = gid / per_row;
@@ -473,26 +520,42 @@ __global__ __launch_bounds__(256) void rope_rows(RopeParams a) {
   const int tsel = (int)(r / rows);
   const int64_t rr = r % rows;
   const int64_t b = rr / ((int64_t)a.H * a.n), h = (rr / a.n) % a.H, i = rr % a.n;
-  const int h2 = a.d / 2, j = 2 * (int)(gid % per_row);  // columns j, j + 1 and j + h2, j + h2 + 1
+  const int h2 = a.d / 2, j = 8 * (int)(gid % per_row);
   const int64_t co = b * a.c_sb + i * a.c_si;
-  const float2 c1 = rope_trig(a, a.cos, co + j), c2 = rope_trig(a, a.cos, co + j + h2);
-  const float2 s1 = rope_trig(a, a.sin, co + j), s2 = rope_trig(a, a.sin, co + j + h2);
+  float cl[8], ch[8], sl[8], sh[8];
+  rope_trig8(a, a.cos, co + j, cl);
+  rope_trig8(a, a.cos, co + j + h2, ch);
+  rope_trig8(a, a.sin, co + j, sl);
+  rope_trig8(a, a.sin, co + j + h2, sh);
   const bool bf = a.trig_bf16;
   const int64_t xo = b * a.x_sb[tsel] + h * a.x_sh[tsel] + i * a.x_si[tsel];
-  float x1[2], x2[2];
+  float x1[8], x2[8];
   if constexpr (kBackward) {
     const float* xr = static_cast<const float*>(a.x[tsel]) + xo;
-    const float2 u = *reinterpret_cast<const float2*>(xr + j), v = *reinterpret_cast<const float2*>(xr + j + h2);
-    x1[0] = u.x; x1[1] = u.y; x2[0] = v.x; x2[1] = v.y;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const floatx4 u = *reinterpret_cast<const floatx4*>(xr + j + 4 * half);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(xr + j + h2 + 4 * half);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x1[4 * half + e] = u[e];
+        x2[4 * half + e] = v[e];
+      }
+    }
   } else {
     const uint16_t* xr = static_cast<const uint16_t*>(a.x[tsel]) + xo;
-    const uint32_t u = *reinterpret_cast<const uint32_t*>(xr + j), v = *reinterpret_cast<const uint32_t*>(xr + j + h2);
-    x1[0] = lo_bf(u); x1[1] = hi_bf(u); x2[0] = lo_bf(v); x2[1] = hi_bf(v);
-  }
-  const float cl[2] = {c1.x, c1.y}, ch[2] = {c2.x, c2.y}, sl[2] = {s1.x, s1.y}, sh[2] = {s2.x, s2.y};
-  float y1[2], y2[2];
+    const u32x4 u = ld16(xr + j), v = ld16(xr + j + h2);
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < 4; ++e) {
+      x1[2 * e] = lo_bf(u[e]);
+      x1[2 * e + 1] = hi_bf(u[e]);
+      x2[2 * e] = lo_bf(v[e]);
+      x2[2 * e + 1] = hi_bf(v[e]);
+    }
+  }
+  float y1[8], y2[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
     if constexpr (kBackward) {  // dx1 = dy1 cos1 + dy2 sin2, dx2 = dy2 cos2 - dy1 sin1, each product rounded to bf16
       y1[e] = __fadd_rn(rbf(__fmul_rn(x1[e], cl[e])), rbf(__fmul_rn(x2[e], sh[e])));
       y2[e] = __fadd_rn(rbf(__fmul_rn(x2[e], ch[e])), -rbf(__fmul_rn(x1[e], sl[e])));
@@ -502,8 +565,8 @@ __global__ __launch_bounds__(256) void rope_rows(RopeParams a) {
     }
   }
   uint16_t* yr = a.y[tsel] + b * a.y_sb[tsel] + h * a.y_sh[tsel] + i * a.y_si[tsel];
-  *reinterpret_cast<uint32_t*>(yr + j) = pack2(y1[0], y1[1]);
-  *reinterpret_cast<uint32_t*>(yr + j + h2) = pack2(y2[0], y2[1]);
+  st16(yr + j, u32x4{pack2(y1[0], y1[1]), pack2(y1[2], y1[3]), pack2(y1[4], y1[5]), pack2(y1[6], y1[7])});
+  st16(yr + j + h2, u32x4{pack2(y2[0], y2[1]), pack2(y2[2], y2[3]), pack2(y2[4], y2[5]), pack2(y2[6], y2[7])});
 }
 
 int rope_launch(bool backward, int32_t count, const void* const* x, const int64_t* x_strides, void* const* y,
@@ -511,14 +574,13 @@ int rope_launch(bool backward, int32_t count, const void* const* x, const int64_
                 const void* cos, const void* sin, int64_t c_sb, int64_t c_si, int32_t trig_bf16, void* stream) {
   HLA_REQUIRE(count >= 1 && count <= 2 && batch >= 0 && heads >= 1 && chunk >= 0, HLA_S6_EINVAL,
               "rope_rows: bad tensor count, batch, head or chunk count");
-  HLA_REQUIRE(head_dim >= 4 && head_dim % 4 == 0, HLA_S6_EUNSUPPORTED, "rope_rows: head_dim %d not a multiple of 4",
-              head_dim);
+  HLA_REQUIRE(head_dim >= 16 && head_dim % 16 == 0, HLA_S6_EUNSUPPORTED,
+              "rope_rows: head_dim %d not a multiple of 16", head_dim);
   const int64_t rows = (int64_t)batch * heads * chunk;
   if (rows == 0) return HLA_S6_OK;
   HLA_REQUIRE(x && x_strides && y && y_strides && cos && sin, HLA_S6_EINVAL, "rope_rows: null pointer argument");
-  const int ex = backward ? 8 : 4;  // bytes of the pairs x is read in
-  HLA_REQUIRE(((uintptr_t)cos | (uintptr_t)sin) % (trig_bf16 ? 4 : 8) == 0 && c_sb % 2 == 0 && c_si % 2 == 0,
-              HLA_S6_EINVAL, "rope_rows: cos / sin pairs must be aligned (even strides)");
+  HLA_REQUIRE(((uintptr_t)cos | (uintptr_t)sin) % 16 == 0 && c_sb % 8 == 0 && c_si % 8 == 0, HLA_S6_EINVAL,
+              "rope_rows: cos / sin rows must be 16-byte aligned with a unit last stride");
   RopeParams p = {};
   p.count = count;
   p.B = batch;
@@ -527,11 +589,11 @@ int rope_launch(bool backward, int32_t count, const void* const* x, const int64_
   p.d = head_dim;
   for (int t = 0; t < count; ++t) {
     HLA_REQUIRE(x[t] && y[t], HLA_S6_EINVAL, "rope_rows: null tensor %d", t);
-    HLA_REQUIRE((uintptr_t)x[t] % ex == 0 && (uintptr_t)y[t] % 4 == 0, HLA_S6_EINVAL,
-                "rope_rows: tensor %d must be aligned to its column pairs", t);
+    HLA_REQUIRE((uintptr_t)x[t] % 16 == 0 && (uintptr_t)y[t] % 16 == 0, HLA_S6_EINVAL,
+                "rope_rows: tensor %d must be 16-byte aligned", t);
     for (int k = 0; k < 3; ++k)
-      HLA_REQUIRE(x_strides[3 * t + k] % 2 == 0 && y_strides[3 * t + k] % 2 == 0, HLA_S6_EINVAL,
-                  "rope_rows: strides of tensor %d must be even", t);
+      HLA_REQUIRE(x_strides[3 * t + k] % 8 == 0 && y_strides[3 * t + k] % 8 == 0, HLA_S6_EINVAL,
+                  "rope_rows: strides of tensor %d must be multiples of 8 (16-byte rows)", t);
     p.x[t] = x[t];
     p.x_sb[t] = x_strides[3 * t];
     p.x_sh[t] = x_strides[3 * t + 1];
@@ -546,7 +608,7 @@ int rope_launch(bool backward, int32_t count, const void* const* x, const int64_
   p.c_sb = c_sb;
   p.c_si = c_si;
   p.trig_bf16 = trig_bf16 != 0;
-  const int64_t threads = rows * count * (head_dim / 4);
+  const int64_t threads = rows * count * (head_dim / 16);
   const dim3 grid((unsigned)((threads + 255) / 256));
   if (backward) hipLaunchKernelGGL(rope_rows<true>, grid, dim3(256), 0, as_stream(stream), p);
   else hipLaunchKernelGGL(rope_rows<false>, grid, dim3(256), 0, as_stream(stream), p);

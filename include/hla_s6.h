@@ -391,7 +391,7 @@ int hla_s6_hf_chunk_backward(const void *q, int64_t q_sb, int64_t q_sh, int64_t 
 /* ---- a11: the joint softmax's merge and B_t projection with backward ------------------------------------------
  * Replaces the LSE merge and the B_t product of batched_engine.mixed_attention (hla/latent/batched_engine.py:
  * 171-181): with the chunk part (o_c [B, H, n, 128] fp32, strides (oc_sb, oc_sh, oc_si), unit last; lse_c [B, H, n]
- * fp32 contiguous) and `parts` (at most 8) history blocks (z[p] [B, H, n, width] bf16, strides z_strides[3p ..
+ * fp32 contiguous) and `parts` (1 to 8) history blocks (z[p] [B, H, n, width] bf16, strides z_strides[3p ..
  * 3p+2] = (sb, sh, si), unit last; lse_z[p] [B, H, n] fp32 contiguous; -inf where the query sees no row of the
  * block), w_j = exp(lse_j - logsumexp(lse_c, lse_z[0], ..)) and
  *   out = bf16(w_c o_c + bf16(sum_p w_p z[p]) @ Bt[h])      (Bt [H, width, 128] bf16, strides (b_sh, b_sr, 1))
@@ -418,10 +418,11 @@ int hla_s6_mixed_merge_backward(int32_t batch, int32_t num_heads, int32_t chunk,
 /* a11: RoPE of the chunk's queries and keys (batched_engine.py:156 with register.apply_rope, register.py:14-20):
  * y = bf16(x cos + rotate_half(x) sin) for `count` (1 or 2) tensors x[t] [B, H, n, d] bf16 (strides x_strides[3t ..
  * 3t+2] = (sb, sh, si), unit last) into y[t] (bf16, its own strides), cos / sin [B, n, d] broadcast over the heads
- * (strides (c_sb, c_si, 1), both tables alike; fp32, or bf16 with trig_bf16 != 0), evaluated as torch does: each
+ * (strides (c_sb, c_si, 1), both tables alike, 16-byte aligned rows; fp32, or bf16 with trig_bf16 != 0), evaluated as torch does: each
  * product and the sum rounded to the tables' precision, then once to bf16. Backward: dx[t] = bf16(bf16(dy cos) +
  * rotate_half^T(bf16(dy sin))) from dy[t] fp32 (its own strides), the roundings of autograd for a bf16 x. `x`, `y`,
- * `dy`, `dx` and their strides are host arrays of `count` entries. d even; one launch each. */
+ * `dy`, `dx` and their strides are host arrays of `count` entries. d a multiple of 16, rows 16-byte aligned
+ * (strides multiples of 8 elements); one launch each. */
 int hla_s6_rope_rows_forward(int32_t count, const void *const *x, const int64_t *x_strides, void *const *y,
                              const int64_t *y_strides, int32_t batch, int32_t num_heads, int32_t chunk,
                              int32_t head_dim, const void *cos, const void *sin, int64_t c_sb, int64_t c_si,
