@@ -8,7 +8,9 @@
 * ragged decode: 32 rows with contexts drawn from U[1024, 8192] on 65,536-page pools (2 GiB main latent, 1 GiB
   loop-1 latent: page ids up to 65,535, byte offsets past 2^31);
 * short-chunk prefill: 4 requests x 3 tokens on 8192 latent rows (against ``O.attend_chunk``), on the fused path and
-  the reference's op sequence, and a mixed step of decode rows and chunks of 2..15 tokens.
+  the reference's op sequence, and a mixed step of decode rows and chunks of 2..15 tokens;
+* steps whose longest chunk has 2 or 3 tokens over ragged histories (one-token requests beside them, an empty
+  history, padding).
 
 Caches live on the device; page 0 and every page no request references are +inf-poisoned, so a read outside a row's
 pages cannot go unseen. The oracle reads host copies of the referenced pages only (through a remapped table).
@@ -194,3 +196,16 @@ def test_short_chunk_prefill(ops, layer):
     mixed = DeviceDecode([3000, 17, 900, 0, 5000, 40, 1200], pad=3, seed=61, lens=[1, 15, 4, 5, 2, 1, 9])
     splits = {w: ops.mi355x_kv_splits(int(mixed.seq.max()), mixed.T, 256, width=w) for w in WIDTHS}
     _check(mixed, layer, ops, splits, loops=(0, 1))
+
+
+@pytest.mark.parametrize('hist,lens,pad', [([2000, 700, 4100, 33], [2, 2, 2, 2], 1),
+                                           ([1500, 0, 3100, 260, 90], [3, 1, 2, 3, 3], 2),
+                                           ([6000, 40, 2500], [2, 1, 2], 0)])
+def test_two_and_three_token_chunks(ops, layer, hist, lens, pad):
+    """Steps whose longest chunk has 2 or 3 tokens on the fused path (one token per history workgroup, the chunk's
+    exact keys from the exact cache): ragged histories, one-token requests beside the chunks, an empty history and
+    padding, all four loops, against the oracle and the reference's op sequence."""
+    case = DeviceDecode([h + W for h in hist], pad=pad, seed=62 + len(hist), lens=lens)
+    splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
+    wants = _check(case, layer, ops, splits)
+    _check(case, layer, ops, splits, wants=wants, fused=False)
