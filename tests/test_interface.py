@@ -2,6 +2,7 @@
 the declared arity; the Python mirror keeps the reference's operator names and parameter lists and its host-side
 error behaviour; the product package never reaches the oracle."""
 import ast
+import importlib
 import inspect
 import json
 import os
@@ -199,3 +200,32 @@ def test_static_decode_refuses_sizes_past_its_array(pkg):
     args[3] = 384
     with pytest.raises(ValueError, match='width'):
         lib.call('hla_s6_attend_decode_static', *args)
+
+
+def test_joint_attention_kernels_refuse_bad_shapes_before_any_launch(pkg):
+    """The merge / B_t and RoPE entry points of the HF engine's joint attention check their sizes first: no history
+    block or more than 8, a width outside {256, 512}, a head_dim other than 128 (merge) or not a multiple of 16
+    (RoPE), a tensor count outside {1, 2} raise ValueError without touching the device."""
+    lib = pkg._lib
+
+    def merge_args(parts, width, head_dim):
+        args = [None if t is lib.P else 0 for t in lib.SIGNATURES['hla_s6_mixed_merge_forward']]
+        args[0], args[1], args[2], args[3], args[4], args[10] = 2, 16, 8, width, head_dim, parts
+        return args
+
+    for parts, width, head_dim, match in ((0, 512, 128, 'history blocks'), (9, 512, 128, 'history blocks'),
+                                          (1, 384, 128, 'width'), (1, 512, 64, 'head_dim')):
+        with pytest.raises(ValueError, match=match):
+            lib.call('hla_s6_mixed_merge_forward', *merge_args(parts, width, head_dim))
+        bwd = [None if t is lib.P else 0 for t in lib.SIGNATURES['hla_s6_mixed_merge_backward']]
+        bwd[:5], bwd[10] = merge_args(parts, width, head_dim)[:5], parts
+        with pytest.raises(ValueError, match=match):
+            lib.call('hla_s6_mixed_merge_backward', *bwd)
+    for name in ('hla_s6_rope_rows_forward', 'hla_s6_rope_rows_backward'):
+        for count, head_dim, match in ((3, 128, 'tensor count'), (0, 128, 'tensor count'), (2, 120, 'multiple of 16')):
+            args = [None if t is lib.P else 0 for t in lib.SIGNATURES[name]]
+            args[0], args[5], args[6], args[7], args[8] = count, 2, 16, 8, head_dim
+            with pytest.raises(ValueError, match=match):
+                lib.call(name, *args)
+    be = importlib.import_module('hybrid-latent-attention_amd.batched_engine')
+    assert be.MAX_BLOCKS == 8
