@@ -1484,7 +1484,8 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
 
   // 1. history output of the TB tokens. Every load of the phase is issued before the first wait: the split
   //    partials and their lse (an empty split left no partial; a select drops it, so its bytes never matter),
-  //    then this lane's B rows for the GEMV; the splits are reduced online in chunks of eight.
+  //    then this lane's B rows for the GEMV; the splits are reduced online in chunks of eight (with one token per
+  //    workgroup, which meets many slots, each chunk's loads are issued before the previous chunk is reduced).
   if (S > 1) {
     // Round one issues, before any wait: the lse of every slot of the TB tokens (into LDS), the first slots'
     // partials whatever the plan (an unused slot holds lse = -inf and is dropped by a select), and this lane's B
@@ -1503,9 +1504,10 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       den[it] = 0.f;
       acc[it] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    float ls[IPT][8];
-    floatx4 o[IPT][8];
-    auto load = [&](int s0, const int (&lim)[IPT]) {  // slots s0 + sg + SG*u, u < 8
+    float ls[IPT][8], ls2[IPT][8];  // two register sets: a round in flight while the previous one is reduced
+    floatx4 o[IPT][8], o2[IPT][8];
+    auto load_to = [&](int s0, const int (&lim)[IPT], float (&ls)[IPT][8], floatx4 (&o)[IPT][8]) {
+      // slots s0 + sg + SG*u, u < 8
 #pragma unroll
       for (int it = 0; it < IPT; ++it) {
         const int item = (SG > 1 ? tid % ITEMS : tid) + it * kThreads, tb = item / C4, c4 = item % C4, t = t0 + tb;
@@ -1521,7 +1523,9 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
         }
       }
     };
-    auto reduce = [&]() {  // online LSE combine of the eight loaded slots
+    auto load = [&](int s0, const int (&lim)[IPT]) { load_to(s0, lim, ls, o); };
+    // online LSE combine of the eight loaded slots
+    auto reduce_from = [&](const float (&ls)[IPT][8], const floatx4 (&o)[IPT][8]) {
 #pragma unroll
       for (int it = 0; it < IPT; ++it) {
         float mx = m[it];
@@ -1566,10 +1570,27 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
       used[it] = used_s[tb];
       s_end = max(s_end, used[it]);
     }
-    reduce();
-    for (int s0 = 8 * SG; s0 < s_end; s0 += 8 * SG) {
-      load(s0, used);
-      reduce();
+    if constexpr (TB == 1) {  // many slots per token: each round's loads are in flight while the previous one is
+                              // reduced (same rounds, same order)
+      int s0 = 8 * SG;
+      if (s0 < s_end) load_to(s0, used, ls2, o2);
+      reduce_from(ls, o);
+      while (s0 < s_end) {
+        const int s1 = s0 + 8 * SG;
+        if (s1 < s_end) load_to(s1, used, ls, o);
+        reduce_from(ls2, o2);
+        if (s1 >= s_end) break;
+        const int s2 = s1 + 8 * SG;
+        if (s2 < s_end) load_to(s2, used, ls2, o2);
+        reduce_from(ls, o);
+        s0 = s2;
+      }
+    } else {
+      reduce_from(ls, o);
+      for (int s0 = 8 * SG; s0 < s_end; s0 += 8 * SG) {
+        load(s0, used);
+        reduce_from(ls, o);
+      }
     }
     if constexpr (SG > 1) {  // merge the slot groups' partial reductions
       const int item = tid % ITEMS;
