@@ -14,6 +14,7 @@
 //   * chunk_dkdv: per query tile S = Q K^T and dP = dO V^T against the block's K^T / V^T in registers, then
 //     dV^T += dO^T P and dK^T += Q^T dS.
 // P and dS are rounded to bf16 as MFMA operands (fp32 accumulation); dO is rounded to bf16 for the products.
+// Each kernel loads its next tile (rows, row constants and valid bytes) while it computes the current one.
 #include "common.h"
 
 namespace hla {
@@ -93,16 +94,28 @@ __global__ __launch_bounds__(64) void chunk_fwd(HfChunkParams a) {
   for (int nt = 0; nt < 8; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;
   const int kend = key_end(vrow, a.n, q0, hq);
-  for (int k0 = 0; k0 < kend; k0 += 16) {
+  const bool q_valid = qi < a.n && vrow[qr] != 0;
+  // tile k0's K rows (A operand: key k0 + hq), V rows k0 .. k0 + 15 (piece c = it * 64 + lane is row c / 16,
+  // 16 c % 16) and the valid bytes of keys k0 + 4g + r; the next tile's are loaded while a tile is computed
+  auto load_tile = [&](int k0, u32x4 (&kA)[4], u32x4 (&vr)[4], uint8_t (&kv)[4]) {
     const int key = min(k0 + hq, a.n - 1);
-    u32x4 kA[4], vr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) kA[i] = ld16(kh + (int64_t)key * a.k_si + 32 * i + 8 * g);
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {  // V rows k0 .. k0 + 15: piece c = it * 64 + lane is row c / 16, 16 c % 16
+    for (int it = 0; it < 4; ++it) {
       const int c = it * 64 + lane, row = min(k0 + (c >> 4), a.n - 1);
       vr[it] = ld16(vh + (int64_t)row * a.v_si + (c & 15) * 8);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) kv[r] = vrow[min(k0 + 4 * g + r, a.n - 1)];
+  };
+  u32x4 kA[4], vr[4];
+  uint8_t kv[4];
+  if (kend > 0) load_tile(0, kA, vr, kv);
+  for (int k0 = 0; k0 < kend; k0 += 16) {
+    u32x4 kN[4], vN[4];
+    uint8_t kvN[4];
+    if (k0 + 16 < kend) load_tile(k0 + 16, kN, vN, kvN);
     floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) s = mfma16x16x32(kA[i], qb[i], s);
@@ -113,7 +126,11 @@ __global__ __launch_bounds__(64) void chunk_fwd(HfChunkParams a) {
     }
     float sc[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = visible(vrow, a.n, qi, k0 + 4 * g + r) ? s[r] * a.scale_log2 : -INFINITY;
+    for (int r = 0; r < 4; ++r) {  // visible(): a valid query sees the valid keys up to itself, an invalid one all
+      const int j = k0 + 4 * g + r;
+      const bool vis = qi < a.n && j < a.n && (q_valid ? (kv[r] != 0 && j <= qi) : true);
+      sc[r] = vis ? s[r] * a.scale_log2 : -INFINITY;
+    }
     const float mx = wave_max16x4_nn(max_nn(max_nn(sc[0], sc[1]), max_nn(sc[2], sc[3])));
     const bool raise = mx > m + 8.f;  // lazy rescale (the exponentials stay below 2^8)
     if (__any(raise)) {
@@ -134,6 +151,12 @@ __global__ __launch_bounds__(64) void chunk_fwd(HfChunkParams a) {
     const short4v pb = pack4(p);
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) oacc[nt] = mfma16x16x16(tile_t(vs, nt, g, hq), pb, oacc[nt]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kA[i] = kN[i];
+      vr[i] = vN[i];
+      kv[i] = kvN[i];
+    }
   }
   l = wave_sum16x4(l);
   if (qi < a.n) {
@@ -184,14 +207,26 @@ __global__ __launch_bounds__(64) void chunk_dq(HfChunkParams a) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) acc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
   const int kend = key_end(vrow, a.n, q0, hq);
-  for (int k0 = 0; k0 < kend; k0 += 16) {
+  const bool q_valid = qi < a.n && vrow[qr] != 0;
+  // tile k0's K and V rows (A operands: key k0 + hq) and the valid bytes of keys k0 + 4g + r; the next tile's are
+  // loaded while a tile is computed
+  auto load_tile = [&](int k0, u32x4 (&kA)[4], u32x4 (&vA)[4], uint8_t (&kv)[4]) {
     const int key = min(k0 + hq, a.n - 1);
-    u32x4 kA[4], vA[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kA[i] = ld16(kh + (int64_t)key * a.k_si + 32 * i + 8 * g);
       vA[i] = ld16(vh + (int64_t)key * a.v_si + 32 * i + 8 * g);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) kv[r] = vrow[min(k0 + 4 * g + r, a.n - 1)];
+  };
+  u32x4 kA[4], vA[4];
+  uint8_t kv[4];
+  if (kend > 0) load_tile(0, kA, vA, kv);
+  for (int k0 = 0; k0 < kend; k0 += 16) {
+    u32x4 kN[4], vN[4];
+    uint8_t kvN[4];
+    if (k0 + 16 < kend) load_tile(k0 + 16, kN, vN, kvN);
     floatx4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -202,14 +237,21 @@ __global__ __launch_bounds__(64) void chunk_dq(HfChunkParams a) {
     for (int i = 0; i < 4; ++i) st16(ks + hq * kTS + 32 * i + 8 * g, kA[i]);  // K tile rows k0 + hq (row-major)
     float ds[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool vis = visible(vrow, a.n, qi, k0 + 4 * g + r);
+    for (int r = 0; r < 4; ++r) {  // visible(): a valid query sees the valid keys up to itself, an invalid one all
+      const int j = k0 + 4 * g + r;
+      const bool vis = qi < a.n && j < a.n && (q_valid ? (kv[r] != 0 && j <= qi) : true);
       const float p = vis ? fast_exp2(s[r] * a.scale_log2 - lse2) : 0.f;
       ds[r] = p * (dp[r] - delta + dl) * a.scale;
     }
     const short4v dsb = pack4(ds);
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) acc[nt] = mfma16x16x16(tile_t(ks, nt, g, hq), dsb, acc[nt]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kA[i] = kN[i];
+      vA[i] = vN[i];
+      kv[i] = kvN[i];
+    }
   }
   if (qi < a.n) {
     float* gp = a.dq + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)qi * a.g_si + 4 * g;
@@ -239,25 +281,48 @@ __global__ __launch_bounds__(64) void chunk_dkdv(HfChunkParams a) {
   floatx4 dka[8], dva[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) dka[nt] = dva[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
-  for (int q0 = 0; q0 < a.n; q0 += 16) {
-    const int qi = q0 + hq;
-    // a block of queries before the keys contributes only through its invalid queries (which see every key)
-    if (q0 + 15 < j0 && !__any(qi < a.n && vrow[qi] == 0)) continue;
-    const int qr = min(qi, a.n - 1);
+  const bool k_valid = kj < a.n && vrow[kr] != 0;
+  // the first query tile at or after q0 that contributes: a block of queries before the keys does so only through
+  // its invalid queries (which see every key)
+  auto next_tile = [&](int q0) {
+    while (q0 < a.n && q0 + 15 < j0 && !__any(q0 + hq < a.n && vrow[q0 + hq] == 0)) q0 += 16;
+    return q0;
+  };
+  // query tile q0's Q rows and dO rows (bf16, A operands: query q0 + hq), the row constants and valid bytes of the
+  // four queries 4g + r of this lane's part of S; the next contributing tile's are loaded while a tile is computed
+  struct QTile {
     u32x4 qA[4], dA[4];
+    float lse2[4], del[4], dl[4];
+    uint8_t qv[4];
+  };
+  auto load_tile = [&](int q0, QTile& t) {
+    const int qr = min(q0 + hq, a.n - 1);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      qA[i] = ld16(qh + (int64_t)qr * a.q_si + 32 * i + 8 * g);
-      dA[i] = f32x8_to_bf16(dh + (int64_t)qr * a.d_si + 32 * i + 8 * g);
+      t.qA[i] = ld16(qh + (int64_t)qr * a.q_si + 32 * i + 8 * g);
+      t.dA[i] = f32x8_to_bf16(dh + (int64_t)qr * a.d_si + 32 * i + 8 * g);
     }
-    float lse2[4], del[4], dl[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {  // the four queries 4g + r of this lane's part of S
+    for (int r = 0; r < 4; ++r) {
       const int q = min(q0 + 4 * g + r, a.n - 1);
-      lse2[r] = a.lse[lrow + q] * kLog2e;
-      del[r] = a.delta[lrow + q];
-      dl[r] = a.dlse ? a.dlse[lrow + q] : 0.f;
+      t.lse2[r] = a.lse[lrow + q] * kLog2e;
+      t.del[r] = a.delta[lrow + q];
+      t.dl[r] = a.dlse ? a.dlse[lrow + q] : 0.f;
+      t.qv[r] = vrow[q];
     }
+  };
+  QTile cur;
+  int q0 = next_tile(0);
+  if (q0 < a.n) load_tile(q0, cur);
+  while (q0 < a.n) {
+    const int q1 = next_tile(q0 + 16);
+    QTile nxt;
+    if (q1 < a.n) load_tile(q1, nxt);
+    const u32x4 (&qA)[4] = cur.qA;
+    const u32x4 (&dA)[4] = cur.dA;
+    const float (&lse2)[4] = cur.lse2;
+    const float (&del)[4] = cur.del;
+    const float (&dl)[4] = cur.dl;
     floatx4 s = {0.f, 0.f, 0.f, 0.f}, dp = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -271,8 +336,9 @@ __global__ __launch_bounds__(64) void chunk_dkdv(HfChunkParams a) {
     }
     float p[4], ds[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool vis = visible(vrow, a.n, q0 + 4 * g + r, kj);
+    for (int r = 0; r < 4; ++r) {  // visible(): a valid query sees the valid keys up to itself, an invalid one all
+      const int qq = q0 + 4 * g + r;
+      const bool vis = qq < a.n && kj < a.n && (cur.qv[r] != 0 ? (k_valid && kj <= qq) : true);
       p[r] = vis ? fast_exp2(s[r] * a.scale_log2 - lse2[r]) : 0.f;
       ds[r] = p[r] * (dp[r] - del[r] + dl[r]) * a.scale;
     }
@@ -282,6 +348,8 @@ __global__ __launch_bounds__(64) void chunk_dkdv(HfChunkParams a) {
       dva[nt] = mfma16x16x16(tile_t(dos, nt, g, hq), pb, dva[nt]);
       dka[nt] = mfma16x16x16(tile_t(qs, nt, g, hq), dsb, dka[nt]);
     }
+    cur = nxt;
+    q0 = q1;
   }
   if (kj < a.n) {
     float* kp = a.dk + (int64_t)b * a.g_sb + (int64_t)h * a.g_sh + (int64_t)kj * a.g_si + 4 * g;
