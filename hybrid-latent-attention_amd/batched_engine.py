@@ -2,9 +2,9 @@
 (``hla/latent/batched_engine.py:154-182``, ``mixed_attention``) on MI355X kernels, differentiable.
 
 One softmax spans the current chunk's exact keys and every history block's latent rows. Written as an LSE merge of
-its parts, which is the same softmax: the current chunk (per-head causal attention over the RoPE'd q / k of the
-chunk with the reference's visibility rule) gives ``(o_c, lse_c)`` from the HIP chunk kernels
-(``hla_s6_hf_chunk_forward`` / ``_backward``); each history block gives ``(z_k, lse_k)`` from
+its parts, which is the same softmax: the current chunk (per-head causal attention over the chunk's q / k, RoPE'd
+by one HIP launch for both, ``hla_s6_rope_rows_forward`` / ``_backward``, with the reference's visibility rule) gives
+``(o_c, lse_c)`` from the HIP chunk kernels (``hla_s6_hf_chunk_forward`` / ``_backward``); each history block gives ``(z_k, lse_k)`` from
 ``history_gemm.causal_history_gemm`` (bf16 MFMA kernels, differentiable in the latent query and the packed rows)
 with the block's ``[B, N]`` mask shared by the chunk's queries; then ``out = w_c o_c + bf16(sum_k w_k z_k) @ B``
 with ``w = exp(lse - logsumexp(all lse))`` in one HIP launch (``hla_s6_mixed_merge_forward``; its backward
@@ -88,16 +88,10 @@ class _CurrentChunk(torch.autograd.Function):
 
 
 def _trig(cos, sin, B, n, D):
-    """cos / sin broadcast to ``[B, n, D]`` with one layout for both (16-byte rows), fp32 or bf16."""
-    tabs = []
-    for t in (cos, sin):
-        t = t.expand(B, n, D)
-        if t.dtype not in (torch.float32, torch.bfloat16) or t.dtype != cos.dtype:
-            t = t.to(torch.float32)
-        tabs.append(t)
-    c, s = tabs
-    if c.dtype != s.dtype:
-        c, s = c.float(), s.float()
+    """cos / sin broadcast to ``[B, n, D]`` with one layout for both (16-byte rows): bf16 when both tables are (torch
+    then rotates in bf16), else fp32 (torch's precision for a bf16 x with fp32 or fp16 tables)."""
+    dt = torch.bfloat16 if cos.dtype == sin.dtype == torch.bfloat16 else torch.float32
+    c, s = (t.to(dt).expand(B, n, D) for t in (cos, sin))
     if (c.stride() != s.stride() or c.stride(-1) != 1 or c.stride(0) % 8 or c.stride(1) % 8 or c.data_ptr() % 16
             or s.data_ptr() % 16):
         c, s = c.contiguous(), s.contiguous()
