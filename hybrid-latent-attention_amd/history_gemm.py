@@ -119,9 +119,13 @@ def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv, b
     # key tiles of the dk / dv kernel: 64 keys on the multi-query form (widths 512 / 256, N a multiple of 16),
     # whose causal load is balanced best with about 8 workgroups per CU (12 ranges at B=4, L=2880: 3.78 ms
     # forward + backward against 4.15 ms with 6 and 4.11 ms with 32); 4 per CU on the 32-key form
-    # (row ranges split a tile's query rows, which the kernels take two at a time: at most ceil(Lq / 2) of them)
+    # (row ranges split a tile's query rows, which the kernels take two at a time: at most ceil(Lq / 2) of them).
+    # Few queries over many keys (a chunk against history rows it sees alike) give every key tile the same work:
+    # one workgroup per CU, no more ranges than fill the GPU (B=8, a 256-token chunk over 2048 rows: the
+    # joint-attention step 2.40 -> 2.08 ms; with 8 per CU, 8 ranges and their fp32 partials)
     mq = R in (256, 512) and N % 16 == 0
-    splits = min(_key_splits(-(-N // (64 if mq else 32)) * B, dev, 8 if mq else 4), -(-Lq // 2)) if need_kv else 1
+    per_cu = (8 if 2 * Lq >= N else 1) if mq else 4
+    splits = min(_key_splits(-(-N // (64 if mq else 32)) * B, dev, per_cu), -(-Lq // 2)) if need_kv else 1
     splits = max(1, splits)
     floats = _lib.load().hla_s6_khop_backward_workspace(B, Lq, N, R, splits)
     ws = torch.empty(floats, dtype=torch.float32, device=dev) if floats > 0 else None
