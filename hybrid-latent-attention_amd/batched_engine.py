@@ -153,7 +153,7 @@ def _history_block(qt, ck, cv, mask, scale):
     H, r]`` (bf16, token-linear) over the rows ck / cv ``[B, N, r]`` that mask ``[B, N]`` shows to every query of the
     chunk."""
     B, n = qt.shape[:2]
-    m = mask[:, None, :].expand(B, n, mask.shape[1]).contiguous()
+    m = mask[:, None, :].expand(B, n, mask.shape[1])  # (query stride 0: the kernels read one row per batch row)
     z, lse = history_gemm.causal_history_gemm(qt, ck, cv, m, scale, precision='bf16')
     return z.transpose(1, 2), lse
 

@@ -178,8 +178,9 @@ int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
-                    int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
-                    void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream);  // history.hip
+                    int Lq, int N, int width, const uint8_t* mask, int64_t mask_sb, int64_t mask_st,
+                    const int32_t* bound, float scale, void* z, int64_t z_st, int64_t z_sh, float* lse,
+                    hipStream_t stream);  // history.hip
 }  // namespace hla
 
 #define HLA_REQUIRE(cond, code, ...) \

@@ -89,10 +89,12 @@ struct HistoryParams {
   WindowPart win;
   // contiguous-row form (history_mq2 only): with bt == null, token t reads table row t / tok_per_row whose page p
   // is row * bt_cols + p; lse then goes to [rows, 16, tok_per_row]; mask (when set) hides key j of token t where
-  // mask[t * mask_st + j] == 0
+  // mask[t * mask_st + j] == 0, or with mask_split mask[row * mask_sb + (t - row * tok_per_row) * mask_st + j] == 0
+  // for token t of table row `row` (mask_st 0: one mask row shown to every token of the table row)
   int tok_per_row;
   const uint8_t* mask;
-  int64_t mask_st;
+  int64_t mask_st, mask_sb;
+  bool mask_split;
   bool lse_rows;  // lse of history_split / history_combine in [rows][16][tok_per_row] instead of [16][T]
   bool reverse_groups;  // history_mq5 / history_group: workgroup b takes token group gridDim.x - 1 - b (the K-hop
                         // causal rows put the longest groups last in token order; dispatching them first shortens
@@ -474,6 +476,12 @@ __device__ void window_jobs(const WindowPart& w, int T, float scale_log2, int v,
   }
 }
 
+// mask bytes of token t whose table row is `row` (contiguous-row forms)
+__device__ __forceinline__ const uint8_t* mask_row(const HistoryParams& a, int64_t row, int t) {
+  return a.mask + (a.mask_split ? row * a.mask_sb + ((int64_t)t - row * a.tok_per_row) * a.mask_st
+                                : (int64_t)t * a.mask_st);
+}
+
 // lse index of (token t, head h): [16][T], or [rows][16][tok_per_row] with lse_rows (contiguous rows)
 __device__ __forceinline__ int64_t lse_index(const HistoryParams& a, int t, int h) {
   if (!a.lse_rows) return (int64_t)h * a.T + t;
@@ -542,8 +550,9 @@ void history_split(HistoryParams a) {
   } else {
     RowSource src{};
     if constexpr (kRows) {
-      src.base = (int64_t)(t / a.tok_per_row) * a.page_stride;
-      src.mrow = a.mask ? a.mask + (int64_t)t * a.mask_st : nullptr;
+      const int64_t row = t / a.tok_per_row;
+      src.base = row * a.page_stride;
+      src.mrow = a.mask ? mask_row(a, row, t) : nullptr;
     } else {
       src.btr = a.bt + (a.bt_rows ? a.bt_rows[t] : (int64_t)t) * a.bt_stride;
     }
@@ -713,17 +722,17 @@ __device__ __forceinline__ void store_split(const HistoryParams& a, int t, int s
   if (wave == 0 && g == 0) a.ws_lse[part_row] = lse;
 }
 
-// Mask bytes of keys kb .. kb+3 (kb = key0 + 4g) of the pass's tokens tp + u (u < count): bytes at or past a
-// token's bound n[u] are not read (the bound hides those keys); 0xffffffff without a mask.
+// Mask bytes of keys kb .. kb+3 (kb = key0 + 4g) of the pass's tokens tp + u (u < count) of table row `row`: bytes
+// at or past a token's bound n[u] are not read (the bound hides those keys); 0xffffffff without a mask.
 template <int NQ>
-__device__ __forceinline__ void load_token_masks(const HistoryParams& a, int tp, int count, const int (&n)[NQ],
-                                                 int key0, int lane, uint32_t (&mk)[NQ]) {
+__device__ __forceinline__ void load_token_masks(const HistoryParams& a, int64_t row, int tp, int count,
+                                                 const int (&n)[NQ], int key0, int lane, uint32_t (&mk)[NQ]) {
   const int kb = key0 + 4 * (lane >> 4);
 #pragma unroll
   for (int u = 0; u < NQ; ++u) {
     mk[u] = 0xffffffffu;
     if (!a.mask || u >= count) continue;
-    const uint8_t* mr = a.mask + (int64_t)(tp + u) * a.mask_st;
+    const uint8_t* mr = mask_row(a, row, tp + u);
     if (kb + 4 <= n[u] && (reinterpret_cast<uintptr_t>(mr) & 3u) == 0) {
       mk[u] = *reinterpret_cast<const uint32_t*>(mr + kb);
     } else {
@@ -806,7 +815,7 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
 #pragma unroll
       for (int u = 0; u < NQ; ++u) mk_next[u] = 0xffffffffu;
       load_tile<R, false, kRows>(a, src, n_max, j_begin, col0, lane, regs);
-      if (kRows) load_token_masks<NQ>(a, tp, count, n, j_begin * kTile, lane, mk_next);
+      if (kRows) load_token_masks<NQ>(a, row, tp, count, n, j_begin * kTile, lane, mk_next);
       for (int jt = j_begin; jt < j_end; ++jt) {
         floatx4 sa[NQ];
         group_stage_a<R, NQ>(regs, qreg, v_lds[wave], k_lds[wave], lane, count, sa);
@@ -814,7 +823,7 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
         for (int u = 0; u < NQ; ++u) mk[u] = mk_next[u];
         if (jt + 1 < j_end) {
           load_tile<R, false, kRows>(a, src, n_max, jt + 1, col0, lane, regs);
-          if (kRows) load_token_masks<NQ>(a, tp, count, n, (jt + 1) * kTile, lane, mk_next);
+          if (kRows) load_token_masks<NQ>(a, row, tp, count, n, (jt + 1) * kTile, lane, mk_next);
         }
         group_stage_b<R, NQ, kRows>(sa, s_lds[par], v_lds[wave], jt * kTile, n, count, a.scale_log2, wave, lane,
                                     oacc, m, l, mk);
@@ -900,7 +909,7 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
     if (k0 < k1) {  // uniform over the workgroup
       const int32_t* btr = kContig ? nullptr : a.bt + row * a.bt_stride;
       const int tq = tp + min(u, count - 1);
-      const uint8_t* mrow = kContig && a.mask ? a.mask + (int64_t)tq * a.mask_st : nullptr;
+      const uint8_t* mrow = kContig && a.mask ? mask_row(a, row, tq) : nullptr;
       u32x4 qf[G::KS];
       {
         const uint16_t* qp = a.q + (int64_t)tq * a.q_st + (int64_t)l16 * a.q_sh + col0 + 8 * g;
@@ -1190,12 +1199,13 @@ __global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_
           }
         }
       };
+      // lane l < 2 TPW copies mask bytes of the wave's token l / 2
+      const uint8_t* mk_src = kMask ? mask_row(a, row, tp + min(TPW * wave + (lane >> 1), count - 1)) : nullptr;
       auto copy_tile = [&](int j) {  // tile j (K, V and this wave's mask bytes) into the buffers of parity j & 1
         const int kt = k0 + j * kMq4Keys;
         if (kMask && lane < 2 * TPW) {  // token l / 2, bytes 16 (l % 2) .. (chunks past the row: its end)
-          const int tq = tp + min(TPW * wave + (lane >> 1), count - 1);
           const int c0 = min(kt + 16 * (lane & 1), (int)cap - 16);
-          copy16_to_lds_v(a.mask + (int64_t)tq * a.mask_st + c0, &mk_lds[j & 1][wave][0]);
+          copy16_to_lds_v(mk_src + c0, &mk_lds[j & 1][wave][0]);
         }
         copy_rows(kt_lds[j & 1], a.k, kt);
         copy_rows(vt_lds[j & 1], a.v, kt);
@@ -1834,15 +1844,17 @@ int dispatch_combine(const HistoryParams& p, int width, hipStream_t st) {
 namespace hla {
 // Multi-query forward over contiguous rows for the K-hop op (hla_s6_khop_forward): q / z [B * Lq, 16, width]
 // (token strides q_st / z_st), k / v [B, N, width] with row stride k_sn (batch stride N * k_sn, N a multiple of
-// 16), mask [B * Lq, N] bytes (row stride mask_st) or null, bound [B * Lq]. Returns HLA_S6_EUNSUPPORTED when the
+// 16), mask [B, Lq, N] bytes (strides mask_sb, mask_st; mask_st 0 shows one row to all of a batch row's queries)
+// or null, bound [B * Lq]. Returns HLA_S6_EUNSUPPORTED when the
 // shapes do not fit this kernel or another kernel is faster for them (the caller then uses its own).
 int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, const void* v, int64_t k_sn, int B,
-                    int Lq, int N, int width, const uint8_t* mask, int64_t mask_st, const int32_t* bound, float scale,
-                    void* z, int64_t z_st, int64_t z_sh, float* lse, hipStream_t stream) {
+                    int Lq, int N, int width, const uint8_t* mask, int64_t mask_sb, int64_t mask_st,
+                    const int32_t* bound, float scale, void* z, int64_t z_st, int64_t z_sh, float* lse,
+                    hipStream_t stream) {
   // widths 512 and 256 run faster here than in khop_fwd; history_mq5 takes a positive scale and a mask whose rows
   // start on 16-byte boundaries (its bytes are copied in 16-byte pieces), history_mq2 (width 512) anything else
   const bool mq5 = (width == 512 || width == 256) && scale > 0.f &&
-                   (!mask || (((uintptr_t)mask & 15u) == 0 && mask_st % 16 == 0));
+                   (!mask || (((uintptr_t)mask & 15u) == 0 && mask_st % 16 == 0 && mask_sb % 16 == 0));
   if (N % kTile != 0 || (width != 1024 && !(mq5 || width == 512))) return HLA_S6_EUNSUPPORTED;
   HistoryParams p{};
   p.q = static_cast<const uint16_t*>(q);
@@ -1870,6 +1882,8 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
   p.direct = true;
   p.mask = mask;
   p.mask_st = mask_st;
+  p.mask_sb = mask_sb;
+  p.mask_split = mask_sb != (int64_t)Lq * mask_st;  // (token-linear rows keep the one-stride form)
   p.reverse_groups = kKhopReverse;
   if (width == 1024) {  // kKhop1024Tokens tokens per workgroup on the 16x16 MFMA group kernel (one wave per 128 columns)
     p.lse_rows = true;

@@ -1056,13 +1056,13 @@ extern "C" int hla_s6_khop_forward(const void* q, int64_t q_sb, int64_t q_si, in
   if (Lq == 0) return HLA_S6_OK;
   HLA_REQUIRE(bound && z && lse, HLA_S6_EINVAL, "khop_forward: null bound / output");
   const bool linear = q_sb == (int64_t)Lq * q_si && z_sb == (int64_t)Lq * z_si && k_sn == v_sn &&
-                      k_sb == (int64_t)N * k_sn && v_sb == (int64_t)N * v_sn && (!mask || m_sb == (int64_t)Lq * m_si);
+                      k_sb == (int64_t)N * k_sn && v_sb == (int64_t)N * v_sn;
   HLA_REQUIRE(width != 1024 || (linear && N % 16 == 0), HLA_S6_EUNSUPPORTED,
-              "khop_forward: width 1024 needs token-linear q / z / mask rows, contiguous k / v and N a multiple of 16");
+              "khop_forward: width 1024 needs token-linear q / z rows, contiguous k / v and N a multiple of 16");
   // rows linear in the token index (t = b * Lq + i): the multi-query history kernel of the serving path runs it
   if (linear) {
-    rc = khop_forward_mq(q, q_si, q_sh, k, v, k_sn, B, Lq, N, width, mask, m_si, bound, scale, z, z_si, z_sh, lse,
-                         as_stream(stream));
+    rc = khop_forward_mq(q, q_si, q_sh, k, v, k_sn, B, Lq, N, width, mask, m_sb, m_si, bound, scale, z, z_si, z_sh,
+                         lse, as_stream(stream));
     if (rc != HLA_S6_EUNSUPPORTED) return rc;
   }
   HLA_REQUIRE(width != 1024, HLA_S6_EUNSUPPORTED, "khop_forward: width 1024 runs on the multi-query form only");

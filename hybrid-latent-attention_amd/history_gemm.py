@@ -71,7 +71,7 @@ class _CausalHistory(torch.autograd.Function):
             if N % KEY_ALIGN:
                 raise ValueError(f'width 1024 needs a key count that is a multiple of {KEY_ALIGN} (got {N})')
         m = mask if mask.dtype == torch.bool else mask.bool()
-        if m.stride(-1) != 1 or (R == 1024 and m.stride(0) != Lq * m.stride(1)):
+        if m.stride(-1) != 1:
             m = m.contiguous()
         m8 = m.view(torch.uint8)
         bound = torch.empty(B * Lq, dtype=torch.int32, device=dev)

@@ -318,7 +318,8 @@ int hla_s6_gather_packed_rows(const int64_t *cache_addrs, int32_t num_layers, in
 /* ---- multi-query causal history attention with backward (K-hop replay / training) ---------------------------
  * Replaces causal_history_gemm (hla/latent/history_gemm.py:159-220,270-294) for bf16 GEMM operands with fp32
  * accumulation: q [B, Lq, 16, width] (strides q_sb, q_si, q_sh), k / v [B, N, width] (strides *_sb, *_sn), mask
- * [B, Lq, N] bytes (nonzero = visible; strides m_sb, m_si, unit last stride; NULL = all keys below the bound),
+ * [B, Lq, N] bytes (nonzero = visible; strides m_sb, m_si, unit last stride, m_si 0 for one row shown to every
+ * query of a batch row; NULL = all keys below the bound),
  * width in {128, 256, 512}, bf16 rows 16-byte aligned with unit last stride.
  * hla_s6_khop_bounds: bound[b * Lq + i] = 1 + the last key mask row (b, i) shows (0 if none; N without a mask).
  * hla_s6_khop_forward: z [B, Lq, 16, width] bf16 and lse [B, 16, Lq] fp32 (natural log; -inf and z = 0 for a row

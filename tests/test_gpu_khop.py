@@ -161,6 +161,43 @@ def test_mask_rows_off_16_byte_boundaries_and_no_mask(R):
     assert_grad_close(dq.cpu().numpy(), dqo, 'dq (no mask)')
 
 
+@pytest.mark.parametrize('R,N', [(256, 64), (512, 64), (512, 50), (256, 50), (1024, 64)])
+def test_one_mask_row_per_batch_row_broadcast_over_queries(R, N):
+    """A [B, N] key mask expanded over the queries (query stride 0, the joint-attention history blocks' form) gives
+    bitwise the results of the same mask copied out per query, forward and (widths below 1024) backward, and
+    matches the oracle."""
+    B, Lq = 3, 21
+    rng = np.random.default_rng(R + N)
+    q, k, v, _ = case(R + N, B, Lq, N, R, 'any')
+    rows = rng.random((B, N)) < 0.6
+    rows[1] = False                            # a batch row without history
+    rows[2, N // 3:] = False
+    mask = np.broadcast_to(rows[:, None], (B, Lq, N)).copy()
+    scale = 1 / math.sqrt(R)
+    dz = bf16.round_bf16(rng.standard_normal((B, Lq, 16, R)).astype(np.float32))
+    dlse = rng.standard_normal((B, 16, Lq)).astype(np.float32)
+    outs = []
+    for broadcast in (False, True):
+        grad = R != 1024
+        qt, kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16).requires_grad_(grad) for x in (q, k, v))
+        mt = torch.tensor(rows, device='cuda')[:, None].expand(B, Lq, N)
+        if not broadcast:
+            mt = mt.contiguous()
+        assert (mt.stride(1) == 0) == broadcast
+        z, lse = hg.causal_history_gemm(qt, kt, vt, mt, scale, precision='bf16')
+        out = [z.detach().float().cpu(), lse.detach().cpu()]
+        if grad:
+            obj = (z.float() * torch.tensor(dz, device='cuda')).sum() + torch.where(
+                torch.isfinite(lse), lse * torch.tensor(dlse, device='cuda'), 0.).sum()
+            out += [g.float().cpu() for g in torch.autograd.grad(obj, [qt, kt, vt])]
+        outs.append(out)
+    for name, a, b in zip(('z', 'lse', 'dq', 'dk', 'dv'), *outs):
+        assert torch.equal(a, b), f'{name}: broadcast mask differs from the per-query copy'
+    zo, lo = O.causal_history(q, k, v, mask, scale)
+    assert_attention_close(outs[1][0].numpy(), zo, 'z (broadcast mask)')
+    assert_lse_close(outs[1][1].numpy(), lo)
+
+
 def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
     q, k, v, mask = case(3, 2, 30, 30, 256, 'benchmark')
     rng = np.random.default_rng(4)
