@@ -130,9 +130,10 @@ __device__ __forceinline__ int used_slots(int32_t ctx, int64_t cap, int chunk) {
   return (row_tiles(ctx, cap) + chunk - 1) / chunk;
 }
 
-// The plan's chunk. Must be called by every thread of the block (a multiple of 64 threads); `red` holds 2 * waves
-// int64.
-__device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_t* red) {
+// The plan's chunk. With `fill` (the multi-token kernels, launched on a grid of one workgroup per (token group,
+// slot) whether the slot has work or not) it is ceil(max_tiles / S) instead: the longest row fills all S slots.
+// Must be called by every thread of the block (a multiple of 64 threads); `red` holds 2 * waves int64.
+__device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_t* red, bool fill = false) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
   int mx = 0;
   int64_t sum = 0;
@@ -157,7 +158,7 @@ __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_
     sum += red[2 * w + 1];
   }
   const int64_t slots = (int64_t)T * S;
-  return (int)max((int64_t)1, max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
+  return (int)max((int64_t)1, fill ? (m + S - 1) / S : max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
 }
 
 // Workgroups of the split kernel: the plan puts at most T*S/2 + T (row, chunk) items in the list; a multiple of 8
@@ -765,7 +766,7 @@ __global__ __launch_bounds__(Geo<R>::THREADS) void history_group(HistoryParams a
 
   // Split partition: a fixed tile chunk for every row of the step, sized from the longest row, so that rows of a
   // ragged batch get split counts proportional to their length and every split has equal work.
-  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds, true) : (1 << 30);
   const int grp = a.reverse_groups ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
   const int t_begin = grp * NQ, t_end = min(t_begin + NQ, a.T);
 
@@ -881,7 +882,7 @@ __global__ __launch_bounds__(512) void history_mq2(HistoryParams a) {
   const int u = wave >> 1, half = wave & 1, col0 = half * G::C;
   const int S = a.num_splits, s = blockIdx.y;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;
-  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds, true) : (1 << 30);
   const int t_begin = blockIdx.x * kMqTokens, t_end = min(t_begin + kMqTokens, a.T);
   int par = 0;  // parity of the partial exchange buffer, continued across passes
 
@@ -1120,7 +1121,7 @@ __global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_
   const int l16 = lane & 15, g = lane >> 4;
   const int S = a.num_splits, s = blockIdx.y;
   const int64_t cap = (int64_t)a.bt_cols * a.block_size;
-  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds) : (1 << 30);
+  const int chunk = S > 1 ? split_chunk(a.ctx, a.T, cap, S, red_lds, true) : (1 << 30);
   const int grp = a.reverse_groups ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
   const int t_begin = grp * kMq4Tokens, t_end = min(t_begin + kMq4Tokens, a.T);
 
@@ -1370,7 +1371,7 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
   int S = S_all;
   if (a.ctx) {
     const int64_t cap = (int64_t)a.bt_cols * a.block_size;
-    S = min(S_all, used_slots(a.ctx[t], cap, split_chunk(a.ctx, a.T, cap, S_all, red)));
+    S = min(S_all, used_slots(a.ctx[t], cap, split_chunk(a.ctx, a.T, cap, S_all, red, a.group > 1)));
   }
   const float* ls = a.ws_lse + (int64_t)t * S_all * kHeads + h;
   float mq = -INFINITY;

@@ -161,12 +161,13 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per
     row (so that filled slots hold at least that many keys) nor 1024. A function of constants and the row count only
     (graph-stable).
 
-    Multi-query steps (``tokens_per_group`` 4) want about one 8-wave workgroup of eight tokens per CU for the
-    512-wide latent (two of four tokens for narrower ones): ``ceil(2 * CUs / groups)`` slots for ``groups`` four-token
-    groups, at least 1 (with 512-token chunks of four requests, one slot: no split reduction at all)."""
+    Multi-query steps (``tokens_per_group`` 4) run one workgroup of eight tokens per (token group, slot), and every
+    slot of the longest row holds work: ``ceil(2 * CUs / groups)`` slots for ``groups`` four-token groups make one
+    busy workgroup per CU (8 waves at width 512, 4 at 256), never more than one per ``min_keys_per_split`` keys of
+    the longest row, at least 1 (with 512-token chunks of four requests, one slot: no split reduction at all)."""
     if tokens_per_group > 1:
         groups = -(-max(1, num_tokens) // tokens_per_group)
-        by_length = max(1, 2 * -(-max_seq_len // min_keys_per_split))
+        by_length = max(1, -(-max_seq_len // min_keys_per_split))
         return max(1, min(-(-2 * cu_count // groups), by_length, 1024))
     waves_per_split = max(1, width // 128)
     busy = -(-waves_per_cu * cu_count // waves_per_split)

@@ -184,6 +184,38 @@ def test_grouped_history_matches_oracle(ops, width, splits, group):
     assert_lse_close(lse, lse1)
 
 
+@pytest.mark.parametrize('width,group', [(512, 4), (256, 4), (1024, 2)])
+def test_grouped_history_fills_every_slot(ops, width, group):
+    """The multi-token kernels run one workgroup per (token group, slot): every slot of the longest row holds
+    work (a finite partial lse in the workspace), shorter rows a prefix of the slots, and the result matches the
+    oracle."""
+    rng = np.random.default_rng(width + group)
+    block, num_blocks, splits = 16, 400, 6
+    lens = [8, 4]
+    req = np.repeat(np.arange(len(lens)), lens)
+    ctx = np.concatenate([np.full(8, 3000), np.full(4, 1000)]).astype(np.int32)
+    per_req = np.array([ctx[req == r].max() for r in range(len(lens))])
+    table = token_tables(rng, per_req, block, num_blocks, -(-3000 // block))
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    q_bits = random_bits(rng, (len(ctx), 16, width))
+    q, cache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    ws = ops.S6Workspace(16, width, len(ctx) * splits)
+    o, lse = ops.history_attention_kv(q, cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx), SCALE,
+                                      splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=group,
+                                      shared_rows=True)
+    T = len(ctx)
+    flat = ws.ensure(q.device)
+    part_lse = host_f32(flat[T * splits * 16 * width:T * splits * 16 * (width + 1)]).reshape(T, splits, 16)
+    tiles = -(-3000 // 16)
+    chunk = -(-tiles // splits)
+    for t in range(T):
+        used = -(-(-(-int(ctx[t]) // 16)) // chunk)
+        assert np.isfinite(part_lse[t, :used]).all(), (t, used)
+        assert np.isneginf(part_lse[t, used:]).all(), (t, used)
+    assert used < splits and np.isfinite(part_lse[0]).all()
+    check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
+
+
 @pytest.mark.parametrize('width,block,long_ctx,splits', [(512, 16, 33000, 1),  # more pages than the LDS list holds
                                                          (512, 16, 33000, 3),
                                                          (512, 32, 5003, 1),   # pages of 32 rows

@@ -107,10 +107,11 @@ def test_mi355x_split_policy(ops):
     assert ops.mi355x_kv_splits(32769, 8, 256, width=256) == 256
     assert ops.mi355x_kv_splits(300, 1, 256) == 4
     assert ops.mi355x_kv_splits(1, 4096, 256) == 2
-    # multi-query steps: two 4-token workgroups per CU
+    # multi-query steps: one busy 8-token workgroup per CU, every slot filled, at least 256 keys per slot
     assert ops.mi355x_kv_splits(8704, 2048, 256, tokens_per_group=4) == 1
+    assert ops.mi355x_kv_splits(8704, 1024, 256, tokens_per_group=4) == 2
     assert ops.mi355x_kv_splits(8704, 64, 256, tokens_per_group=4) == 32
-    assert ops.mi355x_kv_splits(300, 64, 256, tokens_per_group=4) == 4
+    assert ops.mi355x_kv_splits(300, 64, 256, tokens_per_group=4) == 2
     assert ops.mi355x_kv_splits(10 ** 6, 1, 256, width=128) == 1024    # the kernel's maximum
 
 
