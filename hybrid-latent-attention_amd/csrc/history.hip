@@ -1091,21 +1091,23 @@ constexpr int kKhop1024Tokens = 2;      // tokens per workgroup of the 1024-wide
 // waited for explicitly (s_waitcnt vmcnt counting the copies issued after the awaited ones) and the loop
 // synchronizes with plain s_barrier behind those waits, so a copy still in flight for a later tile is never waited
 // for at a barrier.
-//   R = 256: 4 waves of 2 tokens, 74 KB of LDS: two workgroups per CU, whose tiles run out of step;
-//   R = 512: 8 waves of 1 token (the registers hold 16 query rows x 512 columns), 139 KB of LDS.
+//   R = 512: 8 waves of 1 token (the registers hold 16 query rows x 512 columns), 139 KB of LDS;
+//   R = 256: 74 KB of LDS; 4 waves of 2 tokens when the grid has more workgroups than CUs (two workgroups per CU,
+//   whose tiles run out of step), else 8 waves of 1 token (one workgroup per CU at two waves per SIMD instead of
+//   one).
 constexpr int kMq5Pages = 1024;  // block-table entries of a pass kept in LDS (longer passes read them from memory)
 
-template <int R>
+template <int R, int kTpw = 1>
 struct Mq5Geo {
-  static constexpr int TPW = R == 256 ? 2 : 1;  // tokens per wave
+  static constexpr int TPW = kTpw;              // tokens per wave
   static constexpr int NW = kMq4Tokens / TPW;   // waves per workgroup
   static constexpr int RPW = kMq4Keys / NW;     // tile rows each wave copies (K and V each)
 };
 
-template <int R, int kMode>
-__global__ __launch_bounds__(64 * Mq5Geo<R>::NW, R == 256 ? 2 : 1) void history_mq5(HistoryParams a) {
+template <int R, int kMode, int kTpw = 1>
+__global__ __launch_bounds__((64 * Mq5Geo<R, kTpw>::NW), R == 256 ? 2 : 1) void history_mq5(HistoryParams a) {
   static_assert(R == 256 || R == 512, "rows of 512 B (half a copy instruction) or 1 KB");
-  using G = Mq5Geo<R>;
+  using G = Mq5Geo<R, kTpw>;
   constexpr int TPW = G::TPW, NW = G::NW, RPW = G::RPW;
   constexpr bool kContig = kMode != 0, kMask = kMode == 2;
   constexpr int TOPS = 2 * RPW + (kMask ? 1 : 0);  // copy instructions per wave for a tile (K, V rows, mask)
@@ -1733,14 +1735,34 @@ int launch_combine(const HistoryParams& p, hipStream_t stream) {
   return check_launch("history_combine");
 }
 
+// CUs of the current device (256 if the runtime cannot say)
+inline int current_device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return 256;
+  return cus;
+}
+
+// history_mq5 on a grid of (token groups, slots): at R = 256 two tokens per wave when the grid outnumbers the CUs
+template <int R, int kMode>
+void launch_mq5(const HistoryParams& p, unsigned groups, unsigned slots, hipStream_t stream) {
+  const dim3 grid(groups, slots);
+  if constexpr (R == 256) {
+    if ((uint64_t)groups * slots > (uint64_t)current_device_cus()) {
+      hipLaunchKernelGGL((history_mq5<256, kMode, 2>), grid, dim3(64 * Mq5Geo<256, 2>::NW), 0, stream, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((history_mq5<R, kMode, 1>), grid, dim3(64 * Mq5Geo<R, 1>::NW), 0, stream, p);
+}
+
 template <int R>
 int launch(const HistoryParams& p, hipStream_t stream) {
   if (p.group > 1) {
     const dim3 grid((unsigned)((p.T + p.group - 1) / p.group), p.num_splits);
     if (p.group == 4 && (R == 256 || R == 512) && p.scale_log2 > 0.f)  // history_mq5 folds a positive scale
-      hipLaunchKernelGGL((history_mq5<R == 256 ? 256 : 512, 0>),
-                         dim3((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits), dim3(64 * Mq5Geo<R == 256 ? 256 : 512>::NW),
-                         0, stream, p);
+      launch_mq5<R == 256 ? 256 : 512, 0>(p, (unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), p.num_splits, stream);
     else if (p.group == 4 && R <= 512)
       hipLaunchKernelGGL((history_mq2<R <= 512 ? R : 512, false>), grid, dim3(512), 0, stream, p);
     else  // two tokens per workgroup (four 1024-wide tokens would spill registers and run twice as slow)
@@ -1893,11 +1915,11 @@ int khop_forward_mq(const void* q, int64_t q_st, int64_t q_sh, const void* k, co
                        dim3((unsigned)((p.T + kKhop1024Tokens - 1) / kKhop1024Tokens), 1), dim3(Geo<1024>::THREADS), 0,
                        stream, p);
   } else if (mq5) {
-    const dim3 grid5((unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens), 1);
-    if (width == 512 && mask) hipLaunchKernelGGL((history_mq5<512, 2>), grid5, dim3(512), 0, stream, p);
-    else if (width == 512) hipLaunchKernelGGL((history_mq5<512, 1>), grid5, dim3(512), 0, stream, p);
-    else if (mask) hipLaunchKernelGGL((history_mq5<256, 2>), grid5, dim3(256), 0, stream, p);
-    else hipLaunchKernelGGL((history_mq5<256, 1>), grid5, dim3(256), 0, stream, p);
+    const unsigned groups = (unsigned)((p.T + kMq4Tokens - 1) / kMq4Tokens);
+    if (width == 512 && mask) launch_mq5<512, 2>(p, groups, 1, stream);
+    else if (width == 512) launch_mq5<512, 1>(p, groups, 1, stream);
+    else if (mask) launch_mq5<256, 2>(p, groups, 1, stream);
+    else launch_mq5<256, 1>(p, groups, 1, stream);
   } else {
     const dim3 grid((unsigned)((p.T + kMqTokens - 1) / kMqTokens), 1);
     hipLaunchKernelGGL((history_mq2<512, true>), grid, dim3(512), 0, stream, p);

@@ -247,6 +247,36 @@ def test_grouped_history_page_geometry(ops, width, block, long_ctx, splits):
     check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
 
 
+def test_grouped_history_width_256_both_wave_forms(ops):
+    """At width 256 the multi-query kernel takes two tokens per wave when its grid has more workgroups than the
+    device has CUs, else one: a step of 8 x (CUs + 8) tokens (the first form) and its first request's 16 tokens
+    alone (the second form) both match the oracle on those tokens (the two forms may round the row sum's update
+    differently, so they agree to the attention tolerance, not bit for bit)."""
+    width, block, n_ctx = 256, 16, 100
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    T = 8 * (cus + 8)
+    rng = np.random.default_rng(256)
+    req = np.arange(T) // 16
+    R = int(req[-1]) + 1
+    num_blocks = 64
+    table = rng.integers(1, num_blocks, (R, -(-n_ctx // block))).astype(np.int32)
+    ctx = (n_ctx - (np.arange(T) % 16)).astype(np.int32)
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    q_bits = random_bits(rng, (T, 16, width))
+    cache = dev_bf16(cache_bits)
+    outs = []
+    for n in (T, 16):
+        q = dev_bf16(q_bits[:n])
+        o, lse = ops.history_attention_kv(q, cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx[:n]),
+                                          SCALE, 1, None, None, None, 'hip', bt_rows=dev_i64(req[:n]),
+                                          tokens_per_group=4, shared_rows=True)
+        outs.append((o[:16].clone(), lse[:, :16].clone()))
+    want = oracle_history(q_bits[:16], cache_bits, table[req[:16]], ctx[:16])
+    for o, lse in outs:
+        check(host_f32(o), host_f32(lse), *want, ctx[:16])
+    assert_attention_close(host_f32(outs[0][0]), host_f32(outs[1][0]), 'two-token vs one-token waves')
+
+
 def test_grouped_history_rejects_unsupported_group(ops):
     q = torch.zeros(2, 16, 512, dtype=torch.bfloat16, device='cuda')
     cache = torch.zeros(4, 1, 16, 1024, dtype=torch.bfloat16, device='cuda')

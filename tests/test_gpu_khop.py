@@ -198,6 +198,24 @@ def test_one_mask_row_per_batch_row_broadcast_over_queries(R, N):
     assert_lse_close(outs[1][1].numpy(), lo)
 
 
+def test_width_256_forward_in_both_wave_forms():
+    """At width 256 the forward takes two tokens per wave when its grid has more 8-token workgroups than the device
+    has CUs, else one: batch row 0 of a call with 8 x (CUs + 8) queries and row 0 alone both match the oracle."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    R, Lq, N = 256, 64, 96
+    B = -(-8 * (cus + 8) // Lq)
+    q, k, v, mask = case(5, B, Lq, N, R, 'any')
+    scale = 1 / math.sqrt(R)
+    qt, kt, vt = (torch.tensor(x, device='cuda').to(torch.bfloat16) for x in (q, k, v))
+    mt = torch.tensor(mask, device='cuda')
+    z_all, l_all = hg.causal_history_gemm(qt, kt, vt, mt, scale, precision='bf16')
+    z_one, l_one = hg.causal_history_gemm(qt[:1], kt[:1], vt[:1], mt[:1], scale, precision='bf16')
+    zo, lo = O.causal_history(q[:1], k[:1], v[:1], mask[:1], scale)
+    for z, lse in ((z_all[:1], l_all[:1]), (z_one, l_one)):
+        assert_attention_close(z.float().cpu().numpy(), zo, 'z')
+        assert_lse_close(lse.cpu().numpy(), lo)
+
+
 def test_backward_is_bitwise_repeatable_and_needs_only_what_is_asked():
     q, k, v, mask = case(3, 2, 30, 30, 256, 'benchmark')
     rng = np.random.default_rng(4)
