@@ -67,15 +67,16 @@ int launch_exact(const ExactParams& p, hipStream_t stream, const char* what) {
   return check_launch(what);
 }
 
-// Causal attention inside each request's chunk: one workgroup of kChunkWaves waves per (kChunkQ consecutive tokens,
-// head), 16 queries per wave. The tokens of a workgroup that belong to one request read that request's keys in tiles
-// of 16 rows, each tile loaded once for the workgroup (one coalesced 16-byte piece of K and of V per thread, a few
-// tiles ahead in registers) and staged in LDS, double-buffered, one barrier per tile. Each wave then computes
+// Causal attention inside each request's chunk: one workgroup of NW waves per (16 NW consecutive tokens, head), 16
+// queries per wave. The tokens of a workgroup that belong to one request read that request's keys in tiles
+// of 16 rows, each tile loaded once for the workgroup (coalesced 16-byte pieces of K and of V, 4 / NW per thread, a
+// few tiles ahead in registers) and staged in LDS, double-buffered, one barrier per tile. Each wave then computes
 //   S^T[16 keys x 16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows from LDS as the A operand, Q^T in
 //   registers), causal mask key <= query, online softmax per query column, and
 //   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x16_bf16 with V^T read from LDS by ds_read_b64_tr_b16,
 // skipping the tiles wholly past its last query. Sharing the tiles over 64 queries instead of 16 cuts the L2 requests
-// of the causal re-reads fourfold, which bound the one-wave-per-16-tokens form.
+// of the causal re-reads fourfold, which bound an earlier one-wave form that gathered K in 64-byte pieces; the
+// single-wave blocks here copy whole coalesced tiles and run only where 64-token blocks would leave CUs idle.
 struct ChunkParams {
   const uint16_t *q, *k, *v;
   int64_t q_st, q_sh, k_st, k_sh, v_st, v_sh;
@@ -97,12 +98,20 @@ struct ChunkParams {
 
 constexpr int kChunkVS = kExactDim + 16;    // LDS row stride of the V tile (conflict-free transposed reads)
 constexpr int kChunkKS = kExactDim + 8;     // LDS row stride of the K tile (conflict-free 16-byte row reads)
-constexpr int kChunkWaves = 4;              // waves per workgroup, 16 queries each
-constexpr int kChunkQ = 16 * kChunkWaves;   // queries per workgroup
-constexpr int kChunkDepth = 4;              // key tiles in flight (registers) per thread
+// Waves per workgroup, 16 queries each: 4 (the tiles shared by 64 queries), or 1 for steps of short requests whose
+// grid of 64-token blocks leaves CUs idle (such a block would run several requests' passes one after another on one
+// CU; 16-token blocks spread them).
+template <int NW>
+struct ChunkGeo {
+  static constexpr int Q = 16 * NW;               // queries per workgroup
+  static constexpr int P = 256 / (64 * NW);       // 16-byte pieces of a 16-row tile per thread (K and V each)
+  static constexpr int DEPTH = NW == 1 ? 2 : 4;   // key tiles in flight (registers) per thread
+};
 
-template <bool kWin>
-__global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
+template <bool kWin, int NW>
+__global__ __launch_bounds__(64 * NW) void chunk_mfma(ChunkParams a) {
+  using G = ChunkGeo<NW>;
+  constexpr int kChunkQ = G::Q, kChunkDepth = G::DEPTH, P = G::P;
   __shared__ __attribute__((aligned(16))) uint16_t ks_l[2][16 * kChunkKS];
   __shared__ __attribute__((aligned(16))) uint16_t vs_l[2][16 * kChunkVS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hq = lane & 15, g = lane >> 4;
@@ -157,23 +166,27 @@ __global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
     const int q_pos = qw + hq;  // this column's query token (keys <= q_pos are visible)
     const int nwt = (w_hi - w_lo + 15) / 16;  // window tiles, taken before the chunk's (one online softmax)
     const int nct = ke > kb ? (ke - kb + 15) / 16 : 0;
-    // this thread's pieces of tile ti: row tid / 16, bytes 16 * (tid % 16) of K and of V (rows past the tile's
-    // keys zeroed)
-    auto load = [&](int ti, u32x4& kx, u32x4& vx) {
+    // this thread's pieces u of tile ti: piece c = tid + 64 NW u is row c / 16, bytes 16 * (c % 16) of K and of V
+    // (rows past the tile's keys zeroed)
+    auto load = [&](int ti, u32x4 (&kx)[P], u32x4 (&vx)[P]) {
       const bool wt = kWin && ti < nwt;
       const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
       const int kend = wt ? w_hi : ke;
-      const int row = tid >> 4, d0 = (tid & 15) * 8, key = min(k0 + row, kend - 1);
-      if (wt) {
-        const uint16_t *kp, *vp;
-        src.rows(key, h, d0, kp, vp);
-        kx = ld16(kp);
-        vx = ld16(vp);
-      } else {
-        kx = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + d0);
-        vx = ld16(a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + d0);
+#pragma unroll
+      for (int u = 0; u < P; ++u) {
+        const int c = tid + 64 * NW * u;
+        const int row = c >> 4, d0 = (c & 15) * 8, key = min(k0 + row, kend - 1);
+        if (wt) {
+          const uint16_t *kp, *vp;
+          src.rows(key, h, d0, kp, vp);
+          kx[u] = ld16(kp);
+          vx[u] = ld16(vp);
+        } else {
+          kx[u] = ld16(a.k + (int64_t)key * a.k_st + (int64_t)h * a.k_sh + d0);
+          vx[u] = ld16(a.v + (int64_t)key * a.v_st + (int64_t)h * a.v_sh + d0);
+        }
+        if (k0 + row >= kend) kx[u] = vx[u] = u32x4{0u, 0u, 0u, 0u};
       }
-      if (k0 + row >= kend) kx = vx = u32x4{0u, 0u, 0u, 0u};
     };
     // this wave's part of tile ti from LDS: S^T, causal mask, online softmax, O^T += V^T P^T
     auto compute = [&](int ti, const uint16_t* ks, const uint16_t* vs) {
@@ -235,7 +248,7 @@ __global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
     // its tile is in LDS (compile-time indices: no register copies). LDS buffer ti % 2 is rewritten two tiles later,
     // after the barrier that every wave passes only once it has computed the tile before
     const int ntl = nwt + nct;
-    u32x4 kx[kChunkDepth], vx[kChunkDepth];
+    u32x4 kx[kChunkDepth][P], vx[kChunkDepth][P];
 #pragma unroll
     for (int d = 0; d < kChunkDepth; ++d)
       if (d < ntl) load(d, kx[d], vx[d]);
@@ -246,8 +259,12 @@ __global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
         if (ti < ntl) {  // (uniform over the workgroup)
           uint16_t* ks = ks_l[ti & 1];
           uint16_t* vs = vs_l[ti & 1];
-          st16(ks + (tid >> 4) * kChunkKS + (tid & 15) * 8, kx[d]);
-          st16(vs + (tid >> 4) * kChunkVS + (tid & 15) * 8, vx[d]);
+#pragma unroll
+          for (int u = 0; u < P; ++u) {
+            const int c = tid + 64 * NW * u;
+            st16(ks + (c >> 4) * kChunkKS + (c & 15) * 8, kx[d][u]);
+            st16(vs + (c >> 4) * kChunkVS + (c & 15) * 8, vx[d][u]);
+          }
           if (ti + kChunkDepth < ntl) load(ti + kChunkDepth, kx[d], vx[d]);
           __syncthreads();
           compute(ti, ks, vs);
@@ -269,6 +286,24 @@ __global__ __launch_bounds__(64 * kChunkWaves) void chunk_mfma(ChunkParams a) {
     }
     __syncthreads();  // the next pass rewrites the LDS tiles
     tp += count;
+  }
+}
+
+// 16-token single-wave blocks when the requests average fewer than 64 tokens (a 64-token block would run several
+// requests' passes one after another) and 64-token blocks x heads leave CUs idle; the 4-wave form otherwise
+template <bool kWin>
+void launch_chunk(ChunkParams& p, hipStream_t stream) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    cus = 256;
+  const int64_t blocks4 = (p.T + ChunkGeo<4>::Q - 1) / ChunkGeo<4>::Q;
+  if (blocks4 * p.heads >= cus || (int64_t)p.T >= (int64_t)ChunkGeo<4>::Q * p.num_reqs) {
+    p.nblk = (int)blocks4;
+    hipLaunchKernelGGL((chunk_mfma<kWin, 4>), dim3((unsigned)p.nblk * (unsigned)p.heads), dim3(64 * 4), 0, stream, p);
+  } else {
+    p.nblk = (p.T + ChunkGeo<1>::Q - 1) / ChunkGeo<1>::Q;
+    hipLaunchKernelGGL((chunk_mfma<kWin, 1>), dim3((unsigned)p.nblk * (unsigned)p.heads), dim3(64), 0, stream, p);
   }
 }
 
@@ -369,10 +404,8 @@ extern "C" int hla_s6_chunk_attention(const void* q, const void* k, const void* 
   p.o_st = o_st;
   p.o_sh = o_sh;
   p.lse = lse;
-  p.nblk = (num_tokens + kChunkQ - 1) / kChunkQ;
   p.heads = num_heads;
-  hipLaunchKernelGGL(chunk_mfma<false>, dim3((unsigned)p.nblk * (unsigned)num_heads), dim3(64 * kChunkWaves), 0,
-                     as_stream(stream), p);
+  launch_chunk<false>(p, as_stream(stream));
   return check_launch("chunk_attention");
 }
 
@@ -431,9 +464,7 @@ extern "C" int hla_s6_chunk_window_attention(const void* q, const void* k, const
   p.bt_cols = bt_cols;
   p.seq_lens = seq_lens;
   p.window = window;
-  p.nblk = (num_tokens + kChunkQ - 1) / kChunkQ;
   p.heads = num_heads;
-  hipLaunchKernelGGL(chunk_mfma<true>, dim3((unsigned)p.nblk * (unsigned)num_heads), dim3(64 * kChunkWaves), 0,
-                     as_stream(stream), p);
+  launch_chunk<true>(p, as_stream(stream));
   return check_launch("chunk_window_attention");
 }

@@ -245,8 +245,12 @@ def test_window_history(ops, window):
 
 
 @pytest.mark.parametrize('qsl,T', [((0, 5, 6, 20, 20, 20), 24),        # empty requests, four padding tokens
-                                   ((0, 100, 101, 400, 413), 420)])     # long chunks crossing 16-token blocks
+                                   ((0, 100, 101, 400, 413), 420),      # long chunks crossing 16-token blocks
+                                   ((0, 300, 301, 1000, 1100), 1104),   # 4-wave blocks (one per CU or more)
+                                   ((0, 15, 45, 46, 70, 100, 131, 160, 190, 222, 250, 280, 300), 304)])
 def test_chunk_attention(ops, qsl, T):
+    """Single-wave 16-token blocks for steps of short requests (fewer than 64 tokens on average) whose 64-token
+    blocks x 16 heads would leave CUs idle (the first and last cases), 4-wave 64-token blocks otherwise."""
     rng = np.random.default_rng(9 + T)
     H, d = 16, 128
     qsl = np.array(qsl, np.int32)
@@ -261,7 +265,8 @@ def test_chunk_attention(ops, qsl, T):
 
 
 @pytest.mark.parametrize('lens,hist,pad', [((5, 1, 14, 0, 0), (0, 40, 7, 3, 0), 4),   # no history, short history,
-                                           ((100, 1, 299, 13), (33, 90, 0, 17), 7)])  # empty requests, padding
+                                           ((100, 1, 299, 13), (33, 90, 0, 17), 7),   # empty requests, padding
+                                           ((600, 1, 450, 13), (33, 90, 0, 17), 7)])  # the 4-wave blocks
 def test_chunk_window_attention(ops, lens, hist, pad):
     """The one-softmax chunk + exact window against the oracle's chunk, window history and LSE merge."""
     rng = np.random.default_rng(sum(lens) + pad)
