@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -35,6 +35,9 @@ SIGNATURES = {
     'hla_s6_history_partials': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I32, I64, P, I64, I32, P, P, F32, I32, P,
                                 I64, P, I64, P],
     'hla_s6_history_reduce': [P, I64, I32, I32, I32, I32, P, I64, I64, P, P],
+    'hla_s6_history_partials_grouped': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I32, I64, P, I64, I32, P, P, F32,
+                                        I32, P, I64, I32, P],
+    'hla_s6_split_epilogue': [P, I64, I32, I32, I32, I32, P, I64, I64, P, P, P, P, I64, I64, P],
     'hla_s6_window_attention': [P, I32, I32, I32, I64, I64, P, P, I64, I64, I64, I32, I64, P, I64, I32, P, I32, P, P,
                                 I32, P, I32, F32, P, I64, I64, P, P],
     'hla_s6_chunk_attention': [P, P, P, I32, I32, I32, I64, I64, I64, I64, I64, I64, P, I32, F32, P, I64, I64, P, P],

@@ -2056,6 +2056,71 @@ extern "C" int hla_s6_history_partials(const void* q, int32_t num_tokens, int32_
   return dispatch(p, width, as_stream(stream));
 }
 
+extern "C" int hla_s6_history_partials_grouped(const void* q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                                               int64_t q_st, int64_t q_sh, const void* k_cache, const void* v_cache,
+                                               int64_t page_stride, int64_t row_stride, int32_t block_size,
+                                               int64_t num_blocks, const int32_t* block_table, int64_t bt_stride,
+                                               int32_t bt_cols, const int64_t* bt_rows, const int32_t* ctx,
+                                               float scale, int32_t num_splits, float* workspace,
+                                               int64_t workspace_floats, int32_t group, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(group == 2 || group == 4, HLA_S6_EUNSUPPORTED,
+              "history_partials_grouped: group of %d tokens (built for 2, 4)", group);
+  HistoryParams p;
+  int rc = fill_history(p, q, num_tokens, num_heads, width, q_st, q_sh, k_cache, v_cache, page_stride, row_stride,
+                        block_size, num_blocks, block_table, bt_stride, bt_cols, bt_rows, ctx, scale, num_splits,
+                        workspace, workspace_floats, nullptr, 0, 0, nullptr, true);
+  if (rc != HLA_S6_OK || num_tokens == 0) return rc;
+  p.group = group;
+  p.shared_rows = true;
+  return dispatch(p, width, as_stream(stream));
+}
+
+extern "C" int hla_s6_split_epilogue(const float* workspace, int64_t workspace_floats, int32_t num_tokens,
+                                     int32_t num_heads, int32_t width, int32_t num_splits, const void* B, int64_t b_sh,
+                                     int64_t b_sr, const void* o_win, const float* lse_win, const uint8_t* invalid,
+                                     void* out, int64_t o_st, int64_t o_sh, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0, HLA_S6_EINVAL, "split_epilogue: negative token count");
+  HLA_REQUIRE(num_heads == kHeads, HLA_S6_EUNSUPPORTED, "split_epilogue: %d query heads (the kernel is built for 16)",
+              num_heads);
+  HLA_REQUIRE(width == 128 || width == 256 || width == 512 || width == 1024, HLA_S6_EUNSUPPORTED,
+              "split_epilogue: latent width %d not in {128, 256, 512, 1024}", width);
+  HLA_REQUIRE(num_splits >= 2 && num_splits <= kMaxSplits, HLA_S6_EINVAL,
+              "split_epilogue: num_kv_splits must be in [2, %d]", kMaxSplits);
+  if (num_tokens == 0) return HLA_S6_OK;
+  const int64_t need = (int64_t)num_tokens * num_splits * kHeads * (width + 1);
+  HLA_REQUIRE(workspace != nullptr && workspace_floats >= need, HLA_S6_EWORKSPACE,
+              "S6 workspace overflow: need %lld floats, have %lld", (long long)need, (long long)workspace_floats);
+  HLA_REQUIRE(aligned16(workspace), HLA_S6_EINVAL, "split_epilogue: workspace must be 16-byte aligned");
+  HLA_REQUIRE(B && o_win && lse_win && out, HLA_S6_EINVAL, "split_epilogue: null pointer argument");
+  HLA_REQUIRE(aligned16(o_win), HLA_S6_EINVAL, "split_epilogue: o_win must be 16-byte aligned");
+  HLA_REQUIRE((reinterpret_cast<uintptr_t>(B) & 3u) == 0 && b_sh % 2 == 0 && b_sr % 2 == 0 &&
+                  (reinterpret_cast<uintptr_t>(out) & 3u) == 0 && o_st % 2 == 0 && o_sh % 2 == 0,
+              HLA_S6_EINVAL, "split_epilogue: B and out need 4-byte aligned pairs");
+  EpilogueParams e = {};
+  e.T = num_tokens;
+  e.S = num_splits;
+  e.ws_o = workspace;
+  e.ws_lse = workspace + (int64_t)num_tokens * num_splits * kHeads * width;
+  e.B = static_cast<const uint16_t*>(B);
+  e.b_sh = b_sh;
+  e.b_sr = b_sr;
+  e.o_win = static_cast<const uint16_t*>(o_win);
+  e.lse_win = lse_win;
+  e.invalid = invalid;
+  e.out = static_cast<uint16_t*>(out);
+  e.o_st = o_st;
+  e.o_sh = o_sh;
+  const hipStream_t st = as_stream(stream);
+  switch (width) {
+    case 128: return launch_epilogue<128>(e, st);
+    case 256: return launch_epilogue<256>(e, st);
+    case 512: return launch_epilogue<512>(e, st);
+    default: return launch_epilogue<1024>(e, st);
+  }
+}
+
 extern "C" int hla_s6_history_reduce(const float* workspace, int64_t workspace_floats, int32_t num_tokens,
                                      int32_t num_heads, int32_t width, int32_t num_splits, void* out, int64_t o_st,
                                      int64_t o_sh, float* lse, void* stream) {

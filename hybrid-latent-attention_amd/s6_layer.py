@@ -90,7 +90,8 @@ class StepContext:
         self.history_group = 4 if (max_query_len or 1) >= 16 else 1
         self.history_needed = True
         # chunks shorter than FUSED_CHUNK_TOKENS attend through the fused decode path, reading their own keys from
-        # the exact cache (which the adapter writes before attending); False: the reference's op sequence
+        # the exact cache (which the adapter writes before attending), and longer ones with split history reduce
+        # their splits, apply B_t and merge in one epilogue; False: the reference's op sequence
         self.fused_chunks = True
         self.md_present = query_start_loc is not None
         if not self.md_present:
@@ -184,8 +185,10 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
     ``FUSED_CHUNK_TOKENS`` tokens (``ctx.fused_chunks``): their exact part is one softmax per query over the exact
     cache's rows ``[ctx - W, p]``, the window history and the chunk up to the query, which the adapter has written
     to the exact cache before attending (``hla/vllm_latent/ouro_latent.py:120-122``), so it equals the reference's
-    causal chunk of ``k_rope`` / ``v`` merged with its window history. Other steps compose the single ops in the
-    reference's order.
+    causal chunk of ``k_rope`` / ``v`` merged with its window history. Longer chunks with split history
+    (``kv_splits > 1``) compute their chunk + window partial as the reference does, then the history kernels' split
+    partials, and one epilogue reduces the splits, applies ``B_t`` and merges (the decode step's epilogue). Other
+    steps compose the single ops in the reference's order.
     """
     fused = window is not None and ctx.md_present and (ctx.max_query_len == 1 or
                                                        (ctx.fused_chunks and ctx.max_query_len < FUSED_CHUNK_TOKENS))
@@ -206,6 +209,16 @@ def attend(sl, loop, q_lat, q_rope, k_rope, v, cache, block_table, k_scale, v_sc
         return o_chunk.masked_fill_(ctx.invalid[:, None, None], 0)
     _, B, _ = sl.readers(loop)
     w = q_lat.shape[-1]
+    if window is not None and ctx.fused_chunks and ctx.history_group > 1 and ctx.kv_splits(w) > 1:
+        # multi-query step with split history: the grouped kernels' split partials, then the fused decode step's
+        # epilogue (LSE reduction, B_t, merge with the chunk + window partial) in place of history_attention,
+        # the B_t einsum and merge_states
+        for kind in ('history', 'merge'):
+            s6_ops._backend(kind, getattr(ctx.backends, kind))
+        ws = s6_ops.history_partials_grouped(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
+                                             ctx.scale, ctx.kv_splits(w), ctx.workspace, bt_rows=ctx.token_requests,
+                                             tokens_per_group=ctx.history_group)
+        return s6_ops.split_epilogue(ws, B, o_chunk, lse_chunk, ctx.invalid)
     o_hist, lse_hist = s6_ops.history_attention_kv(q_lat, cache[..., :w], cache[..., w:], block_table, ctx.ctx_latent,
                                                    ctx.scale, ctx.kv_splits(w), ctx.workspace, k_scale, v_scale,
                                                    ctx.backends.history, ctx.empty_latent, bt_rows=ctx.token_requests,

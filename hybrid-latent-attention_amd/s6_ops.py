@@ -310,6 +310,49 @@ def history_reduce(partials):
     return o, lse
 
 
+def history_partials_grouped(q, k, v, block_table, ctx, scale, num_kv_splits, workspace, bt_rows=None,
+                             tokens_per_group=4):
+    """The split kernel of ``history_attention_kv(..., tokens_per_group=2 or 4)`` writing only its per-slot partials
+    (every slot, empty ones with lse = -inf) to ``workspace``; returns the workspace view ``[T, H, splits, width + 1]``
+    for ``split_epilogue``. Operands and checks as ``history_attention_kv``."""
+    T, H, L, ctx, rows = _history_operands(q, k, v, block_table, ctx, False, bt_rows)
+    splits = int(num_kv_splits)
+    if workspace is None:
+        raise RuntimeError('history partials need an S6Workspace')
+    ws = workspace.attn_logits(T, H, splits, L, q.device)
+    _lib.call('hla_s6_history_partials_grouped', _lib.ptr(q), T, H, L, q.stride(0), q.stride(1), _lib.ptr(k),
+              _lib.ptr(v), k.stride(0), k.stride(2), k.shape[2], k.shape[0], _lib.ptr(block_table),
+              block_table.stride(0), block_table.shape[1], _lib.ptr(rows), _lib.ptr(ctx), float(scale), splits,
+              _lib.ptr(ws), ws.numel(), int(tokens_per_group), _lib.stream(q.device))
+    return ws
+
+
+def split_epilogue(partials, B, o_win, lse_win, invalid):
+    """``merge_states(bf16(o_hist) @ B, lse_hist, o_win, lse_win, invalid)`` with ``(o_hist, lse_hist)`` the LSE
+    reduction of the split partials (``history_partials_grouped``) in one launch, the epilogue of the fused decode
+    step; ``num_kv_splits >= 2``. B ``[16, width, 128]``, o_win ``[T, 16, 128]`` bf16 and lse_win ``[16, T]``
+    contiguous. Returns ``[T, 16, 128]`` bf16 with ``invalid`` rows zeroed."""
+    _dev(partials, B, o_win, lse_win, invalid)
+    if partials.dtype != torch.float32 or partials.dim() != 4 or not partials.is_contiguous():
+        raise ValueError('split_epilogue expects the fp32 workspace view returned by history_partials_grouped')
+    T, H, S, L1 = partials.shape
+    _bf16('B', B)
+    _bf16('o_win', o_win)
+    if tuple(B.shape) != (H, L1 - 1, o_win.shape[-1]) or B.stride(-1) != 1:
+        raise ValueError(f'B must be [{H}, {L1 - 1}, {o_win.shape[-1]}] with a unit last stride, got {tuple(B.shape)}')
+    if not o_win.is_contiguous() or tuple(o_win.shape[:2]) != (T, H) or tuple(lse_win.shape) != (H, T):
+        raise ValueError('o_win [T, 16, 128] and lse_win [16, T] must be contiguous partials of the same tokens')
+    lse_win = lse_win.to(torch.float32).contiguous()
+    inv = _mask(invalid)
+    if inv is not None and tuple(inv.shape) != (T,):
+        raise ValueError(f'invalid must be [{T}] bool')
+    out = torch.empty(T, H, o_win.shape[-1], dtype=BF16, device=o_win.device)
+    _lib.call('hla_s6_split_epilogue', _lib.ptr(partials), partials.numel(), T, H, L1 - 1, S, _lib.ptr(B),
+              B.stride(0), B.stride(1), _lib.ptr(o_win), _lib.ptr(lse_win), _lib.ptr(inv), _lib.ptr(out),
+              out.stride(0), out.stride(1), _lib.stream(o_win.device))
+    return out
+
+
 def _history_operands(q, k, v, block_table, ctx, mla, bt_rows):
     """Checks of the history operands; returns ``(T, H, L, ctx int32, bt_rows int64 or None)``."""
     if mla:

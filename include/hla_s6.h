@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 8
+#define HLA_S6_ABI_VERSION 9
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -137,6 +137,27 @@ int hla_s6_history_partials(const void *q, int32_t num_tokens, int32_t num_heads
 int hla_s6_history_reduce(const float *workspace, int64_t workspace_floats, int32_t num_tokens, int32_t num_heads,
                           int32_t width, int32_t num_splits, void *out, int64_t o_st, int64_t o_sh, float *lse,
                           void *stream);
+
+/* hla_s6_history_partials_grouped and hla_s6_split_epilogue: no counterpart in the reference. Together with
+ * hla_s6_chunk_window_attention they replace the op sequence of s6_layer.attend for multi-token steps with split
+ * history (hla/vllm_latent/s6_layer.py:101-115: history_attention, the B_t einsum, merge_states) by three launches:
+ * hla_s6_history_partials_grouped runs the kernels of hla_s6_history_attention_grouped (group 2 or 4 tokens per
+ * workgroup, same arguments and checks) but only writes the split partials to `workspace` (layout as for
+ * hla_s6_history_partials; every slot is written, slots without keys with lse = -inf), and hla_s6_split_epilogue
+ * (num_splits >= 2) reduces them by LSE, rounds o_hist to bf16 as the history op returns it, and writes
+ * out = merge(bf16(o_hist @ B[h]), o_win) with the merge_states conventions (invalid rows zeroed; o_win
+ * [T, 16, 128] bf16 and lse_win [16, T] contiguous, e.g. the chunk + window partial of
+ * hla_s6_chunk_window_attention): the epilogue of hla_s6_attend_decode. */
+int hla_s6_history_partials_grouped(const void *q, int32_t num_tokens, int32_t num_heads, int32_t width,
+                                    int64_t q_st, int64_t q_sh, const void *k_cache, const void *v_cache,
+                                    int64_t page_stride, int64_t row_stride, int32_t block_size, int64_t num_blocks,
+                                    const int32_t *block_table, int64_t bt_stride, int32_t bt_cols,
+                                    const int64_t *bt_rows, const int32_t *ctx, float scale, int32_t num_splits,
+                                    float *workspace, int64_t workspace_floats, int32_t group, void *stream);
+int hla_s6_split_epilogue(const float *workspace, int64_t workspace_floats, int32_t num_tokens, int32_t num_heads,
+                          int32_t width, int32_t num_splits, const void *B, int64_t b_sh, int64_t b_sr,
+                          const void *o_win, const float *lse_win, const uint8_t *invalid, void *out, int64_t o_st,
+                          int64_t o_sh, void *stream);
 
 /* ---- a6/a7: exact-window attention over the per-loop exact paged cache --------------------------
  * The exact cache is the TRITON_ATTN layout [num_blocks, block, H, 2d] (K then V per head); key row j of

@@ -138,12 +138,16 @@ def test_latent_query_then_attend_matches_fp32_reference(ops, layer):
 
 
 @pytest.mark.parametrize('lens,splits,fused', [((6, 1, 3), 1, True), ((6, 1, 3), 8, True), ((6, 1, 3), 4, False),
-                                               ((15, 1, 2), 8, True), ((40, 1, 17), 1, True), ((40, 1, 17), 4, True)])
+                                               ((15, 1, 2), 8, True), ((40, 1, 17), 1, True), ((40, 1, 17), 4, True),
+                                               ((40, 1, 17), 4, False), ((70, 1, 20), 8, True),
+                                               ((70, 1, 20), 8, False)])
 def test_prefill_and_mixed_branch(ops, layer, lens, splits, fused):
     """max_query_len > 1: causal chunk + exact window over history rows [ctx - W, ctx) + latent history. Chunks
     shorter than 16 tokens take the fused decode path (exact rows [ctx - W, p] of the exact cache, which holds the
     chunk as the adapter writes it first); longer ones the multi-query history kernel (eight tokens of a request
-    per workgroup) with the chunk from k_rope / v. Both against the oracle's reference composite."""
+    per workgroup) with the chunk from k_rope / v, and with split history (fused) the split partials reduced, B_t
+    applied and merged in one epilogue (one and four tokens per epilogue workgroup: 60 and 93 rows), or (not fused)
+    the reference's op sequence. All against the oracle's reference composite."""
     rng = np.random.default_rng(4 + sum(lens) + splits + fused)
     w = 512
     # request 0: prefill after 900 history rows; request 1: decode after 40; request 2: fresh prompt
