@@ -184,6 +184,50 @@ def test_grouped_history_matches_oracle(ops, width, splits, group):
     assert_lse_close(lse, lse1)
 
 
+@pytest.mark.parametrize('width,T', [(512, 40), (256, 40), (512, 80)])
+def test_grouped_partials_and_split_epilogue(ops, layer, width, T):
+    """hla_s6_history_partials_grouped + hla_s6_history_reduce give the grouped history op's result (the reduce
+    reads every slot, the op only the used ones: the same terms, summed in groups that can differ); the split
+    epilogue over those partials equals merge_states(absorb_out(o_hist, B), lse_hist, o_win, lse_win, invalid) to the
+    attention tolerance (its B_t product sums in another order), with invalid rows zeroed; bad arguments raise
+    before any launch."""
+    rng = np.random.default_rng(width + T)
+    block, num_blocks, splits = 16, 500, 5
+    lens = [T // 2, T // 4, T - T // 2 - T // 4]
+    req = np.repeat(np.arange(3), lens)
+    ctx = np.concatenate([np.full(lens[0], 2000), np.full(lens[1], 0), 300 + np.arange(lens[2])]).astype(np.int32)
+    per_req = np.array([max(1, ctx[req == r].max()) for r in range(3)])
+    table = token_tables(rng, per_req, block, num_blocks, -(-2000 // block))
+    cache_bits = latent_cache_bits(rng, num_blocks, block, width)
+    q = dev_bf16(random_bits(rng, (T, 16, width)))
+    cache = dev_bf16(cache_bits)
+    k, v, bt, c, rows = cache[..., :width], cache[..., width:], dev_i32(table), dev_i32(ctx), dev_i64(req)
+    ws = ops.S6Workspace(16, width, T * splits)
+    o_ref, lse_ref = ops.history_attention_kv(q, k, v, bt, c, SCALE, splits, ws, None, None, 'hip', bt_rows=rows,
+                                              tokens_per_group=4, shared_rows=True)
+    o_ref, lse_ref = o_ref.clone(), lse_ref.clone()
+    part = ops.history_partials_grouped(q, k, v, bt, c, SCALE, splits, ws, bt_rows=rows, tokens_per_group=4)
+    o, lse = ops.history_reduce(part)
+    assert_attention_close(host_f32(o), host_f32(o_ref), 'grouped partials + reduce vs the grouped op')
+    assert_lse_close(host_f32(lse), host_f32(lse_ref))
+    B = dev_bf16(random_bits(rng, (16, width, 128), 1 / math.sqrt(2048)))
+    o_win = dev_bf16(random_bits(rng, (T, 16, 128)))
+    lse_win = torch.tensor(rng.standard_normal((16, T)).astype(np.float32), device='cuda')
+    lse_win[:, 1] = -math.inf                       # a row whose chunk part is empty
+    invalid = torch.zeros(T, dtype=torch.bool, device='cuda')
+    invalid[-1] = True
+    got = ops.split_epilogue(part, B, o_win, lse_win, invalid)
+    want = ops.merge_states(layer.absorb_out(o_ref, B), lse_ref, o_win, lse_win, invalid, 'hip')
+    assert_attention_close(host_f32(got), host_f32(want), 'split epilogue vs op sequence')
+    assert (host_f32(got)[-1] == 0).all()
+    with pytest.raises(ValueError, match='num_kv_splits'):
+        ops.split_epilogue(ws.attn_logits(T, 16, 1, width, q.device), B, o_win, lse_win, invalid)
+    with pytest.raises(ValueError, match='B must be'):
+        ops.split_epilogue(part, B[:, :64], o_win, lse_win, invalid)
+    with pytest.raises(ValueError, match='group'):
+        ops.history_partials_grouped(q, k, v, bt, c, SCALE, splits, ws, bt_rows=rows, tokens_per_group=3)
+
+
 @pytest.mark.parametrize('width,group', [(512, 4), (256, 4), (1024, 2)])
 def test_grouped_history_fills_every_slot(ops, width, group):
     """The multi-token kernels run one workgroup per (token group, slot): every slot of the longest row holds
