@@ -69,11 +69,12 @@ int launch_exact(const ExactParams& p, hipStream_t stream, const char* what) {
 
 // Causal attention inside each request's chunk: one workgroup of NW waves per (16 NW consecutive tokens, head), 16
 // queries per wave. The tokens of a workgroup that belong to one request read that request's keys in tiles
-// of 16 rows, each tile loaded once for the workgroup (coalesced 16-byte pieces of K and of V, 4 / NW per thread, a
-// few tiles ahead in registers) and staged in LDS, double-buffered, one barrier per tile. Each wave then computes
-//   S^T[16 keys x 16 queries] = K . Q^T on v_mfma_f32_16x16x32_bf16 (K rows from LDS as the A operand, Q^T in
-//   registers), causal mask key <= query, online softmax per query column, and
-//   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x16_bf16 with V^T read from LDS by ds_read_b64_tr_b16,
+// of 32 rows (16 with one wave), each tile loaded once for the workgroup (coalesced 16-byte pieces of K and of V,
+// two tiles ahead in registers) and staged in LDS, double-buffered, one barrier per tile. Each wave then computes
+//   S^T[16 keys x 16 queries] = K . Q^T per 16-key block on v_mfma_f32_16x16x32_bf16 (K rows from LDS as the A
+//   operand, Q^T in registers), causal mask key <= query, online softmax per query column, and
+//   O^T[128 x 16 queries] += V^T . P^T on v_mfma_f32_16x16x32_bf16 over the tile's 32 keys (16x16x16 over 16)
+//   with V^T read from LDS by ds_read_b64_tr_b16,
 // skipping the tiles wholly past its last query. Sharing the tiles over 64 queries instead of 16 cuts the L2 requests
 // of the causal re-reads fourfold, which bound an earlier one-wave form that gathered K in 64-byte pieces; the
 // single-wave blocks here copy whole coalesced tiles and run only where 64-token blocks would leave CUs idle.
@@ -104,16 +105,18 @@ constexpr int kChunkKS = kExactDim + 8;     // LDS row stride of the K tile (con
 template <int NW>
 struct ChunkGeo {
   static constexpr int Q = 16 * NW;               // queries per workgroup
-  static constexpr int P = 256 / (64 * NW);       // 16-byte pieces of a 16-row tile per thread (K and V each)
-  static constexpr int DEPTH = NW == 1 ? 2 : 4;   // key tiles in flight (registers) per thread
+  static constexpr int TK = NW == 1 ? 16 : 32;    // keys per tile
+  static constexpr int KB = TK / 16;              // 16-key blocks per tile
+  static constexpr int P = TK * 16 / (64 * NW);   // 16-byte pieces of a tile per thread (K and V each)
+  static constexpr int DEPTH = 2;                  // key tiles in flight (registers) per thread
 };
 
 template <bool kWin, int NW>
 __global__ __launch_bounds__(64 * NW) void chunk_mfma(ChunkParams a) {
   using G = ChunkGeo<NW>;
-  constexpr int kChunkQ = G::Q, kChunkDepth = G::DEPTH, P = G::P;
-  __shared__ __attribute__((aligned(16))) uint16_t ks_l[2][16 * kChunkKS];
-  __shared__ __attribute__((aligned(16))) uint16_t vs_l[2][16 * kChunkVS];
+  constexpr int kChunkQ = G::Q, kChunkDepth = G::DEPTH, P = G::P, TK = G::TK, KB = G::KB;
+  __shared__ __attribute__((aligned(16))) uint16_t ks_l[2][TK * kChunkKS];
+  __shared__ __attribute__((aligned(16))) uint16_t vs_l[2][TK * kChunkVS];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, hq = lane & 15, g = lane >> 4;
   // Workgroup b runs on XCD b % 8 (workgroups are dealt to the XCDs round-robin). With a multiple of 8 heads, the
   // token blocks of head h all run on XCD h % 8, so the re-reads of a request's K/V rows by its token blocks hit
@@ -164,13 +167,13 @@ __global__ __launch_bounds__(64 * NW) void chunk_mfma(ChunkParams a) {
     for (int nt = 0; nt < 8; ++nt) oacc[nt] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m = -INFINITY, l = 0.f;
     const int q_pos = qw + hq;  // this column's query token (keys <= q_pos are visible)
-    const int nwt = (w_hi - w_lo + 15) / 16;  // window tiles, taken before the chunk's (one online softmax)
-    const int nct = ke > kb ? (ke - kb + 15) / 16 : 0;
+    const int nwt = (w_hi - w_lo + TK - 1) / TK;  // window tiles, taken before the chunk's (one online softmax)
+    const int nct = ke > kb ? (ke - kb + TK - 1) / TK : 0;
     // this thread's pieces u of tile ti: piece c = tid + 64 NW u is row c / 16, bytes 16 * (c % 16) of K and of V
     // (rows past the tile's keys zeroed)
     auto load = [&](int ti, u32x4 (&kx)[P], u32x4 (&vx)[P]) {
       const bool wt = kWin && ti < nwt;
-      const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
+      const int k0 = wt ? w_lo + TK * ti : kb + TK * (ti - nwt);
       const int kend = wt ? w_hi : ke;
 #pragma unroll
       for (int u = 0; u < P; ++u) {
@@ -191,32 +194,45 @@ __global__ __launch_bounds__(64 * NW) void chunk_mfma(ChunkParams a) {
     // this wave's part of tile ti from LDS: S^T, causal mask, online softmax, O^T += V^T P^T
     auto compute = [&](int ti, const uint16_t* ks, const uint16_t* vs) {
       const bool wt = kWin && ti < nwt;
-      const int k0 = wt ? w_lo + 16 * ti : kb + 16 * (ti - nwt);
+      const int k0 = wt ? w_lo + TK * ti : kb + TK * (ti - nwt);
       const int kend = wt ? w_hi : ke;
       if (cw == 0 || (!wt && k0 > last_q)) return;  // no query of the wave sees a key of the tile (wave-uniform)
-      floatx4 s = {0.f, 0.f, 0.f, 0.f};
+      floatx4 s[KB];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        s = mfma16x16x32(*reinterpret_cast<const u32x4*>(ks + hq * kChunkKS + 32 * i + 8 * g), qb[i], s);
-      float sc[4];
+      for (int b2 = 0; b2 < KB; ++b2) {
+        s[b2] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          s[b2] = mfma16x16x32(*reinterpret_cast<const u32x4*>(ks + (16 * b2 + hq) * kChunkKS + 32 * i + 8 * g), qb[i],
+                               s[b2]);
+      }
+      float sc[KB][4];
       // wave-uniform: every key of the tile is visible to every query of the wave (a window tile inside the
       // window, or a chunk tile wholly before the wave's first query)
-      const bool full = wt ? k0 + 16 <= kend : k0 + 16 <= ke && k0 + 15 <= qw;
+      const bool full = wt ? k0 + TK <= kend : k0 + TK <= ke && k0 + TK - 1 <= qw;
       if (full) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = hq < cw ? s[r] * a.scale_log2 : -INFINITY;
+        for (int b2 = 0; b2 < KB; ++b2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sc[b2][r] = hq < cw ? s[b2][r] * a.scale_log2 : -INFINITY;
       } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = k0 + 4 * g + r;
-          const bool vis = wt ? key < kend : key < ke && key <= q_pos;
-          sc[r] = (vis && hq < cw) ? s[r] * a.scale_log2 : -INFINITY;
-        }
+        for (int b2 = 0; b2 < KB; ++b2)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = k0 + 16 * b2 + 4 * g + r;
+            const bool vis = wt ? key < kend : key < ke && key <= q_pos;
+            sc[b2][r] = (vis && hq < cw) ? s[b2][r] * a.scale_log2 : -INFINITY;
+          }
       }
       // (scores are finite or -inf: masked keys never reach a maximum); the running maximum is raised lazily, only
       // when a tile exceeds it by more than 2^8 (the exponentials stay below 2^8), which skips the rescale of the
       // accumulators on most tiles
-      const float mx = wave_max16x4_nn(max_nn(max_nn(sc[0], sc[1]), max_nn(sc[2], sc[3])));
+      float mloc = max_nn(max_nn(sc[0][0], sc[0][1]), max_nn(sc[0][2], sc[0][3]));
+#pragma unroll
+      for (int b2 = 1; b2 < KB; ++b2)
+        mloc = max_nn(mloc, max_nn(max_nn(sc[b2][0], sc[b2][1]), max_nn(sc[b2][2], sc[b2][3])));
+      const float mx = wave_max16x4_nn(mloc);
       const bool raise = mx > m + 8.f;  // false while the column has no visible key (mx = -inf)
       if (__any(raise)) {
         const float m_new = raise ? mx : m;
@@ -229,19 +245,39 @@ __global__ __launch_bounds__(64 * NW) void chunk_mfma(ChunkParams a) {
         for (int nt = 0; nt < 8; ++nt) oacc[nt] = oacc[nt] * alpha;
       }
       const float m_use = m == -INFINITY ? 0.f : m;
-      float p[4];
+      float p[KB][4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_use);
-      l += (p[0] + p[1]) + (p[2] + p[3]);  // this lane's share of the column sum (summed over the 4 lanes at the end)
-      const uint32_t p01 = pack2_hw(p[0], p[1]), p23 = pack2_hw(p[2], p[3]);
-      const short4v pb = {(short)(p01 & 0xffffu), (short)(p01 >> 16), (short)(p23 & 0xffffu), (short)(p23 >> 16)};
+      for (int b2 = 0; b2 < KB; ++b2) {
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        // lane (g, hq) of the A operand: V[4g + e][16nt + hq]; the transposing read takes row 4g + hq/4,
-        // columns 16nt + 4(hq%4) .. +3 in each 16-lane group
-        const uint16_t* vp = vs + (4 * g + (hq >> 2)) * kChunkVS + 16 * nt + 4 * (hq & 3);
-        const short4v va = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
-        oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
+        for (int r = 0; r < 4; ++r) p[b2][r] = fast_exp2(sc[b2][r] - m_use);
+        l += (p[b2][0] + p[b2][1]) + (p[b2][2] + p[b2][3]);  // this lane's share of the column sum
+      }
+      if constexpr (KB == 1) {
+        const uint32_t p01 = pack2_hw(p[0][0], p[0][1]), p23 = pack2_hw(p[0][2], p[0][3]);
+        const short4v pb = {(short)(p01 & 0xffffu), (short)(p01 >> 16), (short)(p23 & 0xffffu), (short)(p23 >> 16)};
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          // lane (g, hq) of the A operand: V[4g + e][16nt + hq]; the transposing read takes row 4g + hq/4,
+          // columns 16nt + 4(hq%4) .. +3 in each 16-lane group
+          const uint16_t* vp = vs + (4 * g + (hq >> 2)) * kChunkVS + 16 * nt + 4 * (hq & 3);
+          const short4v va =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
+          oacc[nt] = mfma16x16x16(va, pb, oacc[nt]);
+        }
+      } else {
+        // 32 keys on 16x16x32: k slot 8g + e holds key 4g + e of block 0 (e < 4) and of block 1 (e >= 4), for P^T
+        // (the lane's own scores) and for V^T (two transposing reads, rows of block 0 then of block 1)
+        const u32x4 pb = {pack2_hw(p[0][0], p[0][1]), pack2_hw(p[0][2], p[0][3]), pack2_hw(p[1][0], p[1][1]),
+                          pack2_hw(p[1][2], p[1][3])};
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          const uint16_t* vp = vs + (4 * g + (hq >> 2)) * kChunkVS + 16 * nt + 4 * (hq & 3);
+          const short4v lo =
+              __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)vp);
+          const short4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) short4v*)(vp + 16 * kChunkVS));
+          oacc[nt] = mfma16x16x32(join_tr(lo, hi), pb, oacc[nt]);
+        }
       }
     };
     // kChunkDepth register sets in rotation: set d holds tiles d, d + kChunkDepth, ... and is reloaded as soon as
