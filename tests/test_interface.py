@@ -156,6 +156,12 @@ def test_cpu_tensors_are_rejected(ops):
     with pytest.raises(RuntimeError, match='GPU only'):
         ops.history_attention(q, cache, torch.zeros(1, 1, dtype=torch.int32), torch.zeros(1, dtype=torch.int32),
                               1.0, 1, None, None, None, 'hip')
+    with pytest.raises(RuntimeError, match='GPU only'):
+        ops.history_partials_grouped(q, cache[..., :512], cache[..., 512:], torch.zeros(1, 1, dtype=torch.int32),
+                                     torch.zeros(1, dtype=torch.int32), 1.0, 2, None)
+    with pytest.raises(RuntimeError, match='GPU only'):
+        ops.split_epilogue(torch.zeros(1, 16, 2, 513), torch.zeros(16, 512, 128, dtype=torch.bfloat16),
+                           torch.zeros(1, 16, 128, dtype=torch.bfloat16), torch.zeros(16, 1), None)
 
 
 def test_select_backends_needs_a_gpu(ops):
