@@ -5,9 +5,12 @@ One step = the attention path of one full S6 decode step: 24 layers x 4 loops, e
 (A_t GEMM + latent RoPE), the exact window over the last 32 tokens plus the current one, the paged latent history
 (loop 0 reads the 256-wide loop-1 latent, loops 1-3 the 512-wide main latent), the B_t projection and the LSE merge.
 Inputs are synthetic and random-init, resident in HBM before timing; the whole step is captured once in a HIP graph
-and replayed. Prints one JSON line (the value is microseconds per layer = step time / 24; lower is better); its
-"configs" key holds the same measurement of the other configurations (B=32 ragged contexts, B=8 at context 32768,
-and chunked prefill of 4 requests x 3 and x 512 tokens on 8192 latent rows), each with its roofline fraction.
+and replayed. The step is driven as the reference adapter drives it (one split count for the step from the
+reference formula and the workspace it allocates; the layer code picks each latent width's count). Prints one JSON
+line (the value is microseconds per layer = step time / 24; lower is better); its "configs" key holds the same
+measurement of the other configurations (B=1 at context 1024 for one main loop; B=32 ragged contexts over 65,536-page
+pools; B=8 at context 32768; chunked prefill of 4 requests x 3 and x 512 tokens on 8192 latent rows), each with its
+roofline fraction and a CPU baseline (a torch-on-CPU restatement of the same layer path on the host's cores).
 """
 from __future__ import annotations
 
@@ -39,23 +42,27 @@ def parse():
     p.add_argument('--gpus', type=int, default=1)
     p.add_argument('--steps', type=int, default=20)
     p.add_argument('--warmup', type=int, default=3)
-    p.add_argument('--workload', choices=('decode', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop', 'rows',
-                                          'mixed'),
+    p.add_argument('--workload', choices=('decode', 'single', 'ragged', 'long', 'prefill', 'writer', 'export', 'khop',
+                                          'rows', 'mixed'),
                    default='decode',
-                   help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); ragged: B=32 '
-                        'decode rows with contexts drawn from U[1024, 8192]; long: B=8 decode rows at context 32768, '
-                        'one layer x 4 loops; prefill: B=4 requests of --queries new tokens each on a context-8192 '
-                        'history, one layer x 4 loops; writer: the row writer and commit; export: the rollout-cache '
-                        'gather; khop: multi-query history with backward (B=4, L=2880); rows: single-query history '
-                        'over contiguous rows with a key mask (B=8, 8192 rows); mixed: the HF rolling engine\'s joint '
-                        'attention of a chunk over its history blocks with backward (B=8, 256-token chunk, blocks of '
-                        '2048 and 256 rows). Only decode prints the headline line.')
-    p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 32 / 8 / 4 by workload)')
+                   help='decode: the headline decode step (B=64, context 8192, 24 layers x 4 loops); single: B=1 '
+                        'at context 1024, one layer x one main loop; ragged: B=32 decode rows with contexts drawn '
+                        'from U[1024, 8192] over 65,536-page pools; long: B=8 decode rows at context 32768; prefill: '
+                        'B=4 requests of --queries new tokens each on a context-8192 history (ragged, long and '
+                        'prefill: 4 loops over 4 / 4 / 8 layers with distinct caches, reported per layer); writer: '
+                        'the row writer and commit; export: the rollout-cache gather; khop: multi-query history with '
+                        'backward (B=4, L=2880); rows: single-query history over contiguous rows with a key mask '
+                        '(B=8, 8192 rows); mixed: the HF rolling engine\'s joint attention of a chunk over its '
+                        'history blocks with backward (B=8, 256-token chunk, blocks of 2048 and 256 rows). Only '
+                        'decode prints the headline line.')
+    p.add_argument('--batch', type=int, default=0, help='rows (default: 64 / 1 / 32 / 8 / 4 by workload)')
     p.add_argument('--context', type=int, default=0, help='history tokens before the step (default by workload)')
     p.add_argument('--queries', type=int, default=512, help='new tokens per request of --workload prefill')
     p.add_argument('--writer-queries', type=int, default=1, help='new tokens per request of --workload writer')
-    p.add_argument('--layers', type=int, default=0, help='layers (default: 24 for decode/ragged, 1 otherwise)')
-    p.add_argument('--splits', type=int, default=0, help='KV splits of every latent width (0: the MI355X policy)')
+    p.add_argument('--layers', type=int, default=0, help='layers (default by workload: 24 / 1 / 4 / 4 / 8)')
+    p.add_argument('--splits', type=int, default=0,
+                   help='KV splits of every latent width (0: the reference count, which StepContext turns into the '
+                        'MI355X count per width)')
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
     p.add_argument('--width', type=int, default=512, choices=(256, 512, 1024),
                    help='latent width of --kernel-only (256 / 512) and --workload khop / rows (1024: forward only)')
@@ -64,24 +71,39 @@ def parse():
                         'of a PMC profile to bytes)')
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-secondary', action='store_true',
-                   help='decode: skip the other configurations (ragged, long context, multi-query Q=3 and Q=512) '
-                        'that the default run appends to the headline line under "configs"')
+                   help='decode: skip the other configurations (single decode, ragged, long context, multi-query Q=3 '
+                        'and Q=512) that the default run appends to the headline line under "configs"')
     p.add_argument('--seed', type=int, default=0)
     p.add_argument('--table', choices=('random', 'identity'), default='random',
                    help='latent block tables: a random permutation of the page pool, or pages in order')
     return p.parse_args()
 
 
+# The adapter's step constants (hla/vllm_latent/ouro_latent.py:205-212): the largest CUDA-graph batch (vLLM's
+# default capture size) bounds the split steps, and the workspace covers the scheduler's token budget
+SPLIT_MAX_TOKENS, MAX_BATCHED_TOKENS = 512, 8192
+
+
 class Workload:
     """Random-init caches, tables and readers of the model's attention path for one step: request r has ``hist[r]``
     history tokens and ``queries`` new tokens (1: a decode step; more: a chunked-prefill step whose tokens are
-    already written to the exact cache), ``layers`` layers x 4 loops."""
+    already written to the exact cache), ``layers`` layers (each with its own caches) x the loops in ``loops``, run
+    loop-major as the model runs them (every layer's loop 0, then every layer's loop 1, ...).
 
-    def __init__(self, ops, layer, hist, queries, splits, seed, device, table='random', layers=LAYERS):
+    The latent page pool of each width holds ``lat_pool`` pages (at least the pages the step uses plus the null
+    page); each width's table is a slice of one random permutation of its pool. The step is driven as the
+    reference adapter drives it (``hla/vllm_latent/ouro_latent.py:203-212,257-265``): one ``num_kv_splits`` count
+    for the step from the reference formula, the workspace the adapter allocates, ``max_seqlen_k`` = the model
+    length (here the step's longest sequence); ``StepContext`` picks each width's count itself. ``splits_override``
+    instead fixes every width's count (``kv_splits_by_width``)."""
+
+    def __init__(self, ops, layer, hist, queries, seed, device, cus, table='random', layers=LAYERS, lat_pool=0,
+                 splits_override=0, loops=tuple(range(LOOPS))):
         g = torch.Generator(device=device).manual_seed(seed)
         hist = [int(h) for h in hist]
         B, Q = len(hist), int(queries)
         self.B, self.Q, self.T, self.hist, self.layers, self.device = B, Q, B * Q, hist, layers, device
+        self.loops = tuple(loops)
         self.seq = [h + Q for h in hist]                          # the step's tokens are already in the exact cache
         self.n_latent = [max(h - WINDOW, 0) for h in hist]
         cols = [-(-s // BLOCK) for s in self.seq]
@@ -90,7 +112,7 @@ class Workload:
                                          ).to(torch.bfloat16)
         perm = lambda n: (torch.randperm(n - 1, generator=g, device=device) + 1).to(torch.int32)
         lat_pages = perm if table == 'random' else (lambda n: torch.arange(1, n, dtype=torch.int32, device=device))
-        pool = sum(cols) + 1                                      # page 0: the null page
+        self.pool = max(int(lat_pool), sum(cols) + 1)             # page 0: the null page
 
         def paged_table(first, last, pages):
             t = torch.zeros(B, self.cols, dtype=torch.int32, device=device)
@@ -101,9 +123,9 @@ class Workload:
                 used += n
             return t
 
-        self.lat_table = {w: paged_table([0] * B, [c - 1 for c in cols], lat_pages(pool)) for w in (RANK, RANK1)}
-        self.lat = [{w: torch.empty(pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(generator=g)
-                     for w in (RANK, RANK1)} for _ in range(layers)]
+        self.lat_table = {w: paged_table([0] * B, [c - 1 for c in cols], lat_pages(self.pool)) for w in (RANK, RANK1)}
+        self.lat = [{w: torch.empty(self.pool, 1, BLOCK, 2 * w, dtype=torch.bfloat16, device=device).normal_(
+                     generator=g) for w in (RANK, RANK1)} for _ in range(layers)]
         # exact caches: the window rows and the step's tokens per request and loop; freed pages are the null page
         first = [max(0, h - WINDOW) // BLOCK for h in hist]
         last = [(s - 1) // BLOCK for s in self.seq]
@@ -124,17 +146,32 @@ class Workload:
         self.positions = torch.tensor([h + i for h in hist for i in range(Q)], dtype=torch.int64, device=device)
         self.qsl = (torch.arange(B + 1, dtype=torch.int32, device=device) * Q).contiguous()
         self.seq_lens = torch.tensor(self.seq, dtype=torch.int32, device=device)
-        self.splits = splits                                      # {latent width: KV splits}
-        self.workspace = ops.S6Workspace.for_splits(HEADS, T, splits)
         self.ops, self.layer = ops, layer
+        self.max_model_len = max(self.seq)
+        if splits_override:
+            self.by_width = {RANK: int(splits_override), RANK1: int(splits_override)}
+            self.ref_splits = int(splits_override)
+            self.workspace = ops.S6Workspace.for_splits(HEADS, T, self.by_width)
+        else:
+            self.by_width = None
+            ref = lambda t: ops.num_kv_splits(self.max_model_len, t, SPLIT_MAX_TOKENS, cus)
+            self.ref_splits = ref(T)
+            rows = max(MAX_BATCHED_TOKENS, max(t * ref(t) for t in range(1, SPLIT_MAX_TOKENS + 1)))
+            self.workspace = ops.S6Workspace(HEADS, RANK, rows)
+        ctx = self.context()
+        self.splits = {w: ctx.kv_splits(w) for w in (RANK, RANK1)}   # {latent width: KV splits} the step runs
+
+    def context(self):
+        """The step's StepContext, built with the adapter's arguments (``ouro_latent.py:263-265``)."""
+        return self.layer.StepContext(self.positions, self.qsl, self.seq_lens, self.Q, self.T, self.tables,
+                                      HEAD_DIM ** -0.5, self.ops.HIP_BACKENDS, self.workspace, self.ref_splits,
+                                      window=WINDOW, max_seqlen_k=self.max_model_len,
+                                      kv_splits_by_width=self.by_width)
 
     def step(self):
-        ops, layer = self.ops, self.layer
-        ctx = layer.StepContext(self.positions, self.qsl, self.seq_lens, self.Q, self.T, self.tables,
-                                HEAD_DIM ** -0.5, ops.HIP_BACKENDS, self.workspace, self.splits[RANK], window=WINDOW,
-                                max_seqlen_k=max(self.seq), kv_splits_by_width=self.splits)
+        ctx, layer = self.context(), self.layer
         outs = []
-        for loop in range(LOOPS):
+        for loop in self.loops:
             w = RANK1 if loop == 0 else RANK
             for i in range(self.layers):
                 sl = self.readers[i]
@@ -144,17 +181,29 @@ class Workload:
                                          (self.exact[i][loop], self.ex_table[loop])))
         return outs
 
+    def setup(self):
+        """The step's per-step launches alone: metadata and the split plan of each width that the fused path
+        reads (shared by every layer of the step)."""
+        ctx = self.context()
+        if self.Q < self.layer.FUSED_CHUNK_TOKENS:
+            for w in (RANK, RANK1):
+                if any((RANK1 if l == 0 else RANK) == w for l in self.loops) and ctx.kv_splits(w) > 1:
+                    ctx.split_plan(ctx.kv_splits(w), self.lat_table[w].shape[1] * BLOCK)
+
+    def widths(self):
+        return [RANK1 if loop == 0 else RANK for loop in self.loops]
+
     def history_bytes_per_layer(self):
-        """Latent rows read once per request: (256 + 256) + 3 x (512 + 512) bf16 columns per row."""
-        return sum(self.n_latent) * (2 * RANK1 + 3 * 2 * RANK) * 2
+        """Latent rows read once per request and loop: 2 x (256 or 512) bf16 columns per row."""
+        return sum(self.n_latent) * sum(2 * w * 2 for w in self.widths())
 
     def history_flops_per_layer(self):
         """4 flops per (query row, latent row, latent column): scores and weighted values."""
-        return sum(4 * self.Q * HEADS * n * (RANK1 + 3 * RANK) for n in self.n_latent)
+        return sum(4 * self.Q * HEADS * n * sum(self.widths()) for n in self.n_latent)
 
     def window_bytes_per_layer(self):
         keys = sum(min(s, WINDOW + self.Q) for s in self.seq)
-        return LOOPS * keys * HEADS * 2 * HEAD_DIM * 2
+        return len(self.loops) * keys * HEADS * 2 * HEAD_DIM * 2
 
 
 class _Reader:
@@ -238,140 +287,163 @@ def history_roofline(wl, iters=50, width=RANK):
     return us, us_reduce, nbytes
 
 
-def cpu_baseline(wl, sample=8):
-    """The numpy oracle of one loop-1 call and one main-latent call of layer 0 on a sample of the step's query rows
-    (``sample`` decode rows, or the first ``sample`` query tokens of request 0 in a multi-query step), timed on the
-    host cores (median of 3 after a warm-up) and scaled to the whole step per layer (1 + 3 loops) by latent history
-    rows read, which dominate the oracle's time."""
-    from oracle import s6_oracle as O
+def cpu_baseline(wl, timed_loops, per_request=0):
+    """The torch-on-CPU restatement of the layer's attention path (``oracle/torch_cpu.py``: A_t + latent RoPE, paged
+    latent history, B_t, the exact window or chunk, LSE merge; float32 GEMMs from bf16 inputs on all of the host's
+    cores) over layer 0's caches, one call per loop in ``timed_loops`` (median of 3 after a warm-up). Decode steps
+    run every row; multi-query steps every request, on its first ``per_request`` tokens when that is set (scaled to
+    all of its tokens). Loops not timed are the main-latent loop 1's time again (loops 1-3 read the same
+    caches and shapes). Returns the baseline dict (microseconds per layer, or per call for a one-loop step)."""
+    from oracle import torch_cpu as TC
     cores = len(os.sched_getaffinity(0))
-    f32 = lambda t: t.float().cpu().numpy()
-    if wl.Q == 1:
-        rows = list(range(min(sample, wl.B)))
-        tokens = rows
-        qsl = np.arange(len(rows) + 1)
-    else:
-        rows = [0]
-        tokens = list(range(min(sample, wl.Q)))
-        qsl = np.array([0, len(tokens)])
-    n_rows = [wl.n_latent[r] for r in rows]
+    torch.set_num_threads(cores)
+    cpu = lambda t: t.cpu()
+    multi = wl.Q > 1
+    take = per_request if (multi and per_request) else wl.Q
+    tokens = torch.tensor([r * wl.Q + i for r in range(wl.B) for i in range(take)], device=wl.device)
+    T = tokens.numel()
     timings = {}
-    for w in (RANK, RANK1):
-        loop = 0 if w == RANK1 else 1
-        lat, table = wl.lat[0][w], wl.lat_table[w]
-        cols = max(1, -(-max(n_rows) // BLOCK))
-        pages = table[rows, :cols].long()                                   # [rows, cols]; 0 past a row's pages
-        lat_h = f32(lat[pages.reshape(-1)]).reshape(len(rows) * cols, 1, BLOCK, 2 * w)
-        lat_table = np.arange(len(rows) * cols, dtype=np.int32).reshape(len(rows), cols)
-        ex_h = f32(wl.exact[0][loop])
-        ex_table = wl.ex_table[loop][rows].cpu().numpy()
-        _, Bw, _ = wl.readers[0].readers(loop)
-        Bw = f32(Bw)
-        q = f32((torch.randn(len(tokens), HEADS, w, device=wl.device) * w ** -0.5).to(torch.bfloat16))
-        q_rope = f32(wl.q_rope[loop][tokens])
-        invalid = np.zeros(len(tokens), bool)
-        if wl.Q == 1:
-            seq = np.array([wl.seq[r] for r in rows])
+    for loop in timed_loops:
+        w = RANK1 if loop == 0 else RANK
+        A, Bw, _ = wl.readers[0].readers(loop)
+        cols = max(1, -(-max(wl.n_latent) // BLOCK))
+        pages = wl.lat_table[w][:, :cols].long()                       # the pages the requests read, compacted
+        lat_h = cpu(wl.lat[0][w][pages.reshape(-1)]).view(wl.B * cols, 1, BLOCK, 2 * w)
+        lat_tab = torch.arange(wl.B * cols, dtype=torch.int32).view(wl.B, cols)
+        ex_h, ex_tab = cpu(wl.exact[0][loop]), cpu(wl.ex_table[loop])
+        q_pre, rows = cpu(wl.q_pre[loop][tokens]), cpu(wl.tables[w][wl.positions[tokens]])
+        q_rope = cpu(wl.q_rope[loop][tokens])
+        A, Bw = cpu(A), cpu(Bw)
+        invalid = torch.zeros(T, dtype=torch.bool)
+        n_lat = torch.tensor(wl.n_latent, dtype=torch.int32)
+        if multi:
+            k_rope, v = cpu(wl.k_rope[loop][tokens]), cpu(wl.v[loop][tokens])
+            qsl = [r * take for r in range(wl.B + 1)]
 
             def run():
-                return O.attend_decode(q, q_rope, Bw, lat_h[..., :w], lat_h[..., w:], lat_table, np.array(n_rows),
-                                       ex_h[..., :HEAD_DIM], ex_h[..., HEAD_DIM:], ex_table, qsl, seq, WINDOW,
-                                       HEAD_DIM ** -0.5, invalid)
+                q_lat = TC.latent_query(q_pre, A, rows)
+                return TC.attend_chunk(q_lat, q_rope, k_rope, v, Bw, lat_h, lat_tab, qsl, wl.hist, n_lat, ex_h,
+                                       ex_tab, WINDOW, HEAD_DIM ** -0.5, invalid)
         else:
-            k_rope, v = f32(wl.k_rope[loop][tokens]), f32(wl.v[loop][tokens])
-            n_tok = len(tokens)
-            tabs = {'latent': np.repeat(lat_table, n_tok, 0), 'exact': np.repeat(ex_table, n_tok, 0)}
-            ctx = np.full(n_tok, wl.hist[0])
-            ctx_lat = np.full(n_tok, n_rows[0])
+            req = torch.arange(wl.B)
+            seq = torch.tensor(wl.seq, dtype=torch.int32)
 
             def run():
-                return O.attend_chunk(q, q_rope, k_rope, v, Bw, lat_h[..., :w], lat_h[..., w:], tabs, ctx, ctx_lat,
-                                      qsl, WINDOW, HEAD_DIM ** -0.5, invalid, ex_h[..., :HEAD_DIM],
-                                      ex_h[..., HEAD_DIM:])
+                q_lat = TC.latent_query(q_pre, A, rows)
+                return TC.attend_decode(q_lat, q_rope, Bw, lat_h, lat_tab, n_lat, ex_h, ex_tab, req, seq, WINDOW,
+                                        HEAD_DIM ** -0.5, invalid)
         run()
         reps = []
         for _ in range(3):
             t0 = time.perf_counter()
             run()
             reps.append(time.perf_counter() - t0)
-        timings[w] = float(np.median(reps))
-    sampled = sum(n_rows) * len(tokens) / len(rows)                    # (query row, latent row) pairs sampled
-    total = sum(n * wl.Q for n in wl.n_latent)
-    scale = total / max(sampled, 1)
-    per_layer_s = (timings[RANK1] + 3 * timings[RANK]) * scale
-    what = (f'{len(rows)} of the {wl.B} decode rows' if wl.Q == 1 else
-            f'the first {len(tokens)} query tokens of request 0 ({wl.B} requests x {wl.Q} tokens)')
-    return {'value': per_layer_s * 1e6, 'unit': 'us/layer', 'cores': cores, 'kind': 'port',
-            'sample': f'numpy oracle of s6_layer.attend (fp32 from bf16 inputs) on {what}: one loop-1 call and one '
-                      f'main-latent call of layer 0 (median of 3 after 1 warm-up), scaled x{scale:.1f} by latent '
-                      f'history rows read and x(1 + 3) loops; extrapolated'}
+        timings[loop] = float(np.median(reps))
+    per_loop = [timings.get(loop, timings.get(1)) for loop in wl.loops]
+    scale = wl.Q / take
+    value = sum(per_loop) * scale * 1e6
+    whole = set(timed_loops) == set(wl.loops) and scale == 1
+    what = (f'all {wl.B} decode rows' if not multi else
+            f'all {wl.B} requests x {take} of their {wl.Q} tokens' if take < wl.Q else f'all {wl.T} tokens')
+    note = ('the whole call' if whole else
+            f'loops {list(timed_loops)} timed, the untimed main loops counted at loop 1\'s time'
+            + (f', x{scale:.0f} tokens' if scale > 1 else '') + '; extrapolated')
+    return {'value': round(value, 1), 'unit': 'us/call' if len(wl.loops) == 1 else 'us/layer', 'cores': cores,
+            'kind': 'port',
+            'sample': f'torch-on-CPU restatement of the layer path (A_t + latent RoPE, paged history, B_t, exact '
+                      f'window or chunk, LSE merge; float32 GEMMs from bf16, {cores} threads) on {what} of layer 0, '
+                      f'median of 3 after a warm-up: {note}'}
 
 
-def secondary_metrics(kind, wl, B, context, layers, queries, splits, steps, warmup):
-    """Step time and roofline fractions of a ragged / long-context / multi-query workload (HIP-graph replay)."""
+def secondary_metrics(name, kind, wl, B, context, queries, steps, warmup):
+    """Step time and roofline fractions of a configuration other than the headline (HIP-graph replay). ``value`` is
+    the step time per layer (per call when the step is one loop); the step's setup launches, shared by its layers
+    as in the model, are timed alone beside it."""
     ms = time_graph(wl.step, steps, warmup)
-    us_layer = ms * 1000 / layers
+    setup_ms = time_graph(wl.setup, steps, warmup)
+    per = 'call' if len(wl.loops) == 1 else 'layer'
+    us_layer = ms * 1000 / wl.layers
     hist_bytes, flops = wl.history_bytes_per_layer(), wl.history_flops_per_layer()
     gbps, tflops = hist_bytes / (us_layer * 1e3), flops / (us_layer * 1e6)
-    return {'workload': kind, 'value': round(us_layer, 2), 'unit': 'us/layer', 'B': B, 'queries': queries,
-            'context': context, 'contexts': wl.hist if kind == 'ragged' else None, 'layers': layers,
-            'loops': LOOPS, 'kv_splits': splits, 'steps': steps, 'ms_per_step': round(ms, 4),
+    return {'workload': name, 'value': round(us_layer, 2), 'unit': f'us/{per}', 'B': B, 'queries': queries,
+            'context': context, 'contexts': wl.hist if kind == 'ragged' else None, 'layers': wl.layers,
+            'loops': len(wl.loops), 'latent_pool_pages': wl.pool, 'kv_splits': wl.splits,
+            'reference_kv_splits': wl.ref_splits, 'steps': steps, 'ms_per_step': round(ms, 4),
+            'setup_us_per_step': round(setup_ms * 1000, 2),
             'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
             'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
             'history_tflops': round(tflops, 1), 'mfma_frac': round(tflops / PEAK_BF16_TFLOPS, 4),
-            'bound': 'mfma' if kind == 'prefill' and queries >= 64 else 'hbm',
+            'bound': 'mfma' if kind == 'prefill' and queries >= 64 else 'hbm' if kind != 'single' else 'latency',
             'data': 'synthetic (random-init caches, readers and queries)', 'hip_graph': True}
 
 
-def secondary(args, wl, B, context, layers, queries, splits):
-    """One JSON line for the ragged / long-context / multi-query workloads (not the headline metric)."""
-    out = secondary_metrics(args.workload, wl, B, context, layers, queries, splits, args.steps, args.warmup)
-    out['cpu_baseline'] = None if args.no_cpu_baseline else cpu_baseline(wl)
-    print(json.dumps(out), flush=True)
+# The benchmark configurations besides the headline (name: workload, B, context, queries, layers, latent pool pages,
+# loops, CPU-baseline loops, CPU-baseline tokens per request). Layers are distinct caches run loop-major, so
+# that a loop's history reads (over all the step's layers) exceed the 256 MB MALL as in the 24-layer model and no
+# loop re-reads the previous loop's rows from it; the ragged step reads its rows from 65,536-page pools per width.
+SECONDARY = (
+    ('single_b1_ctx1024', 'single', 1, 1024, 1, 1, 0, (1,), (1,), 0),
+    ('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, 1, 4, 65536, (0, 1, 2, 3), (0, 1, 2, 3), 0),
+    ('long_b8_ctx32768', 'long', 8, 32768, 1, 4, 0, (0, 1, 2, 3), (0, 1, 2, 3), 0),
+    ('prefill_b4_q3_ctx8192', 'prefill', 4, 8192, 3, 8, 0, (0, 1, 2, 3), (0, 1, 2, 3), 0),
+    ('prefill_b4_q512_ctx8192', 'prefill', 4, 8192, 512, 8, 0, (0, 1, 2, 3), (0, 1), 16),
+)
 
 
-# The other benchmark configurations measured by the default run (name: workload, B, context, layers, queries)
-SECONDARY = (('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, 1, 1),
-             ('long_b8_ctx32768', 'long', 8, 32768, 1, 1),
-             ('prefill_b4_q3_ctx8192', 'prefill', 4, 8192, 1, 3),
-             ('prefill_b4_q512_ctx8192', 'prefill', 4, 8192, 1, 512))
-
-
-def workload_shape(kind, B, context, queries, seed):
-    """History lengths of the requests of a workload and whether its steps take the multi-query kernels."""
+def workload_shape(kind, B, context, seed):
+    """History lengths of the requests of a workload."""
     if kind == 'ragged':
-        hist = np.random.default_rng(seed).integers(1024, context + 1, B).tolist()
-    elif kind == 'prefill':
-        hist = [context + WINDOW] * B                          # `context` latent rows + the exact window
-    else:
-        hist = [context] * B
-    return hist, (4 if queries >= 16 else 1)                   # the step's history_group (StepContext)
+        return np.random.default_rng(seed).integers(1024, context + 1, B).tolist()
+    if kind == 'prefill':
+        return [context + WINDOW] * B                          # `context` latent rows + the exact window
+    return [context] * B
 
 
 def build_workload(ops, layer, kind, B, context, layers, queries, seed, device, cus, splits_override=0,
-                   table='random'):
-    hist, group = workload_shape(kind, B, context, queries, seed)
-    splits = {w: splits_override or ops.mi355x_kv_splits(max(hist) + queries, B * queries, cus, width=w,
-                                                         tokens_per_group=group)
-              for w in (RANK, RANK1)}
+                   table='random', lat_pool=0, loops=tuple(range(LOOPS))):
+    hist = workload_shape(kind, B, context, seed)
     print(f'bench: building workload {kind} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
-          f'splits={splits} cus={cus}', file=sys.stderr, flush=True)
-    wl = Workload(ops, layer, hist, queries, splits, seed, device, table, layers)
+          f'pool={lat_pool} loops={loops} cus={cus}', file=sys.stderr, flush=True)
+    wl = Workload(ops, layer, hist, queries, seed, device, cus, 'identity' if kind == 'single' else table, layers,
+                  lat_pool, splits_override, loops)
     torch.cuda.synchronize()
-    return wl, splits
+    return wl
 
 
-def measure_secondaries(ops, layer, args, device, cus):
-    """The ragged, long-context and both multi-query configurations, one after another (each workload freed before
-    the next is built): a dict of their metrics for the headline line."""
+def measure_secondaries(ops, layer, args, device, cus, with_cpu):
+    """Every configuration of SECONDARY, one after another (each workload freed before the next is built): a dict
+    of their metrics (with their CPU baselines) for the headline line."""
     out = {}
-    for name, kind, B, context, layers, queries in SECONDARY:
-        wl, splits = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus)
-        out[name] = secondary_metrics(kind, wl, B, context, layers, queries, splits, args.steps, args.warmup)
+    for name, kind, B, context, queries, layers, pool, loops, cpu_loops, cpu_tokens in SECONDARY:
+        wl = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus, lat_pool=pool,
+                            loops=loops)
+        out[name] = secondary_metrics(name, kind, wl, B, context, queries, args.steps, args.warmup)
+        if with_cpu:
+            print(f'bench: cpu baseline of {name}', file=sys.stderr, flush=True)
+            out[name]['cpu_baseline'] = cpu_baseline(wl, cpu_loops, cpu_tokens)
         del wl
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
     return out
+
+
+def single_config(args, ops, layer, device, cus):
+    """One JSON line for one configuration of SECONDARY (``--workload single|ragged|long|prefill``; prefill picks
+    the entry of ``--queries`` tokens when there is one, else the 512-token entry's shape); ``--batch``,
+    ``--context``, ``--layers`` and ``--splits`` override its shape."""
+    entries = [e for e in SECONDARY if e[1] == args.workload]
+    if args.workload == 'prefill':
+        entries = [e for e in entries if e[4] == args.queries] or [e for e in entries if e[4] == 512]
+    name, kind, B, context, queries, layers, pool, loops, cpu_loops, cpu_tokens = entries[0]
+    if kind == 'prefill':
+        queries = args.queries
+        cpu_tokens = min(cpu_tokens, queries) if cpu_tokens else 0
+    B, context, layers = args.batch or B, args.context or context, args.layers or layers
+    wl = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus, args.splits,
+                        args.table, pool, loops)
+    out = secondary_metrics(name, kind, wl, B, context, queries, args.steps, args.warmup)
+    out['cpu_baseline'] = None if args.no_cpu_baseline else cpu_baseline(wl, cpu_loops, cpu_tokens)
+    print(json.dumps(out), flush=True)
 
 
 HIDDEN = 2048
@@ -662,10 +734,12 @@ class EngineLatent:
         return self.A[loop], self.B[loop], RANK1 if loop == 0 else RANK
 
     def query(self, loop, q, cos, sin):
+        """``apply_rope(einsum('bhid,hdr->bhir', q, A), c, s)`` in the dtype of q and A (bf16), as
+        ``register.LatentLayer.query`` computes it (``hla/latent/register.py:68-71``)."""
         A, _, rank = self.readers(loop)
         idx = torch.arange(rank // 2, device=cos.device) % (cos.shape[-1] // 2)
         c, s = torch.cat((cos[..., idx], cos[..., idx]), -1), torch.cat((sin[..., idx], sin[..., idx]), -1)
-        return self.be.apply_rope(torch.matmul(q.float(), A.float()[None]).to(q.dtype), c, s)
+        return self.be.apply_rope(torch.matmul(q.contiguous(), A.contiguous()[None]), c, s)
 
     def fields(self, loop, packed):
         if loop == 0:
@@ -789,15 +863,11 @@ def main():
     if args.workload == 'mixed':
         return mixed_workload(args, pkg, device)
     cus = pkg._lib.device_cus(0)
-    defaults = {'decode': (64, 8192, LAYERS), 'ragged': (32, 8192, 1), 'long': (8, 32768, 1),
-                'prefill': (4, 8192, 1)}[args.workload]
-    B, context, layers = args.batch or defaults[0], args.context or defaults[1], args.layers or defaults[2]
-    queries = args.queries if args.workload == 'prefill' else 1
-    wl, splits = build_workload(ops, layer, args.workload, B, context, layers, queries, args.seed, device, cus,
-                                args.splits, args.table)
     if args.workload != 'decode' and not args.kernel_only:
-        return secondary(args, wl, B, context, layers, queries, splits)
-
+        return single_config(args, ops, layer, device, cus)
+    B, context, layers = args.batch or 64, args.context or 8192, args.layers or LAYERS
+    wl = build_workload(ops, layer, 'decode', B, context, layers, 1, args.seed, device, cus, args.splits, args.table)
+    splits = wl.splits
     if args.kernel_only:
         us, us_reduce, nbytes = history_roofline(wl, iters=max(args.steps, 1), width=args.width)
         print(json.dumps({'kernel': f'history_split width {args.width}', 'splits': splits[args.width],
@@ -815,14 +885,15 @@ def main():
     base = None
     if not args.no_cpu_baseline:
         print('bench: cpu baseline', file=sys.stderr, flush=True)
-        base = cpu_baseline(wl)
+        base = cpu_baseline(wl, (0, 1))
+    ref_splits = wl.ref_splits
     others = None
     if not args.no_secondary:
         del wl
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
         print('bench: the other configurations', file=sys.stderr, flush=True)
-        others = measure_secondaries(ops, layer, args, device, cus)
+        others = measure_secondaries(ops, layer, args, device, cus, not args.no_cpu_baseline)
     result = {
         'metric': METRIC, 'value': round(us_layer, 3), 'unit': 'us/layer', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': False, 'scaling': 'weak',
@@ -830,7 +901,9 @@ def main():
         'config': {'workload': f'Ouro-1.4B S6 decode attention path, {layers} layers x {LOOPS} loops, '
                                f'B={B}, context {context}, W={WINDOW}, block {BLOCK}',
                    'global_batch': B, 'seq_len': context, 'parallelism': 'none (1 GPU)',
-                   'kv_splits': splits, 'hip_graph': True},
+                   'kv_splits': splits, 'reference_kv_splits': ref_splits,
+                   'driven_as': 'the reference adapter drives it: one num_kv_splits count and its workspace; '
+                                'StepContext picks the per-width counts', 'hip_graph': True},
         'tokens_per_s': round(B / (ms / 1000), 1),
         'hbm_gbps': round(layer_gbps, 1), 'hbm_frac': round(layer_gbps / PEAK_HBM_GBPS, 4),
         'bytes_per_layer': {'latent_history': hist_bytes, 'exact_window': win_bytes},

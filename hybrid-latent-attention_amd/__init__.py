@@ -4,7 +4,8 @@
 ``hla/vllm_latent/s6_layer.py``; every op runs hand-written HIP kernels from ``libhla_s6.so`` through the C ABI of
 ``include/hla_s6.h``. The directory name is not a Python identifier: import it with
 ``importlib.import_module('hybrid-latent-attention_amd')`` with the repository root on ``sys.path``.
-``rollout_cache`` writes and reads the ``s6-rollout-cache-v1`` snapshot of a finished request; ``history_gemm`` is
+``rollout_cache`` gathers a finished request's committed rows and writes its ``s6-rollout-cache-v1`` snapshot (the
+reference's own loader reads it back); ``history_gemm`` is
 the differentiable history attention over contiguous rows (multi-query for K-hop replay, single-query for the HF
 engine); ``batched_engine`` is the HF rolling engine's joint attention over history rows and the current chunk.
 """

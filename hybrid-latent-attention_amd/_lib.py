@@ -127,7 +127,13 @@ def stream(device=None) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_CUS: dict = {}
+
+
 def device_cus(device: int = 0) -> int:
-    out = ctypes.c_int(0)
-    check(load().hla_s6_device_cus(device, ctypes.byref(out)))
-    return out.value
+    """Compute units of HIP device ``device`` (queried once per device)."""
+    if device not in _CUS:
+        out = ctypes.c_int(0)
+        check(load().hla_s6_device_cus(device, ctypes.byref(out)))
+        _CUS[device] = out.value
+    return _CUS[device]

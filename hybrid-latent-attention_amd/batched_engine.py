@@ -10,7 +10,9 @@ with the block's ``[B, N]`` mask shared by the chunk's queries; then ``out = w_c
 with ``w = exp(lse - logsumexp(all lse))`` in one HIP launch (``hla_s6_mixed_merge_forward``; its backward
 ``hla_s6_mixed_merge_backward`` gives the gradients of every part). The reference rounds the joint probabilities to
 bf16 before its products; here the parts are normalized in fp32 inside the kernels and z is rounded once to bf16, so
-outputs agree within bf16 rounding.
+outputs agree within bf16 rounding. The kernels take bf16 operands: float32 q / k / v and latent queries are rounded
+to bf16 once on entry (the reference computes in the input dtype), which keeps every result within the same bf16
+rounding of the float32 reference.
 """
 from __future__ import annotations
 
@@ -235,6 +237,11 @@ def mixed_attention(sl, loop, q, k, v, cos, sin, valid, blocks, masks):
     if H != 16 or D != 128 or k.shape != q.shape or v.shape != q.shape or tuple(valid.shape) != (B, n):
         raise ValueError(f'the chunk kernels take q / k / v [B, 16, n, 128] and valid [B, n] (got {tuple(q.shape)}, '
                          f'{tuple(k.shape)}, {tuple(v.shape)}, {tuple(valid.shape)})')
+    blocks, masks = list(blocks or ()), list(masks or ())
+    if len(blocks) != len(masks):
+        raise ValueError(f'mixed_attention: {len(blocks)} history blocks but {len(masks)} masks')
+    if len(blocks) > MAX_BLOCKS:   # checked before any launch
+        raise ValueError(f'mixed_attention: {len(blocks)} history blocks (the merge kernel takes at most {MAX_BLOCKS})')
     with torch.autocast(q.device.type, enabled=False):         # qrot, krot = apply_rope(q / k, cos, sin), then the chunk
         o_c, lse_c = _RopedChunk.apply(q, k, v, valid, cos, sin, float(scale))
     if not blocks:
@@ -248,8 +255,6 @@ def mixed_attention(sl, loop, q, k, v, cos, sin, valid, blocks, masks):
     for block, mask in zip(blocks, masks):
         ck, cv = sl.fields(loop, block)
         parts.append(_history_block(qt, ck, cv, mask, scale))
-    if len(parts) > MAX_BLOCKS:
-        raise ValueError(f'mixed_attention: {len(parts)} history blocks (the merge kernel takes at most {MAX_BLOCKS})')
     _, B_read, _ = sl.readers(loop)
     with torch.autocast(q.device.type, enabled=False):
         out = _Merge.apply(o_c, lse_c, B_read, *[t for part in parts for t in part])

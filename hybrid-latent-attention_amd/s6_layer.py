@@ -72,8 +72,15 @@ class StepContext:
     no cache writes (``md_present`` False), workspace still allocated. ``tables`` maps a latent width to its
     persistent ``[max_position, w]`` RoPE table. Token -> request, ``ctx`` and ``ctx_latent`` come from one HIP
     launch; all shapes depend only on ``num_tokens`` and host ints; nothing here syncs with the host.
-    ``kv_splits_by_width`` optionally overrides ``num_kv_splits`` per latent width (the history kernel's occupancy
-    depends on the width); the workspace must hold the largest of them.
+
+    Split counts: the reference adapter passes one ``num_kv_splits`` for both latent widths
+    (``hla/vllm_latent/ouro_latent.py:257``). The history kernel's occupancy depends on the width (one wave per 128
+    columns), so when the step has metadata, ``max_seqlen_k`` and a workspace, each width takes the MI355X count
+    ``s6_ops.mi355x_kv_splits(max_seqlen_k, num_tokens, CUs, width, history_group)`` if the workspace holds its
+    partials, and ``num_kv_splits`` otherwise. Like the reference's count it depends on the row count and
+    constants only (``max_query_len`` picks the kernel family, as ``history_group`` always has), so a graph captured
+    for a batch size replays the counts it was captured with; a split count changes only the order of the fp32
+    sums. ``kv_splits_by_width`` overrides the counts per width (the workspace must hold the largest of them).
     """
 
     def __init__(self, positions, query_start_loc, seq_lens, max_query_len, num_tokens, tables, scale, backends,
@@ -115,6 +122,21 @@ class StepContext:
         self._slots = {}
         if workspace is not None:
             workspace.ensure(device)
+            if kv_splits_by_width is None and self.md_present and max_seqlen_k:
+                self.kv_splits_by_width = self._mi355x_splits(workspace, num_tokens, device)
+
+    def _mi355x_splits(self, workspace, num_tokens, device):
+        """``{width: splits}`` of the MI355X policy for every latent width with a RoPE table, where the workspace
+        holds ``num_tokens * heads * splits * (width + 1)`` partials (other widths keep ``num_kv_splits``)."""
+        cus = _lib.device_cus(device.index or 0)
+        heads = getattr(workspace, 'heads', None) or 16
+        out = {}
+        for width in self.tables:
+            s = s6_ops.mi355x_kv_splits(int(self.max_seqlen_k), int(num_tokens), cus, width=int(width),
+                                        tokens_per_group=self.history_group)
+            if s == 1 or num_tokens * heads * s * (int(width) + 1) <= workspace.floats:
+                out[int(width)] = s
+        return out
 
     @property
     def empty(self):

@@ -185,6 +185,7 @@ class S6Workspace:
     """
 
     def __init__(self, heads, width_max, rows_x_splits):
+        self.heads = heads
         self.floats = rows_x_splits * heads * (width_max + 1)
         self.buffer = None
 

@@ -155,3 +155,26 @@ def test_chunk_rope_kernels_match_torch_bitwise(trig):
     dx = torch.empty_like(q)
     be._rope_call('hla_s6_rope_rows_backward', [dy.float().contiguous()], [dx], c, s)
     assert want.dtype == torch.bfloat16 and torch.equal(dx, want)
+
+
+def test_mixed_attention_at_the_bench_shape():
+    """The benchmark's shape: 8 rows of a 256-token loop-2 chunk (row 0 left-padded by 20 tokens) over history
+    blocks of 2,048 and 256 packed rows, 80 % of them visible. Rows 0 and 5 (every head, every valid query) against
+    the oracle's joint softmax (a row's output depends on that row's inputs only); the gradients are checked at the
+    smaller shapes above, whose oracle backward finishes in seconds."""
+    B, n, sizes, loop = 8, 256, (2048, 256), 2
+    sl, q, k, v, cos, sin, valid, blocks, masks = make_case(97, B, n, sizes, loop, 'all')
+    valid[0, :20] = False
+    print('case bench shape B=8 n=256 blocks=(2048, 256) loop=2', flush=True)
+    with torch.no_grad():
+        out = be.mixed_attention(sl, loop, q, k, v, cos, sin, valid, tuple(blocks), tuple(masks))
+    rows = [0, 5]
+    pick = lambda t: t.detach()[rows].double().cpu().numpy()
+    fields = [sl.fields(loop, pick(blk)) for blk in blocks]
+    args = (pick(q), pick(k), pick(v), pick(cos), pick(sin), valid[rows].cpu().numpy(), [a for a, _ in fields],
+            [b for _, b in fields], [m[rows].cpu().numpy() for m in masks], f64(sl.A[loop]), f64(sl.B[loop]),
+            1 / math.sqrt(HD))
+    want = O.mixed_attention(*args, dtype=np.float32)
+    vq = valid[rows].cpu().numpy()
+    got = out[rows].float().cpu().numpy().transpose(0, 2, 1, 3)[vq]
+    assert_attention_close(got, want.transpose(0, 2, 1, 3)[vq], 'mixed attention at the bench shape')

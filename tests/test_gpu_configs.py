@@ -10,7 +10,9 @@
 * short-chunk prefill: 4 requests x 3 tokens on 8192 latent rows (against ``O.attend_chunk``), on the fused path and
   the reference's op sequence, and a mixed step of decode rows and chunks of 2..15 tokens;
 * steps whose longest chunk has 2 or 3 tokens over ragged histories (one-token requests beside them, an empty
-  history, padding).
+  history, padding);
+* chunked prefill of 4 requests x 512 and x 128 tokens over 8,192 latent rows (the multi-query configuration at
+  full size), sampled tokens of every request.
 
 Caches live on the device; page 0 and every page no request references are +inf-poisoned, so a read outside a row's
 pages cannot go unseen. The oracle reads host copies of the referenced pages only (through a remapped table).
@@ -106,10 +108,12 @@ class DeviceDecode:
         return layer.attend(self.sl, loop, self.q_lat[loop], self.q_rope[loop], k_rope, v, self.lat[w],
                             self.dev_tables[w], None, None, ctx, (self.exact[loop], self.dev_ex_table))
 
-    def oracle(self, loop):
+    def oracle(self, loop, sample=None):
         """The oracle composite on host copies of the pages the rows reference (the table remapped to them):
         O.attend_decode for a decode step, O.attend_chunk (the reference's causal chunk of k_rope / v + window
-        history + latent history) otherwise, with the chunk's k / v read back from the exact cache."""
+        history + latent history) otherwise, with the chunk's k / v read back from the exact cache. ``sample`` (a
+        token mask) limits a chunked step's oracle to those tokens (every valid token still serves as a key of the
+        chunk); the other rows come back zero."""
         w = 256 if loop == 0 else 512
         table = self.tables[w]
         ctx_lat = np.maximum(self.hist - W, 0)
@@ -131,9 +135,11 @@ class DeviceDecode:
             p = int(self.hist[req[t]] + t - self.qsl[req[t]])
             row = ex[self.ex_table[req[t], p // BLOCK], :, p % BLOCK]
             k_rope[t], v[t] = row[:, :D], row[:, D:]
+        attend = valid if sample is None else valid & sample
+        ctx, ctx_lat_t = np.where(attend, ctx, 0), np.where(attend, ctx_lat_t, 0)
         return O.attend_chunk(q_lat, q_rope, k_rope, v, B, lat[..., :w], lat[..., w:],
                               {'latent': tok_table, 'exact': self.ex_table[req]}, ctx, ctx_lat_t, self.qsl, W, SCALE,
-                              ~valid, ex[..., :D], ex[..., D:], rounding=False)
+                              ~attend, ex[..., :D], ex[..., D:], rounding=False)
 
 
 def _check(case, layer, ops, splits_by_width, loops=range(4), wants=None, fused=True):
@@ -209,3 +215,27 @@ def test_two_and_three_token_chunks(ops, layer, hist, lens, pad):
     splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
     wants = _check(case, layer, ops, splits)
     _check(case, layer, ops, splits, wants=wants, fused=False)
+
+
+@pytest.mark.parametrize('queries', [512, 128])
+def test_multi_query_prefill_full_size(ops, layer, queries):
+    """Chunked prefill of 4 requests x ``queries`` tokens over 8,192 latent rows + the 32-row window (the
+    multi-query configuration at its full size), all four loops, at the MI355X split policy: one slot at 512
+    tokens per request (the multi-query history kernel, then the reference's op sequence), four at 128 (the split
+    partials reduced with B_t and the merge in one epilogue). The first, middle and last 8 tokens of each request
+    are checked against the oracle, every head; the chunk's other tokens still serve as its keys."""
+    case = DeviceDecode([8192 + W] * 4, pad=1, seed=70 + queries, lens=[queries] * 4)
+    splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w, tokens_per_group=4) for w in WIDTHS}
+    assert splits == ({512: 1, 256: 1} if queries == 512 else {512: 4, 256: 4})
+    picks = np.concatenate([np.r_[0:8, queries // 2 - 4:queries // 2 + 4, queries - 8:queries] + r * queries
+                            for r in range(4)])
+    sample = np.zeros(case.T, bool)
+    sample[picks] = True
+    ctx = case.context(layer, ops, splits)
+    assert ctx.history_group == 4
+    for loop in range(4):
+        print(f'case 4 x {queries} tokens over 8192 + {W} rows loop={loop} splits={splits}', flush=True)
+        out = host_f32(case.run(layer, ctx, loop))
+        want = case.oracle(loop, sample)
+        assert_attention_close(out[picks], want[picks], f'loop {loop}')
+        assert (out[case.T - 1:] == 0).all()

@@ -74,6 +74,34 @@ class Step:
         return out
 
 
+def test_static_entry_under_graph_capture():
+    """The first call of the static entry point in this process is made under HIP graph capture (its per-device
+    array lookup included); replays with new queries between them, each after eager work and a synchronization,
+    are bitwise equal to the allocating entry point's eager result, and so is an eager call of the static entry
+    point between replays (which shares the array with the graph's kernels)."""
+    step = Step(np.random.default_rng(4).integers(1, 5000, 32), pad=1, width=512, splits=16, seed=4)
+    step.allocating()                       # the step's plan and the library's kernels, loaded outside the capture
+    torch.cuda.synchronize()
+    print('case graph capture of the first static call (33 rows, width 512, 16 slots)', flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        out = step.static()
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.Generator(device='cuda').manual_seed(5)
+    for i in range(3):
+        step.q_lat.copy_((torch.randn(step.q_lat.shape, generator=g, device='cuda') * 512 ** -0.5).to(torch.bfloat16))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = step.allocating()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f'replay {i}: max diff {(out.float() - want.float()).abs().max().item()}'
+        eager = step.static()
+        torch.cuda.synchronize()
+        assert torch.equal(eager, want), f'eager static call after replay {i} differs'
+
+
 def test_static_entry_equals_the_allocating_one_on_two_calls():
     big = Step(np.random.default_rng(1).integers(1, 6000, 64), pad=2, width=512, splits=16, seed=1)
     small = Step([700, 0, 45, 2900, 20], pad=1, width=256, splits=4, seed=2)
