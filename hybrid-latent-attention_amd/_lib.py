@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -70,6 +70,12 @@ SIGNATURES = {
     'hla_s6_khop_backward': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32, F32,
                              P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P, I64, I64,
                              I32, P, I64, I32, P],
+    'hla_s6_khop_forward_f32': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32,
+                                F32, P, I64, I64, I64, P, P],
+    'hla_s6_khop_backward_f32_workspace': [I32, I32, I32, I32, I32],
+    'hla_s6_khop_backward_f32': [P, I64, I64, I64, P, I64, I64, P, I64, I64, P, I64, I64, P, I32, I32, I32, I32, I32,
+                                 F32, P, I64, I64, I64, P, P, I64, I64, I64, P, P, P, I64, I64, I64, P, I64, I64, P,
+                                 I64, I64, I32, P, I64, P],
     'hla_s6_mixed_merge_forward': [I32, I32, I32, I32, I32, P, I64, I64, I64, P, I32, P, P, P, P, I64, I64, P, I64,
                                    I64, I64, P],
     'hla_s6_mixed_merge_backward': [I32, I32, I32, I32, I32, P, I64, I64, I64, P, I32, P, P, P, P, I64, I64, P, I64,
@@ -79,7 +85,7 @@ SIGNATURES = {
 }
 
 RESTYPES = {'hla_s6_last_error': ctypes.c_char_p, 'hla_s6_split_plan_ints': ctypes.c_int64,
-            'hla_s6_khop_backward_workspace': ctypes.c_int64}
+            'hla_s6_khop_backward_workspace': ctypes.c_int64, 'hla_s6_khop_backward_f32_workspace': ctypes.c_int64}
 
 _LIB = None
 

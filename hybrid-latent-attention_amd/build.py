@@ -19,7 +19,7 @@ LIB_NAME = 'libhla_s6.so'
 ARCH = os.environ.get('HLA_OFFLOAD_ARCH', 'gfx950')
 
 SOURCES = ('api.hip', 'history.hip', 'window.hip', 'elementwise.hip', 'absorb.hip', 'writer.hip', 'rollout.hip', 'khop.hip',
-           'hf_chunk.hip', 'mixed.hip')
+           'khop_f32.hip', 'hf_chunk.hip', 'mixed.hip')
 
 FLAGS = [
     f'--offload-arch={ARCH}', '-O3', '-std=c++17', '-fPIC', '-Wall', '-Wno-unused-function',

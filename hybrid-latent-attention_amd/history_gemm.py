@@ -1,16 +1,22 @@
 """History attention over contiguous latent rows with backward on MI355X: the interface of
 ``hla/latent/history_gemm.py`` (``causal_history_gemm``) and of ``hla/latent/fused_history.py`` (the single-query
 ``history_attention`` of lines 49-54 and the multi-query ``causal_history_attention`` of lines 126-153) over the HIP
-kernels of ``khop.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward``, ``hla_s6_khop_backward``) and
-``history.hip`` (``hla_s6_masked_history``, the single-query forward).
+kernels of ``khop.hip`` / ``khop_f32.hip`` (``hla_s6_khop_bounds``, ``hla_s6_khop_forward[_f32]``,
+``hla_s6_khop_backward[_f32]``) and ``history.hip`` (``hla_s6_masked_history``, the single-query forward).
 
 Every query row ``(b, i, h)`` attends over the latent rows ``k[b, j], v[b, j]`` that ``mask[b, i, j]`` shows (all
-heads share the rows). The kernels compute with bf16 GEMM operands and fp32 accumulation and softmax: the
-reference's ``precision='bf16'`` mode, which callers select explicitly. The reference's default modes (``'fp32'``,
-IEEE fp32 GEMMs, and ``'tf32'``; ``hla/latent/history_gemm.py:19-24,270-271``) and its fp32 CUDA-core ``'triton'``
-backend (``hla/latent/fused_history.py:129-130``) have no kernels here and raise ``ValueError``, so that no call
-narrows its arithmetic without asking. The kernels derive each query's key bound from the mask, so ``causal`` needs
-no promise and only documents intent. No ``[B, H, Lq, N]`` tensor is ever formed.
+heads share the rows). Two arithmetics, as the reference's precision modes (``hla/latent/history_gemm.py:19-24``):
+
+* ``precision='fp32'`` (the reference's default) and ``'tf32'``: fp32 operands on fp32 MFMA, fp32 softmax and
+  accumulation (``khop_f32.hip``); tf32 runs the same fp32 kernels (wider than tf32, never narrower). The
+  reference's fp32 ``'triton'`` (default) and ``'reference'`` backends of ``causal_history_attention`` run them too.
+  Inputs of any floating dtype are converted to fp32 once (the reference's ``.to(acc)``); float64 inputs, which the
+  reference computes in float64, raise ``ValueError`` (no float64 kernel) rather than narrow.
+* ``precision='bf16'``: bf16 GEMM operands with fp32 accumulation and softmax (``khop.hip`` and the multi-query
+  history kernels); the width-1024 backward runs on the fp32 kernels (bf16 inputs, wider arithmetic).
+
+The kernels derive each query's key bound from the mask, so ``causal`` needs no promise and only documents intent.
+No ``[B, H, Lq, N]`` tensor is ever formed.
 """
 from __future__ import annotations
 
@@ -20,13 +26,15 @@ from torch.autograd.function import once_differentiable
 from . import _lib, s6_ops
 
 PRECISIONS = ('fp32', 'tf32', 'bf16')   # the reference's modes
-KERNEL_PRECISIONS = ('bf16',)          # the modes the HIP kernels compute
+KERNEL_PRECISIONS = PRECISIONS           # every mode has kernels ('tf32' runs the fp32 ones)
 DEFAULT_CHUNK = 128
 DEFAULT_MAX_ELEMENTS = 1 << 26
 KEY_ALIGN = 16
 HEADS = 16
-WIDTHS = (128, 256, 512)          # forward and backward
-FORWARD_WIDTHS = WIDTHS + (1024,)  # 1024: forward only (token-linear rows, N a multiple of 16)
+WIDTHS = (128, 256, 512)          # bf16 forward and backward on the bf16 kernels
+FORWARD_WIDTHS = WIDTHS + (1024,)  # 1024: bf16 forward on the multi-query kernel (N a multiple of 16), backward on
+                                   # the fp32 kernels
+FP32_WIDTHS = (128, 256, 512, 1024)
 
 
 def bf16_fp32_output_supported(device) -> bool:
@@ -35,13 +43,9 @@ def bf16_fp32_output_supported(device) -> bool:
 
 
 def _check_precision(precision):
-    """``ValueError`` unless ``precision`` is a mode the kernels compute (the reference's message for unknown modes,
-    ``hla/latent/history_gemm.py:287-288``; a clear refusal for its fp32 / tf32 modes)."""
+    """``ValueError`` for a mode the reference does not know (its message, ``hla/latent/history_gemm.py:287-288``)."""
     if precision not in PRECISIONS:
         raise ValueError(f'Unknown precision {precision!r}; expected one of {PRECISIONS}')
-    if precision not in KERNEL_PRECISIONS:
-        raise ValueError(f'precision={precision!r} has no MI355X kernel: the HIP kernels compute with bf16 operands '
-                         f'and fp32 accumulation; pass precision="bf16"')
 
 
 def _bf16_rows(name, t):
@@ -93,11 +97,13 @@ class _CausalHistory(torch.autograd.Function):
         qb, kb, vb, m8, bound, lse, z = ctx.saved_tensors
         scale, q_dtype, k_dtype, v_dtype = ctx.settings
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
-        if qb.shape[-1] not in WIDTHS:
-            raise ValueError(f'causal_history_gemm backward: the HIP kernels take widths {WIDTHS} '
-                             f'(got {qb.shape[-1]}; 1024 is forward only)')
-        bf = q_dtype == k_dtype == v_dtype == torch.bfloat16
-        dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v, bf)
+        if qb.shape[-1] not in WIDTHS:   # width 1024: the fp32 kernels on the bf16 operands (wider arithmetic)
+            f32 = lambda t: t.float().contiguous()
+            dq, dk, dv = _backward_f32(f32(qb), f32(kb), f32(vb), m8, bound, lse, f32(z), dz, dlse, scale, need_q,
+                                       need_k or need_v)
+        else:
+            bf = q_dtype == k_dtype == v_dtype == torch.bfloat16
+            dq, dk, dv = _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v, bf)
         return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
                 dv.to(v_dtype) if need_v else None, None, None)
 
@@ -141,15 +147,112 @@ def _backward(qb, kb, vb, m8, bound, lse, z, dz, dlse, scale, need_q, need_kv, b
     return dq, dk, dv
 
 
+def _f32_rows(t):
+    """fp32 rows for the fp32 kernels: 16-byte aligned, unit last stride (a copy only when needed)."""
+    t = t.to(torch.float32)
+    if t.stride(-1) != 1 or any(s % 4 for s in t.stride()[:-1]) or t.data_ptr() % 16:
+        t = t.contiguous()
+    return t
+
+
+def _mask_bytes(mask, B, Lq, N, dev):
+    """The mask as bytes with a unit last stride and each token's key bound (``hla_s6_khop_bounds``)."""
+    m = mask if mask.dtype == torch.bool else mask.bool()
+    if m.stride(-1) != 1:
+        m = m.contiguous()
+    m8 = m.view(torch.uint8)
+    bound = torch.empty(B * Lq, dtype=torch.int32, device=dev)
+    _lib.call('hla_s6_khop_bounds', _lib.ptr(m8), m8.stride(0), m8.stride(1), B, Lq, N, _lib.ptr(bound),
+              _lib.stream(dev))
+    return m8, bound
+
+
+def _forward_f32(q32, k32, v32, m8, bound, scale):
+    """z [B, Lq, 16, R] fp32 and lse [B, 16, Lq] of the fp32 kernels."""
+    B, Lq, H, R = q32.shape
+    N = k32.shape[1]
+    dev = q32.device
+    z = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    _lib.call('hla_s6_khop_forward_f32', _lib.ptr(q32), q32.stride(0), q32.stride(1), q32.stride(2), _lib.ptr(k32),
+              k32.stride(0), k32.stride(1), _lib.ptr(v32), v32.stride(0), v32.stride(1), _lib.ptr(m8), m8.stride(0),
+              m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, float(scale), _lib.ptr(z), z.stride(0), z.stride(1),
+              z.stride(2), _lib.ptr(lse), _lib.stream(dev))
+    return z, lse
+
+
+def _f32_key_splits(B, Lq, N, R, dev):
+    """Token ranges per key block of the fp32 dk / dv kernel: about 4 workgroups per CU over the B * key blocks
+    (16 * 8 / (R / 128) keys each), at most 16, each range at least 64 tokens."""
+    blocks = B * -(-N // (16 * max(1, 1024 // R)))
+    cus = _lib.device_cus(dev.index or 0)
+    return max(1, min(16, -(-4 * cus // max(1, blocks)), max(1, Lq // 64)))
+
+
+def _backward_f32(q32, k32, v32, m8, bound, lse, z32, dz, dlse, scale, need_q, need_kv):
+    """dq [B, Lq, 16, R], dk / dv [B, N, R] (fp32; None where not needed) on the fp32 kernels, for the cotangents
+    dz (any floating dtype, None = 0) and dlse [B, 16, Lq] (None = 0); delta = dz . z uses the fp32 forward
+    output z32."""
+    B, Lq, H, R = q32.shape
+    N = k32.shape[1]
+    dev = q32.device
+    dz32 = _f32_rows(dz) if dz is not None else torch.zeros_like(z32)
+    dl = None if dlse is None else dlse.to(torch.float32).contiguous()
+    delta = torch.empty(B, H, Lq, dtype=torch.float32, device=dev)
+    dq = torch.empty(B, Lq, H, R, dtype=torch.float32, device=dev) if need_q else None
+    dk = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+    dv = torch.empty(B, N, R, dtype=torch.float32, device=dev) if need_kv else None
+    splits = _f32_key_splits(B, Lq, N, R, dev) if need_kv else 1
+    floats = _lib.load().hla_s6_khop_backward_f32_workspace(B, Lq, N, R, splits)
+    ws = torch.empty(floats, dtype=torch.float32, device=dev) if floats > 0 else None
+    _lib.call('hla_s6_khop_backward_f32', _lib.ptr(q32), q32.stride(0), q32.stride(1), q32.stride(2), _lib.ptr(k32),
+              k32.stride(0), k32.stride(1), _lib.ptr(v32), v32.stride(0), v32.stride(1), _lib.ptr(m8), m8.stride(0),
+              m8.stride(1), _lib.ptr(bound), B, Lq, N, H, R, float(scale), _lib.ptr(z32), z32.stride(0),
+              z32.stride(1), z32.stride(2), _lib.ptr(lse), _lib.ptr(dz32), dz32.stride(0), dz32.stride(1),
+              dz32.stride(2), _lib.ptr(dl), _lib.ptr(delta), _lib.ptr(dq), 0 if dq is None else dq.stride(0),
+              0 if dq is None else dq.stride(1), 0 if dq is None else dq.stride(2), _lib.ptr(dk),
+              0 if dk is None else dk.stride(0), 0 if dk is None else dk.stride(1), _lib.ptr(dv),
+              0 if dv is None else dv.stride(0), 0 if dv is None else dv.stride(1), splits, _lib.ptr(ws),
+              0 if ws is None else ws.numel(), _lib.stream(dev))
+    return dq, dk, dv
+
+
+class _CausalHistoryF32(torch.autograd.Function):
+    """fp32 arithmetic (``precision='fp32'`` / ``'tf32'``, and the fp32 backends of ``causal_history_attention``):
+    z in q.dtype, lse fp32; gradients in the inputs' dtypes."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, mask, scale):
+        B, Lq, H, R = q.shape
+        N = k.shape[1]
+        q32, k32, v32 = _f32_rows(q), _f32_rows(k), _f32_rows(v)
+        m8, bound = _mask_bytes(mask, B, Lq, N, q.device)
+        z, lse = _forward_f32(q32, k32, v32, m8, bound, scale)
+        ctx.save_for_backward(q32, k32, v32, m8, bound, lse, z)
+        ctx.settings = (float(scale), q.dtype, k.dtype, v.dtype)
+        return z.to(q.dtype), lse
+
+    @staticmethod
+    @once_differentiable
+    def backward(ctx, dz, dlse):
+        q32, k32, v32, m8, bound, lse, z = ctx.saved_tensors
+        scale, q_dtype, k_dtype, v_dtype = ctx.settings
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        dq, dk, dv = _backward_f32(q32, k32, v32, m8, bound, lse, z, dz, dlse, scale, need_q, need_k or need_v)
+        return (dq.to(q_dtype) if need_q else None, dk.to(k_dtype) if need_k else None,
+                dv.to(v_dtype) if need_v else None, None, None)
+
+
 def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHUNK, precision='fp32',
                         max_elements=DEFAULT_MAX_ELEMENTS):
     """Causal history attention (``hla/latent/history_gemm.py:270-294``).
 
     q: [B, Lq, 16, R], k: [B, N, R], v: [B, N, R], mask: [B, Lq, N] (True = visible). Returns z [B, Lq, 16, R] in
     q.dtype and lse [B, 16, Lq] (fp32, -inf on rows with no visible history, where z is 0); differentiable in q, k
-    and v. ``precision`` must be ``'bf16'`` (bf16 operands, fp32 accumulation); the reference's default ``'fp32'``
-    and ``'tf32'`` raise ``ValueError``. ``causal`` asks for the reference's promise check only; ``chunk`` and
-    ``max_elements`` are accepted for signature parity (the kernels do not chunk).
+    and v. ``precision`` ``'fp32'`` (default) and ``'tf32'`` compute in fp32 (widths 128-1024), ``'bf16'`` with bf16
+    operands and fp32 accumulation (widths 128-512, and 1024 with N a multiple of 16). ``causal`` asks for the
+    reference's promise check only; ``chunk`` and ``max_elements`` are accepted for signature parity (the kernels
+    do not chunk).
     """
     if q.ndim != 4 or k.ndim != 3 or v.ndim != 3 or mask.ndim != 3:
         raise ValueError(f'Expected Q[B,Lq,H,R], K[B,N,R], V[B,N,Rv], mask[B,Lq,N], got '
@@ -164,11 +267,23 @@ def causal_history_gemm(q, k, v, mask, scale, *, causal=False, chunk=DEFAULT_CHU
     _check_precision(precision)
     if chunk < 1 or max_elements < 1:
         raise ValueError('chunk and max_elements must be positive')
-    if H != HEADS or v.shape[-1] != Rk or Rk not in FORWARD_WIDTHS:
-        raise ValueError(f'the HIP kernels take {HEADS} heads and equal K/V widths in {FORWARD_WIDTHS} '
-                         f'(got H={H}, Rk={Rk}, Rv={v.shape[-1]})')
+    return _apply(q, k, v, mask, scale, precision)
+
+
+def _apply(q, k, v, mask, scale, precision):
+    """The kernels of ``precision`` after the shape checks of the reference's entry points."""
+    H, Rk = q.shape[2], q.shape[-1]
+    widths = FORWARD_WIDTHS if precision == 'bf16' else FP32_WIDTHS
+    if H != HEADS or v.shape[-1] != Rk or Rk not in widths:
+        raise ValueError(f'the HIP kernels take {HEADS} heads and equal K/V widths in {widths} for precision '
+                         f'{precision!r} (got H={H}, Rk={Rk}, Rv={v.shape[-1]})')
     s6_ops._dev(q, k, v, mask)
-    return _CausalHistory.apply(q, k, v, mask, float(scale))
+    if precision == 'bf16':
+        return _CausalHistory.apply(q, k, v, mask, float(scale))
+    if torch.float64 in (q.dtype, k.dtype, v.dtype):
+        raise ValueError(f'precision={precision!r} computes float64 inputs in float64 in the reference; the MI355X '
+                         f'kernels compute in fp32: pass float32 or bfloat16 inputs')
+    return _CausalHistoryF32.apply(q, k, v, mask, float(scale))
 
 
 SINGLE_WIDTHS = (128, 256, 512, 1024)  # forward; the backward takes WIDTHS
@@ -246,20 +361,20 @@ HISTORY_BACKENDS = ('triton', 'reference', 'gemm')
 
 def causal_history_attention(q, k, v, mask, scale, reference_forward=False, *, backend='triton', precision='fp32',
                              chunk=None, causal=False):
-    """``hla/latent/fused_history.py:129-153``: ``backend='gemm'`` runs ``causal_history_gemm`` with ``precision``
-    (``'bf16'``: the HIP kernels). The reference's default ``'triton'`` backend (fp32 CUDA-core kernels) and its
-    ``'reference'`` backend (dense fp32 torch autograd) compute in fp32, which no kernel here does: both raise
-    ``ValueError`` rather than run at bf16."""
+    """``hla/latent/fused_history.py:129-153``: ``backend='gemm'`` runs ``causal_history_gemm`` with ``precision``;
+    the reference's default ``'triton'`` backend (fp32 CUDA-core kernels) and its ``'reference'`` backend (dense
+    fp32 torch autograd) compute in fp32, as the fp32 kernels here do (``precision`` and ``chunk`` apply to
+    ``'gemm'`` only, as in the reference). ``reference_forward`` selects the reference's dense torch forward inside
+    its Triton backend; both forwards compute the same fp32 attention, and here the fp32 kernel is the only one."""
     if q.ndim != 4 or k.ndim != 3 or v.ndim != 3 or mask.ndim != 3:
         raise ValueError(f'Expected Q[B,Lq,H,R], K/V[B,N,R], mask[B,Lq,N], got {tuple(q.shape)}, {tuple(k.shape)}, '
                          f'{tuple(v.shape)}, {tuple(mask.shape)}')
+    if backend == 'gemm':
+        return causal_history_gemm(q, k, v, mask, scale, causal=causal, chunk=chunk or DEFAULT_CHUNK,
+                                   precision=precision)
     if backend not in HISTORY_BACKENDS:
         raise ValueError(f'Unknown causal history backend {backend!r}; expected one of {HISTORY_BACKENDS}')
-    if backend != 'gemm':
-        raise ValueError(f'backend={backend!r} computes in fp32, which has no MI355X kernel: use backend="gemm", '
-                         f'precision="bf16" (bf16 MFMA operands, fp32 accumulation)')
-    return causal_history_gemm(q, k, v, mask, scale, causal=causal, chunk=chunk or DEFAULT_CHUNK,
-                               precision=precision)
+    return _apply(q, k, v, mask, scale, 'fp32')
 
 
 def flops(visible_pairs: int, heads: int, width: int, with_backward: bool = False) -> float:

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 9
+#define HLA_S6_ABI_VERSION 10
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -373,6 +373,32 @@ int hla_s6_khop_backward(const void *q, int64_t q_sb, int64_t q_si, int64_t q_sh
                          float *dk, int64_t dk_sb, int64_t dk_sn, float *dv, int64_t dv_sb, int64_t dv_sn,
                          int32_t key_splits, float *workspace, int64_t workspace_floats, int32_t grads_bf16,
                          void *stream);
+
+/* ---- the same in fp32 arithmetic (the reference's default precision) ------------------------------------------
+ * Replace causal_history_gemm with precision 'fp32' / 'tf32' (hla/latent/history_gemm.py:19-24,37,46-66,270-294)
+ * and causal_history_attention's fp32 'triton' / 'reference' backends (hla/latent/fused_history.py:62-153):
+ * every GEMM on fp32 MFMA (fp32 operands, fp32 accumulation), softmax in fp32. Arguments as hla_s6_khop_forward /
+ * hla_s6_khop_backward with fp32 q / k / v / z / dz (rows 16-byte aligned, unit last stride), width in {128, 256,
+ * 512, 1024}, no grads_bf16 (dq / dk / dv are fp32). z is the fp32 forward output (delta = dz.z uses it).
+ * key_splits > 1 splits each key block's query tokens into that many ranges, with fp32 partials in `workspace` (at
+ * least hla_s6_khop_backward_f32_workspace floats; dk / dv then contiguous) summed in a fixed order: deterministic
+ * for a given key_splits. The forward is one launch, the backward up to 5. */
+int hla_s6_khop_forward_f32(const float *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const float *k, int64_t k_sb,
+                            int64_t k_sn, const float *v, int64_t v_sb, int64_t v_sn, const uint8_t *mask,
+                            int64_t m_sb, int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N,
+                            int32_t heads, int32_t width, float scale, float *z, int64_t z_sb, int64_t z_si,
+                            int64_t z_sh, float *lse, void *stream);
+/* hla_s6_khop_backward_f32_workspace: 2 * key_splits * B * N * width floats with key_splits > 1, else 0. */
+int64_t hla_s6_khop_backward_f32_workspace(int32_t B, int32_t Lq, int32_t N, int32_t width, int32_t key_splits);
+int hla_s6_khop_backward_f32(const float *q, int64_t q_sb, int64_t q_si, int64_t q_sh, const float *k, int64_t k_sb,
+                             int64_t k_sn, const float *v, int64_t v_sb, int64_t v_sn, const uint8_t *mask,
+                             int64_t m_sb, int64_t m_si, const int32_t *bound, int32_t B, int32_t Lq, int32_t N,
+                             int32_t heads, int32_t width, float scale, const float *z, int64_t z_sb, int64_t z_si,
+                             int64_t z_sh, const float *lse, const float *dz, int64_t dz_sb, int64_t dz_si,
+                             int64_t dz_sh, const float *dlse, float *delta, float *dq, int64_t dq_sb, int64_t dq_si,
+                             int64_t dq_sh, float *dk, int64_t dk_sb, int64_t dk_sn, float *dv, int64_t dv_sb,
+                             int64_t dv_sn, int32_t key_splits, float *workspace, int64_t workspace_floats,
+                             void *stream);
 
 /* ---- single-query history attention over contiguous rows with a key mask (HF rolling engine) ---------------
  * Replaces the forward of fused_history.history_attention (hla/latent/fused_history.py:23-35,49-54; Triton

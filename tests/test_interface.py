@@ -69,25 +69,23 @@ def test_reference_default_values(pkg, module):
             assert params[name].default == want, f'{module}.{qual}({name}=...): {params[name].default!r} != {want!r}'
 
 
-def test_history_precisions_refuse_what_has_no_kernel(pkg):
-    """The reference's fp32 / tf32 modes and fp32 backends raise before any device work; unknown names raise the
-    reference's error (hla/latent/history_gemm.py:287-288, fused_history.py:146-147)."""
+def test_history_precisions_and_backends(pkg):
+    """Every precision and backend of the reference has kernels: on host tensors each refuses with the GPU-only
+    error (no CPU path); unknown names raise the reference's errors (hla/latent/history_gemm.py:287-288,
+    fused_history.py:146-147)."""
     hg = pkg.history_gemm
     q, k, m = torch.zeros(1, 2, 16, 256), torch.zeros(1, 2, 256), torch.ones(1, 2, 2, dtype=torch.bool)
-    for kwargs in ({}, {'precision': 'fp32'}, {'precision': 'tf32'}):
-        with pytest.raises(ValueError, match='no MI355X kernel'):
+    for kwargs in ({}, {'precision': 'fp32'}, {'precision': 'tf32'}, {'precision': 'bf16'}):
+        with pytest.raises(RuntimeError, match='GPU only'):
             hg.causal_history_gemm(q, k, k, m, 1.0, **kwargs)
     with pytest.raises(ValueError, match='Unknown precision'):
         hg.causal_history_gemm(q, k, k, m, 1.0, precision='fp16')
-    for backend in ('triton', 'reference'):
-        with pytest.raises(ValueError, match='fp32'):
+    for backend in ('triton', 'reference', 'gemm'):
+        with pytest.raises(RuntimeError, match='GPU only'):
             hg.causal_history_attention(q, k, k, m, 1.0, backend=backend)
     with pytest.raises(ValueError, match='Unknown causal history backend'):
         hg.causal_history_attention(q, k, k, m, 1.0, backend='hip')
-    with pytest.raises(ValueError, match='no MI355X kernel'):
-        hg.causal_history_attention(q, k, k, m, 1.0, backend='gemm')
-    with pytest.raises(RuntimeError, match='GPU only'):      # a supported mode still has no CPU path
-        hg.causal_history_gemm(q, k, k, m, 1.0, precision='bf16')
+    assert hg.KERNEL_PRECISIONS == hg.PRECISIONS
 
 
 @pytest.mark.parametrize('case', KNOWN['num_kv_splits']['cases'], ids=lambda c: str(c['args']))
