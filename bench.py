@@ -32,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = 'latent decode-attn µs/layer + HBM GB/s (% peak), Ouro-1.4B S6, B=64 ctx 8K'
 PEAK_HBM_GBPS = 8000.0
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 TRAFFIC_PROFILE = os.path.join(ROOT, 'profiles', 'history_split_512_b64_ctx8192_pmc.md')
 LAYERS, LOOPS, HEADS, HEAD_DIM, RANK, RANK1, WINDOW, BLOCK = 24, 4, 16, 128, 512, 256, 32, 16
 MAX_POSITION = 65536
@@ -73,6 +74,8 @@ def parse():
     p.add_argument('--no-secondary', action='store_true',
                    help='decode: skip the other configurations (single decode, ragged, long context, multi-query Q=3 '
                         'and Q=512) that the default run appends to the headline line under "configs"')
+    p.add_argument('--precision', choices=('bf16', 'fp32', 'tf32'), default='bf16',
+                   help='--workload khop: the history GEMM precision (fp32 / tf32: fp32 leaves and fp32 kernels)')
     p.add_argument('--seed', type=int, default=0)
     p.add_argument('--table', choices=('random', 'identity'), default='random',
                    help='latent block tables: a random permutation of the page pool, or pages in order')
@@ -590,33 +593,38 @@ def khop_workload(args, pkg, device):
     (hla/latent/benchmark_history_gemm.py:79-101): B = 4, 16 heads, L = 2880 queries and keys, latent width
     ``--width`` (512 default), valid lengths L, 0.9 L, 0.8 L, 0.7 L, query i sees keys j < i. Times the forward (in
     a HIP graph) and the forward + backward (dq, dk, dv through autograd, returned as the reference's benchmark does
-    with torch.autograd.grad; bf16 leaves here, fp32 there); reports TFLOP/s of the algorithmic work (2 GEMMs
-    forward, 7 with the backward, over the visible pairs) against the 2.5 PFLOP/s bf16 peak. One JSON line."""
+    with torch.autograd.grad) at ``--precision`` (bf16: bf16 leaves and operands; fp32 / tf32: fp32 leaves, the fp32
+    kernels, as the reference benchmark's gemm-fp32 / gemm-tf32 rows); reports TFLOP/s of the algorithmic work (2
+    GEMMs forward, 7 with the backward, over the visible pairs) against the dense MFMA peak of the arithmetic (bf16
+    2.5 PFLOP/s, fp32 157.3 TFLOP/s) and the reference's published A100 times of the same backend and shape. One
+    JSON line."""
     hg = pkg.history_gemm
     B, L, R = args.batch or 4, args.context or 2880, args.width
     g = torch.Generator(device=device).manual_seed(args.seed)
-    q = torch.randn(B, L, HEADS, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
-    k = torch.randn(B, L, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
-    v = torch.randn(B, L, R, generator=g, device=device).to(torch.bfloat16).requires_grad_(True)
+    prec = args.precision
+    leaf = torch.bfloat16 if prec == 'bf16' else torch.float32
+    q = torch.randn(B, L, HEADS, R, generator=g, device=device).to(leaf).requires_grad_(True)
+    k = torch.randn(B, L, R, generator=g, device=device).to(leaf).requires_grad_(True)
+    v = torch.randn(B, L, R, generator=g, device=device).to(leaf).requires_grad_(True)
     lengths = torch.tensor([max(2, int(L * (1 - 0.1 * i))) for i in range(B)], device=device)
     valid = torch.arange(L, device=device)[None] < lengths[:, None]
     order = torch.arange(L, device=device)[:, None] > torch.arange(L, device=device)[None]
     mask = valid[:, :, None] & valid[:, None, :] & order[None]
     pairs = int(mask.sum().item())
     scale = 1 / math.sqrt(HEAD_DIM)
-    dz = torch.randn(B, L, HEADS, R, generator=g, device=device).to(torch.bfloat16)
+    dz = torch.randn(B, L, HEADS, R, generator=g, device=device).to(leaf)
     dlse = torch.randn(B, HEADS, L, generator=g, device=device)
 
     def fwd():
         with torch.no_grad():
-            hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision='bf16')
+            hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision=prec)
 
     def train():  # gradients returned, not accumulated into .grad (as the reference's operator benchmark does)
-        z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision='bf16')
+        z, lse = hg.causal_history_gemm(q, k, v, mask, scale, causal=True, precision=prec)
         torch.autograd.grad([z, lse], [q, k, v], [dz, dlse])
 
     ms_f = time_graph(fwd, args.steps, args.warmup)
-    ms_t = time_eager(train, args.steps, args.warmup) if R in hg.WIDTHS else None   # 1024: forward only
+    ms_t = time_eager(train, args.steps, args.warmup)
     f_fwd, f_all = hg.flops(pairs, HEADS, R), hg.flops(pairs, HEADS, R, with_backward=True)
     base = None
     if not args.no_cpu_baseline:
@@ -648,16 +656,21 @@ def khop_workload(args, pkg, device):
                           f'queries of request 0 '
                           f'({sample_pairs} visible pairs), median of 3, scaled by visible pairs ({pairs}); '
                           f'extrapolated'}
-    # the reference's published bf16 GEMM forward at this shape (A100, benchmark_history_gemm summary)
-    published = {1024: 19.0, 256: 13.3}.get(R) if (B, L) == (4, 2880) else None
-    print(json.dumps({'workload': 'khop', 'value': round(ms_t if ms_t else ms_f, 3),
-                      'unit': 'ms per forward+backward' if ms_t else 'ms per forward',
-                      'forward_ms': round(ms_f, 3), 'B': B, 'L': L, 'heads': HEADS, 'width': R,
-                      'visible_pairs': pairs, 'forward_tflops': round(f_fwd / (ms_f * 1e9), 1),
-                      'train_tflops': round(f_all / (ms_t * 1e9), 1) if ms_t else None,
-                      'forward_mfma_frac': round(f_fwd / (ms_f * 1e9) / PEAK_BF16_TFLOPS, 4),
-                      'train_mfma_frac': round(f_all / (ms_t * 1e9) / PEAK_BF16_TFLOPS, 4) if ms_t else None,
-                      'reference_forward_ms_a100': published, 'steps': args.steps,
+    # the reference's published A100 times (ms) at this shape: forward, forward + backward of dq, dk, dv
+    # (results/latent/history-gemm-bench-0923-summary.json, gemm-<precision> rows at length 2880)
+    published = {('bf16', 1024): (19.02, 60.33), ('bf16', 256): (13.34, 38.34), ('fp32', 1024): (76.07, 261.84),
+                 ('fp32', 256): (30.39, 99.20), ('tf32', 1024): (23.08, 73.50),
+                 ('tf32', 256): (13.71, 39.18)}.get((prec, R)) if (B, L) == (4, 2880) else None
+    peak = PEAK_BF16_TFLOPS if prec == 'bf16' else PEAK_FP32_TFLOPS
+    print(json.dumps({'workload': 'khop', 'precision': prec, 'value': round(ms_t, 3),
+                      'unit': 'ms per forward+backward', 'forward_ms': round(ms_f, 3), 'B': B, 'L': L,
+                      'heads': HEADS, 'width': R, 'visible_pairs': pairs,
+                      'forward_tflops': round(f_fwd / (ms_f * 1e9), 1), 'train_tflops': round(f_all / (ms_t * 1e9), 1),
+                      'mfma_peak_tflops': peak, 'forward_mfma_frac': round(f_fwd / (ms_f * 1e9) / peak, 4),
+                      'train_mfma_frac': round(f_all / (ms_t * 1e9) / peak, 4),
+                      'reference_a100_ms': None if published is None else {'forward': published[0],
+                                                                          'forward_backward': published[1]},
+                      'steps': args.steps,
                       'data': 'synthetic (randn q, k, v, cotangents)', 'forward_hip_graph': True,
                       'cpu_baseline': base}), flush=True)
 

@@ -24,8 +24,7 @@
 namespace hla {
 namespace {
 
-constexpr int kFThreads = 512;  // 8 waves
-constexpr int kFKeys = 16;      // keys (forward, dq) or query heads (dk / dv) per step
+constexpr int kFKeys = 16;  // keys (forward, dq) or query heads (dk / dv) per step
 
 __device__ __forceinline__ floatx4 mfma_f32(float a, float b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
@@ -58,86 +57,95 @@ struct KfParams {
   int64_t kv_ss;
 };
 
-// Geometry of a kernel over width R with RC columns per wave: CS waves per token (key block), G tokens (key
-// blocks) per workgroup.
-template <int R, int RC>
+// Geometry of a kernel over width R with RC columns per wave and W waves: CS waves per token (key block), G tokens
+// (key blocks) per workgroup.
+template <int R, int RC, int W>
 struct KfGeo {
+  static constexpr int THREADS = 64 * W;
   static constexpr int CS = R / RC;
-  static constexpr int G = 8 / CS;
+  static constexpr int G = W / CS;
   static constexpr int NC = RC / 16;   // 16-column chunks of a wave (products over the columns)
   static constexpr int NB = RC / 64;   // 64-column blocks of a wave (products over keys / heads)
   static constexpr int RS = R + 4;     // LDS row stride of a tile, floats
-  static constexpr int TL = kFKeys * R / 4 / kFThreads;  // 16-byte pieces per thread per tile
-  static_assert(CS >= 1 && CS <= 8 && 8 % CS == 0 && NB >= 1 && TL >= 1, "unsupported width / column split");
+  static constexpr int TL = kFKeys * R / 4 / THREADS;  // 16-byte pieces per thread per tile
+  // the score and dP exchanges share one LDS buffer (one more barrier) when two would not fit beside the tiles
+  static constexpr bool ONE_X = 2 * kFKeys * RS * 4 + 2 * W * 64 * 16 > 160 * 1024;
+  static_assert(CS >= 1 && CS <= W && W % CS == 0 && NB >= 1 && TL >= 1, "unsupported width / column split");
 };
 
-template <int R, int RC>
-using KfRegs = floatx4[KfGeo<R, RC>::TL];   // one tile's share of a thread
-template <int R, int RC>
-using KfAcc = floatx4[KfGeo<R, RC>::NB][4];  // a wave's 16 x RC accumulator (see kf_rows)
-template <int R, int RC>
-using KfCols = floatx4[KfGeo<R, RC>::NC];   // a lane's B operand over the wave's columns (see kf_cols)
+// A compiler-only fence: LDS operand reads are not hoisted across it (each 16-byte read feeds four 32-cycle MFMAs, so
+// reads two steps ahead keep the matrix pipe fed; hoisting all of them would cost registers the kernels lack).
+__device__ __forceinline__ void kf_fence() { asm volatile("" ::: "memory"); }
 
-// 16 rows x R of a row-major fp32 matrix into registers (piece p = it * 512 + tid is row p / (R / 4), columns
+template <int R, int RC, int W>
+using KfRegs = floatx4[KfGeo<R, RC, W>::TL];   // one tile's share of a thread
+template <int R, int RC, int W>
+using KfAcc = floatx4[KfGeo<R, RC, W>::NB][4];  // a wave's 16 x RC accumulator (see kf_rows)
+template <int R, int RC, int W>
+using KfCols = floatx4[KfGeo<R, RC, W>::NC];   // a lane's B operand over the wave's columns (see kf_cols)
+
+// 16 rows x R of a row-major fp32 matrix into registers (piece p = it * THREADS + tid is row p / (R / 4), columns
 // 4 (p % (R / 4)) .. +4); rowp(r) is an in-bounds row pointer.
-template <int R, int RC, class RowP>
-__device__ __forceinline__ void kf_load(KfRegs<R, RC>& reg, RowP rowp) {
+template <int R, int RC, int W, class RowP>
+__device__ __forceinline__ void kf_load(KfRegs<R, RC, W>& reg, RowP rowp) {
 #pragma unroll
-  for (int it = 0; it < KfGeo<R, RC>::TL; ++it) {
-    const int p = it * kFThreads + threadIdx.x;
+  for (int it = 0; it < KfGeo<R, RC, W>::TL; ++it) {
+    const int p = it * KfGeo<R, RC, W>::THREADS + threadIdx.x;
     reg[it] = *reinterpret_cast<const floatx4*>(rowp(p / (R / 4)) + 4 * (p % (R / 4)));
   }
 }
 
-template <int R, int RC>
-__device__ __forceinline__ void kf_store(float* tile, const KfRegs<R, RC>& reg) {
+template <int R, int RC, int W>
+__device__ __forceinline__ void kf_store(float* tile, const KfRegs<R, RC, W>& reg) {
 #pragma unroll
-  for (int it = 0; it < KfGeo<R, RC>::TL; ++it) {
-    const int p = it * kFThreads + threadIdx.x;
-    *reinterpret_cast<floatx4*>(tile + (p / (R / 4)) * KfGeo<R, RC>::RS + 4 * (p % (R / 4))) = reg[it];
+  for (int it = 0; it < KfGeo<R, RC, W>::TL; ++it) {
+    const int p = it * KfGeo<R, RC, W>::THREADS + threadIdx.x;
+    *reinterpret_cast<floatx4*>(tile + (p / (R / 4)) * KfGeo<R, RC, W>::RS + 4 * (p % (R / 4))) = reg[it];
   }
 }
 
 // Partial D[m][n] = sum over the wave's columns [c0, c0 + RC) of A[m][c] B[n][c], with A's 16 rows a row-major LDS
 // tile and B held by the lane as breg[c][t] = B[l % 16][c0 + 16 c + 4 (l / 16) + t]. Lane l gets D[4 (l / 16) + i]
 // [l % 16] in element i.
-template <int R, int RC>
-__device__ __forceinline__ floatx4 kf_cols(const float* tile, int c0, const KfCols<R, RC>& breg) {
+template <int R, int RC, int W>
+__device__ __forceinline__ floatx4 kf_cols(const float* tile, int c0, const KfCols<R, RC, W>& breg) {
   const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
-  const float* ap = tile + l16 * KfGeo<R, RC>::RS + c0 + 4 * g;
+  const float* ap = tile + l16 * KfGeo<R, RC, W>::RS + c0 + 4 * g;
   floatx4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int c = 0; c < KfGeo<R, RC>::NC; ++c) {
+  for (int c = 0; c < KfGeo<R, RC, W>::NC; ++c) {
     const floatx4 a = *reinterpret_cast<const floatx4*>(ap + 16 * c);
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc = mfma_f32(a[t], breg[c][t], acc);
+    if (c % 2 == 1) kf_fence();
   }
   return acc;
 }
 
 // acc[nb][cb] += T^T . W over the 16 rows of a row-major LDS tile T (row r = 4 (l / 16) + st holds the lane's
 // weight w[st] for its output column l % 16): output row m of block (nb, cb) is column c0 + 64 nb + 4 m + cb.
-template <int R, int RC>
-__device__ __forceinline__ void kf_rows(KfAcc<R, RC>& acc, const float* tile, int c0, const floatx4& w) {
+template <int R, int RC, int W>
+__device__ __forceinline__ void kf_rows(KfAcc<R, RC, W>& acc, const float* tile, int c0, const floatx4& w) {
   const int lane = threadIdx.x & 63, l16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-    const float* rp = tile + (4 * g + st) * KfGeo<R, RC>::RS + c0 + 4 * l16;
+    const float* rp = tile + (4 * g + st) * KfGeo<R, RC, W>::RS + c0 + 4 * l16;
 #pragma unroll
-    for (int nb = 0; nb < KfGeo<R, RC>::NB; ++nb) {
+    for (int nb = 0; nb < KfGeo<R, RC, W>::NB; ++nb) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(rp + 64 * nb);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) acc[nb][cb] = mfma_f32(a[cb], w[st], acc[nb][cb]);
     }
+    if (st % 2 == 1) kf_fence();
   }
 }
 
 // Store of a kf_rows accumulator scaled by s: the lane's 16 columns c0 + 64 nb + 16 (l / 16) + 4 i + cb of row ptr.
-template <int R, int RC>
-__device__ __forceinline__ void kf_store_rows(float* row, int c0, const KfAcc<R, RC>& acc, float s) {
+template <int R, int RC, int W>
+__device__ __forceinline__ void kf_store_rows(float* row, int c0, const KfAcc<R, RC, W>& acc, float s) {
   const int g = (threadIdx.x & 63) >> 4;
 #pragma unroll
-  for (int nb = 0; nb < KfGeo<R, RC>::NB; ++nb)
+  for (int nb = 0; nb < KfGeo<R, RC, W>::NB; ++nb)
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       *reinterpret_cast<floatx4*>(row + c0 + 64 * nb + 16 * g + 4 * i) =
@@ -163,14 +171,42 @@ __device__ __forceinline__ void kf_mask4(const uint8_t* row, int key0, int N, ui
   for (int e = 0; e < 4; ++e) m[e] = row ? row[min(key0 + e, N - 1)] : (uint8_t)1;
 }
 
+// Direct global -> LDS copy of a 16-row tile (rowp(r) an in-bounds row pointer, R floats per row) into a padded LDS
+// tile at LDS byte address `tile`: 1 KB per wave instruction, the workgroup's waves taking the rows in turn. Every
+// address is wave-uniform and kept in scalar registers (the wave index is read through readfirstlane). The copies
+// are not counted by the compiler: the caller waits with kf_wait_copies() before the barrier after which the tile
+// is read.
+template <int R, int RC, int W, class RowP>
+__device__ __forceinline__ void kf_copy_tile(uint32_t tile, RowP rowp) {
+  constexpr int PER_ROW = R / 256;
+  constexpr int PER_WAVE = kFKeys * PER_ROW / W;
+  static_assert(PER_ROW >= 1 && PER_WAVE >= 1 && kFKeys * PER_ROW % W == 0, "tile copy split");
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t lane_off = 16u * (threadIdx.x & 63);
+#pragma unroll
+  for (int i = 0; i < PER_WAVE; ++i) {
+    const int c = wave * PER_WAVE + i, r = c / PER_ROW, j = c % PER_ROW;
+    const int64_t row = uniform64(reinterpret_cast<int64_t>(rowp(r)));
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(tile + (uint32_t)((r * KfGeo<R, RC, W>::RS + 256 * j) * 4));
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(dst), "v"(lane_off + 1024u * j),
+                 "s"(reinterpret_cast<const void*>(row))
+                 : "memory", "m0");
+  }
+}
+// LDS byte address of a shared array
+__device__ __forceinline__ uint32_t kf_lds(const void* p) {
+  return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+__device__ __forceinline__ void kf_wait_copies() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ---- forward: one workgroup per G consecutive tokens of a batch row (longest rows first) ------------------------
-template <int R, int RC>
-__global__ __launch_bounds__(kFThreads) void khf_fwd(KfParams a) {
-  using G_ = KfGeo<R, RC>;
+template <int R, int RC, int W>
+__global__ __launch_bounds__(64 * W) void khf_fwd(KfParams a) {
+  using G_ = KfGeo<R, RC, W>;
   constexpr int CS = G_::CS, TG = G_::G;
   __shared__ __attribute__((aligned(16))) float ks[kFKeys * G_::RS];
   __shared__ __attribute__((aligned(16))) float vs[kFKeys * G_::RS];
-  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? 8 : 1][64];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? W : 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int tok = wave / CS, c0 = (wave % CS) * RC;
   const int b = blockIdx.y;
@@ -201,21 +237,21 @@ __global__ __launch_bounds__(kFThreads) void khf_fwd(KfParams a) {
   floatx4 kr[G_::TL], vr[G_::TL];
   uint8_t m_next[4] = {1, 1, 1, 1}, m_cur[4];
   auto load = [&](int kt) {
-    kf_load<R, RC>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
-    kf_load<R, RC>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
+    kf_load<R, RC, W>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
+    kf_load<R, RC, W>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
     kf_mask4(mrow, kt + 4 * g, a.N, m_next);
   };
   if (nkeys > 0) load(0);
   for (int kt = 0; kt < nkeys; kt += kFKeys) {
     __syncthreads();  // the previous tile's readers are done
-    kf_store<R, RC>(ks, kr);
-    kf_store<R, RC>(vs, vr);
+    kf_store<R, RC, W>(ks, kr);
+    kf_store<R, RC, W>(vs, vr);
 #pragma unroll
     for (int e = 0; e < 4; ++e) m_cur[e] = m_next[e];
     __syncthreads();
     if (kt + kFKeys < nkeys) load(kt + kFKeys);
     // S^T[key 4 g + i][head l16]
-    const floatx4 s = kf_exchange<CS>(kf_cols<R, RC>(ks, c0, qv), xs, wave, tok * CS);
+    const floatx4 s = kf_exchange<CS>(kf_cols<R, RC, W>(ks, c0, qv), xs, wave, tok * CS);
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -235,26 +271,28 @@ __global__ __launch_bounds__(kFThreads) void khf_fwd(KfParams a) {
     for (int nb = 0; nb < G_::NB; ++nb)
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) acc[nb][cb] *= alpha;
-    kf_rows<R, RC>(acc, vs, c0, p);  // O^T += V^T P^T
+    kf_rows<R, RC, W>(acc, vs, c0, p);  // O^T += V^T P^T
   }
   const float l = wave_sum16x4(l_part);
   if (tok_ok) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    kf_store_rows<R, RC>(a.z + (int64_t)b * a.z_sb + (int64_t)ti * a.z_si + (int64_t)l16 * a.z_sh, c0, acc, inv);
+    kf_store_rows<R, RC, W>(a.z + (int64_t)b * a.z_sb + (int64_t)ti * a.z_si + (int64_t)l16 * a.z_sh, c0, acc, inv);
     if (g == 0 && c0 == 0)
       a.lse[((int64_t)b * 16 + l16) * a.Lq + ti] = l > 0.f ? (m_run + log2f(l)) * kLn2 : -INFINITY;
   }
 }
 
 // ---- dq: the forward's layout; per key tile S and dP, then dQ^T += K^T dS^T ------------------------------------
-template <int R, int RC>
-__global__ __launch_bounds__(kFThreads) void khf_dq(KfParams a) {
-  using G_ = KfGeo<R, RC>;
+template <int R, int RC, int W>
+__global__ __launch_bounds__(64 * W) void khf_dq(KfParams a) {
+  using G_ = KfGeo<R, RC, W>;
   constexpr int CS = G_::CS, TG = G_::G;
+  // width 1024: the V tile goes global -> LDS directly (the registers of a second staged tile do not fit)
+  constexpr bool DMA = R >= 1024;
   __shared__ __attribute__((aligned(16))) float ks[kFKeys * G_::RS];
   __shared__ __attribute__((aligned(16))) float vs[kFKeys * G_::RS];
-  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? 8 : 1][64];
-  __shared__ __attribute__((aligned(16))) floatx4 xd[CS > 1 ? 8 : 1][64];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? W : 1][64];
+  __shared__ __attribute__((aligned(16))) floatx4 xd[CS > 1 && !G_::ONE_X ? W : 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int tok = wave / CS, c0 = (wave % CS) * RC;
   const int b = blockIdx.y;
@@ -294,21 +332,32 @@ __global__ __launch_bounds__(kFThreads) void khf_dq(KfParams a) {
   floatx4 kr[G_::TL], vr[G_::TL];
   uint8_t m_next[4] = {1, 1, 1, 1}, m_cur[4];
   auto load = [&](int kt) {
-    kf_load<R, RC>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
-    kf_load<R, RC>(vr, [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
+    kf_load<R, RC, W>(kr, [&](int r) { return a.k + (int64_t)b * a.k_sb + (int64_t)min(kt + r, a.N - 1) * a.k_sn; });
+    if (!DMA)
+      kf_load<R, RC, W>(vr,
+                        [&](int r) { return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn; });
     kf_mask4(mrow, kt + 4 * g, a.N, m_next);
   };
   if (nkeys > 0) load(0);
   for (int kt = 0; kt < nkeys; kt += kFKeys) {
     __syncthreads();
-    kf_store<R, RC>(ks, kr);
-    kf_store<R, RC>(vs, vr);
+    kf_store<R, RC, W>(ks, kr);
+    if constexpr (DMA)  // the V tile, read first by the dP product after the score exchange
+      kf_copy_tile<R, RC, W>(kf_lds(vs), [&](int r) {
+        return a.v + (int64_t)b * a.v_sb + (int64_t)min(kt + r, a.N - 1) * a.v_sn;
+      });
+    else
+      kf_store<R, RC, W>(vs, vr);
 #pragma unroll
     for (int e = 0; e < 4; ++e) m_cur[e] = m_next[e];
     __syncthreads();
-    if (kt + kFKeys < nkeys) load(kt + kFKeys);
-    const floatx4 s = kf_exchange<CS>(kf_cols<R, RC>(ks, c0, qv), xs, wave, tok * CS);
-    const floatx4 dpv = kf_exchange<CS>(kf_cols<R, RC>(vs, c0, dzv), xd, wave, tok * CS);
+    if (!DMA && kt + kFKeys < nkeys) load(kt + kFKeys);
+    const floatx4 s_part = kf_cols<R, RC, W>(ks, c0, qv);
+    if (DMA) kf_wait_copies();  // this wave's V copies; the exchange's barrier then publishes every wave's
+    const floatx4 s = kf_exchange<CS>(s_part, xs, wave, tok * CS);
+    if (DMA && kt + kFKeys < nkeys) load(kt + kFKeys);
+    if (G_::ONE_X && CS > 1) __syncthreads();  // every wave has its sums before the buffer is reused
+    const floatx4 dpv = kf_exchange<CS>(kf_cols<R, RC, W>(vs, c0, dzv), G_::ONE_X ? xs : xd, wave, tok * CS);
     floatx4 ds;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -317,24 +366,27 @@ __global__ __launch_bounds__(kFThreads) void khf_dq(KfParams a) {
       const float p = vis ? fast_exp2(s[i] * a.scale_log2 - lse2) : 0.f;
       ds[i] = p * (dpv[i] - dd) * a.scale;
     }
-    kf_rows<R, RC>(acc, ks, c0, ds);  // dQ^T += K^T dS^T
+    kf_rows<R, RC, W>(acc, ks, c0, ds);  // dQ^T += K^T dS^T
   }
   if (tok_ok)
-    kf_store_rows<R, RC>(a.dq + (int64_t)b * a.dq_sb + (int64_t)ti * a.dq_si + (int64_t)l16 * a.dq_sh, c0, acc,
+    kf_store_rows<R, RC, W>(a.dq + (int64_t)b * a.dq_sb + (int64_t)ti * a.dq_si + (int64_t)l16 * a.dq_sh, c0, acc,
                          1.f);
 }
 
 // ---- dk / dv: one workgroup per (G blocks of 16 keys, batch row, token range); query tokens stream through LDS --
 // (their 16 head rows of q and dz), per token S = Q K^T and dP = dZ V^T (16 heads x 16 keys), then
 // dV^T += dZ^T P and dK^T += Q^T dS over the wave's columns.
-template <int R, int RC>
-__global__ __launch_bounds__(kFThreads) void khf_dkdv(KfParams a) {
-  using G_ = KfGeo<R, RC>;
+template <int R, int RC, int W>
+__global__ __launch_bounds__(64 * W) void khf_dkdv(KfParams a) {
+  using G_ = KfGeo<R, RC, W>;
   constexpr int CS = G_::CS, KBW = G_::G;
+  // widths 512 and 1024: the Q and dZ tiles go global -> LDS directly (their staging registers do not fit beside
+  // the resident K / V operands and dK / dV accumulators)
+  constexpr bool DMA = R >= 512;
   __shared__ __attribute__((aligned(16))) float qs[kFKeys * G_::RS];
   __shared__ __attribute__((aligned(16))) float zs[kFKeys * G_::RS];
-  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? 8 : 1][64];
-  __shared__ __attribute__((aligned(16))) floatx4 xd[CS > 1 ? 8 : 1][64];
+  __shared__ __attribute__((aligned(16))) floatx4 xs[CS > 1 ? W : 1][64];
+  __shared__ __attribute__((aligned(16))) floatx4 xd[CS > 1 && !G_::ONE_X ? W : 1][64];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, l16 = lane & 15, g = lane >> 4;
   const int kb = wave / CS, c0 = (wave % CS) * RC;
   const int b = blockIdx.y;
@@ -363,19 +415,24 @@ __global__ __launch_bounds__(kFThreads) void khf_dkdv(KfParams a) {
 #pragma unroll
     for (int cb = 0; cb < 4; ++cb) dk_acc[nb][cb] = dv_acc[nb][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // the next token of the range that sees any key of the block (its bound is above key0)
-  auto next_token = [&](int t) {
-    while (t < t_hi && a.bound[trow + t] <= key0) ++t;
-    return t;
+  // The range's tokens that see any key of the block (bound above key0), last to first: the workgroups of a batch
+  // row and range all start at the range's last token and step down together, so the token tiles they stream are
+  // read about once per XCD and served to the others from L2. prev_token(t) is the highest such token below t
+  // (t_lo - 1 if none), found 64 tokens per probe.
+  auto prev_token = [&](int t) {
+    while (t > t_lo) {
+      const int base = max(t_lo, t - 64);
+      const bool seen = base + lane < t && a.bound[trow + base + lane] > key0;
+      const uint64_t m = __ballot(seen);
+      if (m) return base + 63 - __clzll(m);
+      t = base;
+    }
+    return t_lo - 1;
   };
-  floatx4 qr[G_::TL], zr[G_::TL];
   float c_lse[4], c_dd[4], n_lse[4], n_dd[4];  // row constants of heads 4 g + i (current / next token)
   int c_bound = 0, n_bound = 0;
   uint8_t c_m = 1, n_m = 1;
-  auto load = [&](int t) {
-    kf_load<R, RC>(qr, [&](int r) { return a.q + (int64_t)b * a.q_sb + (int64_t)t * a.q_si + (int64_t)r * a.q_sh; });
-    kf_load<R, RC>(zr,
-                   [&](int r) { return a.dz + (int64_t)b * a.dz_sb + (int64_t)t * a.dz_si + (int64_t)r * a.dz_sh; });
+  auto load_consts = [&](int t) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t ridx = ((int64_t)b * 16 + 4 * g + i) * a.Lq + t;
@@ -387,12 +444,7 @@ __global__ __launch_bounds__(kFThreads) void khf_dkdv(KfParams a) {
     n_bound = min(a.bound[trow + t], a.N);
     n_m = a.mask ? a.mask[(int64_t)b * a.m_sb + (int64_t)t * a.m_si + kc] : (uint8_t)1;
   };
-  int t = next_token(t_lo);
-  if (t < t_hi) load(t);
-  while (t < t_hi) {
-    __syncthreads();
-    kf_store<R, RC>(qs, qr);
-    kf_store<R, RC>(zs, zr);
+  auto take_consts = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       c_lse[i] = n_lse[i];
@@ -400,27 +452,81 @@ __global__ __launch_bounds__(kFThreads) void khf_dkdv(KfParams a) {
     }
     c_bound = n_bound;
     c_m = n_m;
-    __syncthreads();
-    const int t_next = next_token(t + 1);
-    if (t_next < t_hi) load(t_next);
-    // S[head 4 g + i][key l16], dP likewise
-    const floatx4 s = kf_exchange<CS>(kf_cols<R, RC>(qs, c0, kv), xs, wave, kb * CS);
-    const floatx4 dpv = kf_exchange<CS>(kf_cols<R, RC>(zs, c0, vv), xd, wave, kb * CS);
+  };
+  const auto qrow = [&](int t) {
+    return [&, t](int r) { return a.q + (int64_t)b * a.q_sb + (int64_t)t * a.q_si + (int64_t)r * a.q_sh; };
+  };
+  const auto zrow = [&](int t) {
+    return [&, t](int r) { return a.dz + (int64_t)b * a.dz_sb + (int64_t)t * a.dz_si + (int64_t)r * a.dz_sh; };
+  };
+  // P and dS of the step from the score and dP sums (head 4 g + i, key l16)
+  auto p_ds = [&](const floatx4& s, const floatx4& dpv, floatx4& p, floatx4& ds) {
     const bool vis = key_ok && key < c_bound && c_m != 0;
-    floatx4 p, ds;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       p[i] = vis ? fast_exp2(s[i] * a.scale_log2 - c_lse[i]) : 0.f;
       ds[i] = p[i] * (dpv[i] - c_dd[i]) * a.scale;
     }
-    kf_rows<R, RC>(dv_acc, zs, c0, p);   // dV^T += dZ^T P
-    kf_rows<R, RC>(dk_acc, qs, c0, ds);  // dK^T += Q^T dS
-    t = t_next;
+  };
+  int t = prev_token(t_hi);
+  if constexpr (DMA) {
+    // width 1024: both tiles go global -> LDS directly. dZ(t) is copied while S is computed; Q(t) is last read by
+    // the dK product, which runs before dV, so Q of the next token is copied while dV is computed.
+    if (t >= t_lo) {
+      kf_copy_tile<R, RC, W>(kf_lds(qs), qrow(t));
+      load_consts(t);
+    }
+    while (t >= t_lo) {
+      kf_wait_copies();  // this wave's Q copies
+      __syncthreads();   // Q visible to every wave; every wave is done with the previous token's dZ tile
+      kf_copy_tile<R, RC, W>(kf_lds(zs), zrow(t));
+      take_consts();
+      const int t_next = prev_token(t);
+      if (t_next >= t_lo) load_consts(t_next);
+      const floatx4 s_part = kf_cols<R, RC, W>(qs, c0, kv);
+      kf_wait_copies();  // this wave's dZ copies; the exchange's barrier then publishes every wave's
+      const floatx4 s = kf_exchange<CS>(s_part, xs, wave, kb * CS);
+      if (G_::ONE_X && CS > 1) __syncthreads();
+      const floatx4 dpv = kf_exchange<CS>(kf_cols<R, RC, W>(zs, c0, vv), G_::ONE_X ? xs : xd, wave, kb * CS);
+      floatx4 p, ds;
+      p_ds(s, dpv, p, ds);
+      kf_rows<R, RC, W>(dk_acc, qs, c0, ds);  // dK^T += Q^T dS
+      __syncthreads();                         // every wave is done with the Q tile
+      if (t_next >= t_lo) kf_copy_tile<R, RC, W>(kf_lds(qs), qrow(t_next));
+      kf_rows<R, RC, W>(dv_acc, zs, c0, p);   // dV^T += dZ^T P
+      t = t_next;
+    }
+  } else {
+    floatx4 qr[G_::TL], zr[G_::TL];
+    auto load = [&](int t) {
+      kf_load<R, RC, W>(qr, qrow(t));
+      kf_load<R, RC, W>(zr, zrow(t));
+      load_consts(t);
+    };
+    if (t >= t_lo) load(t);
+    while (t >= t_lo) {
+      __syncthreads();
+      kf_store<R, RC, W>(qs, qr);
+      kf_store<R, RC, W>(zs, zr);
+      take_consts();
+      __syncthreads();
+      const int t_next = prev_token(t);
+      if (t_next >= t_lo) load(t_next);
+      // S[head 4 g + i][key l16], dP likewise
+      const floatx4 s = kf_exchange<CS>(kf_cols<R, RC, W>(qs, c0, kv), xs, wave, kb * CS);
+      if (G_::ONE_X && CS > 1) __syncthreads();  // every wave has its sums before the buffer is reused
+      const floatx4 dpv = kf_exchange<CS>(kf_cols<R, RC, W>(zs, c0, vv), G_::ONE_X ? xs : xd, wave, kb * CS);
+      floatx4 p, ds;
+      p_ds(s, dpv, p, ds);
+      kf_rows<R, RC, W>(dv_acc, zs, c0, p);   // dV^T += dZ^T P
+      kf_rows<R, RC, W>(dk_acc, qs, c0, ds);  // dK^T += Q^T dS
+      t = t_next;
+    }
   }
   if (key_ok) {
     const int64_t off = a.key_splits > 1 ? (int64_t)split * a.kv_ss : 0;
-    kf_store_rows<R, RC>(a.dv + off + (int64_t)b * a.dv_sb + (int64_t)key * a.dv_sn, c0, dv_acc, 1.f);
-    kf_store_rows<R, RC>(a.dk + off + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_sn, c0, dk_acc, 1.f);
+    kf_store_rows<R, RC, W>(a.dv + off + (int64_t)b * a.dv_sb + (int64_t)key * a.dv_sn, c0, dv_acc, 1.f);
+    kf_store_rows<R, RC, W>(a.dk + off + (int64_t)b * a.dk_sb + (int64_t)key * a.dk_sn, c0, dk_acc, 1.f);
   }
 }
 
@@ -476,10 +582,15 @@ int kf_check(const void* q, int64_t q_sb, int64_t q_si, int64_t q_sh, const void
 }
 
 // Columns per wave of each kernel and width (forward: 256 from width 256 up; dq and dk / dv: 128).
-#define HLA_KF_LAUNCH(KERNEL, R, RC, GRID, P, ST) hipLaunchKernelGGL((KERNEL<R, RC>), GRID, dim3(kFThreads), 0, ST, P)
+#define HLA_KF_LAUNCH(KERNEL, R, RC, W, GRID, P, ST) \
+  hipLaunchKernelGGL((KERNEL<R, RC, W>), GRID, dim3(64 * (W)), 0, ST, P)
 
-int kf_groups(int R, int RC) { return 8 / (R / RC); }
+int kf_groups(int R, int RC, int W) { return W / (R / RC); }
 int kf_fwd_rc(int R) { return R >= 256 ? 256 : 128; }
+// dq and dk / dv: 8 waves of 128 columns. (At width 1024 these spill: the next step's 128 KB tile in flight beside
+// the resident operands and accumulators exceeds two waves' registers per SIMD; 16 waves of 64 columns spill more.)
+int kf_bwd_rc(int) { return 128; }
+int kf_bwd_waves(int) { return 8; }
 
 }  // namespace
 }  // namespace hla
@@ -507,13 +618,13 @@ extern "C" int hla_s6_khop_forward_f32(const float* q, int64_t q_sb, int64_t q_s
   p.z = z; p.z_sb = z_sb; p.z_si = z_si; p.z_sh = z_sh;
   p.lse = lse;
   hipStream_t st = as_stream(stream);
-  const int rcw = kf_fwd_rc(width);
-  const dim3 grid((unsigned)((Lq + kf_groups(width, rcw) - 1) / kf_groups(width, rcw)), (unsigned)B);
+  const int rcw = kf_fwd_rc(width), tg = kf_groups(width, rcw, 8);
+  const dim3 grid((unsigned)((Lq + tg - 1) / tg), (unsigned)B);
   switch (width) {
-    case 128: HLA_KF_LAUNCH(khf_fwd, 128, 128, grid, p, st); break;
-    case 256: HLA_KF_LAUNCH(khf_fwd, 256, 256, grid, p, st); break;
-    case 512: HLA_KF_LAUNCH(khf_fwd, 512, 256, grid, p, st); break;
-    default: HLA_KF_LAUNCH(khf_fwd, 1024, 256, grid, p, st); break;
+    case 128: HLA_KF_LAUNCH(khf_fwd, 128, 128, 8, grid, p, st); break;
+    case 256: HLA_KF_LAUNCH(khf_fwd, 256, 256, 8, grid, p, st); break;
+    case 512: HLA_KF_LAUNCH(khf_fwd, 512, 256, 8, grid, p, st); break;
+    default: HLA_KF_LAUNCH(khf_fwd, 1024, 256, 8, grid, p, st); break;
   }
   return check_launch("khop_forward_f32");
 }
@@ -581,12 +692,13 @@ extern "C" int hla_s6_khop_backward_f32(const float* q, int64_t q_sb, int64_t q_
   }
   if (need_q && Lq > 0) {
     p.dq = dq; p.dq_sb = dq_sb; p.dq_si = dq_si; p.dq_sh = dq_sh;
-    const dim3 grid((unsigned)((Lq + kf_groups(width, 128) - 1) / kf_groups(width, 128)), (unsigned)B);
+    const int tg = kf_groups(width, kf_bwd_rc(width), kf_bwd_waves(width));
+    const dim3 grid((unsigned)((Lq + tg - 1) / tg), (unsigned)B);
     switch (width) {
-      case 128: HLA_KF_LAUNCH(khf_dq, 128, 128, grid, p, st); break;
-      case 256: HLA_KF_LAUNCH(khf_dq, 256, 128, grid, p, st); break;
-      case 512: HLA_KF_LAUNCH(khf_dq, 512, 128, grid, p, st); break;
-      default: HLA_KF_LAUNCH(khf_dq, 1024, 128, grid, p, st); break;
+      case 128: HLA_KF_LAUNCH(khf_dq, 128, 128, 8, grid, p, st); break;
+      case 256: HLA_KF_LAUNCH(khf_dq, 256, 128, 8, grid, p, st); break;
+      case 512: HLA_KF_LAUNCH(khf_dq, 512, 128, 8, grid, p, st); break;
+      default: HLA_KF_LAUNCH(khf_dq, 1024, 128, 8, grid, p, st); break;
     }
     if ((rc = check_launch("khop_dq_f32")) != HLA_S6_OK) return rc;
   }
@@ -599,13 +711,13 @@ extern "C" int hla_s6_khop_backward_f32(const float* q, int64_t q_sb, int64_t q_
     p.dk_sn = split ? width : dk_sn;
     p.dv_sb = split ? (int64_t)N * width : dv_sb;
     p.dv_sn = split ? width : dv_sn;
-    const int keys = 16 * kf_groups(width, 128);
+    const int keys = 16 * kf_groups(width, kf_bwd_rc(width), kf_bwd_waves(width));
     const dim3 grid((unsigned)((N + keys - 1) / keys), (unsigned)B, (unsigned)key_splits);
     switch (width) {
-      case 128: HLA_KF_LAUNCH(khf_dkdv, 128, 128, grid, p, st); break;
-      case 256: HLA_KF_LAUNCH(khf_dkdv, 256, 128, grid, p, st); break;
-      case 512: HLA_KF_LAUNCH(khf_dkdv, 512, 128, grid, p, st); break;
-      default: HLA_KF_LAUNCH(khf_dkdv, 1024, 128, grid, p, st); break;
+      case 128: HLA_KF_LAUNCH(khf_dkdv, 128, 128, 8, grid, p, st); break;
+      case 256: HLA_KF_LAUNCH(khf_dkdv, 256, 128, 8, grid, p, st); break;
+      case 512: HLA_KF_LAUNCH(khf_dkdv, 512, 128, 8, grid, p, st); break;
+      default: HLA_KF_LAUNCH(khf_dkdv, 1024, 128, 8, grid, p, st); break;
     }
     if ((rc = check_launch("khop_dkdv_f32")) != HLA_S6_OK) return rc;
     if (split) {
