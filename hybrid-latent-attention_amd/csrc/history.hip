@@ -1430,15 +1430,16 @@ __global__ __launch_bounds__(combine_threads<R>()) void history_combine(HistoryP
 }
 
 // ---- decode epilogue --------------------------------------------------------------------------------------------
-// out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for TB tokens of one head per workgroup (4, or
-// 1 for small steps so that the split reduction spreads over enough workgroups):
+// out[t, h, :] = merge(bf16(o_hist[t, h, :] @ B[h]), o_win[t, h, :]) for TB tokens of one head per workgroup of W
+// waves (4 tokens and 4 waves, or 1 token and 8 waves for small steps, so that the split reduction spreads over
+// enough workgroups and each round of loads covers enough slots):
 //   1. o_hist: LSE reduction of the split partials (or the direct bf16 output with one split), rounded to bf16 as the
 //      history op's output is, kept in LDS as bf16 pairs;
-//   2. the B_t product as a GEMV on bf16 pairs: wave q sums rows [q*R/4, (q+1)*R/4) of B[h]; lane (g, c) =
+//   2. the B_t product as a GEMV on bf16 pairs: wave q sums rows [q*R/W, (q+1)*R/W) of B[h]; lane (g, c) =
 //      (lane/16, lane%16) reads rows k = 8*step + 2g and k + 1, output columns [8c, 8c+8) (16-byte loads: a wave
 //      instruction covers 4 whole B rows), pairs the two rows' values of each column (v_perm_b32) and accumulates
-//      TB x 8 outputs with v_dot2_f32_bf16 against (o[k], o[k+1]) (exact bf16 products, fp32 sums); the 16 partials
-//      of each output (4 waves x 4 lane groups) are summed in LDS;
+//      TB x 8 outputs with v_dot2_f32_bf16 against (o[k], o[k+1]) (exact bf16 products, fp32 sums); the 4 W partials
+//      of each output (W waves x 4 lane groups) are summed in LDS in a fixed order;
 //   3. the merge_states LSE merge with the window partial (invalid rows zeroed), rounded once to bf16. The window
 //      partial of a thread's merge item is loaded at the start, with the split partials.
 
@@ -1461,19 +1462,21 @@ struct EpilogueParams {
 template <int TB>
 constexpr int kEpiSlots = TB == 1 ? kMaxSplits : 256;
 
-template <int R, int TB>
-__global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
+template <int R, int TB, int W>
+__global__ __launch_bounds__(64 * W) void decode_epilogue(EpilogueParams a) {
+  constexpr int kThreads = 64 * W;  // W waves (shadows the file's 4-wave default)
   constexpr int D = kExactDim, C4 = R / 4;
   constexpr int ITEMS = TB * C4;                               // combine items (token, 4 columns)
   constexpr int IPT = ITEMS > kThreads ? ITEMS / kThreads : 1;  // items per thread
   constexpr int SG = ITEMS < kThreads ? kThreads / ITEMS : 1;   // slot groups: threads sharing one item's slots
-  constexpr int NB = R / 32;                                   // GEMV steps: two B rows per lane each
+  constexpr int RW = R / W;                                    // B rows per wave in the GEMV
+  constexpr int NB = RW / 8;                                   // GEMV steps: two B rows per lane each
   constexpr int PB = NB <= 16 ? NB : 0;                        // steps whose rows are prefetched into registers
   static_assert(ITEMS % kThreads == 0 || kThreads % ITEMS == 0, "items must tile the workgroup");
   static_assert(TB * D / 2 <= kThreads, "one merge item per thread");
   __shared__ uint32_t o_s[TB][R / 2];  // bf16 pairs
   __shared__ float lse_s[TB];
-  __shared__ floatx4 part[16][TB][D / 4];
+  __shared__ floatx4 part[4 * W][TB][D / 4];
   __shared__ float slot_lse[TB][kEpiSlots<TB>];  // lse of every slot of the TB tokens for head h
   __shared__ int used_s[TB];
   __shared__ float merge_m[SG > 1 ? SG : 1][SG > 1 ? ITEMS : 1], merge_d[SG > 1 ? SG : 1][SG > 1 ? ITEMS : 1];
@@ -1482,7 +1485,7 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
   const int S = a.S;
   const int q = tid >> 6, lane = tid & 63, g = lane >> 4, c = lane & 15;
   u32x4 bv[PB > 0 ? PB : 1][2];
-  const uint16_t* brow = a.B + (int64_t)h * a.b_sh + (int64_t)(q * (R / 4) + 2 * g) * a.b_sr + 8 * c;
+  const uint16_t* brow = a.B + (int64_t)h * a.b_sh + (int64_t)(q * RW + 2 * g) * a.b_sr + 8 * c;
   // the window partial of this thread's merge item (token t0 + tid / 64, columns 2 * (tid % 64) and + 1)
   const int m_tb = tid / (D / 2), m_dp = tid % (D / 2), m_t = t0 + m_tb;
   const bool m_live = tid < TB * D / 2 && m_t < a.T;
@@ -1673,7 +1676,7 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
         bp[2 * e] = __builtin_amdgcn_perm(b1[e], b0[e], 0x05040100u);
         bp[2 * e + 1] = __builtin_amdgcn_perm(b1[e], b0[e], 0x07060302u);
       }
-      const int k2 = (q * (R / 4) + 8 * step + 2 * g) / 2;
+      const int k2 = (q * RW + 8 * step + 2 * g) / 2;
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
         const bf16x2_t o = __builtin_bit_cast(bf16x2_t, o_s[tb][k2]);
@@ -1696,7 +1699,7 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
     float y0 = 0.f, y1 = 0.f;
     const float* pf = reinterpret_cast<const float*>(&part[0][tb][0]) + 2 * dp;
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
+    for (int p = 0; p < 4 * W; ++p) {
       y0 += pf[p * TB * D];
       y1 += pf[p * TB * D + 1];
     }
@@ -1722,10 +1725,16 @@ __global__ __launch_bounds__(kThreads) void decode_epilogue(EpilogueParams a) {
 
 template <int R>
 int launch_epilogue(const EpilogueParams& e, hipStream_t stream) {
-  if (e.T < 64 || e.S > kEpiSlots<4>)  // small steps: one token per workgroup, 16*T workgroups for the reduction
-    hipLaunchKernelGGL((decode_epilogue<R, 1>), dim3((unsigned)e.T, kHeads), dim3(kThreads), 0, stream, e);
+  // small steps: one token per workgroup, 16*T workgroups for the reduction; with at most 8 tokens (128 or fewer
+  // workgroups, fewer than the CUs) 8 waves each, twice the slots per round of loads and half the B rows per wave
+  // (B=8 at context 32768: 393.1 -> 389.6 us/layer; B=1: 41.5 -> 39.3 us per call; at 12 and 32 tokens, where two
+  // 8-wave workgroups no longer fit a CU beside each other, slower: 183.3 -> 185.4 and 295.1 -> 316.5 us/layer)
+  if ((e.T < 64 || e.S > kEpiSlots<4>) && e.T <= 8)
+    hipLaunchKernelGGL((decode_epilogue<R, 1, 8>), dim3((unsigned)e.T, kHeads), dim3(512), 0, stream, e);
+  else if (e.T < 64 || e.S > kEpiSlots<4>)
+    hipLaunchKernelGGL((decode_epilogue<R, 1, 4>), dim3((unsigned)e.T, kHeads), dim3(256), 0, stream, e);
   else
-    hipLaunchKernelGGL((decode_epilogue<R, 4>), dim3((unsigned)((e.T + 3) / 4), kHeads), dim3(kThreads), 0, stream, e);
+    hipLaunchKernelGGL((decode_epilogue<R, 4, 4>), dim3((unsigned)((e.T + 3) / 4), kHeads), dim3(256), 0, stream, e);
   return check_launch("decode_epilogue");
 }
 
