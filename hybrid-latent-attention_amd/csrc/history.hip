@@ -130,9 +130,12 @@ __device__ __forceinline__ int used_slots(int32_t ctx, int64_t cap, int chunk) {
   return (row_tiles(ctx, cap) + chunk - 1) / chunk;
 }
 
-// The plan's chunk. With `fill` (the multi-token kernels, launched on a grid of one workgroup per (token group,
-// slot) whether the slot has work or not) it is ceil(max_tiles / S) instead: the longest row fills all S slots.
-// Must be called by every thread of the block (a multiple of 64 threads); `red` holds 2 * waves int64.
+// The plan's chunk. Without `fill`, the formula's chunk grows until the step has at most T*S/2 items: the tails of
+// ragged rows add up to T more, and the items past T*S/2 (the split counts aim it at two workgroups per CU) would
+// give some CUs a third item, on which the whole call waits. With `fill` (the multi-token kernels, launched on a
+// grid of one workgroup per (token group, slot) whether the slot has work or not) it is ceil(max_tiles / S)
+// instead: the longest row fills all S slots. Must be called by every thread of the block (a multiple of 64
+// threads); `red` holds 2 * waves int64.
 __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_t* red, bool fill = false) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
   int mx = 0;
@@ -158,7 +161,21 @@ __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_
     sum += red[2 * w + 1];
   }
   const int64_t slots = (int64_t)T * S;
-  return (int)max((int64_t)1, fill ? (m + S - 1) / S : max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
+  int c = (int)max((int64_t)1, fill ? (m + S - 1) / S : max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
+  if (fill) return c;
+  for (const int64_t target = slots / 2; c < m; ++c) {  // c and the sums are uniform over the block
+    int64_t items = 0;
+    for (int i = tid; i < T; i += blockDim.x) items += (row_tiles(ctx[i], cap) + c - 1) / c;
+    for (int off = 32; off > 0; off >>= 1) items += __shfl_xor(items, off);
+    __syncthreads();  // every thread has read red
+    if (lane == 0) red[wave] = items;
+    __syncthreads();
+    items = 0;
+    for (int w = 0; w < waves; ++w) items += red[w];
+    if (items <= target) break;
+  }
+  __syncthreads();  // red may be reused by the caller
+  return c;
 }
 
 // Workgroups of the split kernel: the plan puts at most T*S/2 + T (row, chunk) items in the list; a multiple of 8

@@ -291,6 +291,46 @@ def test_grouped_history_page_geometry(ops, width, block, long_ctx, splits):
     check(host_f32(o), host_f32(lse), *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
 
 
+@pytest.mark.parametrize('splits', [1, 5])
+def test_grouped_history_scores_that_outgrow_the_first_tile(ops, splits):
+    """Rows whose scores rise far above their first tile's (the online softmax raises its maximum and rescales the
+    accumulators many times): requests 0 and 2 of the 512-wide multi-query kernel have keys from position 100 on
+    scaled by 5 (their row maxima rise by 2^40 and more over the first 32 keys'), 1 and 3 do not; the first
+    workgroup holds two passes (requests 0 and 1). Against the oracle and the one-token-per-workgroup kernel."""
+    width, block, num_blocks = 512, 16, 400
+    rng = np.random.default_rng(512 + splits)
+    lens = [3, 6, 7, 5]
+    req = np.repeat(np.arange(len(lens)), lens)
+    ctx = np.concatenate([np.full(3, 600), 500 - 7 * np.arange(6), 640 + np.arange(7), np.full(5, 90)])
+    ctx = ctx.astype(np.int32)
+    per_req = np.array([ctx[req == r].max() for r in range(len(lens))])
+    table = token_tables(rng, per_req, block, num_blocks, -(-700 // block), distinct=True)
+    cache = bf16.to_f32(latent_cache_bits(rng, num_blocks, block, width))
+    for r in (0, 2):
+        for pos in range(100, int(per_req[r])):
+            cache[table[r, pos // block], 0, pos % block, :width] *= 5
+    cache_bits = bf16.from_f32(cache)
+    q_bits = random_bits(rng, (len(ctx), 16, width))
+    kf, qf = bf16.to_f32(cache_bits)[:, 0, :, :width], bf16.to_f32(q_bits)
+    growth = []  # per token: the largest rise of a row's maximum (log2 units) over its first 32 keys' maximum
+    for t, n in enumerate(ctx):
+        pos = np.arange(n)
+        sc = qf[t] @ kf[table[req[t], pos // block], pos % block].T * (SCALE * math.log2(math.e))
+        growth.append((sc.max(-1) - sc[:, :32].max(-1)).max())
+    growth = np.array(growth)
+    assert (growth[req == 0] > 24).all() and (growth[req == 1] < 24).all()
+    q, dcache = dev_bf16(q_bits), dev_bf16(cache_bits)
+    ws = ops.S6Workspace(16, width, len(ctx) * splits)
+    o, lse = ops.history_attention_kv(q, dcache[..., :width], dcache[..., width:], dev_i32(table), dev_i32(ctx),
+                                      SCALE, splits, ws, None, None, 'hip', bt_rows=dev_i64(req), tokens_per_group=4,
+                                      shared_rows=True)
+    o, lse = host_f32(o), host_f32(lse)
+    check(o, lse, *oracle_history(q_bits, cache_bits, table[req], ctx), ctx)
+    o1, lse1 = run_history(ops, q_bits, cache_bits, table, ctx, splits, bt_rows=req)
+    assert_attention_close(o, o1, 'grouped vs one token per workgroup')
+    assert_lse_close(lse, lse1)
+
+
 def test_grouped_history_width_256_both_wave_forms(ops):
     """At width 256 the multi-query kernel takes two tokens per wave when its grid has more workgroups than the
     device has CUs, else one: a step of 8 x (CUs + 8) tokens (the first form) and its first request's 16 tokens

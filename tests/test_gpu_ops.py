@@ -336,11 +336,14 @@ def test_merge_lse(ops):
 
 def _plan_restated(ctx, cap, S, qsl=None):
     """The split plan's documented formula in plain Python (an independent restatement for the integer check): the
-    (row, chunk) items in row order, except that the rows of a request of 2..16 tokens with equal slot counts list
-    theirs chunk-major (chunk 0 of every row, then chunk 1, ...)."""
+    chunk is the smallest one at or above max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S))) that leaves at
+    most T*S/2 items (or max_tiles); the (row, chunk) items in row order, except that the rows of a request of 2..16
+    tokens with equal slot counts list theirs chunk-major (chunk 0 of every row, then chunk 1, ...)."""
     tiles = [-(-min(int(c), cap) // 16) for c in ctx]
     T = len(ctx)
     chunk = max(1, -(-max(tiles) // S), -(-2 * sum(tiles) // (T * S)))
+    while chunk < max(tiles) and sum(-(-t // chunk) for t in tiles) > T * S // 2:
+        chunk += 1
     used = [-(-t // chunk) for t in tiles]
     ni = T if S == 1 else -(-T * ((S + 1) // 2 + 1) // 8) * 8
     groups, r = [], 0                                        # runs of rows listed together
@@ -397,6 +400,7 @@ def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped):
     assert max(used) <= S                                  # every row fits its slots
     tiles = [-(-min(int(c), cap) // 16) for c in ctx]
     assert all(u * chunk >= t > (u - 1) * chunk for u, t in zip(used, tiles) if t)
+    assert sum(used) <= T * S // 2 or chunk == max(tiles)  # at most two items per CU at the policy's counts
 
 
 def test_split_plan_rejects_a_short_buffer(ops):
