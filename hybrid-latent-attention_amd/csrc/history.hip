@@ -110,7 +110,7 @@ struct Geo {
   static constexpr int VC = QW / 32;        // 16-byte V chunks per lane per tile
   static constexpr int NT = QW / 16;        // 16-column O^T tiles per wave
   static constexpr int CPR = QW / 8;        // 16-byte chunks per V row (wave's columns)
-  static constexpr int VS = QW + 8;         // LDS row stride of the K copy, in bf16 (conflict-free row reads)
+  static constexpr int VS = QW + 16;        // LDS row stride of the K copy, in bf16 (16-byte row reads: +8 conflicts)
   static constexpr int VSV = QW + 16;      // of the V copy (conflict-free transposed reads)
   static constexpr int VBUF = kTile * VSV;  // one wave buffer, in bf16
 };

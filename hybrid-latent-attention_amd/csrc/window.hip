@@ -98,7 +98,7 @@ struct ChunkParams {
 };
 
 constexpr int kChunkVS = kExactDim + 16;    // LDS row stride of the V tile (conflict-free transposed reads)
-constexpr int kChunkKS = kExactDim + 8;     // LDS row stride of the K tile (conflict-free 16-byte row reads)
+constexpr int kChunkKS = kExactDim + 16;    // LDS row stride of the K tile (16-byte row reads: +8 conflicts, +16 not)
 // Waves per workgroup, 16 queries each: 4 (the tiles shared by 64 queries), or 1 for steps of short requests whose
 // grid of 64-token blocks leaves CUs idle (such a block would run several requests' passes one after another on one
 // CU; 16-token blocks spread them).
