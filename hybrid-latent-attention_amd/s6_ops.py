@@ -150,24 +150,27 @@ def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_bloc
     return max(1, min(max(by_length, by_occupancy), 2 * sm_count, -(-max_seq_len // 32)))
 
 
-def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per_cu=8, min_keys_per_split=256,
-                     tokens_per_group=1):
+def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per_cu=8, min_keys_per_split=128,
+                     tokens_per_group=1, min_keys_per_group_split=256):
     """Split slots per row of the history kernel on MI355X for a ``width``-wide latent. The kernel runs one wave per
     128 latent columns, so a split is a workgroup of ``width / 128`` waves; about ``waves_per_cu`` resident waves per
     compute unit (8 keeps enough loads in flight to stream HBM on gfx950) make ``W = waves_per_cu * CUs / (width /
     128)`` busy workgroups. The kernel cuts every row in chunks sized so that about half of the ``num_tokens *
     slots`` workgroups get equal work whatever the row lengths (short rows use few slots, long rows many), so this
     returns ``2 * ceil(W / num_tokens)`` slots, never more than two per ``min_keys_per_split`` keys of the longest
-    row (so that filled slots hold at least that many keys) nor 1024. A function of constants and the row count only
+    row (so that filled slots hold at least that many keys, 8 tiles of 16) nor 1024. Few-token steps on short rows
+    are bound by that cap: their history time is the chain of one workgroup's tiles, so shorter chunks (more slots)
+    shorten it until the epilogue's partial reads grow faster. A function of constants and the row count only
     (graph-stable).
 
     Multi-query steps (``tokens_per_group`` 4) run one workgroup of eight tokens per (token group, slot), and every
     slot of the longest row holds work: ``ceil(2 * CUs / groups)`` slots for ``groups`` four-token groups make one
-    busy workgroup per CU (8 waves at width 512, 4 at 256), never more than one per ``min_keys_per_split`` keys of
-    the longest row, at least 1 (with 512-token chunks of four requests, one slot: no split reduction at all)."""
+    busy workgroup per CU (8 waves at width 512, 4 at 256), never more than one per ``min_keys_per_group_split``
+    keys of the longest row, at least 1 (with 512-token chunks of four requests, one slot: no split reduction at
+    all)."""
     if tokens_per_group > 1:
         groups = -(-max(1, num_tokens) // tokens_per_group)
-        by_length = max(1, -(-max_seq_len // min_keys_per_split))
+        by_length = max(1, -(-max_seq_len // min_keys_per_group_split))
         return max(1, min(-(-2 * cu_count // groups), by_length, 1024))
     waves_per_split = max(1, width // 128)
     busy = -(-waves_per_cu * cu_count // waves_per_split)

@@ -101,9 +101,12 @@ def test_mi355x_split_policy(ops):
     assert ops.mi355x_kv_splits(8192, 32, 256, width=512) == 32
     assert ops.mi355x_kv_splits(32768, 8, 256, width=512) == 128
     assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 64
-    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 64         # capped by 256-key filled slots
+    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 128        # capped by 128-key filled slots
+    assert ops.mi355x_kv_splits(1025, 1, 256, width=512) == 18
+    assert ops.mi355x_kv_splits(8227, 12, 256, width=512) == 86        # 4 x 3-token chunks: by occupancy
+    assert ops.mi355x_kv_splits(8227, 12, 256, width=256) == 130       # and by length
     assert ops.mi355x_kv_splits(32769, 8, 256, width=256) == 256
-    assert ops.mi355x_kv_splits(300, 1, 256) == 4
+    assert ops.mi355x_kv_splits(300, 1, 256) == 6
     assert ops.mi355x_kv_splits(1, 4096, 256) == 2
     # multi-query steps: one busy 8-token workgroup per CU, every slot filled, at least 256 keys per slot
     assert ops.mi355x_kv_splits(8704, 2048, 256, tokens_per_group=4) == 1
