@@ -119,8 +119,16 @@ struct Geo {
 // chunks of `chunk` 16-row tiles; the grid has S slots per row, and
 //   chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S)))
 // keeps every row within its S slots while about T*S/2 slots get work however ragged the rows are (short rows take
-// few slots, long rows many, each holding equal work). Slot s of a row holds tiles [s*chunk, (s+1)*chunk); slots past
-// ceil(tiles / chunk) are empty.
+// few slots, long rows many, each holding equal work), and it is at least kMinChunk tiles (kMinChunkSmall in steps
+// of fewer than kSmallStepTiles tiles over all rows), or the longest row. Slot s of a row holds tiles
+// [s*chunk, (s+1)*chunk); slots past ceil(tiles / chunk) are empty.
+//
+// The floor: an item's time is a chain of dependent tile steps, its partial costs 16 * (R + 1) fp32 writes and as
+// many epilogue reads (as many bytes as a 16-row tile of K and V); a step of many tiles streams, where 8-tile items
+// keep that overhead small, and a step of few tiles is latency-bound, where 4-tile items shorten the chain more than
+// their partials cost (4-tile items were faster at 256 and 504 tiles per step, 8-tile ones at 1016 and more).
+constexpr int kMinChunk = 8, kMinChunkSmall = 4;
+constexpr int64_t kSmallStepTiles = 768;
 __device__ __forceinline__ int row_tiles(int32_t ctx, int64_t cap) {
   return (int)((min((int64_t)ctx, cap) + kTile - 1) / kTile);
 }
@@ -163,6 +171,7 @@ __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_
   const int64_t slots = (int64_t)T * S;
   int c = (int)max((int64_t)1, fill ? (m + S - 1) / S : max((m + S - 1) / S, (2 * sum + slots - 1) / slots));
   if (fill) return c;
+  c = max(c, (int)min(m, (int64_t)(sum < kSmallStepTiles ? kMinChunkSmall : kMinChunk)));
   for (const int64_t target = slots / 2; c < m; ++c) {  // c and the sums are uniform over the block
     int64_t items = 0;
     for (int i = tid; i < T; i += blockDim.x) items += (row_tiles(ctx[i], cap) + c - 1) / c;

@@ -306,7 +306,7 @@ class _History(torch.autograd.Function):
         bound = torch.empty(B, dtype=torch.int32, device=dev)
         st = _lib.stream(dev)
         _lib.call('hla_s6_khop_bounds', _lib.ptr(m8), m8.stride(0), N, B, 1, N, _lib.ptr(bound), st)
-        splits = s6_ops.mi355x_kv_splits(N, B, _lib.device_cus(dev.index or 0), width=R)
+        splits = s6_ops.mi355x_kv_splits(N, B, _lib.device_cus(dev.index or 0), width=R, min_keys_per_split=256)
         ws = torch.empty(B * splits * H * (R + 1), dtype=torch.float32, device=dev) if splits > 1 else None
         z = torch.empty(B, H, R, dtype=torch.bfloat16, device=dev)
         lse = torch.empty(B, H, dtype=torch.float32, device=dev)

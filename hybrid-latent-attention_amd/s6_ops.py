@@ -151,17 +151,18 @@ def num_kv_splits(max_seq_len, num_tokens, split_max_tokens, sm_count, head_bloc
 
 
 def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per_cu=8, min_keys_per_split=128,
-                     tokens_per_group=1, min_keys_per_group_split=256):
+                     tokens_per_group=1, min_keys_per_group_split=256, small_step_tiles=768):
     """Split slots per row of the history kernel on MI355X for a ``width``-wide latent. The kernel runs one wave per
     128 latent columns, so a split is a workgroup of ``width / 128`` waves; about ``waves_per_cu`` resident waves per
     compute unit (8 keeps enough loads in flight to stream HBM on gfx950) make ``W = waves_per_cu * CUs / (width /
     128)`` busy workgroups. The kernel cuts every row in chunks sized so that about half of the ``num_tokens *
     slots`` workgroups get equal work whatever the row lengths (short rows use few slots, long rows many), so this
     returns ``2 * ceil(W / num_tokens)`` slots, never more than two per ``min_keys_per_split`` keys of the longest
-    row (so that filled slots hold at least that many keys, 8 tiles of 16) nor 1024. Few-token steps on short rows
-    are bound by that cap: their history time is the chain of one workgroup's tiles, so shorter chunks (more slots)
-    shorten it until the epilogue's partial reads grow faster. A function of constants and the row count only
-    (graph-stable).
+    row nor 1024. The kernel's plan gives every item at least 8 tiles of 16 keys (128 keys), or 4 tiles in a step
+    of fewer than ``small_step_tiles`` tiles over all rows, where the history is latency-bound and shorter chains
+    pay; a step that is that small even at the longest length (``num_tokens * ceil(max_seq_len / 16)`` below it)
+    gets two slots per ``min_keys_per_split / 2`` keys, room for those 4-tile items. A function of constants and
+    the row count only (graph-stable).
 
     Multi-query steps (``tokens_per_group`` 4) run one workgroup of eight tokens per (token group, slot), and every
     slot of the longest row holds work: ``ceil(2 * CUs / groups)`` slots for ``groups`` four-token groups make one
@@ -175,7 +176,9 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per
     waves_per_split = max(1, width // 128)
     busy = -(-waves_per_cu * cu_count // waves_per_split)
     by_occupancy = 2 * -(-busy // max(1, num_tokens))
-    by_length = max(1, 2 * -(-max_seq_len // min_keys_per_split))
+    small = max(1, num_tokens) * -(-max_seq_len // 16) < small_step_tiles
+    keys = max(1, min_keys_per_split // 2) if small else min_keys_per_split
+    by_length = max(1, 2 * -(-max_seq_len // keys))
     return max(1, min(by_occupancy, by_length, 1024))
 
 

@@ -218,8 +218,9 @@ int hla_s6_merge_states(const void *o_a, int64_t a_st, int64_t a_sh, const float
 
 /* ---- split plan of a step (no reference counterpart: scheduling metadata of the split-KV kernels) -------
  * The history kernels cut every row of a step in chunks of `chunk` 16-row tiles, one chunk per slot (num_splits
- * slots per row), chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S))) with tiles = ceil(min(ctx[t],
- * cap) / 16), grown one tile at a time until the step has at most T * S / 2 chunks with work (or chunk = max_tiles),
+ * slots per row), chunk = max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S)), min(max_tiles, floor)) with
+ * tiles = ceil(min(ctx[t], cap) / 16) and floor = 4 when total_tiles < 768, else 8, grown one tile at a time until
+ * the step has at most T * S / 2 chunks with work (or chunk = max_tiles),
  * and give the chunks to workgroups as one balanced list. hla_s6_split_plan computes that list once
  * per step (one small launch) into `plan` (int32, hla_s6_split_plan_ints(T, S) entries; caller-owned) so that every
  * fused decode call of the step reads it instead of deriving it per workgroup. It depends only on ctx, cap, S and

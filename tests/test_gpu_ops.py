@@ -336,12 +336,14 @@ def test_merge_lse(ops):
 
 def _plan_restated(ctx, cap, S, qsl=None):
     """The split plan's documented formula in plain Python (an independent restatement for the integer check): the
-    chunk is the smallest one at or above max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S))) that leaves at
-    most T*S/2 items (or max_tiles); the (row, chunk) items in row order, except that the rows of a request of 2..16
+    chunk is the smallest one at or above max(ceil(max_tiles / S), ceil(2 * total_tiles / (T * S)), floor) that
+    leaves at most T*S/2 items (or max_tiles), the floor 4 tiles below 768 tiles per step and 8 above (or
+    max_tiles); the (row, chunk) items in row order, except that the rows of a request of 2..16
     tokens with equal slot counts list theirs chunk-major (chunk 0 of every row, then chunk 1, ...)."""
     tiles = [-(-min(int(c), cap) // 16) for c in ctx]
     T = len(ctx)
     chunk = max(1, -(-max(tiles) // S), -(-2 * sum(tiles) // (T * S)))
+    chunk = max(chunk, min(max(tiles), 4 if sum(tiles) < 768 else 8))   # the floor: 4 tiles in small steps, else 8
     while chunk < max(tiles) and sum(-(-t // chunk) for t in tiles) > T * S // 2:
         chunk += 1
     used = [-(-t // chunk) for t in tiles]
@@ -368,11 +370,15 @@ def _plan_restated(ctx, cap, S, qsl=None):
     return chunk, used, rows, slots
 
 
-@pytest.mark.parametrize('T,S,grouped', [(1, 2, False), (5, 7, False), (64, 16, False), (300, 32, False),
-                                         (8, 1024, False), (700, 3, False), (60, 66, True), (300, 32, True)])
-def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped):
+@pytest.mark.parametrize('T,S,grouped,hi', [(1, 2, False, 20000), (5, 7, False, 20000), (64, 16, False, 20000),
+                                            (300, 32, False, 20000), (8, 1024, False, 20000), (700, 3, False, 20000),
+                                            (60, 66, True, 20000), (300, 32, True, 20000),
+                                            # few-tile steps: the 4-tile floor (below 768 tiles) and the 8-tile one
+                                            (3, 34, False, 1100), (2, 66, False, 2200), (4, 130, False, 4400),
+                                            (8, 128, False, 4400)])
+def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped, hi):
     rng = np.random.default_rng(T * 1000 + S)
-    ctx = rng.integers(0, 20000, T).astype(np.int32)
+    ctx = rng.integers(hi // 2 if hi < 20000 else 0, hi, T).astype(np.int32)
     ctx[::7] = 0                                            # rows without history
     qsl = None
     if grouped:   # requests of 1..20 tokens, most with one length per request (short chunks), two padding rows

@@ -101,12 +101,18 @@ def test_mi355x_split_policy(ops):
     assert ops.mi355x_kv_splits(8192, 32, 256, width=512) == 32
     assert ops.mi355x_kv_splits(32768, 8, 256, width=512) == 128
     assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 64
-    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 128        # capped by 128-key filled slots
-    assert ops.mi355x_kv_splits(1025, 1, 256, width=512) == 18
+    assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 256        # 512 tiles: 64-key slots
+    assert ops.mi355x_kv_splits(8192, 2, 256, width=512) == 128        # 1024 tiles: 128-key slots
     assert ops.mi355x_kv_splits(8227, 12, 256, width=512) == 86        # 4 x 3-token chunks: by occupancy
     assert ops.mi355x_kv_splits(8227, 12, 256, width=256) == 130       # and by length
+    assert ops.mi355x_kv_splits(4097, 4, 256, width=512) == 66         # 1028 tiles at the longest length
+    # steps below 768 tiles even at the longest length: room for the plan's 4-tile items (64 keys per slot)
+    assert ops.mi355x_kv_splits(1025, 1, 256, width=512) == 34
+    assert ops.mi355x_kv_splits(2049, 2, 256, width=512) == 66
+    assert ops.mi355x_kv_splits(2049, 4, 256, width=512) == 66
+    assert ops.mi355x_kv_splits(4097, 1, 256, width=512) == 130
     assert ops.mi355x_kv_splits(32769, 8, 256, width=256) == 256
-    assert ops.mi355x_kv_splits(300, 1, 256) == 6
+    assert ops.mi355x_kv_splits(300, 1, 256) == 10
     assert ops.mi355x_kv_splits(1, 4096, 256) == 2
     # multi-query steps: one busy 8-token workgroup per CU, every slot filled, at least 256 keys per slot
     assert ops.mi355x_kv_splits(8704, 2048, 256, tokens_per_group=4) == 1
