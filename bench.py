@@ -64,6 +64,8 @@ def parse():
     p.add_argument('--splits', type=int, default=0,
                    help='KV splits of every latent width (0: the reference count, which StepContext turns into the '
                         'MI355X count per width)')
+    p.add_argument('--max-model-len', type=int, default=0,
+                   help="the adapter's max_model_len, which sizes the split counts (0: the step's longest sequence)")
     p.add_argument('--kernel-only', action='store_true', help='only launch the history op (profiling)')
     p.add_argument('--width', type=int, default=512, choices=(256, 512, 1024),
                    help='latent width of --kernel-only (256 / 512) and --workload khop / rows (1024: forward only)')
@@ -97,11 +99,11 @@ class Workload:
     page); each width's table is a slice of one random permutation of its pool. The step is driven as the
     reference adapter drives it (``hla/vllm_latent/ouro_latent.py:203-212,257-265``): one ``num_kv_splits`` count
     for the step from the reference formula, the workspace the adapter allocates, ``max_seqlen_k`` = the model
-    length (here the step's longest sequence); ``StepContext`` picks each width's count itself. ``splits_override``
-    instead fixes every width's count (``kv_splits_by_width``)."""
+    length (``max_model_len``, by default the step's longest sequence); ``StepContext`` picks each width's count
+    itself. ``splits_override`` instead fixes every width's count (``kv_splits_by_width``)."""
 
     def __init__(self, ops, layer, hist, queries, seed, device, cus, table='random', layers=LAYERS, lat_pool=0,
-                 splits_override=0, loops=tuple(range(LOOPS))):
+                 splits_override=0, loops=tuple(range(LOOPS)), max_model_len=0):
         g = torch.Generator(device=device).manual_seed(seed)
         hist = [int(h) for h in hist]
         B, Q = len(hist), int(queries)
@@ -150,7 +152,7 @@ class Workload:
         self.qsl = (torch.arange(B + 1, dtype=torch.int32, device=device) * Q).contiguous()
         self.seq_lens = torch.tensor(self.seq, dtype=torch.int32, device=device)
         self.ops, self.layer = ops, layer
-        self.max_model_len = max(self.seq)
+        self.max_model_len = max(int(max_model_len), max(self.seq))
         if splits_override:
             self.by_width = {RANK: int(splits_override), RANK1: int(splits_override)}
             self.ref_splits = int(splits_override)
@@ -371,7 +373,8 @@ def secondary_metrics(name, kind, wl, B, context, queries, steps, warmup):
     return {'workload': name, 'value': round(us_layer, 2), 'unit': f'us/{per}', 'B': B, 'queries': queries,
             'context': context, 'contexts': wl.hist if kind == 'ragged' else None, 'layers': wl.layers,
             'loops': len(wl.loops), 'latent_pool_pages': wl.pool, 'kv_splits': wl.splits,
-            'reference_kv_splits': wl.ref_splits, 'steps': steps, 'ms_per_step': round(ms, 4),
+            'reference_kv_splits': wl.ref_splits, 'max_model_len': wl.max_model_len, 'steps': steps,
+            'ms_per_step': round(ms, 4),
             'setup_us_per_step': round(setup_ms * 1000, 2),
             'history_bytes_per_layer': hist_bytes, 'history_gbps': round(gbps, 1),
             'hbm_frac': round(gbps / PEAK_HBM_GBPS, 4), 'history_flops_per_layer': flops,
@@ -403,12 +406,12 @@ def workload_shape(kind, B, context, seed):
 
 
 def build_workload(ops, layer, kind, B, context, layers, queries, seed, device, cus, splits_override=0,
-                   table='random', lat_pool=0, loops=tuple(range(LOOPS))):
+                   table='random', lat_pool=0, loops=tuple(range(LOOPS)), max_model_len=0):
     hist = workload_shape(kind, B, context, seed)
     print(f'bench: building workload {kind} B={B} queries={queries} max ctx={max(hist)} layers={layers} '
           f'pool={lat_pool} loops={loops} cus={cus}', file=sys.stderr, flush=True)
     wl = Workload(ops, layer, hist, queries, seed, device, cus, 'identity' if kind == 'single' else table, layers,
-                  lat_pool, splits_override, loops)
+                  lat_pool, splits_override, loops, max_model_len)
     torch.cuda.synchronize()
     return wl
 
@@ -443,7 +446,7 @@ def single_config(args, ops, layer, device, cus):
         cpu_tokens = min(cpu_tokens, queries) if cpu_tokens else 0
     B, context, layers = args.batch or B, args.context or context, args.layers or layers
     wl = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus, args.splits,
-                        args.table, pool, loops)
+                        args.table, pool, loops, args.max_model_len)
     out = secondary_metrics(name, kind, wl, B, context, queries, args.steps, args.warmup)
     out['cpu_baseline'] = None if args.no_cpu_baseline else cpu_baseline(wl, cpu_loops, cpu_tokens)
     print(json.dumps(out), flush=True)
@@ -879,7 +882,8 @@ def main():
     if args.workload != 'decode' and not args.kernel_only:
         return single_config(args, ops, layer, device, cus)
     B, context, layers = args.batch or 64, args.context or 8192, args.layers or LAYERS
-    wl = build_workload(ops, layer, 'decode', B, context, layers, 1, args.seed, device, cus, args.splits, args.table)
+    wl = build_workload(ops, layer, 'decode', B, context, layers, 1, args.seed, device, cus, args.splits, args.table,
+                        max_model_len=args.max_model_len)
     splits = wl.splits
     if args.kernel_only:
         us, us_reduce, nbytes = history_roofline(wl, iters=max(args.steps, 1), width=args.width)

@@ -552,9 +552,11 @@ void history_split(HistoryParams a) {
     chunk = split_chunk(a.ctx, a.T, cap, S, red_lds);
     find_item(a.ctx, a.T, cap, chunk, b, item_lds, item_lds + G::WAVES, t, s);
   }
-  if (S > 1 && b < a.T && wave == 0 && g == 0) {  // slots of row b past its work: an empty partial for stage 2
+  if (S > 1 && b < a.T) {  // slots of row b past its work: an empty partial for stage 2 (one contiguous range of
+                           // lse, written by the whole workgroup: hundreds of slots when the plan leaves most empty)
     const int used = a.plan ? a.plan[1 + b] : used_slots(a.ctx[b], cap, chunk);
-    for (int e = used; e < S; ++e) a.ws_lse[((int64_t)b * S + e) * kHeads + hq] = -INFINITY;
+    float* l0 = a.ws_lse + ((int64_t)b * S + used) * kHeads;
+    for (int i = tid; i < (S - used) * kHeads; i += G::THREADS) l0[i] = -INFINITY;
   }
   if (t < 0) return;  // past the end of the work list (uniform over the workgroup)
   const int n = (int)min((int64_t)a.ctx[t], cap);
