@@ -1599,11 +1599,13 @@ __global__ __launch_bounds__(64 * W) void decode_epilogue(EpilogueParams a) {
       bv[step][0] = ld16(brow + (int64_t)(8 * step) * a.b_sr);
       bv[step][1] = ld16(brow + (int64_t)(8 * step + 1) * a.b_sr);
     }
+    if (tid < TB) used_s[tid] = S;
     __syncthreads();
-    if (tid < TB) {
-      int u = 0;
-      while (u < S && slot_lse[tid][u] != -INFINITY) ++u;
-      used_s[tid] = u;
+    // a token's used slots end at its first slot with lse = -inf: every thread checks its slots for that boundary
+    // (a serial scan was one dependent LDS read per used slot)
+    for (int k = tid; k < TB * S; k += kThreads) {
+      const int tb = TB == 1 ? 0 : k / S, sl = k - tb * S;
+      if (slot_lse[tb][sl] == -INFINITY && (sl == 0 || slot_lse[tb][sl - 1] != -INFINITY)) atomicMin(&used_s[tb], sl);
     }
     __syncthreads();
     int used[IPT];
