@@ -157,8 +157,9 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per
     compute unit (8 keeps enough loads in flight to stream HBM on gfx950) make ``W = waves_per_cu * CUs / (width /
     128)`` busy workgroups. The kernel cuts every row in chunks sized so that about half of the ``num_tokens *
     slots`` workgroups get equal work whatever the row lengths (short rows use few slots, long rows many), so this
-    returns ``2 * ceil(W / num_tokens)`` slots, never more than two per ``min_keys_per_split`` keys of the longest
-    row nor 1024. The kernel's plan gives every item at least 8 tiles of 16 keys (128 keys), or 4 tiles in a step
+    returns ``2 * floor(W / num_tokens)`` slots (at least 2: the plan's ``num_tokens * slots / 2`` items never
+    exceed W, where a ceiling gave a few CUs a third item and the launch waited on them), never more than two per
+    ``min_keys_per_split`` keys of the longest row nor 1024. The kernel's plan gives every item at least 8 tiles of 16 keys (128 keys), or 4 tiles in a step
     of fewer than ``small_step_tiles`` tiles over all rows, where the history is latency-bound and shorter chains
     pay; a step that is that small even at the longest length (``num_tokens * ceil(max_seq_len / 16)`` below it)
     gets two slots per ``min_keys_per_split / 2`` keys, room for those 4-tile items. A function of constants and
@@ -175,7 +176,7 @@ def mi355x_kv_splits(max_seq_len, num_tokens, cu_count=256, width=512, waves_per
         return max(1, min(-(-2 * cu_count // groups), by_length, 1024))
     waves_per_split = max(1, width // 128)
     busy = -(-waves_per_cu * cu_count // waves_per_split)
-    by_occupancy = 2 * -(-busy // max(1, num_tokens))
+    by_occupancy = 2 * max(1, busy // max(1, num_tokens))
     small = max(1, num_tokens) * -(-max_seq_len // 16) < small_step_tiles
     keys = max(1, min_keys_per_split // 2) if small else min_keys_per_split
     by_length = max(1, 2 * -(-max_seq_len // keys))

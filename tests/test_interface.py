@@ -103,7 +103,9 @@ def test_mi355x_split_policy(ops):
     assert ops.mi355x_kv_splits(8192, 64, 256, width=128) == 64
     assert ops.mi355x_kv_splits(8192, 1, 256, width=512) == 256        # 512 tiles: 64-key slots
     assert ops.mi355x_kv_splits(8192, 2, 256, width=512) == 128        # 1024 tiles: 128-key slots
-    assert ops.mi355x_kv_splits(8227, 12, 256, width=512) == 86        # 4 x 3-token chunks: by occupancy
+    assert ops.mi355x_kv_splits(8227, 12, 256, width=512) == 84        # 4 x 3-token chunks: by occupancy
+    assert ops.mi355x_kv_splits(8192, 24, 256, width=512) == 42        # 504 items: at most two per CU
+    assert ops.mi355x_kv_splits(8192, 600, 256, width=512) == 2
     assert ops.mi355x_kv_splits(8227, 12, 256, width=256) == 130       # and by length
     assert ops.mi355x_kv_splits(4097, 4, 256, width=512) == 66         # 1028 tiles at the longest length
     # steps below 768 tiles even at the longest length: room for the plan's 4-tile items (64 keys per slot)
