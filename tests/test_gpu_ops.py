@@ -375,7 +375,9 @@ def _plan_restated(ctx, cap, S, qsl=None):
                                             (60, 66, True, 20000), (300, 32, True, 20000),
                                             # few-tile steps: the 4-tile floor (below 768 tiles) and the 8-tile one
                                             (3, 34, False, 1100), (2, 66, False, 2200), (4, 130, False, 4400),
-                                            (8, 128, False, 4400)])
+                                            (8, 128, False, 4400),
+                                            # more rows than the plan kernel keeps in LDS: lengths read from memory
+                                            (5000, 3, False, 20000)])
 def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped, hi):
     rng = np.random.default_rng(T * 1000 + S)
     ctx = rng.integers(hi // 2 if hi < 20000 else 0, hi, T).astype(np.int32)
