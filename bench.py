@@ -75,7 +75,7 @@ def parse():
     p.add_argument('--no-cpu-baseline', action='store_true')
     p.add_argument('--no-secondary', action='store_true',
                    help='decode: skip the other configurations (single decode, ragged, long context, multi-query Q=3 '
-                        'and Q=512) that the default run appends to the headline line under "configs"')
+                        'and Q=512) that the default run measures before the headline and reports under "configs"')
     p.add_argument('--precision', choices=('bf16', 'fp32', 'tf32'), default='bf16',
                    help='--workload khop: the history GEMM precision (fp32 / tf32: fp32 leaves and fp32 kernels)')
     p.add_argument('--seed', type=int, default=0)
@@ -384,13 +384,14 @@ def secondary_metrics(name, kind, wl, B, context, queries, steps, warmup):
 
 
 # The benchmark configurations besides the headline (name: workload, B, context, queries, layers, latent pool pages,
-# loops, CPU-baseline loops, CPU-baseline tokens per request). Layers are distinct caches run loop-major, so
+# loops, CPU-baseline loops, CPU-baseline tokens per request), in the order the default run measures them: the
+# long-context step first, which ran 2-4 % slower within about a minute of another heavy step on the box. Layers are distinct caches run loop-major, so
 # that a loop's history reads (over all the step's layers) exceed the 256 MB MALL as in the 24-layer model and no
 # loop re-reads the previous loop's rows from it; the ragged step reads its rows from 65,536-page pools per width.
 SECONDARY = (
-    ('single_b1_ctx1024', 'single', 1, 1024, 1, 1, 0, (1,), (1,), 0),
-    ('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, 1, 4, 65536, (0, 1, 2, 3), (0, 1, 2, 3), 0),
     ('long_b8_ctx32768', 'long', 8, 32768, 1, 4, 0, (0, 1, 2, 3), (0, 1, 2, 3), 0),
+    ('ragged_b32_ctx1024_8192', 'ragged', 32, 8192, 1, 4, 65536, (0, 1, 2, 3), (0, 1, 2, 3), 0),
+    ('single_b1_ctx1024', 'single', 1, 1024, 1, 1, 0, (1,), (1,), 0),
     ('prefill_b4_q3_ctx8192', 'prefill', 4, 8192, 3, 8, 0, (0, 1, 2, 3), (0, 1, 2, 3), 0),
     ('prefill_b4_q512_ctx8192', 'prefill', 4, 8192, 512, 8, 0, (0, 1, 2, 3), (0, 1), 16),
 )
@@ -881,6 +882,13 @@ def main():
     cus = pkg._lib.device_cus(0)
     if args.workload != 'decode' and not args.kernel_only:
         return single_config(args, ops, layer, device, cus)
+    others = None
+    if not args.no_secondary and not args.kernel_only:
+        # the other configurations go first: for about a minute after the 24-layer step (92 GB of caches written and
+        # streamed) HBM-bound work on the box ran 2-4 % slower (long context 378 against 364 us/layer, recovered
+        # after 60 s idle), while the step measured after them ran as fast as on a fresh box
+        print('bench: the other configurations', file=sys.stderr, flush=True)
+        others = measure_secondaries(ops, layer, args, device, cus, not args.no_cpu_baseline)
     B, context, layers = args.batch or 64, args.context or 8192, args.layers or LAYERS
     wl = build_workload(ops, layer, 'decode', B, context, layers, 1, args.seed, device, cus, args.splits, args.table,
                         max_model_len=args.max_model_len)
@@ -904,13 +912,6 @@ def main():
         print('bench: cpu baseline', file=sys.stderr, flush=True)
         base = cpu_baseline(wl, (0, 1))
     ref_splits = wl.ref_splits
-    others = None
-    if not args.no_secondary:
-        del wl
-        torch.cuda.synchronize()
-        torch.cuda.empty_cache()
-        print('bench: the other configurations', file=sys.stderr, flush=True)
-        others = measure_secondaries(ops, layer, args, device, cus, not args.no_cpu_baseline)
     result = {
         'metric': METRIC, 'value': round(us_layer, 3), 'unit': 'us/layer', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(ms, 4), 'higher_is_better': False, 'scaling': 'weak',
