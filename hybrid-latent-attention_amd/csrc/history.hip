@@ -146,10 +146,12 @@ __device__ __forceinline__ int used_slots(int32_t ctx, int64_t cap, int chunk) {
 // threads); `red` holds 2 * waves int64.
 __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_t* red, bool fill = false) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, waves = blockDim.x >> 6;
+  const bool one = T <= (int)blockDim.x;  // one row per thread: its tiles stay in a register
+  const int my_tiles = tid < T ? row_tiles(ctx[tid], cap) : 0;
   int mx = 0;
   int64_t sum = 0;
   for (int i = tid; i < T; i += blockDim.x) {
-    const int tiles = row_tiles(ctx[i], cap);
+    const int tiles = one ? my_tiles : row_tiles(ctx[i], cap);
     mx = max(mx, tiles);
     sum += tiles;
   }
@@ -174,7 +176,7 @@ __device__ int split_chunk(const int32_t* ctx, int T, int64_t cap, int S, int64_
   c = max(c, (int)min(m, (int64_t)(sum < kSmallStepTiles ? kMinChunkSmall : kMinChunk)));
   for (const int64_t target = slots / 2; c < m; ++c) {  // c and the sums are uniform over the block
     int64_t items = 0;
-    for (int i = tid; i < T; i += blockDim.x) items += (row_tiles(ctx[i], cap) + c - 1) / c;
+    for (int i = tid; i < T; i += blockDim.x) items += ((one ? my_tiles : row_tiles(ctx[i], cap)) + c - 1) / c;
     for (int off = 32; off > 0; off >>= 1) items += __shfl_xor(items, off);
     __syncthreads();  // every thread has read red
     if (lane == 0) red[wave] = items;
@@ -266,9 +268,12 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
   }
   for (int i = tid; i < ni; i += 256) rows[i] = -1;
   int total = 0;  // items of the step
+  const bool one = T <= 256;  // one row per thread: its slot count stays in a register for the list below
+  int my_used = 0;
   for (int r = tid; r < T; r += 256) {
     const int u = used_slots(ctx[r], cap, chunk);
     used[r] = u;
+    my_used = u;
     total += u;
   }
   for (int off = 32; off > 0; off >>= 1) total += __shfl_xor(total, off);
@@ -279,7 +284,7 @@ __global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int
   __syncthreads();
   for (int r0 = 0; r0 < T; r0 += 256) {  // rows in blocks of 256: exclusive prefix of the used slots
     const int r = r0 + tid;
-    const int u = r < T ? used[r] : 0;
+    const int u = r < T ? (one ? my_used : used[r]) : 0;
     int x = u;
     for (int off = 1; off < 64; off <<= 1) {
       const int v = __shfl_up(x, off);
