@@ -11,6 +11,7 @@
   the reference's op sequence, and a mixed step of decode rows and chunks of 2..15 tokens;
 * steps whose longest chunk has 2 or 3 tokens over ragged histories (one-token requests beside them, an empty
   history, padding);
+* a few-token decode step planned for a 32768-token model (hundreds of slots, mostly empty) and for its own length;
 * chunked prefill of 4 requests x 512 and x 128 tokens over 8,192 latent rows (the multi-query configuration at
   full size), sampled tokens of every request.
 
@@ -189,6 +190,19 @@ def test_ragged_decode_on_full_pools(ops, layer):
     assert max(int(case.tables[w].max()) for w in WIDTHS) > 65000
     splits = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
     _check(case, layer, ops, splits)
+
+
+def test_few_token_steps_planned_for_a_long_model(ops, layer):
+    """Three decode rows of 2048, 1500 and 40 history tokens (and a padding row) with the slot counts the policy gives
+    for a model length of 32768, as the adapter plans a step (hundreds of slots, of which the plan's 4-tile items
+    fill a few dozen per row: the empty ones get their lse from one coalesced range), and for the step's own length;
+    all four loops, both against the oracle and the same results either way."""
+    case = DeviceDecode([2048, 1500, 40], pad=1, seed=70)
+    wide = {w: ops.mi355x_kv_splits(32768, case.T, 256, width=w) for w in WIDTHS}
+    tight = {w: ops.mi355x_kv_splits(int(case.seq.max()), case.T, 256, width=w) for w in WIDTHS}
+    assert min(wide.values()) >= 256 and max(tight.values()) <= 66
+    wants = _check(case, layer, ops, wide)
+    _check(case, layer, ops, tight, wants=wants)
 
 
 def test_short_chunk_prefill(ops, layer):
