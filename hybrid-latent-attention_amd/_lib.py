@@ -13,7 +13,7 @@ import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get('HLA_S6_LIBRARY') or os.path.join(HERE, 'libhla_s6.so')   # override: another build
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 OK, EINVAL, EUNSUPPORTED, EWORKSPACE, ELAUNCH, EDEVICE = range(6)
 
@@ -52,6 +52,7 @@ SIGNATURES = {
                                     F32, I32, I32, P, I64, I64, P],
     'hla_s6_split_plan_ints': [I32, I32],
     'hla_s6_split_plan': [P, I32, I64, I32, P, I32, P, I64, P],
+    'hla_s6_split_plans': [P, I32, I64, I32, P, P, I32, P, P, P],
     'hla_s6_slot_mapping': [P, I64, I32, P, P, P, I32, I32, P, P],
     'hla_s6_store_rows': [P, I64, P, I64, I32, I32, P, P, I64, I64, I32, I64, P],
     'hla_s6_write_rows': [P, I32, I32, I64, P, I32, I64, P, I64, P, I64, P, P, P, I32, I64, P, I64, I64, I32, I64, P],

@@ -249,8 +249,17 @@ constexpr int kPlanGroup = 16;
 // prefill chunk: they read the same latent rows) list their items chunk-major within the request's range: the
 // tokens' copies of one chunk are consecutive items, land on one XCD at about the same time and read the chunk's
 // rows from HBM once, the other tokens' reads hitting the L2.
-__global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, int S,
-                                                         const int32_t* qsl, int R, int32_t* plan) {
+// Plans of one step for up to kMaxPlans slot counts (the latent widths' counts), one workgroup each: one launch.
+constexpr int kMaxPlans = 4;
+struct PlanSet {
+  int S[kMaxPlans];
+  int32_t* plan[kMaxPlans];
+};
+
+__global__ __launch_bounds__(256) void split_plan_kernel(const int32_t* ctx, int T, int64_t cap, PlanSet set,
+                                                         const int32_t* qsl, int R) {
+  const int S = set.S[blockIdx.x];
+  int32_t* plan = set.plan[blockIdx.x];
   __shared__ int64_t red[8];
   __shared__ int wsum[4];
   __shared__ int carry_s;
@@ -2200,6 +2209,32 @@ extern "C" int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits
   return num_tokens < 0 || num_splits < 1 ? -1 : hla::plan_ints(num_tokens, num_splits);
 }
 
+extern "C" int hla_s6_split_plans(const int32_t* ctx, int32_t num_tokens, int64_t cap, int32_t count,
+                                  const int32_t* num_splits, const int32_t* query_start_loc, int32_t num_reqs,
+                                  int32_t* const* plans, const int64_t* plan_lens, void* stream) {
+  using namespace hla;
+  HLA_REQUIRE(num_tokens >= 0 && cap >= 0 && count >= 1 && count <= kMaxPlans, HLA_S6_EINVAL,
+              "split_plans: bad token count, key capacity or plan count (1..%d)", kMaxPlans);
+  HLA_REQUIRE(num_splits && plans && plan_lens, HLA_S6_EINVAL, "split_plans: null host array");
+  PlanSet set{};
+  for (int i = 0; i < count; ++i) {
+    HLA_REQUIRE(num_splits[i] >= 1 && num_splits[i] <= kMaxSplits, HLA_S6_EINVAL,
+                "split_plans: slot count %d outside 1..%d", num_splits[i], kMaxSplits);
+    HLA_REQUIRE(num_tokens == 0 || plans[i], HLA_S6_EINVAL, "split_plans: null plan %d", i);
+    HLA_REQUIRE(plan_lens[i] >= plan_ints(num_tokens, num_splits[i]), HLA_S6_EINVAL,
+                "split_plans: plan %d has %lld ints, needs %lld", i, (long long)plan_lens[i],
+                (long long)plan_ints(num_tokens, num_splits[i]));
+    set.S[i] = num_splits[i];
+    set.plan[i] = plans[i];
+  }
+  if (num_tokens == 0) return HLA_S6_OK;
+  HLA_REQUIRE(ctx, HLA_S6_EINVAL, "split_plans: null ctx");
+  HLA_REQUIRE(!query_start_loc || num_reqs >= 1, HLA_S6_EINVAL, "split_plans: query_start_loc needs num_reqs >= 1");
+  hipLaunchKernelGGL(split_plan_kernel, dim3((unsigned)count), dim3(256), 0, as_stream(stream), ctx, num_tokens, cap,
+                     set, query_start_loc, num_reqs);
+  return check_launch("split_plans");
+}
+
 extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t cap, int32_t num_splits,
                                  const int32_t* query_start_loc, int32_t num_reqs, int32_t* plan, int64_t plan_len,
                                  void* stream) {
@@ -2211,8 +2246,11 @@ extern "C" int hla_s6_split_plan(const int32_t* ctx, int32_t num_tokens, int64_t
   HLA_REQUIRE(plan_len >= plan_ints(num_tokens, num_splits), HLA_S6_EINVAL, "split_plan: %lld ints, need %lld",
               (long long)plan_len, (long long)plan_ints(num_tokens, num_splits));
   HLA_REQUIRE(!query_start_loc || num_reqs >= 1, HLA_S6_EINVAL, "split_plan: query_start_loc needs num_reqs >= 1");
-  hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, as_stream(stream), ctx, num_tokens, cap, num_splits,
-                     query_start_loc, num_reqs, plan);
+  PlanSet set{};
+  set.S[0] = num_splits;
+  set.plan[0] = plan;
+  hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, as_stream(stream), ctx, num_tokens, cap, set,
+                     query_start_loc, num_reqs);
   return check_launch("split_plan");
 }
 
@@ -2419,9 +2457,12 @@ extern "C" int hla_s6_attend_decode_static(
   if (S > 1) {  // the step's split plan into the scratch (one small launch)
     HLA_REQUIRE(ctx_latent && query_start_loc && num_reqs >= 1, HLA_S6_EINVAL,
                 "attend_decode_static: null ctx_latent or query_start_loc");
+    PlanSet set{};
+    set.S[0] = num_splits;
+    set.plan[0] = plan;
     hipLaunchKernelGGL(split_plan_kernel, dim3(1), dim3(256), 0, st, ctx_latent, num_tokens,
-                       (int64_t)lat_bt_cols * block_size, num_splits, max_query_len > 1 ? query_start_loc : nullptr,
-                       num_reqs, plan);
+                       (int64_t)lat_bt_cols * block_size, set, max_query_len > 1 ? query_start_loc : nullptr,
+                       num_reqs);
     rc = check_launch("attend_decode_static: split plan");
     if (rc != HLA_S6_OK) return rc;
   }

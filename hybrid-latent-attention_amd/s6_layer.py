@@ -158,11 +158,17 @@ class StepContext:
 
     def split_plan(self, splits, cap):
         """The step's split plan of the latent history (``hla_s6_split_plan``) for ``splits`` slots per row and
-        ``cap`` addressable rows: one small launch per distinct (splits, cap) per step, read by every layer."""
+        ``cap`` addressable rows, read by every layer. The first request of a step makes, in the same launch, the
+        plans of the other latent widths' slot counts for the same ``cap`` (``hla_s6_split_plans``: the widths'
+        tables address the same pages), so a step computes its plans with one launch."""
         key = (int(splits), int(cap))
         if key not in self._plans:
             qsl = self.query_start_loc if self.max_query_len > 1 else None   # short chunks share rows
-            self._plans[key] = s6_ops.split_plan(self.ctx_latent, key[1], key[0], qsl)
+            others = sorted({self.kv_splits(w) for w in self.tables} - {key[0]} -
+                            {s for s, c in self._plans if c == key[1]})
+            counts = [key[0]] + [s for s in others if s > 1][:3]
+            for s, plan in zip(counts, s6_ops.split_plans(self.ctx_latent, key[1], counts, qsl)):
+                self._plans[(s, key[1])] = plan
         return self._plans[key]
 
     def slots(self, table, block_size):

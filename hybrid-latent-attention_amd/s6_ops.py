@@ -13,6 +13,8 @@ from __future__ import annotations
 
 from collections import namedtuple
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -301,6 +303,23 @@ def split_plan(ctx, cap, num_kv_splits, query_start_loc=None):
     _lib.call('hla_s6_split_plan', _lib.ptr(ctx), T, int(cap), splits, _lib.ptr(qsl),
               0 if qsl is None else qsl.shape[0] - 1, _lib.ptr(plan), plan.numel(), _lib.stream(ctx.device))
     return plan
+
+
+def split_plans(ctx, cap, splits, query_start_loc=None):
+    """The plans of ``split_plan`` for several slot counts over the same lengths (a step's latent widths run
+    different counts over the same rows) in one launch (``hla_s6_split_plans``, at most 4); returns them in the
+    order of ``splits``."""
+    _dev(ctx, query_start_loc)
+    ctx = _int('ctx', ctx, I32)
+    qsl = None if query_start_loc is None else _int('query_start_loc', query_start_loc, I32)
+    T, splits = ctx.shape[0], [int(s) for s in splits]
+    lib = _lib.load()
+    plans = [torch.empty(max(int(lib.hla_s6_split_plan_ints(T, s)), 1), dtype=I32, device=ctx.device) for s in splits]
+    n = len(plans)
+    _lib.call('hla_s6_split_plans', _lib.ptr(ctx), T, int(cap), n, (ctypes.c_int32 * n)(*splits), _lib.ptr(qsl),
+              0 if qsl is None else qsl.shape[0] - 1, (ctypes.c_void_p * n)(*[p.data_ptr() for p in plans]),
+              (ctypes.c_int64 * n)(*[p.numel() for p in plans]), _lib.stream(ctx.device))
+    return plans
 
 
 def history_reduce(partials):

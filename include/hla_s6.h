@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define HLA_S6_ABI_VERSION 10
+#define HLA_S6_ABI_VERSION 11
 
 #define HLA_S6_OK 0
 #define HLA_S6_EINVAL 1       /* bad shape, stride or argument            (Python: ValueError)   */
@@ -232,6 +232,13 @@ int64_t hla_s6_split_plan_ints(int32_t num_tokens, int32_t num_splits);
 int hla_s6_split_plan(const int32_t *ctx, int32_t num_tokens, int64_t cap, int32_t num_splits,
                       const int32_t *query_start_loc, int32_t num_reqs, int32_t *plan, int64_t plan_len,
                       void *stream);
+/* The plans of `count` (1..4) slot counts over the same ctx, cap and query_start_loc in one launch (one workgroup
+ * per plan): a step's latent widths run different slot counts over the same rows. `num_splits`, `plans` (device
+ * pointers) and `plan_lens` are host arrays of `count` entries; plan i equals hla_s6_split_plan's for
+ * num_splits[i]. No reference counterpart. */
+int hla_s6_split_plans(const int32_t *ctx, int32_t num_tokens, int64_t cap, int32_t count,
+                       const int32_t *num_splits, const int32_t *query_start_loc, int32_t num_reqs,
+                       int32_t *const *plans, const int64_t *plan_lens, void *stream);
 
 /* ---- a9: fused decode attention of one layer x loop --------------------------------------------------
  * Replaces the decode branch of s6_layer.attend (hla/vllm_latent/s6_layer.py:97-100,110-115):

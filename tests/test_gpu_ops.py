@@ -411,6 +411,47 @@ def test_split_plan_is_the_documented_balanced_list(ops, T, S, grouped, hi):
     assert sum(used) <= T * S // 2 or chunk == max(tiles)  # at most two items per CU at the policy's counts
 
 
+@pytest.mark.parametrize('T,counts,grouped', [(64, (16, 32), False), (8, (128, 256), False), (32, (32, 64, 3), False),
+                                               (60, (66, 130), True), (1, (34,), False)])
+def test_split_plans_of_several_slot_counts_in_one_launch(ops, T, counts, grouped):
+    """hla_s6_split_plans: every plan of the set equals hla_s6_split_plan's for its slot count (the widths of a
+    step over the same lengths), with and without the request grouping of short chunks."""
+    rng = np.random.default_rng(T + 7)
+    ctx = rng.integers(1, 20000, T).astype(np.int32)
+    qsl = None
+    if grouped:
+        lens = rng.integers(1, 5, T)
+        qsl = np.concatenate(([0], np.cumsum(lens)))
+        qsl = qsl[qsl <= T].astype(np.int32)
+        for k in range(len(qsl) - 1):
+            ctx[qsl[k]:qsl[k + 1]] = ctx[qsl[k]]
+    ctx_d, qsl_d = dev_i32(ctx), None if qsl is None else dev_i32(qsl)
+    cap = 16 * 1500
+    plans = ops.split_plans(ctx_d, cap, counts, qsl_d)
+    for S, plan in zip(counts, plans):
+        want = ops.split_plan(ctx_d, cap, S, qsl_d).cpu().numpy()
+        got = plan.cpu().numpy()
+        ni = (len(want) - 1 - T) // 2
+        rows = want[1 + T:1 + T + ni]
+        assert (got[:1 + T + ni] == want[:1 + T + ni]).all(), S      # chunk, slot counts, item rows
+        live = rows >= 0                                              # item slots (unused items leave theirs unset)
+        assert (got[1 + T + ni:][live] == want[1 + T + ni:][live]).all(), S
+
+
+def test_split_plans_reject_bad_sets(ops):
+    ctx = torch.ones(4, dtype=torch.int32, device='cuda')
+    plan = torch.empty(3, dtype=torch.int32, device='cuda')
+    arr = lambda ct, *v: (ct * len(v))(*v)
+    import ctypes
+    with pytest.raises(ValueError, match='needs'):
+        ops._lib.call('hla_s6_split_plans', ctx.data_ptr(), 4, 1024, 1, arr(ctypes.c_int32, 8), None, 0,
+                      arr(ctypes.c_void_p, plan.data_ptr()), arr(ctypes.c_int64, plan.numel()), ops._lib.stream())
+    with pytest.raises(ValueError, match='plan count'):
+        ops._lib.call('hla_s6_split_plans', ctx.data_ptr(), 4, 1024, 5, arr(ctypes.c_int32, 8, 8, 8, 8, 8), None, 0,
+                      arr(ctypes.c_void_p, *[plan.data_ptr()] * 5), arr(ctypes.c_int64, *[plan.numel()] * 5),
+                      ops._lib.stream())
+
+
 def test_split_plan_rejects_a_short_buffer(ops):
     plan = torch.empty(3, dtype=torch.int32, device='cuda')
     ctx = torch.ones(4, dtype=torch.int32, device='cuda')
