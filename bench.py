@@ -73,6 +73,9 @@ def parse():
                    help='only run a plain 1 GiB device copy three times (scales the FETCH_SIZE / WRITE_SIZE counters '
                         'of a PMC profile to bytes)')
     p.add_argument('--no-cpu-baseline', action='store_true')
+    p.add_argument('--settle', type=float, default=60.0,
+                   help='seconds of GPU idle between the heavy configurations of the default run (outside the timed '
+                        'regions; 0: none)')
     p.add_argument('--no-secondary', action='store_true',
                    help='decode: skip the other configurations (single decode, ragged, long context, multi-query Q=3 '
                         'and Q=512) that the default run measures before the headline and reports under "configs"')
@@ -384,8 +387,8 @@ def secondary_metrics(name, kind, wl, B, context, queries, steps, warmup):
 
 
 # The benchmark configurations besides the headline (name: workload, B, context, queries, layers, latent pool pages,
-# loops, CPU-baseline loops, CPU-baseline tokens per request), in the order the default run measures them: the
-# long-context step first, which ran 2-4 % slower within about a minute of another heavy step on the box. Layers are distinct caches run loop-major, so
+# loops, CPU-baseline loops, CPU-baseline tokens per request), in the order the default run measures them (each heavy
+# one after `--settle` seconds of GPU idle, see settle()). Layers are distinct caches run loop-major, so
 # that a loop's history reads (over all the step's layers) exceed the 256 MB MALL as in the 24-layer model and no
 # loop re-reads the previous loop's rows from it; the ragged step reads its rows from 65,536-page pools per width.
 SECONDARY = (
@@ -417,21 +420,40 @@ def build_workload(ops, layer, kind, B, context, layers, queries, seed, device, 
     return wl
 
 
+def settle(seconds, last, name):
+    """Idle the GPU until ``seconds`` have passed since the previous heavy measurement ended (``last``, a
+    time.monotonic() stamp; None: nothing measured yet). Within about a minute of a heavy HBM-bound step the next
+    one ran 2-4 % slower on the MI355X (ragged decode 271.8 against 261-264 us/layer right after the long-context
+    step), and 60 s idle restored the fresh-device rate. The wait is outside every timed region and overlaps the
+    previous configuration's CPU baseline."""
+    if last is None or seconds <= 0:
+        return
+    wait = seconds - (time.monotonic() - last)
+    if wait > 0:
+        print(f'bench: {wait:.0f} s idle before {name}', file=sys.stderr, flush=True)
+        time.sleep(wait)
+
+
 def measure_secondaries(ops, layer, args, device, cus, with_cpu):
     """Every configuration of SECONDARY, one after another (each workload freed before the next is built): a dict
-    of their metrics (with their CPU baselines) for the headline line."""
+    of their metrics (with their CPU baselines) for the headline line, and when the last heavy one ended."""
     out = {}
+    last = None
     for name, kind, B, context, queries, layers, pool, loops, cpu_loops, cpu_tokens in SECONDARY:
         wl = build_workload(ops, layer, kind, B, context, layers, queries, args.seed, device, cus, lat_pool=pool,
                             loops=loops)
+        if kind != 'single':
+            settle(args.settle, last, name)
         out[name] = secondary_metrics(name, kind, wl, B, context, queries, args.steps, args.warmup)
+        if kind != 'single':
+            last = time.monotonic()
         if with_cpu:
             print(f'bench: cpu baseline of {name}', file=sys.stderr, flush=True)
             out[name]['cpu_baseline'] = cpu_baseline(wl, cpu_loops, cpu_tokens)
         del wl
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
-    return out
+    return out, last
 
 
 def single_config(args, ops, layer, device, cus):
@@ -882,13 +904,13 @@ def main():
     cus = pkg._lib.device_cus(0)
     if args.workload != 'decode' and not args.kernel_only:
         return single_config(args, ops, layer, device, cus)
-    others = None
+    others, last = None, None
     if not args.no_secondary and not args.kernel_only:
         # the other configurations go first: for about a minute after the 24-layer step (92 GB of caches written and
-        # streamed) HBM-bound work on the box ran 2-4 % slower (long context 378 against 364 us/layer, recovered
-        # after 60 s idle), while the step measured after them ran as fast as on a fresh box
+        # streamed) HBM-bound work ran 2-4 % slower (long context 378 against 364 us/layer, recovered after 60 s
+        # idle); each heavy measurement, this step's included, starts after `--settle` seconds of idle
         print('bench: the other configurations', file=sys.stderr, flush=True)
-        others = measure_secondaries(ops, layer, args, device, cus, not args.no_cpu_baseline)
+        others, last = measure_secondaries(ops, layer, args, device, cus, not args.no_cpu_baseline)
     B, context, layers = args.batch or 64, args.context or 8192, args.layers or LAYERS
     wl = build_workload(ops, layer, 'decode', B, context, layers, 1, args.seed, device, cus, args.splits, args.table,
                         max_model_len=args.max_model_len)
@@ -899,6 +921,7 @@ def main():
                           'us_per_launch': us, 'gbps': nbytes / us / 1e3, 'reduce_us': us_reduce}), flush=True)
         return
 
+    settle(args.settle, last, 'the decode step')
     print('bench: capturing the decode step', file=sys.stderr, flush=True)
     ms = time_graph(wl.step, args.steps, args.warmup)
     us_layer = ms * 1000 / layers
