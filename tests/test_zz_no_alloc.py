@@ -21,13 +21,17 @@ ops = importlib.import_module('hybrid-latent-attention_amd.s6_ops')
 
 
 class Step:
-    """One decode step of ``len(hist)`` requests (+ ``pad`` padding rows) at one latent width, caches on the device."""
+    """One step of ``len(hist)`` requests (+ ``pad`` padding rows) at one latent width, caches on the device: decode
+    (one token per request), or ``lens[r]`` tokens of request r (short prefill chunks, whose keys the exact cache
+    holds)."""
 
-    def __init__(self, hist, pad, width, splits, seed):
+    def __init__(self, hist, pad, width, splits, seed, lens=None):
         g = torch.Generator(device='cuda').manual_seed(seed)
-        self.R, self.T, self.w, self.splits = len(hist), len(hist) + pad, width, splits
         hist = np.asarray(hist)
-        seq = hist + 1
+        lens = np.ones(len(hist), np.int64) if lens is None else np.asarray(lens, np.int64)
+        self.R, self.n, self.Q, self.w, self.splits = len(hist), int(lens.sum()), int(lens.max()), width, splits
+        self.T = self.n + pad
+        seq = hist + lens
         cols = int(-(-seq.max() // BLOCK))
         pool = self.R * cols + 1
         rnd = lambda *s, std=1.0: (torch.randn(*s, generator=g, device='cuda') * std).to(torch.bfloat16)
@@ -40,11 +44,11 @@ class Step:
         self.q_lat = rnd(self.T, H, width, std=width ** -0.5)
         self.q_rope = rnd(self.T, H, D)
         self.B = rnd(H, width, D, std=1 / math.sqrt(2048))
-        positions = np.concatenate((hist, np.ones(pad, np.int64)))
+        positions = np.concatenate([np.arange(h, h + n) for h, n in zip(hist, lens)] + [np.ones(pad, np.int64)])
+        qsl = np.concatenate(([0], np.cumsum(lens))).astype(np.int32)
         ws = ops.S6Workspace(H, width, self.T * splits)
-        self.ctx = layer.StepContext(torch.as_tensor(positions, device='cuda'),
-                                     torch.arange(self.R + 1, dtype=torch.int32, device='cuda'),
-                                     torch.as_tensor(seq.astype(np.int32), device='cuda'), 1, self.T, {}, SCALE,
+        self.ctx = layer.StepContext(torch.as_tensor(positions, device='cuda'), torch.as_tensor(qsl, device='cuda'),
+                                     torch.as_tensor(seq.astype(np.int32), device='cuda'), self.Q, self.T, {}, SCALE,
                                      ops.HIP_BACKENDS, ws, splits, window=W, max_seqlen_k=int(seq.max()))
         A = rnd(H, D, width)
         if width == 512:
@@ -69,8 +73,8 @@ class Step:
                  lib.ptr(ex), lib.ptr(ex[..., d:]), ex.stride(0), ex.stride(2), ex.stride(1), ex.shape[2],
                  ex.shape[0], lib.ptr(self.ex_table), self.ex_table.stride(0), self.ex_table.shape[1],
                  lib.ptr(ctx.query_start_loc), lib.ptr(ctx.seq_lens), self.R, W, lib.ptr(self.B), self.B.stride(0),
-                 self.B.stride(1), lib.ptr(ctx.invalid), self.T, H, SCALE, self.splits, 1, lib.ptr(out), out.stride(0),
-                 out.stride(1), lib.stream(out.device))
+                 self.B.stride(1), lib.ptr(ctx.invalid), self.T, H, SCALE, self.splits, self.Q, lib.ptr(out),
+                 out.stride(0), out.stride(1), lib.stream(out.device))
         return out
 
 
@@ -113,10 +117,27 @@ def test_static_entry_equals_the_allocating_one_on_two_calls():
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all(), name
         assert torch.equal(got, want), f'{name}: max diff {(got.float() - want.float()).abs().max().item()}'
-        assert (got[step.R:] == 0).all()
+        assert (got[step.n:] == 0).all()
     # one slot: the one-slot history output and lse also live in the array
     one = Step([1500, 300, 0], pad=0, width=512, splits=1, seed=3)
     assert torch.equal(one.static(), one.allocating())
+
+
+def test_static_entry_on_short_chunks():
+    """Steps of short prefill chunks (the static entry's plan then lists a request's tokens chunk by chunk, as the
+    step's own plan does): 4 x 3 tokens over about 8,000 history rows, then a smaller mixed step (decode rows and
+    chunks of 2 .. 15 tokens, padding) at the narrower latent; each bitwise equal to the allocating entry point."""
+    chunks = Step([8200, 7900, 8100, 8050], pad=2, width=512, splits=64, seed=6, lens=[3, 3, 3, 3])
+    mixed = Step([3000, 17, 900, 0, 1200], pad=3, width=256, splits=16, seed=7, lens=[1, 15, 4, 2, 1])
+    for name, step in (('4 x 3 tokens, width 512, 64 slots', chunks),
+                       ('chunks of 1 .. 15 tokens, width 256, 16 slots', mixed)):
+        print(f'case {name}', flush=True)
+        want = step.allocating()
+        got = step.static()
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all(), name
+        assert torch.equal(got, want), f'{name}: max diff {(got.float() - want.float()).abs().max().item()}'
+        assert (got[step.n:] == 0).all()
 
 
 def refusal_args(num_tokens, num_splits, width=512):
