@@ -38,7 +38,6 @@ constexpr int kSplitWavesPerEu = 3;
 
 constexpr int kHeads = 16;
 constexpr int kTile = 16;
-constexpr int kThreads = 256;
 constexpr int kMaxSplits = 1024;
 
 struct WindowPart {  // decode exact window, computed by the extra row of workgroups
@@ -1506,7 +1505,7 @@ constexpr int kEpiSlots = TB == 1 ? kMaxSplits : 256;
 
 template <int R, int TB, int W>
 __global__ __launch_bounds__(64 * W) void decode_epilogue(EpilogueParams a) {
-  constexpr int kThreads = 64 * W;  // W waves (shadows the file's 4-wave default)
+  constexpr int kThreads = 64 * W;  // W waves
   constexpr int D = kExactDim, C4 = R / 4;
   constexpr int ITEMS = TB * C4;                               // combine items (token, 4 columns)
   constexpr int IPT = ITEMS > kThreads ? ITEMS / kThreads : 1;  // items per thread

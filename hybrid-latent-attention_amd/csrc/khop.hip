@@ -630,7 +630,6 @@ __global__ __launch_bounds__(kKhThreads) void khop_dkdv(KhopParams a) {
   __shared__ __attribute__((aligned(16))) floatx4 sx[8][64];
   __shared__ __attribute__((aligned(16))) uint16_t pt[kKhKeys * kKhPS];
   __shared__ __attribute__((aligned(16))) uint16_t dst[kKhKeys * kKhPS];
-  __shared__ int skip_s;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int b = blockIdx.y, kt = blockIdx.x * kKhKeys, split = blockIdx.z;
